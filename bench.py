@@ -1,0 +1,269 @@
+"""Benchmark of the weight-quantized linear path on one MI355X.
+
+Headline (BASELINE.json `metric`, config 2): the W4A16 group-128 decode GEMV,
+M=1, K=4096, N=14336 (Llama-3-8B MLP up/gate), as GB/s of algorithmic bytes
+(packed weight + bf16 scales + u8 zeros + x + y) against HBM peak. A "step" is
+one `lnq_int4_linear` call over one batch (one token) with every operand
+resident in HBM; the steps rotate over enough distinct weight copies (> 256 MB,
+the Infinity Cache) that each call streams its weight from HBM. Launches are
+recorded in a HIP graph and replayed, and the timed region is bracketed by HIP
+events on the stream the kernels run on.
+
+Also reported (extra keys): M=4 and M=16 GEMV, the prefill dequant-GEMM
+(config 3: M=2048 over three (K, N)) in TFLOP/s against bf16 MFMA peak beside
+the reference's own prefill strategy (HIP dequantize + hipBLASLt), a measured
+copy-bandwidth ceiling, and the reference's CPU path timed on the host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|all]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+L3_BYTES = 256 << 20  # Infinity Cache
+
+
+def gemv_bytes(m: int, k: int, n: int, group: int = 128) -> int:
+    """Algorithmic bytes of one W4A16 call: N*K/2 packed + N*K/G*2 scales +
+    N*K/G zeros + M*K*2 x + M*N*2 y."""
+    return n * k // 2 + n * (k // group) * 2 + n * (k // group) + m * k * 2 + m * n * 2
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--only", choices=("gemv", "gemm", "all"), default="all")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    return p.parse_args()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the weight-quantized linear path runs on one MI355X "
+              f"(sharding is described, not run); got --gpus {args.gpus}", file=sys.stderr)
+        return 2
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from linnet_amd.torch import kernels
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    props = torch.cuda.get_device_properties(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed_graph(launches: list, steps: int, warmup: int) -> float:
+        """Seconds per launch: the launches recorded once into a HIP graph,
+        replayed until `steps` launches ran, timed by HIP events on the stream."""
+        for f in launches:
+            f()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for f in launches:
+                f()
+        reps = max(1, -(-steps // len(launches)))
+        for _ in range(max(1, warmup // len(launches))):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / 1e3 / (reps * len(launches))
+
+    def int4_layers(n: int, k: int, copies: int, seed: int = 0):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        w = torch.randn(n, k, generator=g, device=dev) * 0.02
+        packed, scale, zero = kernels.quantize_int4(w, 128)
+        del w
+        layers = [(packed, scale.to(torch.bfloat16), zero)]
+        for _ in range(copies - 1):
+            layers.append(tuple(t.clone() for t in layers[0]))
+        return layers
+
+    result: dict[str, object] = {}
+    extra: dict[str, object] = {}
+
+    # --- copy ceiling (1 GiB device-to-device copy).
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    copy_s = timed_graph([lambda: dst.copy_(src)], 20, 4)
+    copy_gbps = 2 * src.numel() / copy_s / 1e9
+    del src, dst
+    extra["copy_gbps"] = round(copy_gbps, 1)
+
+    k, n = 4096, 14336
+    per_copy = gemv_bytes(1, k, n)
+    copies = max(10, -(-(L3_BYTES + (64 << 20)) // per_copy))
+    gemv: dict[str, object] = {}
+    headline = None
+    if args.only in ("gemv", "all"):
+        layers = int4_layers(n, k, copies)
+        g = torch.Generator(device=dev).manual_seed(1)
+        for m in (1, 4, 16):
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            launches = [lambda l=l, x=x: kernels.int4_linear(x, *l) for l in layers]
+            sec = timed_graph(launches, args.steps, args.warmup)
+            gbps = gemv_bytes(m, k, n) / sec / 1e9
+            gemv[f"M{m}"] = {"us": round(sec * 1e6, 3), "gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
+            if m == 1:
+                headline = (sec, gbps)
+        extra["gemv"] = gemv
+        extra["gemv_weight_copies"] = copies
+        del layers
+
+    gemm: dict[str, object] = {}
+    if args.only in ("gemm", "all"):
+        m = 2048
+        g = torch.Generator(device=dev).manual_seed(2)
+        for kk, nn in ((4096, 4096), (4096, 14336), (14336, 4096)):
+            copies_g = max(2, -(-L3_BYTES // (nn * kk // 2 + m * kk * 2)))
+            layers = int4_layers(nn, kk, min(copies_g, 8), seed=3)
+            x = torch.randn(m, kk, generator=g, device=dev).to(torch.bfloat16)
+            ch = max(1, int(0.001 * kk) + (1 if 0.001 * kk % 1 else 0))
+            cols = torch.randperm(kk, generator=torch.Generator().manual_seed(0))[:ch].to(dev)
+            x[:, cols] *= 20
+            flops = 2 * m * nn * kk
+            fused = [lambda l=l: kernels.int4_linear(x, *l) for l in layers]
+            sec = timed_graph(fused, max(8, args.steps // 10), 4)
+            w_deq = [None]
+
+            def dequant_blas(l=layers[0]):
+                w = kernels.int4_weight(*l)
+                return torch.nn.functional.linear(x, w)
+
+            sec_ref = timed_graph([dequant_blas], max(8, args.steps // 10), 4)
+            w = kernels.int4_weight(*layers[0])
+            sec_blas = timed_graph([lambda: torch.nn.functional.linear(x, w)], max(8, args.steps // 10), 4)
+            del w, w_deq, layers
+            gemm[f"K{kk}_N{nn}"] = {
+                "us": round(sec * 1e6, 2),
+                "tflops": round(flops / sec / 1e12, 1),
+                "frac_bf16_peak": round(flops / sec / 1e12 / BF16_PEAK_TFLOPS, 4),
+                "dequant_hipblaslt_tflops": round(flops / sec_ref / 1e12, 1),
+                "hipblaslt_bf16_only_tflops": round(flops / sec_blas / 1e12, 1),
+            }
+        extra["gemm_M2048"] = gemm
+    torch.cuda.synchronize()
+
+    # --- CPU baseline: the reference's CPU path (generated source: the weight
+    # dequantized once at prepare, then bf16 F.linear per call), on host cores.
+    cpu = None
+    if not args.no_cpu and args.only in ("gemv", "all"):
+        cpu = cpu_baseline(k, n, args.cpu_seconds)
+
+    if headline is not None:
+        sec, gbps = headline
+        metric_value, unit, ms = gbps, "GB/s", sec * 1e3
+        config = {"workload": "int4 g128 W4A16 decode GEMV (linear_int4_groups)", "M": 1, "K": k, "N": n,
+                  "group": 128, "dtype": "bf16 activations, bf16 scales, u8 zeros", "baseline_config": 2}
+        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic_from_profiles("int4_skinny_M1"),
+                    "kernel": "int4_skinny_kernel<bf16,16,1>", "bytes_per_launch": gemv_bytes(1, k, n)}
+    else:
+        key = next(iter(gemm))
+        entry = gemm[key]
+        metric_value, unit, ms = entry["tflops"], "TFLOP/s", entry["us"] / 1e3
+        config = {"workload": f"int4 g128 prefill dequant-GEMM M=2048 {key}", "baseline_config": 3}
+        roofline = {"bound": "mfma", "achieved": entry["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": entry["frac_bf16_peak"], "traffic": None}
+    result = {
+        "metric": "W4A16 decode GEMV GB/s (% HBM peak); prefill qGEMM TFLOP/s (% MFMA peak)",
+        "value": round(float(metric_value), 2),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: weights N(0,0.02) quantized int4 g128 on the GPU, x N(0,1) bf16, seeded",
+        "config": config,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "device": {"name": props.name, "arch": getattr(props, "gcnArchName", ""), "cus": props.multi_processor_count},
+        **extra,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+def traffic_from_profiles(name: str) -> float | None:
+    """HBM bytes per launch measured by rocprofv3 PMC runs and committed under
+    profiles/traffic.json (None until such a measurement exists)."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        table = json.loads(path.read_text())
+        value = table.get(name, {}).get("hbm_bytes_per_launch")
+        return None if value is None else float(value)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(k: int, n: int, budget_s: float) -> dict[str, object]:
+    """The reference's CPU path on the host cores, on the full layer: the weight
+    dequantized once (prepare), then per call a bf16 `F.linear` of one token
+    (`src/backend/torch_source.cpp:1501-1504, 1567-1568`). Median over as many
+    calls as fit the budget (at least 3, after 1 warmup). The interpreter path
+    (dequantize every call, `torch/native.py:417-423`) is timed once beside it."""
+    import numpy as np
+    import torch
+
+    from oracle import linear, quant
+
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS"):
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
+    packed, scale, zero = quant.quantize_int4_groups(w, 128)
+    del w
+    p = torch.from_numpy(packed)
+    s = torch.from_numpy(quant.to_bf16_bits(scale).view(np.int16)).view(torch.bfloat16)
+    z = torch.from_numpy(zero)
+    x = torch.randn(1, k, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    prepared = linear.int4_prepare_cpu(p, s, z)
+    linear.int4_linear_generated_cpu(x, prepared, None)
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        linear.int4_linear_generated_cpu(x, prepared, None)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    t0 = time.perf_counter()
+    linear.int4_groups_linear_interpreter(x, p, s, z, None)
+    interp = time.perf_counter() - t0
+    nbytes = gemv_bytes(1, k, n)
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"full layer K={k} N={n} M=1, reference CPU generated-source path (bf16 F.linear over the "
+                   f"prepared weight), median of {len(times)} calls = {med * 1e3:.2f} ms; interpreter path "
+                   f"(dequantize per call) 1 call = {interp * 1e3:.1f} ms = {nbytes / interp / 1e9:.3f} GB/s"),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

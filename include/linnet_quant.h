@@ -1,0 +1,154 @@
+/* linnet_quant.h -- C ABI of the MI355X (gfx950) weight-quantized linear kernels.
+ *
+ * The boundary of `liblinnet_quant_hip.so`: plain pointers to device memory,
+ * element counts and a HIP stream. No PyTorch types cross it. Conventions follow
+ * the reference's native runtime ABI (include/linnet/runtime/runtime.h):
+ *
+ *   - every entry point returns a status: LNQ_OK 0, LNQ_ERROR 1, LNQ_UNAVAILABLE 2
+ *     (runtime.h:37-40), and on failure leaves a message for lnq_last_error(),
+ *     a thread-local string (runtime.h:99, runtime.cpp:28);
+ *   - work is enqueued on `stream` (a hipStream_t; NULL is the null stream) and the
+ *     call returns without waiting for it, as LnExecutable.execute does
+ *     (runtime.h:79-94); no entry point allocates device memory or synchronizes,
+ *     so every call may be recorded into a HIP graph;
+ *   - tensors are borrowed: caller-owned, contiguous, row-major.
+ *
+ * Each entry point below names the reference interface it replaces (paths are
+ * relative to the reference checkout; the Python package is python/linnet/src/linnet).
+ */
+#ifndef LINNET_QUANT_H
+#define LINNET_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LNQ_API __attribute__((visibility("default")))
+
+#define LNQ_ABI_VERSION 1
+
+typedef int32_t LnqStatus;
+#define LNQ_OK 0
+#define LNQ_ERROR 1
+#define LNQ_UNAVAILABLE 2 /* not on this device */
+
+/* Element types of activations, scales and outputs. */
+#define LNQ_BF16 0
+#define LNQ_F16 1
+#define LNQ_F32 2
+
+/* Kernel families lnq_int4_linear may be told to use (LNQ_KERNEL_AUTO picks by rows). */
+#define LNQ_KERNEL_AUTO 0
+#define LNQ_KERNEL_SKINNY 1 /* dequant-GEMV/skinny GEMM on MFMA, rows <= 64 */
+#define LNQ_KERNEL_TILED 2  /* prefill dequant-GEMM, LDS-staged bf16 tiles on MFMA */
+
+/* The ABI version this library implements (LNQ_ABI_VERSION). */
+LNQ_API uint32_t lnq_abi_version(void);
+
+/* The message of the last failed call on this thread ("" if none). */
+LNQ_API const char* lnq_last_error(void);
+
+/* Number of GPUs HIP sees, and whether device `device` is a gfx950 (1) or not (0). */
+LNQ_API LnqStatus lnq_device_probe(int32_t device, int32_t* is_gfx950, int32_t* compute_units);
+
+/* ---------------------------------------------------------------- int4 groups
+ * Layout of std.quant::Int4GroupLinear (stdlib/quant.linnet:156-175):
+ *   packed [out, in/group, group/2] u8, element 2k in the low nibble;
+ *   scale  [out, in/group] in `dtype`;  zero [out, in/group] u8 in 0..15;
+ *   weight[o, i] = (q[o, i] - zero[o, i/group]) * scale[o, i/group].
+ */
+
+/* y[rows, out] = x[rows, in] @ W^T (+ bias[out]), x/scale/bias/y of `dtype` (bf16 or
+ * f16), summed in f32, rounded once to `dtype`; with a bias, the rounded product plus
+ * the bias rounded again (the reference adds the bias after the product).
+ * in % 128 == 0; group 32, 64 or a multiple of 128 dividing `in`.
+ * Replaces: kernels.py:277-323 `int4_linear` and the generated `_int4_linear`
+ * (src/backend/torch_source.cpp:1553-1570; tinygemm below 8 rows, Triton to 128,
+ * dequant + cuBLAS above). */
+LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const void* scale,
+                                  const uint8_t* zero, const void* bias, void* y, int64_t rows,
+                                  int64_t in_features, int64_t out_features, int64_t group,
+                                  int32_t dtype, int32_t kernel, void* stream);
+
+/* out[out, in] = (q - zero) * scale computed in f32 and rounded once to `dtype`
+ * (the scale's dtype: bf16, f16 or f32). Any even group dividing `in`.
+ * Replaces: `_int4_unpack`/`_int4_weight` (torch_source.cpp:1518-1550) and the
+ * dequantized branch of `_int4_pack` (torch_source.cpp:1501-1504). */
+LNQ_API LnqStatus lnq_int4_dequantize(const uint8_t* packed, const void* scale,
+                                      const uint8_t* zero, void* out, int64_t out_features,
+                                      int64_t in_features, int64_t group, int32_t dtype,
+                                      void* stream);
+
+/* Round-to-nearest asymmetric 4-bit quantization of an f32 weight [out, in], bit for
+ * bit as numpy does it: scale = (max - min) / 15 (0 -> 1), zero = clip(rint(-min /
+ * scale), 0, 15), q = clip(rint(w / scale) + zero, 0, 15); writes packed [out, in/2]
+ * u8, scale [out, in/group] f32, zero [out, in/group] u8.
+ * Replaces: linnet/quant.py:83-99 `quantize_int4_groups` + :242-248 `pack_int4_groups`. */
+LNQ_API LnqStatus lnq_int4_quantize(const float* weight, uint8_t* packed, float* scale,
+                                    uint8_t* zero, int64_t out_features, int64_t in_features,
+                                    int64_t group, void* stream);
+
+/* Codes (any integer bytes, wrapped to 4 bits) two a byte, low first: packed[i] =
+ * (codes[2i] & 15) | (codes[2i+1] & 15) << 4, for `pairs` bytes.
+ * Replaces: torch/packed.py:61-75 `pack4` (i4/u4) and quant.py:242-248. */
+LNQ_API LnqStatus lnq_int4_pack(const uint8_t* codes, uint8_t* packed, int64_t pairs,
+                                void* stream);
+
+/* The inverse: 2*pairs codes, u4 as uint8 (is_signed 0) or i4 sign-extended to int8
+ * (is_signed 1). Replaces: torch/packed.py:27-35 `unpack4` (i4/u4). */
+LNQ_API LnqStatus lnq_int4_unpack(const uint8_t* packed, void* codes, int64_t pairs,
+                                  int32_t is_signed, void* stream);
+
+/* ----------------------------------------------------------------- 8-bit
+ * Weights [out, in] of int8 (fp8 0) or FP8 E4M3 bytes (fp8 1). Scales (f32): one per
+ * row ([out], group 0), or [out/row_block, in/group] (int8 groups: row_block 1;
+ * FP8 blocks: group = row_block = block).
+ */
+
+/* Symmetric int8 quantization of an f32 weight [out, in] in groups of `group` inputs:
+ * scale = max|w| / 127 (0 -> 1) rounded to `scale_dtype` first, q = clip(rint(w /
+ * scale), -127, 127); scale written as f32 [out, in/group].
+ * Replaces: linnet/quant.py:102-121 `quantize_int8_groups`. */
+LNQ_API LnqStatus lnq_int8_quantize(const float* weight, int8_t* q, float* scale,
+                                    int64_t out_features, int64_t in_features, int64_t group,
+                                    int32_t scale_dtype, void* stream);
+
+/* y[rows, out] = x[rows, in] @ (w * scale)^T with the weight widened in registers and
+ * x unrounded, f32 sums, rounded once to `dtype`; per-row scales multiply the sum,
+ * group scales each group. in % 128 == 0 (and % group).
+ * Replaces: kernels.py:375-434 `gemv8` (rows 1) and :437-592 `w8a16` (rows <= 64). */
+LNQ_API LnqStatus lnq_w8a16(const void* x, const uint8_t* weight, const float* scale, void* y,
+                            int64_t rows, int64_t out_features, int64_t in_features,
+                            int32_t fp8, int64_t group, int64_t row_block, int32_t dtype,
+                            void* stream);
+
+/* The 8-bit weight dequantized: out[o, i] = widen(w[o, i]) * scale, f32 product
+ * rounded once to `dtype`. Replaces: kernels.py:595-666 `dequantize8`. */
+LNQ_API LnqStatus lnq_dequantize8(const uint8_t* weight, const float* scale, void* out,
+                                  int64_t out_features, int64_t in_features, int32_t fp8,
+                                  int64_t group, int64_t row_block, int32_t dtype, void* stream);
+
+/* Each row of x [rows, in] (`dtype`) rounded to 8 bits with its own scale:
+ * scale[r] = max(max|x[r]|, 1e-12) / (448 | 127), q = e4m3(clamp(x / scale, +-448))
+ * rounded to nearest even, or int8 clamp(trunc(x / scale +- 0.5), +-127).
+ * Replaces: kernels.py:669-753 `fp8_rows` / `int8_rows`. */
+LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t rows,
+                            int64_t in_features, int32_t fp8, int32_t dtype, void* stream);
+
+/* y[rows, out] = (q[rows, in] @ w[out, in]^T) * x_scale[rows] * scale[out] in `dtype`:
+ * int8 x int8 summed exactly in int32 (fp8 0), or e4m3 x e4m3 summed in f32 (fp8 1),
+ * on MFMA. in % 128 == 0.
+ * Replaces: kernels.py:805-915 `int8_mm`, and `torch._scaled_mm` as
+ * torch/quantized.py:129 calls it (row scales, bf16/f16 out). */
+LNQ_API LnqStatus lnq_mm8(const uint8_t* q, const uint8_t* weight, const float* x_scale,
+                          const float* scale, void* y, int64_t rows, int64_t out_features,
+                          int64_t in_features, int32_t fp8, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LINNET_QUANT_H */

@@ -1,0 +1,90 @@
+"""ctypes binding of `liblinnet_quant_hip.so` (the C ABI in include/linnet_quant.h).
+
+The pattern follows the reference's own binding of its native runtime
+(`python/linnet/src/linnet/runtime.py:117-197`): load the library once,
+declare every entry point's argument types, and turn a non-zero status into
+an exception carrying `lnq_last_error()`.
+
+There is no fallback: a missing or unloadable library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+from .errors import LinnetError
+
+LIBRARY = Path(__file__).resolve().parent / "_lib" / "liblinnet_quant_hip.so"
+ABI_VERSION = 1
+
+LNQ_OK, LNQ_ERROR, LNQ_UNAVAILABLE = 0, 1, 2
+BF16, F16, F32 = 0, 1, 2
+KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED = 0, 1, 2
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+# Entry point -> argument types (the return type is always LnqStatus, int32).
+SIGNATURES: dict[str, list[object]] = {
+    "lnq_device_probe": [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
+    "lnq_int4_linear": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
+    "lnq_int4_dequantize": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "lnq_int4_quantize": [_p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "lnq_int4_pack": [_p, _p, _i64, _p],
+    "lnq_int4_unpack": [_p, _p, _i64, _i32, _p],
+    "lnq_int8_quantize": [_p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "lnq_w8a16": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _i64, _i32, _p],
+    "lnq_dequantize8": [_p, _p, _p, _i64, _i64, _i32, _i64, _i64, _i32, _p],
+    "lnq_rows8": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
+    "lnq_mm8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library, its entry points declared (loaded once per process)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIBRARY.exists():
+            raise LinnetError(
+                f"{LIBRARY.name} is not built: run `python -m linnet_amd._build` "
+                "(or __graft_entry__.build()) on a machine with hipcc"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIBRARY))
+        except OSError as error:
+            raise LinnetError(f"cannot load {LIBRARY}: {error}") from error
+        lib.lnq_abi_version.restype = ctypes.c_uint32
+        lib.lnq_abi_version.argtypes = []
+        lib.lnq_last_error.restype = ctypes.c_char_p
+        lib.lnq_last_error.argtypes = []
+        version = lib.lnq_abi_version()
+        if version != ABI_VERSION:
+            raise LinnetError(f"{LIBRARY.name} implements ABI {version}, this package needs {ABI_VERSION}")
+        for name, argtypes in SIGNATURES.items():
+            function = getattr(lib, name)
+            function.restype = ctypes.c_int32
+            function.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return (load().lnq_last_error() or b"").decode("utf-8", "replace")
+
+
+def call(name: str, *args: object) -> None:
+    """Calls entry point `name`; raises LinnetError with the library's message on failure."""
+    status = getattr(load(), name)(*args)
+    if status != LNQ_OK:
+        kind = "unavailable" if status == LNQ_UNAVAILABLE else "failed"
+        raise LinnetError(f"{name} {kind}: {last_error()}")

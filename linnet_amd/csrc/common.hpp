@@ -1,0 +1,163 @@
+// Shared helpers of the gfx950 weight-quantized linear kernels: vector types,
+// bf16/f16 conversions, wave reductions, and the C ABI's error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/linnet_quant.h"
+
+namespace lnq {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Error plumbing (abi.cpp): a thread-local message behind lnq_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// A failed HIP call becomes LNQ_ERROR with the call named.
+#define LNQ_HIP_CHECK(expr)                                                             \
+  do {                                                                                  \
+    hipError_t lnq_err_ = (expr);                                                       \
+    if (lnq_err_ != hipSuccess) {                                                       \
+      ::lnq::set_error("%s failed: %s", #expr, hipGetErrorString(lnq_err_));            \
+      return LNQ_ERROR;                                                                 \
+    }                                                                                   \
+  } while (0)
+
+#define LNQ_REQUIRE(cond, ...)          \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::lnq::set_error(__VA_ARGS__);    \
+      return LNQ_ERROR;                 \
+    }                                   \
+  } while (0)
+
+// The launch's own error, checked right after it is enqueued.
+inline LnqStatus launched(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(err));
+    return LNQ_ERROR;
+  }
+  clear_error();
+  return LNQ_OK;
+}
+
+inline bool aligned(const void* p, size_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+// ------------------------------------------------------------ conversions
+
+__host__ __device__ inline float bf16_bits_to_f32(uint32_t bits) {
+  return __builtin_bit_cast(float, bits << 16);
+}
+
+// f32 -> bf16 bits, round to nearest even (NaN kept NaN).
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ inline float f16_bits_to_f32(uint32_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Element type of activations / scales / outputs, as a compile-time tag.
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<LNQ_BF16> {
+  using storage = uint16_t;
+  // (MAGIC | q) as this type is MAGIC_VALUE + q for a 4-bit q.
+  static constexpr uint32_t MAGIC2 = 0x43004300u;  // bf16 128.0 in both halves
+  static constexpr float MAGIC_VALUE = 128.0f;
+  static constexpr uint32_t ONE2 = 0x3f803f80u;  // bf16 1.0 in both halves
+  __device__ static float load(const storage* p) { return bf16_bits_to_f32(*p); }
+  __device__ static float to_f32(storage v) { return bf16_bits_to_f32(v); }
+  __device__ static storage from_f32(float f) { return f32_to_bf16_bits(f); }
+};
+
+template <>
+struct Elem<LNQ_F16> {
+  using storage = uint16_t;
+  static constexpr uint32_t MAGIC2 = 0x64006400u;  // f16 1024.0 in both halves
+  static constexpr float MAGIC_VALUE = 1024.0f;
+  static constexpr uint32_t ONE2 = 0x3c003c00u;  // f16 1.0 in both halves
+  __device__ static float load(const storage* p) { return f16_bits_to_f32(*p); }
+  __device__ static float to_f32(storage v) { return f16_bits_to_f32(v); }
+  __device__ static storage from_f32(float f) { return f32_to_f16_bits(f); }
+};
+
+template <>
+struct Elem<LNQ_F32> {
+  using storage = float;
+  __device__ static float load(const storage* p) { return *p; }
+  __device__ static float to_f32(storage v) { return v; }
+  __device__ static storage from_f32(float f) { return f; }
+};
+
+// MFMA 16x16x32 on 8 bf16 / f16 values per lane (as four packed dwords).
+template <int DT>
+__device__ inline f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ inline f32x4 mfma16x16x32<LNQ_BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <>
+__device__ inline f32x4 mfma16x16x32<LNQ_F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// 8 packed 4-bit codes (nibble i = element i) as 8 half-precision values
+// MAGIC + q in element order: dword s holds elements 2s (low) and 2s+1 (high).
+template <int DT>
+__device__ inline u32x4 nibbles_to_magic(uint32_t w) {
+  const uint32_t lo = w & 0x0f0f0f0fu;         // bytes: q0 q2 q4 q6
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // bytes: q1 q3 q5 q7
+  u32x4 out;
+  // v_perm_b32: selector bytes 0-3 pick from the second operand, 4-7 from the
+  // first, 0x0c gives zero. Dword s = [lo.byte s, 0, hi.byte s, 0].
+  out.x = __builtin_amdgcn_perm(hi, lo, 0x0c040c00u) | Elem<DT>::MAGIC2;
+  out.y = __builtin_amdgcn_perm(hi, lo, 0x0c050c01u) | Elem<DT>::MAGIC2;
+  out.z = __builtin_amdgcn_perm(hi, lo, 0x0c060c02u) | Elem<DT>::MAGIC2;
+  out.w = __builtin_amdgcn_perm(hi, lo, 0x0c070c03u) | Elem<DT>::MAGIC2;
+  return out;
+}
+
+// Wave-wide reductions (64 lanes).
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ inline float wave_min(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+}  // namespace lnq

@@ -1,0 +1,621 @@
+// 8-bit weights (std.quant::Int8Linear / Int8GroupLinear / Fp8Linear / Fp8BlockLinear)
+// on gfx950:
+//   - w8_skinny:  weight-only product for few rows (gemv8 / w8a16), weights
+//                 widened in registers and multiplied on MFMA, x unrounded;
+//   - dequant8:   the weight widened and scaled, rounded to the output dtype;
+//   - rows8:      dynamic per-token FP8 / int8 rounding of activations;
+//   - mm8:        int8 x int8 (int32 sums) or FP8 x FP8 (f32 sums) tiled MFMA GEMM
+//                 with the row-scale epilogue;
+//   - int8_quantize: symmetric group-wise int8 rounding, bit-exact with numpy.
+#include "common.hpp"
+
+namespace lnq {
+
+// ------------------------------------------------------------------ helpers
+
+// 4 FP8 E4M3 bytes -> 4 f32 (exact) via the hardware conversion.
+__device__ inline void fp8x4_to_f32(uint32_t w, float (&f)[4]) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  f[0] = lo.x;
+  f[1] = lo.y;
+  f[2] = hi.x;
+  f[3] = hi.y;
+}
+
+// Two f32 values that are exact in the 16-bit type, packed (low = a). For bf16
+// the top halves are the value (low halves are zero for these small-mantissa
+// values); f16 converts.
+template <int DT>
+__device__ inline uint32_t pack_exact2(float a, float b) {
+  if constexpr (DT == LNQ_BF16) {
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, a),
+                                 0x07060302u);
+  } else {
+    return static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16);
+  }
+}
+
+// 4 weight bytes as 4 values of the 16-bit type (two dwords, element order).
+// int8: the byte plus 128 (0..255, exact in bf16 / f16), undone by the
+// epilogue's -128 * sum(x); FP8: the value itself.
+template <int DT, int FP8>
+__device__ inline void widen4(uint32_t w, uint32_t& d0, uint32_t& d1) {
+  float f[4];
+  if constexpr (FP8) {
+    fp8x4_to_f32(w, f);
+  } else {
+    const uint32_t u = w ^ 0x80808080u;
+    f[0] = static_cast<float>(u & 0xffu);
+    f[1] = static_cast<float>((u >> 8) & 0xffu);
+    f[2] = static_cast<float>((u >> 16) & 0xffu);
+    f[3] = static_cast<float>(u >> 24);
+  }
+  d0 = pack_exact2<DT>(f[0], f[1]);
+  d1 = pack_exact2<DT>(f[2], f[3]);
+}
+
+// =================================================================== skinny
+// One workgroup (4 waves) owns 16 output features and 16*MT rows of x; the
+// waves split K into contiguous quarters, reduced through LDS. A chunk is 64
+// inputs: lane (col, j) reads 16 bytes of row n0 + col at byte 64c + 16j and
+// feeds MFMA t (t = 0, 1) elements 8t..8t+7 of them. A group (of `group`
+// inputs, or the whole row when the scale is per row) closes with
+//   acc += s * (C - offset * Cx),  Cx = sum of x over the group (B = ones).
+template <int DT, int FP8, int MT>
+__global__ __launch_bounds__(256) void w8_skinny_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ weight,
+    const float* __restrict__ scale, uint16_t* __restrict__ y, int M, int N, int K, int G,
+    int row_block, int scale_cols) {
+  using E = Elem<DT>;
+  constexpr float offset = FP8 ? 0.0f : 128.0f;
+  __shared__ f32x4 red[4][MT][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int j = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int m0 = blockIdx.y * 16 * MT;
+  const int nrow = min(n0 + col, N - 1);
+  const int chunks = K >> 6;
+  const int per_wave = (chunks + 3) >> 2;
+  const int cb = min(chunks, wave * per_wave);
+  const int ce = min(chunks, cb + per_wave);
+  const int chunks_per_group = G >> 6;
+
+  const uint8_t* wrow = weight + static_cast<size_t>(nrow) * K;
+  const float* srow = scale + static_cast<size_t>(nrow / row_block) * scale_cols;
+
+  const uint16_t* xrow[MT];
+  bool mok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + 16 * mt + col;
+    mok[mt] = m < M;
+    xrow[mt] = x + static_cast<size_t>(mok[mt] ? m : 0) * K;
+  }
+  u32x4 ones;
+  ones.x = ones.y = ones.z = ones.w = E::ONE2;
+
+  f32x4 acc[MT], C[MT], Cx[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  u32x4 wnext = {0u, 0u, 0u, 0u};
+  if (cb < ce)
+    wnext = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 64 * cb + 16 * j));
+  for (int c = cb; c < ce; ++c) {
+    const u32x4 w = wnext;
+    if (c + 1 < ce)
+      wnext = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 64 * (c + 1) + 16 * j));
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      uint32_t b0, b1, b2, b3;
+      widen4<DT, FP8>(words[2 * t], b0, b1);
+      widen4<DT, FP8>(words[2 * t + 1], b2, b3);
+      const u32x4 b = {b0, b1, b2, b3};
+      const int k = 64 * c + 16 * j + 8 * t;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 a = *reinterpret_cast<const u32x4*>(xrow[mt] + k);
+        if (!mok[mt]) a = u32x4{0u, 0u, 0u, 0u};
+        C[mt] = mfma16x16x32<DT>(a, b, C[mt]);
+        if constexpr (!FP8) Cx[mt] = mfma16x16x32<DT>(a, ones, Cx[mt]);
+      }
+    }
+    const bool closes = ((c + 1) % chunks_per_group == 0) || (c + 1 == ce);
+    if (closes) {
+      const float s = srow[c / chunks_per_group];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float d = FP8 ? C[mt][r] : fmaf(-offset, Cx[mt][r], C[mt][r]);
+          acc[mt][r] = fmaf(s, d, acc[mt][r]);
+        }
+        C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+  const int olane = threadIdx.x & 63;
+  const int r = threadIdx.x >> 6;
+  const int n = n0 + (olane & 15);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + 16 * mt + 4 * (olane >> 4) + r;
+    const float v = red[0][mt][olane][r] + red[1][mt][olane][r] + red[2][mt][olane][r] +
+                    red[3][mt][olane][r];
+    if (m < M && n < N) y[static_cast<size_t>(m) * N + n] = E::from_f32(v);
+  }
+}
+
+// ================================================================== dequant8
+// 16 weight bytes per thread: out = widen(w) * scale in f32, rounded once.
+template <int DT, int FP8>
+__global__ __launch_bounds__(256) void dequant8_kernel(const uint8_t* __restrict__ weight,
+                                                       const float* __restrict__ scale,
+                                                       typename Elem<DT>::storage* __restrict__ out,
+                                                       int64_t units, int K, int G, int row_block,
+                                                       int scale_cols) {
+  using E = Elem<DT>;
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (u >= units) return;
+  const int64_t per_row = K >> 4;
+  const int64_t n = u / per_row;
+  const int k0 = static_cast<int>(u - n * per_row) << 4;
+  const float* srow = scale + (G == 0 ? n : (n / row_block) * scale_cols);
+  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(weight + (u << 4)));
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+  typename E::storage* dst = out + n * K + k0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float f[4];
+    if constexpr (FP8) {
+      fp8x4_to_f32(words[d], f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        f[i] = static_cast<float>(static_cast<int8_t>((words[d] >> (8 * i)) & 0xffu));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + 4 * d + i;
+      const float s = G == 0 ? srow[0] : srow[k / G];
+      dst[4 * d + i] = E::from_f32(f[i] * s);
+    }
+  }
+}
+
+// ===================================================================== rows8
+// One workgroup per row. scale = max(max|x|, 1e-12) / (448 | 127) in f32;
+// q = x / scale (IEEE divide) then FP8 E4M3 round-to-nearest-even of
+// clamp(q, +-448), or int8 clamp(trunc(q +- 0.5), +-127) with the add in f32.
+
+// f32 (|v| <= 448) -> FP8 E4M3 bits, round to nearest even (software, exact).
+__host__ __device__ inline uint32_t f32_to_e4m3(float v) {
+  const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const uint32_t mag = bits & 0x7fffffffu;
+  uint32_t code;
+  if (mag >= 0x3c800000u) {  // |v| >= 2^-6: normal
+    const uint32_t r = mag + 0x7ffffu + ((mag >> 20) & 1u);
+    code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+  } else {  // subnormal: multiples of 2^-9 (exact scaling by 512, then rint)
+    code = static_cast<uint32_t>(rintf(__builtin_bit_cast(float, mag) * 512.0f));
+  }
+  if (code > 0x7eu) code = 0x7eu;
+  return code | sign;
+}
+
+template <int DT, int FP8>
+__global__ __launch_bounds__(256) void rows8_kernel(const typename Elem<DT>::storage* __restrict__ x,
+                                                    uint8_t* __restrict__ q,
+                                                    float* __restrict__ x_scale, int K) {
+  using E = Elem<DT>;
+  __shared__ float partial[4];
+  const int64_t row = blockIdx.x;
+  const typename E::storage* src = x + row * K;
+  float top = 0.0f;
+  for (int i = threadIdx.x; i < K; i += 256) top = fmaxf(top, fabsf(E::to_f32(src[i])));
+  top = wave_max(top);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = top;
+  __syncthreads();
+  top = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
+  const float largest = FP8 ? 448.0f : 127.0f;
+  const float s = fmaxf(top, 1e-12f) / largest;
+  uint8_t* dst = q + row * K;
+  for (int i = threadIdx.x; i < K; i += 256) {
+    const float v = E::to_f32(src[i]) / s;
+    if constexpr (FP8) {
+      dst[i] = static_cast<uint8_t>(f32_to_e4m3(fminf(fmaxf(v, -448.0f), 448.0f)));
+    } else {
+      const float h = v >= 0.0f ? __fadd_rn(v, 0.5f) : __fsub_rn(v, 0.5f);
+      dst[i] = static_cast<uint8_t>(static_cast<int8_t>(fminf(fmaxf(truncf(h), -127.0f), 127.0f)));
+    }
+  }
+  if (threadIdx.x == 0) x_scale[row] = s;
+}
+
+// ======================================================================= mm8
+// 128 x 128 outputs per workgroup of 4 waves (2 x 2, each 64 x 64 = 2 x 2 MFMA
+// 32x32 tiles); 128 input bytes per step, double-buffered in LDS with 16-byte
+// columns XOR-swizzled by (row & 7). FP8: v_mfma_scale_f32_32x32x64_f8f6f4
+// (unit E8M0 scales); int8: v_mfma_i32_32x32x32_i8.
+namespace mm8 {
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int BK = 128;  // bytes (= elements) per step
+constexpr int THREADS = 256;
+constexpr int GROUP_M = 4;
+constexpr int XCDS = 8;
+}  // namespace mm8
+
+__device__ inline int swz8(int row, int c16) { return row * mm8::BK + ((c16 ^ (row & 7)) << 4); }
+
+__device__ inline void mm8_tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int per_xcd = (total + mm8::XCDS - 1) / mm8::XCDS;
+  const int xcd = b % mm8::XCDS;
+  const int local = b / mm8::XCDS;
+  int logical = xcd * per_xcd + local;
+  if (total % mm8::XCDS != 0) {
+    const int full = total - (per_xcd - 1) * mm8::XCDS;
+    logical = xcd < full ? xcd * per_xcd + local : full * per_xcd + (xcd - full) * (per_xcd - 1) + local;
+  }
+  const int per_group = mm8::GROUP_M * tiles_n;
+  const int first_m = (logical / per_group) * mm8::GROUP_M;
+  const int rows = min(tiles_m - first_m, mm8::GROUP_M);
+  tm = first_m + (logical % per_group) % rows;
+  tn = (logical % per_group) / rows;
+}
+
+template <int DT, int FP8>
+__global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
+    const uint8_t* __restrict__ qx, const uint8_t* __restrict__ weight,
+    const float* __restrict__ x_scale, const float* __restrict__ scale,
+    uint16_t* __restrict__ y, int M, int N, int K) {
+  using namespace mm8;
+  using E = Elem<DT>;
+  __shared__ __attribute__((aligned(16))) uint8_t As[2][BM * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * BK];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  mm8_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  if (tm >= tiles_m || tn >= tiles_n) return;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int steps = K / BK;
+
+  // Loads: 128 rows x 8 columns of 16 bytes per operand = 4 per thread each.
+  const uint8_t* asrc[4];
+  const uint8_t* bsrc[4];
+  int dst[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int id = tid + THREADS * i;
+    const int row = id >> 3, c16 = id & 7;
+    asrc[i] = qx + static_cast<size_t>(min(m0 + row, M - 1)) * K + 16 * c16;
+    bsrc[i] = weight + static_cast<size_t>(min(n0 + row, N - 1)) * K + 16 * c16;
+    dst[i] = swz8(row, c16);
+  }
+  u32x4 areg[4], breg[4];
+  auto load_step = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      areg[i] = *reinterpret_cast<const u32x4*>(asrc[i] + ks * BK);
+      breg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bsrc[i] + ks * BK));
+    }
+  };
+  auto store_step = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<u32x4*>(&As[stage][dst[i]]) = areg[i];
+      *reinterpret_cast<u32x4*>(&Bs[stage][dst[i]]) = breg[i];
+    }
+  };
+
+  typedef int i32x16 __attribute__((ext_vector_type(16)));
+  f32x16 facc[2][2];
+  i32x16 iacc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        facc[a][b][r] = 0.f;
+        iacc[a][b][r] = 0;
+      }
+
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+  const int lrow = lane & 31;
+  const int lk = lane >> 5;
+  for (int ks = 0; ks < steps; ++ks) {
+    const int stage = ks & 1;
+    if (ks + 1 < steps) load_step(ks + 1);
+    const uint8_t* as = As[stage];
+    const uint8_t* bs = Bs[stage];
+    if constexpr (FP8) {
+      // 2 sub-steps of 64 inputs; a lane holds 32 bytes: columns 4kk + 2lk, +1.
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        i32x8 af[2], bf[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          const int row = wm * 64 + a * 32 + lrow;
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(&as[swz8(row, 4 * kk + 2 * lk)]);
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(&as[swz8(row, 4 * kk + 2 * lk + 1)]);
+          af[a] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int row = wn * 64 + b * 32 + lrow;
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(&bs[swz8(row, 4 * kk + 2 * lk)]);
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(&bs[swz8(row, 4 * kk + 2 * lk + 1)]);
+          bf[b] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            facc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                af[a], bf[b], facc[a][b], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+      }
+    } else {
+      // 4 sub-steps of 32 inputs; a lane holds 16 bytes: column 2kk + lk.
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        i32x4 af[2], bf[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+          af[a] = *reinterpret_cast<const i32x4*>(&as[swz8(wm * 64 + a * 32 + lrow, 2 * kk + lk)]);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          bf[b] = *reinterpret_cast<const i32x4*>(&bs[swz8(wn * 64 + b * 32 + lrow, 2 * kk + lk)]);
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            iacc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], iacc[a][b], 0, 0, 0);
+      }
+    }
+    if (ks + 1 < steps) store_step(stage ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int n = n0 + wn * 64 + b * 32 + (lane & 31);
+      if (n >= N) continue;
+      const float ws = scale[n];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < M) {
+          const float acc = FP8 ? facc[a][b][r] : static_cast<float>(iacc[a][b][r]);
+          y[static_cast<size_t>(m) * N + n] = E::from_f32(acc * x_scale[m] * ws);
+        }
+      }
+    }
+  }
+}
+
+// ============================================================= int8 quantize
+// One wave per group, numpy's f32 order of operations (linnet/quant.py:112-120).
+__device__ inline float round_storage(float v, int dtype) {
+  if (dtype == LNQ_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  if (dtype == LNQ_F16) return static_cast<float>(static_cast<_Float16>(v));
+  return v;
+}
+
+__global__ __launch_bounds__(256) void int8_quantize_kernel(const float* __restrict__ w,
+                                                            int8_t* __restrict__ q,
+                                                            float* __restrict__ scale,
+                                                            int64_t total_groups, int G,
+                                                            int dtype) {
+  const int lane = threadIdx.x & 63;
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (grp >= total_groups) return;
+  const float* p = w + grp * G;
+  float top = 0.0f;
+  for (int i = lane; i < G; i += 64) top = fmaxf(top, fabsf(p[i]));
+  top = wave_max(top);
+  float s = top / 127.0f;
+  if (!(s > 0.0f)) s = 1.0f;
+  s = round_storage(s, dtype);
+  int8_t* dst = q + grp * G;
+  for (int i = lane; i < G; i += 64)
+    dst[i] = static_cast<int8_t>(fminf(fmaxf(rintf(p[i] / s), -127.0f), 127.0f));
+  if (lane == 0) scale[grp] = s;
+}
+
+// ================================================================ launchers
+
+template <int DT, int FP8>
+static void launch_w8_skinny(const void* x, const uint8_t* w, const float* s, void* y, int M,
+                             int N, int K, int G, int rb, int cols, hipStream_t stream) {
+  const auto* xs = static_cast<const uint16_t*>(x);
+  auto* ys = static_cast<uint16_t*>(y);
+  if (M <= 16)
+    hipLaunchKernelGGL((w8_skinny_kernel<DT, FP8, 1>), dim3((N + 15) / 16, 1), dim3(256), 0, stream,
+                       xs, w, s, ys, M, N, K, G, rb, cols);
+  else if (M <= 32)
+    hipLaunchKernelGGL((w8_skinny_kernel<DT, FP8, 2>), dim3((N + 15) / 16, 1), dim3(256), 0, stream,
+                       xs, w, s, ys, M, N, K, G, rb, cols);
+  else
+    hipLaunchKernelGGL((w8_skinny_kernel<DT, FP8, 4>), dim3((N + 15) / 16, (M + 63) / 64), dim3(256),
+                       0, stream, xs, w, s, ys, M, N, K, G, rb, cols);
+}
+
+}  // namespace lnq
+
+using namespace lnq;
+
+extern "C" {
+
+LNQ_API LnqStatus lnq_int8_quantize(const float* weight, int8_t* q, float* scale,
+                                    int64_t out_features, int64_t in_features, int64_t group,
+                                    int32_t scale_dtype, void* stream) {
+  LNQ_REQUIRE(scale_dtype == LNQ_BF16 || scale_dtype == LNQ_F16 || scale_dtype == LNQ_F32,
+              "lnq_int8_quantize: scales are stored as bf16, f16 or f32, not dtype %d", scale_dtype);
+  LNQ_REQUIRE(out_features >= 0 && in_features >= 0, "lnq_int8_quantize: bad shape");
+  LNQ_REQUIRE(group > 0 && (in_features == 0 || in_features % group == 0) && group <= INT32_MAX,
+              "lnq_int8_quantize: groups of %lld must divide the %lld inputs", (long long)group,
+              (long long)in_features);
+  const int64_t total = out_features * (in_features / group);
+  if (total == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(weight && q && scale, "lnq_int8_quantize: null pointer");
+  hipLaunchKernelGGL(int8_quantize_kernel, dim3(static_cast<unsigned>((total + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), weight, q, scale, total,
+                     static_cast<int>(group), scale_dtype);
+  return launched("int8_quantize");
+}
+
+static const char* check_scales(int64_t N, int64_t K, int64_t group, int64_t row_block) {
+  if (group < 0 || row_block <= 0) return "group must be >= 0 and row_block > 0";
+  if (group > 0 && (K % group != 0 || N % row_block != 0)) return "scale blocks must tile the weight";
+  return nullptr;
+}
+
+LNQ_API LnqStatus lnq_w8a16(const void* x, const uint8_t* weight, const float* scale, void* y,
+                            int64_t rows, int64_t out_features, int64_t in_features, int32_t fp8,
+                            int64_t group, int64_t row_block, int32_t dtype, void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16, "lnq_w8a16: x is bf16 or f16, not dtype %d", dtype);
+  LNQ_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0 && in_features % 128 == 0,
+              "lnq_w8a16: bad shape rows=%lld out=%lld in=%lld (in %% 128 == 0)", (long long)rows,
+              (long long)out_features, (long long)in_features);
+  const char* bad = check_scales(out_features, in_features, group, row_block);
+  LNQ_REQUIRE(bad == nullptr, "lnq_w8a16: %s", bad ? bad : "");
+  LNQ_REQUIRE(group == 0 || group % 64 == 0,
+              "lnq_w8a16: the fused kernel takes scales per row or per 64k inputs, not %lld",
+              (long long)group);
+  LNQ_REQUIRE(rows <= INT32_MAX && out_features <= INT32_MAX && in_features <= INT32_MAX,
+              "lnq_w8a16: sizes exceed 2^31");
+  LNQ_REQUIRE(x && weight && scale && y, "lnq_w8a16: null pointer");
+  LNQ_REQUIRE(aligned(x, 16) && aligned(weight, 16), "lnq_w8a16: x and weight must be 16-byte aligned");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  const int M = (int)rows, N = (int)out_features, K = (int)in_features;
+  const int G = group == 0 ? K : (int)group;
+  const int rb = group == 0 ? 1 : (int)row_block;
+  const int cols = group == 0 ? 1 : (int)(in_features / group);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == LNQ_BF16) {
+    if (fp8) launch_w8_skinny<LNQ_BF16, 1>(x, weight, scale, y, M, N, K, G, rb, cols, s);
+    else launch_w8_skinny<LNQ_BF16, 0>(x, weight, scale, y, M, N, K, G, rb, cols, s);
+  } else {
+    if (fp8) launch_w8_skinny<LNQ_F16, 1>(x, weight, scale, y, M, N, K, G, rb, cols, s);
+    else launch_w8_skinny<LNQ_F16, 0>(x, weight, scale, y, M, N, K, G, rb, cols, s);
+  }
+  return launched("w8_skinny");
+}
+
+LNQ_API LnqStatus lnq_dequantize8(const uint8_t* weight, const float* scale, void* out,
+                                  int64_t out_features, int64_t in_features, int32_t fp8,
+                                  int64_t group, int64_t row_block, int32_t dtype, void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16 || dtype == LNQ_F32,
+              "lnq_dequantize8: output dtype %d is not bf16, f16 or f32", dtype);
+  LNQ_REQUIRE(out_features >= 0 && in_features >= 0 && in_features % 16 == 0,
+              "lnq_dequantize8: bad shape (in %% 16 == 0)");
+  const char* bad = check_scales(out_features, in_features, group, row_block);
+  LNQ_REQUIRE(bad == nullptr, "lnq_dequantize8: %s", bad ? bad : "");
+  LNQ_REQUIRE(in_features <= INT32_MAX, "lnq_dequantize8: in_features exceeds 2^31");
+  if (out_features == 0 || in_features == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(weight && scale && out, "lnq_dequantize8: null pointer");
+  LNQ_REQUIRE(aligned(weight, 16), "lnq_dequantize8: weight must be 16-byte aligned");
+  const int64_t units = out_features * (in_features / 16);
+  const dim3 grid(static_cast<unsigned>((units + 255) / 256));
+  const int K = (int)in_features, G = (int)group, rb = (int)row_block;
+  const int cols = group == 0 ? 1 : (int)(in_features / group);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define LNQ_DQ8(DT, F)                                                                                  \
+  hipLaunchKernelGGL((dequant8_kernel<DT, F>), grid, dim3(256), 0, s, weight, scale,                   \
+                     static_cast<typename Elem<DT>::storage*>(out), units, K, G, rb, cols)
+  if (dtype == LNQ_BF16) { if (fp8) LNQ_DQ8(LNQ_BF16, 1); else LNQ_DQ8(LNQ_BF16, 0); }
+  else if (dtype == LNQ_F16) { if (fp8) LNQ_DQ8(LNQ_F16, 1); else LNQ_DQ8(LNQ_F16, 0); }
+  else { if (fp8) LNQ_DQ8(LNQ_F32, 1); else LNQ_DQ8(LNQ_F32, 0); }
+#undef LNQ_DQ8
+  return launched("dequant8");
+}
+
+LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t rows,
+                            int64_t in_features, int32_t fp8, int32_t dtype, void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16 || dtype == LNQ_F32,
+              "lnq_rows8: x dtype %d is not bf16, f16 or f32", dtype);
+  LNQ_REQUIRE(rows >= 0 && in_features >= 0 && in_features <= INT32_MAX && rows <= INT32_MAX,
+              "lnq_rows8: bad shape");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(x && q && x_scale, "lnq_rows8: null pointer");
+  const dim3 grid(static_cast<unsigned>(rows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int K = (int)in_features;
+#define LNQ_R8(DT, F)                                                                              \
+  hipLaunchKernelGGL((rows8_kernel<DT, F>), grid, dim3(256), 0, s,                                \
+                     static_cast<const typename Elem<DT>::storage*>(x), q, x_scale, K)
+  if (dtype == LNQ_BF16) { if (fp8) LNQ_R8(LNQ_BF16, 1); else LNQ_R8(LNQ_BF16, 0); }
+  else if (dtype == LNQ_F16) { if (fp8) LNQ_R8(LNQ_F16, 1); else LNQ_R8(LNQ_F16, 0); }
+  else { if (fp8) LNQ_R8(LNQ_F32, 1); else LNQ_R8(LNQ_F32, 0); }
+#undef LNQ_R8
+  return launched("rows8");
+}
+
+LNQ_API LnqStatus lnq_mm8(const uint8_t* qx, const uint8_t* weight, const float* x_scale,
+                          const float* scale, void* y, int64_t rows, int64_t out_features,
+                          int64_t in_features, int32_t fp8, int32_t dtype, void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16, "lnq_mm8: output is bf16 or f16, not dtype %d", dtype);
+  LNQ_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0 && in_features % 128 == 0,
+              "lnq_mm8: bad shape rows=%lld out=%lld in=%lld (in %% 128 == 0)", (long long)rows,
+              (long long)out_features, (long long)in_features);
+  LNQ_REQUIRE(rows <= INT32_MAX && out_features <= INT32_MAX && in_features <= INT32_MAX,
+              "lnq_mm8: sizes exceed 2^31");
+  LNQ_REQUIRE(qx && weight && x_scale && scale && y, "lnq_mm8: null pointer");
+  LNQ_REQUIRE(aligned(qx, 16) && aligned(weight, 16), "lnq_mm8: operands must be 16-byte aligned");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  const int M = (int)rows, N = (int)out_features, K = (int)in_features;
+  const int tiles = ((M + mm8::BM - 1) / mm8::BM) * ((N + mm8::BN - 1) / mm8::BN);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto* ys = static_cast<uint16_t*>(y);
+#define LNQ_MM8(DT, F)                                                                            \
+  hipLaunchKernelGGL((mm8_kernel<DT, F>), dim3(tiles), dim3(mm8::THREADS), 0, s, qx, weight,     \
+                     x_scale, scale, ys, M, N, K)
+  if (dtype == LNQ_BF16) { if (fp8) LNQ_MM8(LNQ_BF16, 1); else LNQ_MM8(LNQ_BF16, 0); }
+  else { if (fp8) LNQ_MM8(LNQ_F16, 1); else LNQ_MM8(LNQ_F16, 0); }
+#undef LNQ_MM8
+  return launched("mm8");
+}
+
+}  // extern "C"

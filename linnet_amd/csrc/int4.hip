@@ -1,0 +1,498 @@
+// Group-wise 4-bit weights (std.quant::Int4GroupLinear) on gfx950:
+//   - int4_skinny: the decode-shape dequant-GEMV / skinny GEMM on MFMA;
+//   - int4_dequant: the whole weight dequantized, bit-exact with the reference;
+//   - int4_quantize: round-to-nearest quantization, bit-exact with numpy;
+//   - int4_pack / int4_unpack: the u4 / i4 byte layout.
+//
+// Layout (stdlib/quant.linnet:156-175, linnet/quant.py:1-12): packed [N, K/G, G/2]
+// u8 with element 2k in the low nibble, scale [N, K/G], zero [N, K/G] u8;
+// W[n, k] = (q[n, k] - zero[n, k/G]) * scale[n, k/G].
+#include "common.hpp"
+
+namespace lnq {
+
+// ===================================================================== skinny
+//
+// One workgroup (4 waves) owns 16 output features (an MFMA column tile) and
+// 16*MT rows of x; its 4 waves split K into contiguous quarters and add their
+// partial sums through LDS at the end. The weight is streamed once from HBM in
+// 128-element chunks (64 bytes of a row): lane (col = lane % 16, j = lane / 16)
+// reads 16 bytes of row n0 + col, so the 64 lanes of a wave read 16 rows x 64
+// contiguous bytes per chunk, fully used cache lines.
+//
+// The codes are widened without arithmetic: (MAGIC | q) read as bf16 is
+// 128 + q (f16: 1024 + q). MFMA 16x16x32 then sums
+//   C[m, n]  = sum_k x[m, k] * (MAGIC + q[n, k])     over one group
+//   Cx[m, n] = sum_k x[m, k] * 1                      (B = ones)
+// and one VALU epilogue per group folds zero point and scale in f32:
+//   acc[m, n] += s[n, g] * (C - (MAGIC + z[n, g]) * Cx)
+// which equals s * sum_k x * (q - z) -- the product with the exactly
+// dequantized weight -- up to f32 rounding of the sums.
+//
+// Which 8 elements a lane contributes to each MFMA (the same for its A and
+// B operands) depends on the group, so that one MFMA never spans two groups:
+//   LOADW 16 (group % 128 == 0): one 16-byte load; dword t -> k = 32j + 8t
+//   LOADW 8  (group 64):         two 8-byte loads; k = 64(t/2) + 16j + 8(t%2)
+//   LOADW 4  (group 32):         four 4-byte loads; k = 32t + 8j
+
+template <int LOADW>
+__device__ inline int chunk_koff(int t, int j) {
+  if constexpr (LOADW == 16) return 32 * j + 8 * t;
+  else if constexpr (LOADW == 8) return 64 * (t >> 1) + 16 * j + 8 * (t & 1);
+  else return 32 * t + 8 * j;
+}
+
+template <int LOADW>
+__device__ inline void load_chunk(const uint8_t* __restrict__ chunk, int j, uint32_t (&w)[4]) {
+  if constexpr (LOADW == 16) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(chunk + 16 * j));
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if constexpr (LOADW == 8) {
+    u32x2 a = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(chunk + 8 * j));
+    u32x2 b = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(chunk + 32 + 8 * j));
+    w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y;
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      w[t] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(chunk + 16 * t + 4 * j));
+  }
+}
+
+template <int DT, int LOADW, int MT>
+__global__ __launch_bounds__(256) void int4_skinny_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G) {
+  using E = Elem<DT>;
+  // Groups an MFMA group-step covers: MFMAs t = 0..3 of a chunk, a group
+  // closes after every `tpg` of them.
+  constexpr int tpg = LOADW == 16 ? 4 : (LOADW == 8 ? 2 : 1);
+  __shared__ f32x4 red[4][MT][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int j = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int m0 = blockIdx.y * 16 * MT;
+  const int nrow = min(n0 + col, N - 1);  // rows past N read row N-1, never stored
+  const int chunks = K >> 7;
+  const int per_wave = (chunks + 3) >> 2;
+  const int cb = min(chunks, wave * per_wave);
+  const int ce = min(chunks, cb + per_wave);
+  const int groups = K / G;
+
+  const uint8_t* wrow = packed + static_cast<size_t>(nrow) * (K >> 1);
+  const uint16_t* srow = scale + static_cast<size_t>(nrow) * groups;
+  const uint8_t* zrow = zero + static_cast<size_t>(nrow) * groups;
+
+  const uint16_t* xrow[MT];
+  bool mok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + 16 * mt + col;
+    mok[mt] = m < M;
+    xrow[mt] = x + static_cast<size_t>(mok[mt] ? m : 0) * K;
+  }
+
+  u32x4 ones;
+  ones.x = ones.y = ones.z = ones.w = E::ONE2;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t wnext[4] = {0, 0, 0, 0};
+  if (cb < ce) load_chunk<LOADW>(wrow + 64 * cb, j, wnext);
+
+  for (int c = cb; c < ce; ++c) {
+    uint32_t w[4] = {wnext[0], wnext[1], wnext[2], wnext[3]};
+    if (c + 1 < ce) load_chunk<LOADW>(wrow + 64 * (c + 1), j, wnext);
+
+    f32x4 C[MT], Cx[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4 b = nibbles_to_magic<DT>(w[t]);
+      const int k = 128 * c + chunk_koff<LOADW>(t, j);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 a = *reinterpret_cast<const u32x4*>(xrow[mt] + k);
+        if (!mok[mt]) a = u32x4{0u, 0u, 0u, 0u};
+        C[mt] = mfma16x16x32<DT>(a, b, C[mt]);
+        Cx[mt] = mfma16x16x32<DT>(a, ones, Cx[mt]);
+      }
+      if ((t + 1) % tpg == 0) {
+        const int g = (128 * c + chunk_koff<LOADW>(t, 0)) / G;
+        const float s = E::to_f32(srow[g]);
+        const float zz = E::MAGIC_VALUE + static_cast<float>(zrow[g]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float d = fmaf(-zz, Cx[mt][r], C[mt][r]);
+            acc[mt][r] = fmaf(s, d, acc[mt][r]);
+          }
+          C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+
+  // 256 threads, one output each per m-tile: (lane, r) of the 16x16 tile.
+  const int olane = threadIdx.x & 63;
+  const int r = threadIdx.x >> 6;
+  const int n = n0 + (olane & 15);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + 16 * mt + 4 * (olane >> 4) + r;
+    const float v = red[0][mt][olane][r] + red[1][mt][olane][r] + red[2][mt][olane][r] +
+                    red[3][mt][olane][r];
+    if (m < M && n < N) {
+      uint16_t out = E::from_f32(v);
+      if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
+      y[static_cast<size_t>(m) * N + n] = out;
+    }
+  }
+}
+
+// =================================================================== dequant
+// out[n, k] = (q - z) * s in f32, rounded once to the scale's dtype: the value
+// the reference's `_int4_unpack` (Triton, f32 then cast) and the CPU
+// `(q.to(T) - z.to(T)) * s` both give, (q - z) * s being exact in f32 for
+// bf16 / f16 scales.
+
+// 16 packed bytes (32 elements of one group) per thread; K % 32 == 0, G % 32 == 0.
+template <int DT>
+__global__ __launch_bounds__(256) void int4_dequant_fast(
+    const uint8_t* __restrict__ packed, const typename Elem<DT>::storage* __restrict__ scale,
+    const uint8_t* __restrict__ zero, typename Elem<DT>::storage* __restrict__ out,
+    int64_t units, int K, int G) {
+  using E = Elem<DT>;
+  using S = typename E::storage;
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (u >= units) return;
+  const int64_t per_row = K >> 5;  // 32-element units a row
+  const int64_t n = u / per_row;
+  const int k0 = static_cast<int>(u - n * per_row) << 5;
+  const int groups = K / G;
+  const int g = k0 / G;
+  const float s = E::load(scale + n * groups + g);
+  const float z = static_cast<float>(zero[n * groups + g]);
+  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + (u << 4)));
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+  S vals[32];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float q = static_cast<float>((words[d] >> (4 * i)) & 15u);
+      vals[8 * d + i] = E::from_f32((q - z) * s);
+    }
+  }
+  S* dst = out + n * K + k0;
+  if constexpr (sizeof(S) == 2) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      u32x4 o;
+      o.x = static_cast<uint32_t>(vals[8 * v + 0]) | (static_cast<uint32_t>(vals[8 * v + 1]) << 16);
+      o.y = static_cast<uint32_t>(vals[8 * v + 2]) | (static_cast<uint32_t>(vals[8 * v + 3]) << 16);
+      o.z = static_cast<uint32_t>(vals[8 * v + 4]) | (static_cast<uint32_t>(vals[8 * v + 5]) << 16);
+      o.w = static_cast<uint32_t>(vals[8 * v + 6]) | (static_cast<uint32_t>(vals[8 * v + 7]) << 16);
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst) + v);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      f32x4 o = {vals[4 * v], vals[4 * v + 1], vals[4 * v + 2], vals[4 * v + 3]};
+      __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(dst) + v);
+    }
+  }
+}
+
+// Any even group: one byte (two elements) per thread.
+template <int DT>
+__global__ __launch_bounds__(256) void int4_dequant_any(
+    const uint8_t* __restrict__ packed, const typename Elem<DT>::storage* __restrict__ scale,
+    const uint8_t* __restrict__ zero, typename Elem<DT>::storage* __restrict__ out,
+    int64_t bytes, int K, int G) {
+  using E = Elem<DT>;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= bytes) return;
+  const int64_t half = K >> 1;
+  const int64_t n = b / half;
+  const int k = static_cast<int>(b - n * half) << 1;
+  const int groups = K / G;
+  const int g = k / G;
+  const float s = E::load(scale + n * groups + g);
+  const float z = static_cast<float>(zero[n * groups + g]);
+  const uint32_t byte = packed[b];
+  out[n * K + k] = E::from_f32((static_cast<float>(byte & 15u) - z) * s);
+  out[n * K + k + 1] = E::from_f32((static_cast<float>(byte >> 4) - z) * s);
+}
+
+// ================================================================== quantize
+// One wave per group of G inputs of a row: min / max over the group, then the
+// codes, in exactly numpy's f32 order of operations (linnet/quant.py:92-98):
+// scale = (max - min) / 15 (not > 0 -> 1), zero = clip(rint(-min / scale), 0, 15),
+// q = clip(rint(w / scale) + zero, 0, 15); rint rounds half to even, divisions
+// are IEEE (hip-clang's default correctly rounded f32 divide).
+__global__ __launch_bounds__(256) void int4_quantize_kernel(const float* __restrict__ w,
+                                                            uint8_t* __restrict__ packed,
+                                                            float* __restrict__ scale,
+                                                            uint8_t* __restrict__ zero,
+                                                            int64_t total_groups, int G) {
+  const int lane = threadIdx.x & 63;
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (grp >= total_groups) return;
+  const float* p = w + grp * G;
+  float lo = __builtin_huge_valf();
+  float hi = -__builtin_huge_valf();
+  for (int i = lane; i < G; i += 64) {
+    const float v = p[i];
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+  }
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  float s = (hi - lo) / 15.0f;
+  if (!(s > 0.0f)) s = 1.0f;
+  const float z = fminf(fmaxf(rintf(-lo / s), 0.0f), 15.0f);
+  uint8_t* dst = packed + grp * (G >> 1);
+  for (int i = 2 * lane; i < G; i += 128) {
+    const float q0 = fminf(fmaxf(rintf(p[i] / s) + z, 0.0f), 15.0f);
+    const float q1 = fminf(fmaxf(rintf(p[i + 1] / s) + z, 0.0f), 15.0f);
+    dst[i >> 1] = static_cast<uint8_t>(static_cast<uint32_t>(q0) | (static_cast<uint32_t>(q1) << 4));
+  }
+  if (lane == 0) {
+    scale[grp] = s;
+    zero[grp] = static_cast<uint8_t>(z);
+  }
+}
+
+// ============================================================ pack / unpack
+
+__global__ __launch_bounds__(256) void int4_pack_kernel(const uint8_t* __restrict__ codes,
+                                                        uint8_t* __restrict__ packed,
+                                                        int64_t pairs) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= pairs) return;
+  packed[i] = static_cast<uint8_t>((codes[2 * i] & 15u) | ((codes[2 * i + 1] & 15u) << 4));
+}
+
+__global__ __launch_bounds__(256) void int4_unpack_kernel(const uint8_t* __restrict__ packed,
+                                                          uint8_t* __restrict__ codes,
+                                                          int64_t pairs, int is_signed) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= pairs) return;
+  const uint32_t b = packed[i];
+  uint32_t lo = b & 15u, hi = b >> 4;
+  if (is_signed) {
+    lo = static_cast<uint32_t>(static_cast<int32_t>(lo ^ 8u) - 8) & 0xffu;
+    hi = static_cast<uint32_t>(static_cast<int32_t>(hi ^ 8u) - 8) & 0xffu;
+  }
+  codes[2 * i] = static_cast<uint8_t>(lo);
+  codes[2 * i + 1] = static_cast<uint8_t>(hi);
+}
+
+// ============================================================ launch helpers
+
+template <int DT, int LOADW>
+static LnqStatus launch_skinny_lw(const void* x, const uint8_t* packed, const void* scale,
+                                  const uint8_t* zero, const void* bias, void* y, int M, int N,
+                                  int K, int G, hipStream_t stream) {
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* ys = static_cast<uint16_t*>(y);
+  const dim3 block(256);
+  if (M <= 16) {
+    const dim3 grid((N + 15) / 16, 1);
+    hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, 1>), grid, block, 0, stream, xs, packed,
+                       ss, zero, bs, ys, M, N, K, G);
+  } else if (M <= 32) {
+    const dim3 grid((N + 15) / 16, 1);
+    hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, 2>), grid, block, 0, stream, xs, packed,
+                       ss, zero, bs, ys, M, N, K, G);
+  } else {
+    const dim3 grid((N + 15) / 16, (M + 63) / 64);
+    hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, 4>), grid, block, 0, stream, xs, packed,
+                       ss, zero, bs, ys, M, N, K, G);
+  }
+  return launched("int4_skinny");
+}
+
+template <int DT>
+static LnqStatus launch_skinny(const void* x, const uint8_t* packed, const void* scale,
+                               const uint8_t* zero, const void* bias, void* y, int M, int N,
+                               int K, int G, hipStream_t stream) {
+  if (G % 128 == 0)
+    return launch_skinny_lw<DT, 16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+  if (G == 64) return launch_skinny_lw<DT, 8>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+  return launch_skinny_lw<DT, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+}
+
+// Defined in int4_gemm.hip: the prefill dequant-GEMM.
+LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale,
+                            const uint8_t* zero, const void* bias, void* y, int M, int N, int K,
+                            int G, int dtype, hipStream_t stream);
+bool int4_tiled_supports(int M, int N, int K, int G, int dtype);
+
+}  // namespace lnq
+
+using namespace lnq;
+
+extern "C" {
+
+LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const void* scale,
+                                  const uint8_t* zero, const void* bias, void* y, int64_t rows,
+                                  int64_t in_features, int64_t out_features, int64_t group,
+                                  int32_t dtype, int32_t kernel, void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16,
+              "lnq_int4_linear: activations are bf16 or f16, not dtype %d", dtype);
+  LNQ_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0,
+              "lnq_int4_linear: bad shape rows=%lld in=%lld out=%lld", (long long)rows,
+              (long long)in_features, (long long)out_features);
+  LNQ_REQUIRE(in_features % 128 == 0, "lnq_int4_linear: in_features %lld is not a multiple of 128",
+              (long long)in_features);
+  LNQ_REQUIRE(group > 0 && in_features % group == 0 && (group == 32 || group == 64 || group % 128 == 0),
+              "lnq_int4_linear: a group of %lld is not 32, 64 or a multiple of 128 dividing %lld",
+              (long long)group, (long long)in_features);
+  LNQ_REQUIRE(rows <= INT32_MAX && in_features <= INT32_MAX && out_features <= INT32_MAX,
+              "lnq_int4_linear: sizes exceed 2^31");
+  LNQ_REQUIRE(x && packed && scale && zero && y, "lnq_int4_linear: null pointer");
+  LNQ_REQUIRE(aligned(x, 16) && aligned(packed, 16),
+              "lnq_int4_linear: x and packed must be 16-byte aligned");
+  LNQ_REQUIRE(kernel >= LNQ_KERNEL_AUTO && kernel <= LNQ_KERNEL_TILED,
+              "lnq_int4_linear: unknown kernel %d", kernel);
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  bool tiled = kernel == LNQ_KERNEL_TILED;
+  if (kernel == LNQ_KERNEL_AUTO) tiled = M > 64 && int4_tiled_supports(M, N, K, G, dtype);
+  if (tiled) {
+    LNQ_REQUIRE(int4_tiled_supports(M, N, K, G, dtype),
+                "lnq_int4_linear: the tiled kernel does not take M=%d N=%d K=%d group=%d", M, N,
+                K, G);
+    return launch_int4_tiled(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
+  }
+  if (dtype == LNQ_BF16)
+    return launch_skinny<LNQ_BF16>(x, packed, scale, zero, bias, y, M, N, K, G, s);
+  return launch_skinny<LNQ_F16>(x, packed, scale, zero, bias, y, M, N, K, G, s);
+}
+
+LNQ_API LnqStatus lnq_int4_dequantize(const uint8_t* packed, const void* scale,
+                                      const uint8_t* zero, void* out, int64_t out_features,
+                                      int64_t in_features, int64_t group, int32_t dtype,
+                                      void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16 || dtype == LNQ_F32,
+              "lnq_int4_dequantize: scales are bf16, f16 or f32, not dtype %d", dtype);
+  LNQ_REQUIRE(out_features >= 0 && in_features >= 0 && in_features % 2 == 0,
+              "lnq_int4_dequantize: bad shape out=%lld in=%lld", (long long)out_features,
+              (long long)in_features);
+  LNQ_REQUIRE(group > 0 && group % 2 == 0 && (in_features == 0 || in_features % group == 0),
+              "lnq_int4_dequantize: groups of %lld must be even and divide %lld", (long long)group,
+              (long long)in_features);
+  LNQ_REQUIRE(in_features <= INT32_MAX, "lnq_int4_dequantize: in_features exceeds 2^31");
+  if (out_features == 0 || in_features == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(packed && scale && zero && out, "lnq_int4_dequantize: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  const bool fast = K % 32 == 0 && G % 32 == 0 && aligned(packed, 16) && aligned(out, 16);
+  if (fast) {
+    const int64_t units = out_features * (K / 32);
+    const dim3 grid(static_cast<unsigned>((units + 255) / 256));
+    if (dtype == LNQ_BF16)
+      hipLaunchKernelGGL((int4_dequant_fast<LNQ_BF16>), grid, dim3(256), 0, s, packed,
+                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out),
+                         units, K, G);
+    else if (dtype == LNQ_F16)
+      hipLaunchKernelGGL((int4_dequant_fast<LNQ_F16>), grid, dim3(256), 0, s, packed,
+                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out),
+                         units, K, G);
+    else
+      hipLaunchKernelGGL((int4_dequant_fast<LNQ_F32>), grid, dim3(256), 0, s, packed,
+                         static_cast<const float*>(scale), zero, static_cast<float*>(out), units,
+                         K, G);
+  } else {
+    const int64_t bytes = out_features * (K / 2);
+    const dim3 grid(static_cast<unsigned>((bytes + 255) / 256));
+    if (dtype == LNQ_BF16)
+      hipLaunchKernelGGL((int4_dequant_any<LNQ_BF16>), grid, dim3(256), 0, s, packed,
+                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out),
+                         bytes, K, G);
+    else if (dtype == LNQ_F16)
+      hipLaunchKernelGGL((int4_dequant_any<LNQ_F16>), grid, dim3(256), 0, s, packed,
+                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out),
+                         bytes, K, G);
+    else
+      hipLaunchKernelGGL((int4_dequant_any<LNQ_F32>), grid, dim3(256), 0, s, packed,
+                         static_cast<const float*>(scale), zero, static_cast<float*>(out), bytes,
+                         K, G);
+  }
+  return launched("int4_dequant");
+}
+
+LNQ_API LnqStatus lnq_int4_quantize(const float* weight, uint8_t* packed, float* scale,
+                                    uint8_t* zero, int64_t out_features, int64_t in_features,
+                                    int64_t group, void* stream) {
+  LNQ_REQUIRE(out_features >= 0 && in_features >= 0, "lnq_int4_quantize: bad shape");
+  LNQ_REQUIRE(group > 0 && group % 2 == 0 && (in_features == 0 || in_features % group == 0),
+              "lnq_int4_quantize: groups of %lld must be even and divide the %lld inputs",
+              (long long)group, (long long)in_features);
+  LNQ_REQUIRE(group <= INT32_MAX, "lnq_int4_quantize: group exceeds 2^31");
+  const int64_t total = out_features * (in_features / group);
+  if (total == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(weight && packed && scale && zero, "lnq_int4_quantize: null pointer");
+  const dim3 grid(static_cast<unsigned>((total + 3) / 4));
+  hipLaunchKernelGGL(int4_quantize_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     weight, packed, scale, zero, total, static_cast<int>(group));
+  return launched("int4_quantize");
+}
+
+LNQ_API LnqStatus lnq_int4_pack(const uint8_t* codes, uint8_t* packed, int64_t pairs,
+                                void* stream) {
+  LNQ_REQUIRE(pairs >= 0, "lnq_int4_pack: negative size");
+  if (pairs == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(codes && packed, "lnq_int4_pack: null pointer");
+  hipLaunchKernelGGL(int4_pack_kernel, dim3(static_cast<unsigned>((pairs + 255) / 256)), dim3(256),
+                     0, static_cast<hipStream_t>(stream), codes, packed, pairs);
+  return launched("int4_pack");
+}
+
+LNQ_API LnqStatus lnq_int4_unpack(const uint8_t* packed, void* codes, int64_t pairs,
+                                  int32_t is_signed, void* stream) {
+  LNQ_REQUIRE(pairs >= 0, "lnq_int4_unpack: negative size");
+  if (pairs == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(codes && packed, "lnq_int4_unpack: null pointer");
+  hipLaunchKernelGGL(int4_unpack_kernel, dim3(static_cast<unsigned>((pairs + 255) / 256)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), packed,
+                     static_cast<uint8_t*>(codes), pairs, is_signed ? 1 : 0);
+  return launched("int4_unpack");
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+"""The helpers generated PyTorch calls for `std.quant::linear_int4_groups`,
+with the reference's names and contract (`src/backend/torch_source.cpp:1478-1571`):
+
+    packed = _int4_pack(p_w, p_s, p_z)                   # in prepare(), once
+    y = _int4_linear(x, packed, bias, p_w, p_s, p_z)     # in main(), per call
+
+`_int4_pack` returns a 3-tuple when the HIP kernels take the layer (a GPU,
+bf16 or f16 scales, a group of 32, 64 or a multiple of 128, In % 128 == 0):
+the parameters themselves, read as they are stored, so nothing is repacked
+and no bytes are held beyond the model's own. Otherwise it returns the
+1-tuple of the weight dequantized once, by the HIP dequantize kernel, as the
+reference's `_int4_pack` falls back (`torch_source.cpp:1501-1504`), and
+`_int4_linear` multiplies it with `F.linear`.
+
+CPU tensors raise: this package has no CPU path.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as functional
+
+from ..errors import LinnetError
+from . import kernels
+
+_FUSED_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def _fused_group(group: int) -> bool:
+    return group in (32, 64) or (group > 0 and group % 128 == 0)
+
+
+def _int4_pack(packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor) -> tuple[torch.Tensor, ...]:
+    """Prepare-time: `(packed, scale, zero)` for the fused kernels, or
+    `(dequantized weight,)`. `packed` is [Out, Groups, Group/2] u8."""
+    if not packed.is_cuda:
+        raise LinnetError("_int4_pack: linnet_amd runs on the GPU; the weight is on " + str(packed.device))
+    out_features, groups, half = packed.shape
+    group = 2 * half
+    in_features = groups * group
+    if scale.dtype in _FUSED_DTYPES and _fused_group(group) and in_features % 128 == 0:
+        return (packed.contiguous(), scale.contiguous(), zero.contiguous())
+    return (kernels.int4_weight(packed, scale, zero),)
+
+
+def _int4_weight(raw: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor) -> torch.Tensor:
+    """The weight dequantized, in `scale`'s dtype: one HIP kernel
+    (`torch_source.cpp:1536-1550`)."""
+    return kernels.int4_weight(raw, scale, zero)
+
+
+def _int4_linear(
+    x: torch.Tensor,
+    packed: tuple[torch.Tensor, ...],
+    bias: torch.Tensor | None,
+    raw: torch.Tensor,
+    scale: torch.Tensor,
+    zero: torch.Tensor,
+) -> torch.Tensor:
+    """`x @ W.T (+ bias)` over `x`'s last axis (`torch_source.cpp:1553-1570`).
+    With the fused 3-tuple, any number of rows runs one HIP kernel (few rows the
+    skinny MFMA kernel, many the tiled dequant-GEMM) with the bias added in its
+    epilogue; with the 1-tuple, `F.linear` over the dequantized weight."""
+    flat = x.reshape(-1, x.shape[-1])
+    if len(packed) == 3 and x.dtype == scale.dtype:
+        p, s, z = packed
+        y = kernels.int4_linear(flat, p, s, z, bias)
+        return y.reshape(*x.shape[:-1], y.shape[-1])
+    if not x.is_cuda:
+        raise LinnetError("_int4_linear: linnet_amd runs on the GPU; x is on " + str(x.device))
+    weight = packed[0] if len(packed) == 1 else kernels.int4_weight(raw, scale, zero)
+    y = functional.linear(flat, weight.to(flat.dtype))
+    y = y.reshape(*x.shape[:-1], y.shape[-1])
+    return y if bias is None else y + bias

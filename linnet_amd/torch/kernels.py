@@ -1,0 +1,314 @@
+"""PyTorch-facing wrappers of the HIP kernels, named as the reference's
+`linnet.torch.kernels` names its Triton ones (`python/linnet/src/linnet/torch/kernels.py`).
+
+Each wrapper checks shapes, dtypes and the device on the host, allocates the
+output with PyTorch on the tensors' device, and calls the C ABI on PyTorch's
+current stream: work is enqueued and never waited for, so every call may be
+captured into a HIP graph. CPU tensors, or a missing library, raise
+`LinnetError`: there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from ..errors import LinnetError
+
+_CODES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
+_HALF = (torch.bfloat16, torch.float16)
+KERNELS = {"auto": _lib.KERNEL_AUTO, "skinny": _lib.KERNEL_SKINNY, "tiled": _lib.KERNEL_TILED}
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _on_gpu(what: str, *tensors: torch.Tensor | None) -> torch.device:
+    device: torch.device | None = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise LinnetError(f"{what}: the HIP kernels take GPU tensors, got one on {t.device}")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise LinnetError(f"{what}: tensors on {device} and {t.device}")
+    assert device is not None
+    return device
+
+
+def _code(dtype: torch.dtype, what: str, allowed: tuple[torch.dtype, ...] = _HALF) -> int:
+    if dtype not in allowed:
+        raise LinnetError(f"{what}: dtype {dtype} is not one of {', '.join(map(str, allowed))}")
+    return _CODES[dtype]
+
+
+# ------------------------------------------------------------------ int4 groups
+
+
+def int4_linear(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scale: torch.Tensor,
+    zero: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    kernel: str = "auto",
+) -> torch.Tensor:
+    """`F.linear(x, W) (+ bias)` for `x` [rows, In] (bf16 or f16) and the group-wise
+    4-bit weight of `std.quant::linear_int4_groups` -- `packed` ([Out, Groups,
+    Group/2] u8, the even value low), `scale` ([Out, Groups], x's dtype) and `zero`
+    ([Out, Groups] u8) -- read once from HBM as they are stored. Few rows run the
+    skinny MFMA kernel, many the LDS-tiled dequant-GEMM (`kernel` may force one).
+    In is a multiple of 128; the group is 32, 64 or a multiple of 128.
+
+    Replaces `kernels.py:277-323` (`int4_linear`) and tinygemm's
+    `aten._weight_int4pack_mm` (`src/backend/torch_source.cpp:1556-1558`)."""
+    device = _on_gpu("int4_linear", x, packed, scale, zero, bias)
+    if x.dim() != 2 or packed.dim() != 3:
+        raise LinnetError(f"int4_linear: x is [rows, In] and packed [Out, Groups, Group/2], got {tuple(x.shape)} and {tuple(packed.shape)}")
+    rows, depth = x.shape
+    width, groups, half = packed.shape
+    group = 2 * half
+    if groups * group != depth:
+        raise LinnetError(f"int4_linear: packed {tuple(packed.shape)} does not hold In={depth}")
+    if packed.dtype != torch.uint8 or zero.dtype != torch.uint8:
+        raise LinnetError("int4_linear: packed and zero are uint8")
+    if tuple(scale.shape) != (width, groups) or tuple(zero.shape) != (width, groups):
+        raise LinnetError(f"int4_linear: scale and zero are [{width}, {groups}]")
+    code = _code(x.dtype, "int4_linear")
+    if scale.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype):
+        raise LinnetError("int4_linear: scale and bias have x's dtype")
+    if bias is not None and tuple(bias.shape) != (width,):
+        raise LinnetError(f"int4_linear: bias is [{width}]")
+    if kernel not in KERNELS:
+        raise LinnetError(f"int4_linear: kernel is one of {', '.join(KERNELS)}")
+    x = x.contiguous()
+    packed, scale, zero = packed.contiguous(), scale.contiguous(), zero.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    y = torch.empty(rows, width, dtype=x.dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call(
+            "lnq_int4_linear", _ptr(x), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),
+            rows, depth, width, group, code, KERNELS[kernel], _stream(device),
+        )
+    return y
+
+
+def int4_weight(raw: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor) -> torch.Tensor:
+    """The weight dequantized, in `scale`'s dtype (bf16, f16 or f32), in one kernel:
+    `(q - z) * s` in f32, rounded once -- bit for bit the reference's `_int4_weight`
+    (`src/backend/torch_source.cpp:1536-1550`). Any even group."""
+    device = _on_gpu("int4_weight", raw, scale, zero)
+    width, groups, half = raw.shape
+    code = _code(scale.dtype, "int4_weight", (torch.bfloat16, torch.float16, torch.float32))
+    if raw.dtype != torch.uint8 or zero.dtype != torch.uint8:
+        raise LinnetError("int4_weight: packed and zero are uint8")
+    if tuple(scale.shape) != (width, groups) or tuple(zero.shape) != (width, groups):
+        raise LinnetError(f"int4_weight: scale and zero are [{width}, {groups}]")
+    raw, scale, zero = raw.contiguous(), scale.contiguous(), zero.contiguous()
+    out = torch.empty(width, groups * 2 * half, dtype=scale.dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_int4_dequantize", _ptr(raw), _ptr(scale), _ptr(zero), _ptr(out),
+                  width, groups * 2 * half, 2 * half, code, _stream(device))
+    return out
+
+
+def quantize_int4(weight: torch.Tensor, group: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """`(packed [Out, In/group, group/2] u8, scale [Out, In/group] f32, zero u8)` of an
+    f32 `[Out, In]` weight, rounded as `linnet.quant.quantize_int4_groups`
+    (`python/linnet/src/linnet/quant.py:83-99`), bit for bit."""
+    device = _on_gpu("quantize_int4", weight)
+    if weight.dim() != 2:
+        raise LinnetError(f"a linear weight is [Out, In]; this one is {list(weight.shape)}")
+    width, depth = weight.shape
+    if group <= 0 or group % 2 != 0 or depth % group != 0:
+        raise LinnetError(f"groups of {group} must be even and divide the {depth} inputs")
+    w = weight.to(torch.float32).contiguous()
+    packed = torch.empty(width, depth // group, group // 2, dtype=torch.uint8, device=device)
+    scale = torch.empty(width, depth // group, dtype=torch.float32, device=device)
+    zero = torch.empty(width, depth // group, dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_int4_quantize", _ptr(w), _ptr(packed), _ptr(scale), _ptr(zero),
+                  width, depth, group, _stream(device))
+    return packed, scale, zero
+
+
+def pack4(codes: torch.Tensor) -> torch.Tensor:
+    """Integer codes (wrapped to 4 bits) two a byte along the last axis, low first
+    (`torch/packed.py:61-75` for `i4`/`u4`)."""
+    device = _on_gpu("pack4", codes)
+    if codes.shape[-1] % 2:
+        raise LinnetError(f"a 4-bit tensor's last axis is even, found shape {tuple(codes.shape)}")
+    if codes.is_floating_point():
+        codes = codes.trunc().to(torch.int64)
+    as_bytes = (codes.to(torch.int64) & 15).to(torch.uint8).contiguous()
+    out = torch.empty(*codes.shape[:-1], codes.shape[-1] // 2, dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_int4_pack", _ptr(as_bytes), _ptr(out), out.numel(), _stream(device))
+    return out
+
+
+def unpack4(packed: torch.Tensor, kind: str) -> torch.Tensor:
+    """Packed bytes widened: `u4` codes as uint8, `i4` sign-extended to int8
+    (`torch/packed.py:27-35`)."""
+    device = _on_gpu("unpack4", packed)
+    if kind not in ("u4", "i4"):
+        raise LinnetError(f"`{kind}` is not an integer 4-bit format (i4, u4)")
+    if packed.dtype != torch.uint8:
+        raise LinnetError("unpack4: packed is uint8")
+    packed = packed.contiguous()
+    dtype = torch.int8 if kind == "i4" else torch.uint8
+    out = torch.empty(*packed.shape[:-1], 2 * packed.shape[-1], dtype=dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_int4_unpack", _ptr(packed), _ptr(out), packed.numel(), int(kind == "i4"), _stream(device))
+    return out
+
+
+# ------------------------------------------------------------------------ 8-bit
+
+
+def _scale_columns(weight: torch.Tensor, scale: torch.Tensor, group: int, row_block: int) -> None:
+    width, depth = weight.shape
+    if group == 0:
+        if scale.numel() != width:
+            raise LinnetError(f"one scale a row: {width} scales, got {tuple(scale.shape)}")
+    else:
+        if depth % group or width % row_block:
+            raise LinnetError(f"scales of {row_block}x{group} blocks do not tile [{width}, {depth}]")
+        if tuple(scale.shape) != (width // row_block, depth // group):
+            raise LinnetError(f"scale is [{width // row_block}, {depth // group}], got {tuple(scale.shape)}")
+
+
+def _bytes(weight: torch.Tensor) -> torch.Tensor:
+    if weight.dtype == torch.float8_e4m3fn:
+        return weight.contiguous().view(torch.uint8)
+    if weight.dtype in (torch.int8, torch.uint8):
+        return weight.contiguous().view(torch.uint8)
+    raise LinnetError(f"8-bit weights are int8 or float8_e4m3fn (or their bytes), not {weight.dtype}")
+
+
+def w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, fp8: bool, group: int = 0, row_block: int = 1) -> torch.Tensor:
+    """`F.linear(x, W)` for `x` [rows, In] (bf16/f16) and 8-bit weights [Out, In]
+    (FP8 E4M3 bits or int8) times `scale` (f32; one a row when `group` is 0, else
+    [Out/row_block, In/group]), widened in registers, x unrounded.
+    Replaces `kernels.py:437-592` (`w8a16`) and, for one row, `gemv8` (`:375-434`)."""
+    device = _on_gpu("w8a16", x, weight, scale)
+    rows, depth = x.shape
+    width = weight.shape[0]
+    if weight.shape[1] != depth:
+        raise LinnetError(f"w8a16: weight {tuple(weight.shape)} does not take In={depth}")
+    _scale_columns(weight, scale, group, row_block)
+    code = _code(x.dtype, "w8a16")
+    if scale.dtype != torch.float32:
+        raise LinnetError("w8a16: scales are f32 (the operands' form)")
+    x, wb, scale = x.contiguous(), _bytes(weight), scale.contiguous()
+    y = torch.empty(rows, width, dtype=x.dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_w8a16", _ptr(x), _ptr(wb), _ptr(scale), _ptr(y), rows, width, depth,
+                  int(fp8), group, row_block, code, _stream(device))
+    return y
+
+
+def gemv8(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, fp8: bool, group: int = 0, row_block: int = 1) -> torch.Tensor:
+    """One row `x` [1, In] times 8-bit weights (`kernels.py:375-434`): `w8a16` at one row."""
+    if x.shape[0] != 1:
+        raise LinnetError(f"gemv8 takes one row, got {x.shape[0]}")
+    return w8a16(x, weight, scale, fp8, group, row_block)
+
+
+def dequantize8(weight: torch.Tensor, scale: torch.Tensor, fp8: bool, group: int, row_block: int, dtype: torch.dtype) -> torch.Tensor:
+    """The 8-bit weight widened, times its scale in f32, rounded to `dtype`
+    (`kernels.py:595-666`)."""
+    device = _on_gpu("dequantize8", weight, scale)
+    width, depth = weight.shape
+    _scale_columns(weight, scale, group, row_block)
+    code = _code(dtype, "dequantize8", (torch.bfloat16, torch.float16, torch.float32))
+    wb, scale = _bytes(weight), scale.to(torch.float32).contiguous()
+    out = torch.empty(width, depth, dtype=dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_dequantize8", _ptr(wb), _ptr(scale), _ptr(out), width, depth, int(fp8),
+                  group, row_block, code, _stream(device))
+    return out
+
+
+def _rows8(x: torch.Tensor, fp8: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    device = _on_gpu("rows8", x)
+    rows, depth = x.shape
+    code = _code(x.dtype, "rows8", (torch.bfloat16, torch.float16, torch.float32))
+    x = x.contiguous()
+    q = torch.empty(rows, depth, dtype=torch.float8_e4m3fn if fp8 else torch.int8, device=device)
+    scale = torch.empty(rows, 1, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_rows8", _ptr(x), _ptr(q), _ptr(scale), rows, depth, int(fp8), code, _stream(device))
+    return q, scale
+
+
+def fp8_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Each row of `x` rounded to FP8 E4M3 with a scale of its own (`kernels.py:669-753`):
+    the rows and the scales ([rows, 1], f32)."""
+    return _rows8(x, True)
+
+
+def int8_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Each row of `x` rounded to int8 with a scale of its own (`kernels.py:669-753`)."""
+    return _rows8(x, False)
+
+
+def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype, fp8: bool) -> torch.Tensor:
+    device = _on_gpu("mm8", q, weight, x_scale, scale)
+    rows, depth = q.shape
+    width = weight.shape[0]
+    if weight.shape[1] != depth:
+        raise LinnetError(f"mm8: weight {tuple(weight.shape)} does not take In={depth}")
+    if x_scale.numel() != rows or scale.numel() != width:
+        raise LinnetError("mm8: one scale per row of x and per row of the weight")
+    code = _code(dtype, "mm8")
+    qb, wb = _bytes(q), _bytes(weight)
+    xs = x_scale.to(torch.float32).contiguous()
+    ws = scale.to(torch.float32).contiguous()
+    y = torch.empty(rows, width, dtype=dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_mm8", _ptr(qb), _ptr(wb), _ptr(xs), _ptr(ws), _ptr(y), rows, width, depth,
+                  int(fp8), code, _stream(device))
+    return y
+
+
+def int8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """`(q @ weight.T) * x_scale * scale` in `dtype` for int8 rows and int8 weights
+    with one scale a row, summed exactly in int32 on MFMA (`kernels.py:805-915`)."""
+    return _mm8(q, weight, x_scale, scale, dtype, False)
+
+
+def fp8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """`(q @ weight.T) * x_scale * scale` in `dtype` for FP8 E4M3 rows and weights on
+    gfx950's FP8 MFMA, summed in f32: what `torch._scaled_mm(q, W.t(), scale_a,
+    scale_b, out_dtype)` computes for the reference (`torch/quantized.py:129`)."""
+    return _mm8(q, weight, x_scale, scale, dtype, True)
+
+
+def quantize_int8(weight: torch.Tensor, group: int, dtype: str) -> tuple[torch.Tensor, torch.Tensor]:
+    """`(q [Out, In] int8, scale [Out, In/group] f32)` as `linnet.quant.quantize_int8_groups`
+    (`python/linnet/src/linnet/quant.py:102-121`), bit for bit."""
+    device = _on_gpu("quantize_int8", weight)
+    if weight.dim() != 2:
+        raise LinnetError(f"a linear weight is [Out, In]; this one is {list(weight.shape)}")
+    codes = {"bf16": _lib.BF16, "f16": _lib.F16, "f32": _lib.F32}
+    if dtype not in codes:
+        raise LinnetError(f"scales are stored as bf16, f16, or f32, not {dtype}")
+    width, depth = weight.shape
+    if group <= 0 or depth % group:
+        raise LinnetError(f"groups of {group} must divide the {depth} inputs")
+    w = weight.to(torch.float32).contiguous()
+    q = torch.empty(width, depth, dtype=torch.int8, device=device)
+    scale = torch.empty(width, depth // group, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_int8_quantize", _ptr(w), _ptr(q), _ptr(scale), width, depth, group, codes[dtype], _stream(device))
+    return q, scale

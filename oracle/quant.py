@@ -1,0 +1,262 @@
+"""numpy restatement of the reference's quantize / pack / dequantize arithmetic.
+
+TEST INFRASTRUCTURE ONLY (see `oracle/__init__.py`): imported by `tests/`,
+`__graft_entry__.smoke()` and `bench.py`'s CPU-baseline leg, never by the
+product path.
+
+bf16 values are carried as their `uint16` bit patterns (numpy has no bf16).
+Every reference citation is relative to the reference checkout's root; the
+Python package lives at `python/linnet/src/linnet/`.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------- bit formats
+
+
+def to_bf16_bits(values: np.ndarray) -> np.ndarray:
+    """f32 values as bf16 bit patterns, rounded to nearest, ties to even.
+
+    Restates `weights.py:74-79` (`to_bf16_bits`).
+    Pin: equals `torch.Tensor.to(torch.bfloat16)` on every finite input
+    (tests/test_oracle.py::test_bf16_rounding_matches_torch)."""
+    bits = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32)
+    rounded = bits + np.uint32(0x7FFF) + ((bits >> np.uint32(16)) & np.uint32(1))
+    return (rounded >> np.uint32(16)).astype(np.uint16)
+
+
+def from_bf16_bits(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns as f32. Restates `weights.py:82-84`. Exact widening."""
+    return (np.asarray(bits).view(np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def round_to_storage(values: np.ndarray, dtype: str) -> np.ndarray:
+    """f32 values rounded to storage dtype `dtype` ("bf16", "f16", "f32") and
+    widened back to f32: `decode_floats(stored, encode_floats(v, stored))` of
+    `weights.py:87-105`, as `quantize_int8_groups` applies it (`quant.py:117-118`)."""
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    if dtype == "bf16":
+        return from_bf16_bits(to_bf16_bits(values)).reshape(values.shape)
+    if dtype == "f16":
+        return values.astype(np.float16).astype(np.float32)
+    if dtype == "f32":
+        return values.copy()
+    raise ValueError(f"scales are stored as bf16, f16, or f32, not {dtype}")
+
+
+def encode_storage(values: np.ndarray, dtype: str) -> np.ndarray:
+    """f32 values as the raw storage array of `dtype`: uint16 bits for bf16,
+    float16 for f16, float32 for f32 (`weights.py:98-105`)."""
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    if dtype == "bf16":
+        return to_bf16_bits(values)
+    if dtype == "f16":
+        return values.astype(np.float16)
+    if dtype == "f32":
+        return values.copy()
+    raise ValueError(f"scales are stored as bf16, f16, or f32, not {dtype}")
+
+
+def decode_storage(raw: np.ndarray, dtype: str) -> np.ndarray:
+    """Inverse of `encode_storage`: the stored values widened to f32."""
+    if dtype == "bf16":
+        return from_bf16_bits(raw)
+    return np.asarray(raw).astype(np.float32)
+
+
+def decode_fp8(bits: np.ndarray) -> np.ndarray:
+    """FP8 E4M3 bytes as f32, by the canonical body of `std.quant::decode_fp8`
+    (`stdlib/quant.linnet:227-235`): a normal value is `(8 + m) * 2**(e - 10)`,
+    a subnormal one `m * 2**-9`; the NaN bytes 0x7F/0xFF read as +-480.
+
+    Pin: equals `torch.float8_e4m3fn` widening on the 254 non-NaN bytes
+    (`tests/test_quant_fp8.py:46-53`, restated in tests/test_oracle.py)."""
+    wide = np.asarray(bits, dtype=np.uint8).astype(np.int32)
+    exponent = (wide >> 3) & 15
+    mantissa = wide & 7
+    magnitude = np.where(exponent == 0, mantissa, mantissa + 8)
+    power = (np.left_shift(1, np.maximum(exponent, 1) - 1)).astype(np.float32) * np.float32(
+        0.001953125
+    )
+    value = magnitude.astype(np.float32) * power
+    return np.where((wide & 128) == 0, value, -value).astype(np.float32)
+
+
+def encode_fp8(values: np.ndarray) -> np.ndarray:
+    """f32 values (already clamped to +-448) as FP8 E4M3 (OCP `e4m3fn`) bytes,
+    rounded to nearest, ties to even: the `.to(float8e4nv)` cast of
+    `torch/kernels.py:688-689` (Triton) and `torch.Tensor.to(float8_e4m3fn)`.
+
+    Pin: equals torch's own `float8_e4m3fn` cast on every f32 input in range,
+    including every tie (tests/test_oracle.py::test_fp8_encode_matches_torch)."""
+    x = np.ascontiguousarray(values, dtype=np.float32)
+    bits = x.view(np.uint32)
+    sign = ((bits >> np.uint32(24)) & np.uint32(0x80)).astype(np.uint8)
+    mag = np.abs(x)
+    # Normal range (|x| >= 2**-6): round the 23-bit mantissa to 3 bits.
+    mbits = mag.view(np.uint32)
+    rounded = mbits + np.uint32(0x7FFFF) + ((mbits >> np.uint32(20)) & np.uint32(1))
+    exp = (rounded >> np.uint32(23)).astype(np.int64) - 127 + 7
+    man = ((rounded >> np.uint32(20)) & np.uint32(7)).astype(np.int64)
+    normal = ((exp << 3) | man).astype(np.int64)
+    # Subnormal range: multiples of 2**-9, rounded half to even (exact scaling).
+    sub = np.rint(mag.astype(np.float64) * 512.0).astype(np.int64)  # 0..8; 8 is 2**-6
+    code = np.where(mag >= np.float32(2.0**-6), normal, sub)
+    code = np.minimum(code, 0x7E)  # saturate at 448
+    return (code.astype(np.uint8) | sign).astype(np.uint8)
+
+
+# ------------------------------------------------------------- 4-bit packing
+
+
+def pack_int4_groups(q: np.ndarray, group: int) -> np.ndarray:
+    """`[Out, In]` codes in 0..15 as `[Out, In/group, group/2]` bytes, the even
+    element in the low nibble. Restates `quant.py:242-248`.
+
+    Pin: closed form of `spec/03-types.md:39` / `torch/test_quant.py:48-59`
+    (tests/test_oracle.py::test_pack_layout_closed_form)."""
+    out_features, in_features = q.shape
+    grouped = q.reshape(out_features, in_features // group, group).astype(np.uint8)
+    return (grouped[..., 0::2] | (grouped[..., 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_int4_codes(packed: np.ndarray) -> np.ndarray:
+    """Each byte's two codes, low first, along the last axis (the last axis
+    doubles). Restates `torch/packed.py:21-24` and `quant.py:133-134`."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    pairs = np.stack([packed & 15, packed >> 4], axis=-1)
+    return pairs.reshape(*packed.shape[:-1], 2 * packed.shape[-1])
+
+
+def unpack4(packed: np.ndarray, kind: str) -> np.ndarray:
+    """`torch/packed.py:27-35` for the integer kinds: `u4` codes as uint8, `i4`
+    sign-extended to int8."""
+    codes = unpack_int4_codes(packed)
+    if kind == "u4":
+        return codes
+    if kind == "i4":
+        return ((codes.astype(np.int8) ^ 8) - 8).astype(np.int8)
+    raise ValueError(f"`{kind}` is not an integer 4-bit format (i4, u4)")
+
+
+def pack4(values: np.ndarray, kind: str) -> np.ndarray:
+    """`torch/packed.py:61-75` for the integer kinds: integers wrap to 4 bits
+    (floats round toward zero first), two a byte, low first."""
+    if kind not in ("i4", "u4"):
+        raise ValueError(f"`{kind}` is not an integer 4-bit format (i4, u4)")
+    values = np.asarray(values)
+    if values.shape[-1] % 2:
+        raise ValueError(f"a 4-bit tensor's last axis is even, found shape {values.shape}")
+    codes = (np.trunc(values).astype(np.int64) if values.dtype.kind == "f" else values.astype(np.int64)) & 15
+    pairs = codes.astype(np.uint8).reshape(*codes.shape[:-1], -1, 2)
+    return (pairs[..., 0] | (pairs[..., 1] << 4)).astype(np.uint8)
+
+
+# ------------------------------------------------------------ int4 quantize
+
+
+def quantize_int4_groups(weight: np.ndarray, group: int = 128) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """`(packed, scale, zero)` for an `[Out, In]` weight; scale is f32.
+
+    Restates `quant.py:83-99` step for step, in f32: `scale = (max - min) / 15`
+    (0 or NaN -> 1), `zero = clip(rint(-min / scale), 0, 15)`,
+    `q = clip(rint(w / scale) + zero, 0, 15)`, rint ties to even.
+
+    Pins: error <= step / 2 (`tests/test_quant_groups.py:48-56`); known answers
+    for ramps and constant groups; brute-force nearest level on tiny groups
+    (tests/test_oracle.py)."""
+    if weight.ndim != 2:
+        raise ValueError(f"a linear weight is [Out, In]; this one is {list(weight.shape)}")
+    out_features, in_features = weight.shape
+    if group <= 0 or group % 2 != 0 or in_features % group != 0:
+        raise ValueError(f"groups of {group} must be even and divide the {in_features} inputs")
+    grouped = weight.astype(np.float32).reshape(out_features, in_features // group, group)
+    low = grouped.min(axis=-1)
+    high = grouped.max(axis=-1)
+    scale = (high - low) / np.float32(15.0)
+    scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
+    zero = np.clip(np.round(-low / scale), 0, 15).astype(np.uint8)
+    q = np.clip(np.round(grouped / scale[..., None]) + zero[..., None].astype(np.float32), 0, 15)
+    return pack_int4_groups(q.reshape(out_features, in_features), group), scale, zero
+
+
+def dequantize_int4_groups(packed: np.ndarray, scale: np.ndarray, zero: np.ndarray) -> np.ndarray:
+    """The f32 `[Out, In]` weight `(q - zero) * scale`. Restates `quant.py:131-136`
+    and the body of `std.quant::dequantize_int4_groups` (`stdlib/quant.linnet:118-126`)
+    before its final cast."""
+    out_features, groups, half = packed.shape
+    q = unpack_int4_codes(packed).reshape(out_features, groups, 2 * half)
+    weight = (q.astype(np.float32) - zero[..., None].astype(np.float32)) * scale[..., None].astype(np.float32)
+    return weight.reshape(out_features, groups * 2 * half)
+
+
+def dequantize_int4_weight(packed: np.ndarray, scale_raw: np.ndarray, zero: np.ndarray, dtype: str) -> np.ndarray:
+    """The dequantized weight in the scale's storage dtype, returned as the raw
+    storage array (bf16 bits / float16 / float32): `(q - z) * s` computed in f32
+    and rounded once. Restates `_int4_weight`/`_int4_unpack`
+    (`src/backend/torch_source.cpp:1518-1550`) and the CPU branch of `_int4_pack`
+    (`torch_source.cpp:1501-1504`).
+
+    Pin: equals torch's `(q.to(bf16) - z.to(bf16)) * s` bit for bit, the
+    reference's own exact check (`tests/test_quant_groups.py:151-162`)."""
+    scale = decode_storage(scale_raw, dtype)
+    weight = dequantize_int4_groups(packed, scale, zero)
+    return encode_storage(weight, dtype)
+
+
+# ------------------------------------------------------------ int8 quantize
+
+
+def quantize_int8_groups(weight: np.ndarray, group: int = 128, dtype: str = "f32") -> tuple[np.ndarray, np.ndarray]:
+    """`(q, scale)` for an `[Out, In]` weight: `scale = max|w| / 127` (0 -> 1)
+    rounded to the storage dtype first, then `q = clip(rint(w / scale), -127, 127)`.
+    Restates `quant.py:102-121`; scale returned as f32.
+
+    Pins: error <= step / 2 (`tests/test_quant_8bit.py:235-242`); the scale is a
+    value of the storage dtype; known answers (tests/test_oracle.py)."""
+    if weight.ndim != 2:
+        raise ValueError(f"a linear weight is [Out, In]; this one is {list(weight.shape)}")
+    out_features, in_features = weight.shape
+    if group <= 0 or in_features % group != 0:
+        raise ValueError(f"groups of {group} must divide the {in_features} inputs")
+    grouped = weight.astype(np.float32).reshape(out_features, in_features // group, group)
+    scale = np.abs(grouped).max(axis=-1) / np.float32(127.0)
+    scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
+    scale = round_to_storage(scale, dtype).reshape(scale.shape)
+    q = np.clip(np.round(grouped / scale[..., None]), -127, 127).astype(np.int8)
+    return q.reshape(out_features, in_features), scale
+
+
+def dequantize_int8_groups(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """Restates `quant.py:124-128`: the f32 weight `q * scale[group]`."""
+    out_features, in_features = q.shape
+    groups = scale.shape[1]
+    grouped = q.astype(np.float32).reshape(out_features, groups, in_features // groups)
+    return (grouped * scale[..., None].astype(np.float32)).reshape(out_features, in_features)
+
+
+# --------------------------------------------------- per-token activation rounding
+
+
+def rows8(x: np.ndarray, fp8: bool) -> tuple[np.ndarray, np.ndarray]:
+    """Each row of `x` (f32 values of the bf16/f16 input) rounded to 8 bits with
+    a scale of its own: `scale = max(max|x|, 1e-12) / (448 or 127)` in f32,
+    `x / scale` in f32, then FP8 E4M3 of `clamp(., +-448)` (round to nearest
+    even) or int8 `clamp(trunc(v +- 0.5), +-127)` (half away from zero, the add
+    done in f32). Returns (codes as uint8 bytes / int8, scale `[rows, 1]` f32).
+
+    Restates `torch/kernels.py:677-707` (`_rows8_kernel`), with IEEE division.
+    Pins: fp8 codes equal torch's `float8_e4m3fn` cast of the same quotients;
+    int8 codes equal round-half-away-from-zero computed exactly in Python on a
+    brute-force sample (tests/test_oracle.py)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    largest = np.float32(448.0 if fp8 else 127.0)
+    top = np.abs(x).max(axis=-1, keepdims=True) if x.shape[-1] else np.zeros((x.shape[0], 1), np.float32)
+    scale = (np.maximum(top, np.float32(1e-12)) / largest).astype(np.float32)
+    v = (x / scale).astype(np.float32)
+    if fp8:
+        return encode_fp8(np.clip(v, np.float32(-448.0), np.float32(448.0))), scale
+    half = np.where(v >= 0, v + np.float32(0.5), v - np.float32(0.5)).astype(np.float32)
+    return np.clip(np.trunc(half), -127, 127).astype(np.int8), scale

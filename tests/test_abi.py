@@ -1,0 +1,140 @@
+"""The C ABI without a GPU: the library loads, exports every entry point
+`include/linnet_quant.h` declares, and rejects bad arguments with a status and a
+message before touching a device. The host wrappers refuse CPU tensors instead
+of falling back to a CPU path."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+from linnet_amd import LinnetError, _lib
+from linnet_amd.torch import generated, kernels, quantized
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "linnet_quant.h"
+
+
+def declared() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"LNQ_API\s+[\w\s\*]+?\b(lnq_\w+)\s*\(", text)
+
+
+def test_header_declares_the_abi() -> None:
+    names = declared()
+    assert "lnq_int4_linear" in names and "lnq_mm8" in names
+    assert len(names) == len(set(names)) == 13
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = _lib.load()
+    for name in declared():
+        assert hasattr(lib, name), name
+    exported = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIBRARY)], capture_output=True, text=True, check=True).stdout
+    for name in declared():
+        assert re.search(rf"\bT {name}\b", exported), name
+    assert set(_lib.SIGNATURES) | {"lnq_abi_version", "lnq_last_error"} == set(declared())
+
+
+def test_abi_version() -> None:
+    assert _lib.load().lnq_abi_version() == _lib.ABI_VERSION == 1
+
+
+def _status(name: str, *args: object) -> tuple[int, str]:
+    status = getattr(_lib.load(), name)(*args)
+    return status, _lib.last_error()
+
+
+NULL = ctypes.c_void_p(0)
+FAKE = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize(
+    ("args", "message"),
+    [
+        ((100, 64, 128, 7), "not a multiple of 128"),  # in_features
+        ((128, 64, 48, 0), "group of 48"),
+        ((128, 64, 128, 9), "dtype 9"),
+    ],
+)
+def test_int4_linear_rejects_bad_arguments(args: tuple[int, int, int, int], message: str) -> None:
+    depth, width, group, dtype = args
+    dtype = dtype if dtype != 7 else _lib.BF16
+    status, error = _status("lnq_int4_linear", FAKE, FAKE, FAKE, FAKE, NULL, FAKE, 1, depth, width, group, dtype, 0, NULL)
+    assert status == _lib.LNQ_ERROR
+    assert message in error
+
+
+def test_unaligned_and_null_pointers_are_rejected() -> None:
+    status, error = _status("lnq_int4_linear", ctypes.c_void_p(4098), FAKE, FAKE, FAKE, NULL, FAKE, 1, 128, 16, 128, _lib.BF16, 0, NULL)
+    assert status == _lib.LNQ_ERROR and "aligned" in error
+    status, error = _status("lnq_int4_linear", NULL, FAKE, FAKE, FAKE, NULL, FAKE, 1, 128, 16, 128, _lib.BF16, 0, NULL)
+    assert status == _lib.LNQ_ERROR and "null" in error
+
+
+def test_other_entry_points_validate() -> None:
+    assert _status("lnq_int4_quantize", FAKE, FAKE, FAKE, FAKE, 4, 130, 64, NULL)[1].startswith("lnq_int4_quantize: groups of 64")
+    assert "dtype 5" in _status("lnq_int4_dequantize", FAKE, FAKE, FAKE, FAKE, 4, 128, 128, 5, NULL)[1]
+    assert "groups" in _status("lnq_int8_quantize", FAKE, FAKE, FAKE, 4, 100, 64, 0, NULL)[1]
+    assert "in % 128" in _status("lnq_w8a16", FAKE, FAKE, FAKE, FAKE, 1, 16, 100, 0, 0, 1, _lib.BF16, NULL)[1]
+    assert "64k" in _status("lnq_w8a16", FAKE, FAKE, FAKE, FAKE, 1, 16, 256, 0, 32, 1, _lib.BF16, NULL)[1]
+    assert "in % 16" in _status("lnq_dequantize8", FAKE, FAKE, FAKE, 4, 100, 0, 0, 1, _lib.BF16, NULL)[1]
+    assert "output is bf16 or f16" in _status("lnq_mm8", FAKE, FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 1, _lib.F32, NULL)[1]
+    assert "negative" in _status("lnq_int4_pack", FAKE, FAKE, -1, NULL)[1]
+
+
+def test_empty_calls_succeed_without_a_device() -> None:
+    assert _status("lnq_int4_linear", FAKE, FAKE, FAKE, FAKE, NULL, FAKE, 0, 128, 16, 128, _lib.BF16, 0, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_int4_dequantize", NULL, NULL, NULL, NULL, 0, 128, 128, _lib.BF16, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_rows8", NULL, NULL, NULL, 0, 128, 1, _lib.BF16, NULL)[0] == _lib.LNQ_OK
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU answer")
+def test_device_probe_without_a_gpu() -> None:
+    a, b = ctypes.c_int32(), ctypes.c_int32()
+    status = _lib.load().lnq_device_probe(0, ctypes.byref(a), ctypes.byref(b))
+    assert status == _lib.LNQ_UNAVAILABLE and "no HIP device" in _lib.last_error()
+
+
+def test_call_raises_with_the_library_message() -> None:
+    with pytest.raises(LinnetError, match="not a multiple of 128"):
+        _lib.call("lnq_int4_linear", FAKE, FAKE, FAKE, FAKE, NULL, FAKE, 1, 100, 16, 100, _lib.BF16, 0, NULL)
+
+
+# --------------------------------------------------------------- host wrappers
+
+
+def test_cpu_tensors_raise_instead_of_falling_back() -> None:
+    x = torch.zeros(1, 128, dtype=torch.bfloat16)
+    packed = torch.zeros(16, 1, 64, dtype=torch.uint8)
+    scale = torch.ones(16, 1, dtype=torch.bfloat16)
+    zero = torch.zeros(16, 1, dtype=torch.uint8)
+    with pytest.raises(LinnetError, match="GPU"):
+        kernels.int4_linear(x, packed, scale, zero)
+    with pytest.raises(LinnetError, match="GPU"):
+        generated._int4_pack(packed, scale, zero)
+    with pytest.raises(LinnetError, match="GPU"):
+        quantized.int8_operands(torch.zeros(16, 128, dtype=torch.int8), torch.ones(16), 0)
+    with pytest.raises(LinnetError, match="GPU"):
+        quantized.fp8_operands(torch.zeros(16, 128, dtype=torch.uint8), torch.ones(16), 1)
+    with pytest.raises(LinnetError, match="GPU"):
+        kernels.fp8_rows(x)
+
+
+def test_fused_group_gate_matches_the_reference() -> None:
+    """`_int4_pack` takes groups 32, 64 and multiples of 128 (`torch_source.cpp:1489-1494`
+    took 32, 64, 128, 256 for tinygemm)."""
+    assert all(generated._fused_group(g) for g in (32, 64, 128, 256, 512))
+    assert not any(generated._fused_group(g) for g in (2, 16, 48, 96))
+
+
+def test_bench_refuses_more_than_one_gpu() -> None:
+    done = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True, timeout=300)
+    assert done.returncode == 2
+    assert "one GPU" in done.stderr

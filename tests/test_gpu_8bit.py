@@ -1,0 +1,192 @@
+"""Parity of the 8-bit HIP path with the oracle, on the GPU, through the C ABI.
+
+- int8 quantize, per-token FP8 / int8 rounding (rows8), dequantize8: bit for bit;
+- weight-only products (gemv8 / w8a16) and 8-bit x 8-bit products (int8_mm, fp8_mm):
+  within the reference's bounds, `0.01 * max|want|` for the weight-only kernels and
+  the product of the rounded operands (`python/linnet/tests/test_quant_8bit.py:315-341`);
+- the `quantized.*_operands / *_linear` dispatch against the reference CPU path,
+  `0.06 * max` where the input is rounded to 8 bits (`test_quant_8bit.py:341`,
+  `test_quant_fp8.py:196-220`).
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from linnet_amd.torch import kernels, quantized
+from oracle import linear, quant
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = Path(__file__).parent / "golden"
+
+
+def _err(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
+    err = float(np.abs(got - want).max()) if got.size else 0.0
+    top = float(np.abs(want).max()) if want.size else 0.0
+    print(f"max abs err {err:.3e}, rel to max {err / max(top, 1e-30):.3e}")
+    return err, top
+
+
+@pytest.mark.parametrize(("out", "width", "group", "dtype"), [(256, 512, 128, "bf16"), (16, 4096, 4096, "f32"), (7, 96, 32, "f16"), (3, 10, 5, "bf16")])
+def test_int8_quantize_matches_numpy(out: int, width: int, group: int, dtype: str) -> None:
+    w = np.random.default_rng(out).standard_normal((out, width)).astype(np.float32)
+    w[0, :group] = 0.0
+    q, s = kernels.quantize_int8(torch.from_numpy(w).to(DEV), group, dtype)
+    wq, ws = quant.quantize_int8_groups(w, group, dtype)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("rows", "width"), [(9, 300), (4, 8192), (1, 16384), (2, 20000), (3, 1)])
+def test_rows8_matches_the_oracle(fp8: bool, dtype: torch.dtype, rows: int, width: int) -> None:
+    g = torch.Generator().manual_seed(rows * 7 + width)
+    x = torch.randn(rows, width, generator=g)
+    x[0, : min(3, width)] *= 40
+    if rows > 2:
+        x[2] = 0.0
+    x = x.to(dtype)
+    q, s = (kernels.fp8_rows if fp8 else kernels.int8_rows)(x.to(DEV))
+    wq, ws = quant.rows8(x.float().numpy(), fp8)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8 if fp8 else torch.int8).numpy(), wq.view(np.uint8) if fp8 else wq)
+
+
+def test_rows8_golden_fixture() -> None:
+    data = np.load(GOLDEN / "rows8.npz")
+    x = torch.from_numpy(data["x_bits"].view(np.int16)).view(torch.bfloat16).to(DEV)
+    q, s = kernels.fp8_rows(x)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), data["fp8_q"])
+    np.testing.assert_array_equal(s.cpu().numpy(), data["fp8_scale"])
+    q, s = kernels.int8_rows(x)
+    np.testing.assert_array_equal(q.cpu().numpy(), data["int8_q"])
+    np.testing.assert_array_equal(s.cpu().numpy(), data["int8_scale"])
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("group", "row_block"), [(0, 1), (128, 1), (128, 128), (16, 1)])
+def test_dequantize8_is_bit_exact(fp8: bool, dtype: torch.dtype, group: int, row_block: int) -> None:
+    out, width = 256, 512
+    g = torch.Generator().manual_seed(group + row_block)
+    full = torch.randn(out, width, generator=g)
+    w = (full * 20).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8) if fp8 else (full * 40).round().clamp(-127, 127).to(torch.int8)
+    cols = 1 if group == 0 else width // group
+    scale = torch.rand(out // row_block if group else out, cols, generator=g) * 0.01 + 1e-4
+    if group == 0:
+        scale = scale.reshape(-1)
+    got = kernels.dequantize8(w.to(DEV), scale.to(DEV), fp8, group, row_block, dtype).cpu()
+    widened = w.view(torch.float8_e4m3fn).float() if fp8 else w.float()
+    if group == 0:
+        full_scale = scale[:, None]
+    else:
+        full_scale = scale.repeat_interleave(row_block, 0).repeat_interleave(group, 1)
+    want = (widened * full_scale).to(dtype)
+    assert torch.equal(got.view(torch.int16 if dtype != torch.float32 else torch.int32), want.view(torch.int16 if dtype != torch.float32 else torch.int32))
+
+
+def _eight_bit(out: int, width: int, fp8: bool, seed: int, group: int = 0, row_block: int = 1):
+    g = torch.Generator().manual_seed(seed)
+    full = torch.randn(out, width, generator=g) * 0.02
+    if group == 0:
+        scale = full.abs().amax(1) / (448.0 if fp8 else 127.0)
+        wide = scale[:, None]
+    else:
+        blocked = full.reshape(out // row_block, row_block, width // group, group)
+        scale = blocked.abs().amax((1, 3)) / (448.0 if fp8 else 127.0)
+        wide = scale.repeat_interleave(row_block, 0).repeat_interleave(group, 1)
+    q = (full / wide).to(torch.float8_e4m3fn).view(torch.uint8) if fp8 else (full / wide).round().clamp(-127, 127).to(torch.int8)
+    deq = ((q.view(torch.float8_e4m3fn).float() if fp8 else q.float()) * wide).numpy()
+    return q, scale.float(), deq
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize(("rows", "out", "group", "row_block", "dtype"), [
+    (1, 256, 0, 1, torch.bfloat16), (3, 72, 0, 1, torch.float16), (17, 256, 128, 1, torch.bfloat16),
+    (64, 256, 128, 128, torch.bfloat16), (1, 4096, 0, 1, torch.bfloat16), (33, 40, 64, 1, torch.float16),
+])
+def test_weight_only_kernels(fp8: bool, rows: int, out: int, group: int, row_block: int, dtype: torch.dtype) -> None:
+    width = 512
+    if group and out % row_block:
+        pytest.skip("blocks tile the weight")
+    q, scale, deq = _eight_bit(out, width, fp8, seed=rows, group=group, row_block=row_block)
+    x = torch.randn(rows, width, generator=torch.Generator().manual_seed(rows)).to(dtype)
+    y = kernels.w8a16(x.to(DEV), q.to(DEV), scale.to(DEV), fp8, group, row_block).float().cpu().numpy()
+    want = linear.product_f64(x.float().numpy(), deq)
+    err, top = _err(y, want)
+    assert err <= 0.01 * top
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize(("rows", "out", "width"), [(33, 256, 512), (256, 200, 1024), (130, 128, 128), (1, 64, 256)])
+def test_8bit_products(fp8: bool, rows: int, out: int, width: int) -> None:
+    q, scale, deq = _eight_bit(out, width, fp8, seed=out)
+    x = torch.randn(rows, width, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+    qx, xs = (kernels.fp8_rows if fp8 else kernels.int8_rows)(x.to(DEV))
+    mm = kernels.fp8_mm if fp8 else kernels.int8_mm
+    y = mm(qx, q.to(DEV), xs, scale.to(DEV), torch.bfloat16).float().cpu().numpy()
+    want = linear.rows8_product_f64(qx.view(torch.uint8).cpu().numpy() if fp8 else qx.cpu().numpy(), xs.cpu().numpy(), q.numpy().view(np.uint8) if fp8 else q.numpy(), scale.numpy(), fp8)
+    err, top = _err(y, want)
+    assert err <= 0.01 * top
+    exact = linear.product_f64(x.float().numpy(), deq)
+    err, top = _err(y, exact)
+    assert err <= 0.06 * top
+
+
+@pytest.mark.parametrize("rows", [1, 3, 17, 64, 100])
+@pytest.mark.parametrize("rounded", [0, 1])
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int8_group", "fp8_block"])
+def test_quantized_dispatch_against_the_reference_cpu_path(kind: str, rounded: int, rows: int) -> None:
+    """`test_quant_8bit.py:315-341`: within bf16's rounding of the product with the
+    dequantized weight; rounded inputs within 8 bits'."""
+    out, width = 256, 512
+    fp8 = kind.startswith("fp8")
+    group = 128 if kind in ("int8_group", "fp8_block") else 0
+    row_block = 128 if kind == "fp8_block" else 1
+    q, scale, deq = _eight_bit(out, width, fp8, seed=rows + rounded, group=group, row_block=row_block)
+    x = torch.randn(rows, width, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+    bias = torch.randn(out, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    xd, qd, sd, bd = x.to(DEV), q.to(DEV), scale.to(DEV), bias.to(DEV)
+    if kind == "fp8":
+        got = quantized.fp8_linear(xd, quantized.fp8_operands(qd, sd.to(torch.bfloat16), rounded), bd)
+        want = linear.fp8_linear_cpu(x, q.view(torch.float8_e4m3fn), scale.to(torch.bfloat16), bias)
+    elif kind == "int8":
+        got = quantized.int8_linear(xd, quantized.int8_operands(qd, sd.to(torch.bfloat16), rounded), bd)
+        want = linear.int8_linear_cpu(x, q, scale.to(torch.bfloat16), bias)
+    elif kind == "int8_group":
+        got = quantized.int8_group_linear(xd, quantized.int8_group_operands(qd, sd.to(torch.bfloat16)), bd)
+        want = linear.int8_group_linear_cpu(x, q, scale.to(torch.bfloat16), bias)
+    else:
+        got = quantized.fp8_block_linear(xd, quantized.fp8_block_operands(qd, sd.to(torch.bfloat16), rounded), bd)
+        decoded = q.view(torch.float8_e4m3fn).float() * scale.to(torch.bfloat16).float().repeat_interleave(128, 0).repeat_interleave(128, 1)
+        want = torch.nn.functional.linear(x, decoded.to(torch.bfloat16)) + bias
+    err, top = _err(got.float().cpu().numpy(), want.float().numpy())
+    is_rounded = rounded and rows > 32 and kind in ("fp8", "int8")
+    assert err <= (0.06 if is_rounded else 0.01) * top
+
+
+@pytest.mark.parametrize("rows", [1, 256])
+def test_fp8_baseline_shape(rows: int) -> None:
+    """BASELINE config 4's shape (K=8192, N=28672), per-tensor scale broadcast into
+    `Fp8Linear`'s per-row scale, the input rounded a token at a time past 32 rows:
+    against dequantize + hipBLASLt within FP8's rounding bound."""
+    k, n = 8192, 28672
+    g = torch.Generator(device=DEV).manual_seed(0)
+    w = torch.randn(n, k, generator=g, device=DEV) * 0.02
+    s = (w.abs().max() / 448.0).float()
+    q = (w / s).to(torch.float8_e4m3fn)
+    scale = s.expand(n).contiguous().to(torch.bfloat16)
+    x = torch.randn(rows, k, generator=g, device=DEV).to(torch.bfloat16)
+    got = quantized.fp8_linear(x, quantized.fp8_operands(q, scale, 1), None).float()
+    deq = kernels.dequantize8(q.view(torch.uint8), scale.float(), True, 0, 1, torch.bfloat16)
+    want = (x.float() @ deq.float().T)
+    err = (got - want).abs().max().item()
+    top = want.abs().max().item()
+    print(f"rows {rows}: max abs err {err:.3e} rel {err / top:.3e}")
+    assert err <= (0.06 if rows > 32 else 0.01) * top

@@ -1,0 +1,283 @@
+"""Pins of the CPU oracle (`oracle/`) against facts fixed independently of its
+own formulas: PyTorch's bf16 / float8_e4m3fn conversions, the reference's
+closed-form layouts and known answers, its tests' invariants
+(`python/linnet/tests/test_quant_groups.py`, `test_quant_8bit.py`,
+`test_quant_fp8.py`, `torch/test_quant.py`, `test_resources.py`), and brute force
+on tiny inputs. Each test names the mistake it would catch."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import linear, quant
+
+
+# ------------------------------------------------------------------ bf16 / fp8
+
+
+def test_bf16_rounding_matches_torch() -> None:
+    """to_bf16_bits is RNE (a truncation or round-half-up would fail the ties)."""
+    rng = np.random.default_rng(0)
+    values = (rng.standard_normal(20000) * 10.0 ** rng.integers(-30, 30, 20000)).astype(np.float32)
+    bits = values.view(np.uint32)
+    ties = ((bits & np.uint32(0xFFFF0000)) | np.uint32(0x8000)).view(np.float32)  # exact ties
+    for v in (values, ties.astype(np.float32), np.array([0.0, -0.0, 1.0, -3.5, 65504.0], np.float32)):
+        want = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        np.testing.assert_array_equal(quant.to_bf16_bits(v), want)
+        np.testing.assert_array_equal(quant.from_bf16_bits(want), torch.from_numpy(v).to(torch.bfloat16).float().numpy())
+
+
+def test_fp8_decode_matches_torch() -> None:
+    """Every non-NaN E4M3 byte decodes as torch's float8_e4m3fn
+    (`tests/test_quant_fp8.py:46-53`); the NaN bytes read as +-480 in the body."""
+    table = np.arange(256, dtype=np.uint8)
+    valid = (table & 0x7F) != 0x7F
+    want = torch.from_numpy(table).view(torch.float8_e4m3fn).float().numpy()
+    got = quant.decode_fp8(table)
+    np.testing.assert_array_equal(got[valid], want[valid])
+    assert got[0x7F] == 480.0 and got[0xFF] == -480.0
+    assert got[0x08] == 2.0**-6 and got[0x01] == 2.0**-9 and got[0x7E] == 448.0
+
+
+def test_fp8_encode_matches_torch() -> None:
+    """encode_fp8 rounds to nearest even with subnormals, as torch's cast does:
+    every representable value, every midpoint (tie) and random values in range."""
+    table = np.arange(256, dtype=np.uint8)
+    valid = (table & 0x7F) != 0x7F
+    exact = quant.decode_fp8(table[valid])
+    positive = np.unique(np.abs(exact))
+    mids = ((positive[:-1].astype(np.float64) + positive[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(1)
+    rand = (rng.standard_normal(50000) * 10.0 ** rng.uniform(-3, 2.5, 50000)).astype(np.float32)
+    values = np.concatenate([exact, mids, -mids, rand, np.float32([0.0, -0.0, 1e-30, -1e-30])])
+    values = np.clip(values, -448, 448).astype(np.float32)
+    want = torch.from_numpy(values).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(quant.encode_fp8(values), want)
+
+
+# ---------------------------------------------------------------- 4-bit layout
+
+
+def test_pack_layout_closed_form() -> None:
+    """Element 2k sits in the low nibble (`spec/03-types.md:39`,
+    `torch/test_quant.py:48-59`); a swapped order fails."""
+    codes = np.arange(16, dtype=np.uint8)[None, :]
+    packed = quant.pack_int4_groups(codes, 16)
+    assert packed.shape == (1, 1, 8)
+    np.testing.assert_array_equal(packed.reshape(-1), np.array([0x10, 0x32, 0x54, 0x76, 0x98, 0xBA, 0xDC, 0xFE], np.uint8))
+    np.testing.assert_array_equal(quant.unpack_int4_codes(packed).reshape(1, 16), codes)
+    # i4: sign-extended (torch/test_quant.py:48-85's widen check).
+    rng = np.random.default_rng(0)
+    q4 = rng.integers(-8, 8, size=(6, 16)).astype(np.int8)
+    low = q4[:, 0::2].astype(np.int32) & 15
+    high = q4[:, 1::2].astype(np.int32) & 15
+    bytes_ = ((high << 4) | low).astype(np.uint8)
+    np.testing.assert_array_equal(quant.unpack4(bytes_, "i4"), q4)
+    np.testing.assert_array_equal(quant.pack4(q4, "i4"), bytes_)
+    np.testing.assert_array_equal(quant.pack4(np.array([2.7, -9.5]), "i4"), np.array([(2 & 15) | ((-9 & 15) << 4)], np.uint8))
+
+
+def test_int4_storage_bytes() -> None:
+    """Int4GroupLinear<256, 64, 128, bf16> holds 64*2*64 + 64*2*2 + 64*2 bytes
+    (`tests/test_resources.py:184-202`)."""
+    w = np.random.default_rng(0).standard_normal((64, 256)).astype(np.float32)
+    packed, scale, zero = quant.quantize_int4_groups(w, 128)
+    total = packed.nbytes + quant.encode_storage(scale, "bf16").nbytes + zero.nbytes
+    assert total == 64 * 2 * 64 + 64 * 2 * 2 + 64 * 2
+
+
+# ------------------------------------------------------------------ int4 codes
+
+
+def test_int4_rounding_within_half_a_step() -> None:
+    """`tests/test_quant_groups.py:48-56`: |dequant - w| <= step / 2."""
+    rng = np.random.default_rng(0)
+    weight = rng.standard_normal((64, 256)).astype(np.float32)
+    packed, scale, zero = quant.quantize_int4_groups(weight, 128)
+    assert packed.shape == (64, 2, 64) and packed.dtype == np.uint8
+    assert scale.shape == zero.shape == (64, 2) and scale.dtype == np.float32
+    error = np.abs(quant.dequantize_int4_groups(packed, scale, zero) - weight)
+    assert np.all(error <= np.repeat(scale, 128, axis=1) / 2 + 1e-6)
+    assert zero.max() <= 15
+
+
+def test_int4_known_answers() -> None:
+    """Ramps and constants with exact answers: a step of (max-min)/16, a zero of
+    the wrong sign, or floor instead of rint fails."""
+    ramp = (np.arange(16, dtype=np.float32) * 0.25)[None, :]
+    packed, scale, zero = quant.quantize_int4_groups(ramp, 16)
+    assert scale[0, 0] == np.float32(0.25) and zero[0, 0] == 0
+    np.testing.assert_array_equal(quant.unpack_int4_codes(packed).reshape(-1), np.arange(16))
+    shifted = ((np.arange(16, dtype=np.float32) - 5) * 0.5)[None, :]
+    packed, scale, zero = quant.quantize_int4_groups(shifted, 16)
+    assert scale[0, 0] == np.float32(0.5) and zero[0, 0] == 5
+    np.testing.assert_array_equal(quant.unpack_int4_codes(packed).reshape(-1), np.arange(16))
+    const = np.full((2, 16), [[0.3], [-2.2]], dtype=np.float32)
+    packed, scale, zero = quant.quantize_int4_groups(const, 16)
+    np.testing.assert_array_equal(scale, np.ones((2, 1), np.float32))
+    np.testing.assert_array_equal(zero.reshape(-1), [0, 2])
+    np.testing.assert_array_equal(quant.unpack_int4_codes(packed).reshape(2, 16), np.zeros((2, 16)))
+    # Half-way codes round to even: w/scale + zero = 0.5 -> 0, 2.5 -> 2.
+    halves = np.array([[0.0, 0.5, 2.5, 15.0] * 4], dtype=np.float32)
+    packed, scale, zero = quant.quantize_int4_groups(halves, 16)
+    assert scale[0, 0] == 1.0 and zero[0, 0] == 0
+    np.testing.assert_array_equal(quant.unpack_int4_codes(packed).reshape(-1)[:4], [0, 0, 2, 15])
+
+
+def test_int4_codes_are_the_nearest_levels() -> None:
+    """Brute force on tiny groups: each code is the level (c - z) * s nearest w
+    among all 16 (off-by-one zero points or truncation fail)."""
+    rng = np.random.default_rng(5)
+    weight = (rng.standard_normal((8, 32)) * 0.02).astype(np.float32)
+    packed, scale, zero = quant.quantize_int4_groups(weight, 16)
+    codes = quant.unpack_int4_codes(packed).reshape(8, 32)
+    for o in range(8):
+        for i in range(32):
+            g = i // 16
+            levels = (np.arange(16) - float(zero[o, g])) * float(scale[o, g])
+            assert codes[o, i] == int(np.argmin(np.abs(levels - float(weight[o, i]))))
+
+
+def test_dequantized_weight_matches_torch_bf16_arithmetic() -> None:
+    """The reference's own bit-exact check (`tests/test_quant_groups.py:151-162`):
+    `(q.to(bf16) - z.to(bf16)) * s` in torch equals the oracle's dequantized bits."""
+    rng = np.random.default_rng(2)
+    out, groups, group = 72, 4, 128
+    packed = rng.integers(0, 256, (out, groups, group // 2), dtype=np.uint8)
+    scale = (rng.random((out, groups)) * 0.02 + 0.001).astype(np.float32)
+    scale_bits = quant.to_bf16_bits(scale)
+    zero = rng.integers(0, 16, (out, groups), dtype=np.uint8)
+    got = quant.dequantize_int4_weight(packed, scale_bits, zero, "bf16")
+    p = torch.from_numpy(packed)
+    levels = torch.stack([p & 15, p >> 4], dim=-1).reshape(out, groups, group)
+    s = torch.from_numpy(scale_bits.view(np.int16)).view(torch.bfloat16)
+    z = torch.from_numpy(zero)
+    want = ((levels.to(torch.bfloat16) - z.to(torch.bfloat16)[..., None]) * s[..., None]).reshape(out, -1)
+    np.testing.assert_array_equal(got, want.view(torch.int16).numpy().view(np.uint16))
+    # f16 and f32 storage follow the same one-rounding rule.
+    for dtype, tdtype in (("f16", torch.float16), ("f32", torch.float32)):
+        raw = quant.encode_storage(scale, dtype)
+        st = torch.from_numpy(np.asarray(raw))
+        want = ((levels.to(tdtype) - z.to(tdtype)[..., None]) * st[..., None]).reshape(out, -1).numpy()
+        np.testing.assert_array_equal(quant.dequantize_int4_weight(packed, raw, zero, dtype), want)
+
+
+# ------------------------------------------------------------------ int8 codes
+
+
+def test_int8_rounding_within_half_a_step() -> None:
+    """`tests/test_quant_8bit.py:235-242`; the scale is a bf16 value."""
+    weight = np.random.default_rng(0).standard_normal((256, 512)).astype(np.float32)
+    q, scale = quant.quantize_int8_groups(weight, 128, "bf16")
+    assert q.dtype == np.int8 and q.shape == (256, 512) and scale.shape == (256, 4)
+    error = np.abs(quant.dequantize_int8_groups(q, scale) - weight)
+    assert np.all(error <= np.repeat(scale, 128, axis=1) / 2 + 1e-6)
+    np.testing.assert_array_equal(quant.round_to_storage(scale, "bf16"), scale)
+    assert np.abs(q).max() <= 127
+
+
+def test_int8_known_answers() -> None:
+    """max|w| = 127 gives scale 1 and q = round-half-even(w); a zero group gives
+    scale 1 (`quant.py:116`); rounding the scale after the codes fails the bf16 case."""
+    w = np.array([[127.0, -3.5, 2.5, 0.4, -127.0, 1.5, 0.0, 100.2]], dtype=np.float32)
+    q, scale = quant.quantize_int8_groups(w, 8, "f32")
+    assert scale[0, 0] == 1.0
+    np.testing.assert_array_equal(q[0], [127, -4, 2, 0, -127, 2, 0, 100])
+    q, scale = quant.quantize_int8_groups(np.zeros((1, 8), np.float32), 8, "bf16")
+    assert scale[0, 0] == 1.0 and not q.any()
+    # 1.0 / 127 is not a bf16 value: the codes are computed against its rounding.
+    w = np.full((1, 4), [1.0, 0.5, 0.25, -1.0], dtype=np.float32)
+    q, scale = quant.quantize_int8_groups(w, 4, "bf16")
+    s = np.float32(torch.tensor(1.0 / 127).to(torch.bfloat16).item())
+    assert scale[0, 0] == s
+    np.testing.assert_array_equal(q[0], np.clip(np.round(w[0] / s), -127, 127))
+
+
+# --------------------------------------------------------- activation rounding
+
+
+def test_rows8_fp8_matches_torch_cast() -> None:
+    """FP8 rows: the per-row scale max|x|/448 and torch's float8_e4m3fn cast of
+    x / scale (a scale over 127, or a missing clamp, fails)."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((9, 300)).astype(np.float32)
+    x[2] *= 50
+    x[4] = 0.0
+    x = quant.from_bf16_bits(quant.to_bf16_bits(x)).reshape(x.shape)
+    q, scale = quant.rows8(x, True)
+    t = torch.from_numpy(x)
+    s = torch.clamp(t.abs().amax(dim=1, keepdim=True), min=1e-12) / 448.0
+    np.testing.assert_array_equal(scale, s.numpy())
+    want = (t / s).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(q, want)
+
+
+def test_rows8_int8_rounds_half_away_in_f32() -> None:
+    """int8 rows: half away from zero, the +-0.5 added in f32 as the reference's
+    kernel does (`torch/kernels.py:690-691`): 2.5 -> 3, -2.5 -> -3, and the f32
+    edge 0.49999997 + 0.5 = 1.0 -> 1."""
+    x = np.array([[127.0, 2.5, -2.5, 0.49999997, -0.5, 1.4999999, 126.5, -126.49]], dtype=np.float32)
+    q, scale = quant.rows8(x, False)
+    assert scale[0, 0] == 1.0
+    np.testing.assert_array_equal(q[0], [127, 3, -3, 1, -1, 1, 127, -126])
+    # Away from the f32 edge it is exact round-half-away (brute force).
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((4, 64)) * 30).astype(np.float32)
+    q, scale = quant.rows8(x, False)
+    v = x.astype(np.float64) / scale.astype(np.float64)
+    exact = np.sign(v) * np.floor(np.abs(v) + 0.5)
+    np.testing.assert_array_equal(q.astype(np.float64), np.clip(exact, -127, 127))
+
+
+# -------------------------------------------------------------- CPU linear paths
+
+
+def test_cpu_int4_paths_agree_with_fp64() -> None:
+    """The interpreter path and the generated CPU path give the same bf16 output,
+    within bf16 rounding of the f64 product with the dequantized weight."""
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((64, 256)) * 0.02).astype(np.float32)
+    packed, scale, zero = quant.quantize_int4_groups(w, 128)
+    scale_bits = quant.to_bf16_bits(scale)
+    p = torch.from_numpy(packed)
+    s = torch.from_numpy(scale_bits.view(np.int16)).view(torch.bfloat16)
+    z = torch.from_numpy(zero)
+    x = torch.randn(3, 256, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    interp = linear.int4_groups_linear_interpreter(x, p, s, z, None)
+    gen = linear.int4_linear_generated_cpu(x, linear.int4_prepare_cpu(p, s, z), None)
+    torch.testing.assert_close(interp, gen, rtol=0, atol=0)
+    ref = linear.int4_reference_f64(x.float().numpy(), packed, quant.from_bf16_bits(scale_bits), zero)
+    assert np.abs(interp.float().numpy() - ref).max() <= 1e-2 * np.abs(ref).max()
+
+
+def test_cpu_8bit_paths_agree_with_fp64() -> None:
+    rng = np.random.default_rng(1)
+    w = rng.standard_normal((32, 256)).astype(np.float32)
+    q, scale = quant.quantize_int8_groups(w, 256, "f32")
+    x = torch.randn(2, 256, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    got = linear.int8_linear_cpu(x, torch.from_numpy(q), torch.from_numpy(scale.reshape(-1)), None)
+    ref = linear.product_f64(x.float().numpy(), quant.dequantize_int8_groups(q, scale))
+    assert np.abs(got.float().numpy() - ref).max() <= 1e-2 * np.abs(ref).max()
+    full = torch.from_numpy(w)
+    fs = full.abs().amax(dim=1, keepdim=True) / 448.0
+    w8 = (full / fs).to(torch.float8_e4m3fn)
+    got = linear.fp8_linear_cpu(x, w8, fs, None)
+    ref = linear.product_f64(x.float().numpy(), (w8.float() * fs).numpy())
+    assert np.abs(got.float().numpy() - ref).max() <= 1e-2 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+def test_rows8_product_reference(fp8: bool) -> None:
+    """The 8-bit product reference equals the dequantized operands' product."""
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, 128)).astype(np.float32)
+    q, xs = quant.rows8(x, fp8)
+    wq = (quant.encode_fp8(np.clip(rng.standard_normal((5, 128)) * 50, -448, 448).astype(np.float32)) if fp8
+          else rng.integers(-127, 128, (5, 128)).astype(np.int8))
+    ws = rng.random(5).astype(np.float32)
+    got = linear.rows8_product_f64(q, xs, wq, ws, fp8)
+    deq_x = (quant.decode_fp8(q) if fp8 else q.astype(np.float32)) * xs
+    deq_w = (quant.decode_fp8(wq) if fp8 else wq.astype(np.float32)) * ws[:, None]
+    np.testing.assert_allclose(got, deq_x.astype(np.float64) @ deq_w.astype(np.float64).T, rtol=1e-6)
