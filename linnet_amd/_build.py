@@ -30,6 +30,7 @@ FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-fvisibility=hidden",
+    "-ffp-contract=off",
     "-Xclang",
     "-target-feature",
     "-Xclang",

@@ -76,7 +76,12 @@ __device__ inline float f16_bits_to_f32(uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
 
+// f32 -> f16 bits, round to nearest even, from the f32 value as it stands: the
+// empty asm keeps the compiler from folding a preceding f32 multiply into a
+// single-rounding mixed-precision FMA (v_fma_mixlo_f16), which would skip the
+// f32 rounding every reference computes first.
 __device__ inline uint16_t f32_to_f16_bits(float f) {
+  __asm__ volatile("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
@@ -144,6 +149,39 @@ __device__ inline u32x4 nibbles_to_magic(uint32_t w) {
   out.y = __builtin_amdgcn_perm(hi, lo, 0x0c050c01u) | Elem<DT>::MAGIC2;
   out.z = __builtin_amdgcn_perm(hi, lo, 0x0c060c02u) | Elem<DT>::MAGIC2;
   out.w = __builtin_amdgcn_perm(hi, lo, 0x0c070c03u) | Elem<DT>::MAGIC2;
+  return out;
+}
+
+// 8 packed 4-bit codes as MAGIC + q, pair order: dword s holds elements s (low)
+// and s + 4 (high) -- one v_and_or per dword after a shift. The A operand must
+// then hold x in the order 0,4,1,5,2,6,3,7 of each 8 (see permute_x8).
+// (a & b) | c in one v_and_or_b32. The operands are VGPRs: a VOP3 instruction
+// on gfx950 takes no literal constants and at most one SGPR, so the compiler
+// would otherwise split it into v_and + v_or with literals.
+__device__ inline uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t d;
+  __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
+// `mask` and `magic` are 0x000f000f and Elem<DT>::MAGIC2, held in VGPRs by the caller.
+template <int DT>
+__device__ inline u32x4 nibbles_to_magic_paired(uint32_t w, uint32_t mask, uint32_t magic) {
+  u32x4 out;
+  out.x = and_or(w, mask, magic);
+  out.y = and_or(w >> 4, mask, magic);
+  out.z = and_or(w >> 8, mask, magic);
+  out.w = and_or(w >> 12, mask, magic);
+  return out;
+}
+
+// 8 consecutive 16-bit values (4 dwords) reordered 0,4,1,5,2,6,3,7.
+__device__ inline u32x4 permute_x8(u32x4 v) {
+  u32x4 out;
+  out.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+  out.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+  out.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+  out.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
   return out;
 }
 

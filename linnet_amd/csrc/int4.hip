@@ -58,24 +58,42 @@ __device__ inline void load_chunk(const uint8_t* __restrict__ chunk, int j, uint
   }
 }
 
-template <int DT, int LOADW, int MT>
+// x (the A operand) comes either from LDS (XL) or from global memory.
+//
+// XL (the decode case, each wave's slice of x small): every wave copies its own
+// K-slice of the workgroup's rows of x into a private LDS region, reordering
+// each 8 elements 0,4,1,5,2,6,3,7 so that the codes widen in pair order (one
+// v_and_or per dword), and issues those loads BEFORE its weight loads: loads
+// retire in order, so a chunk's math then waits only for that chunk's weights.
+// The weights stream in batches of U chunks, double-buffered: batch b + 1 is
+// requested before batch b is multiplied.
+//
+// Otherwise x is read from global memory PD chunks ahead, in element order,
+// and the codes widen in element order (v_perm + or).
+// SV: the scales and zero points of a batch's 4 chunks (4 groups of 128) come in
+// one 8-byte and one 4-byte load per lane (aligned shapes, group 128).
+template <int DT, int LOADW, int MT, bool XL, bool SV>
 __global__ __launch_bounds__(256) void int4_skinny_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G) {
   using E = Elem<DT>;
-  // Groups an MFMA group-step covers: MFMAs t = 0..3 of a chunk, a group
-  // closes after every `tpg` of them.
+  // MFMAs t = 0..3 of a chunk; a group closes after every `tpg` of them.
   constexpr int tpg = LOADW == 16 ? 4 : (LOADW == 8 ? 2 : 1);
+  constexpr int GPC = 4 / tpg;  // groups a chunk spans
+  constexpr int U = 4;          // chunks of weight a batch
+  constexpr int PD = XL ? 1 : 2;  // chunks of x in flight ahead of use
   __shared__ f32x4 red[4][MT][64];
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;
   const int j = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int m0 = blockIdx.y * 16 * MT;
-  const int nrow = min(n0 + col, N - 1);  // rows past N read row N-1, never stored
+  const int mrows = min(M - m0, 16 * MT);  // rows of x this workgroup reads
+  const int nrow = min(n0 + col, N - 1);   // rows past N read row N-1, never stored
   const int chunks = K >> 7;
   const int per_wave = (chunks + 3) >> 2;
   const int cb = min(chunks, wave * per_wave);
@@ -86,61 +104,130 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
   const uint16_t* srow = scale + static_cast<size_t>(nrow) * groups;
   const uint8_t* zrow = zero + static_cast<size_t>(nrow) * groups;
 
-  const uint16_t* xrow[MT];
-  bool mok[MT];
+  // Row of x behind A-operand row `col` of m-tile mt; rows past M read a valid
+  // row and only pollute output rows that are never stored.
+  int xr[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = m0 + 16 * mt + col;
-    mok[mt] = m < M;
-    xrow[mt] = x + static_cast<size_t>(mok[mt] ? m : 0) * K;
+  for (int mt = 0; mt < MT; ++mt) xr[mt] = min(16 * mt + col, mrows - 1);
+
+  // XL: this wave's LDS slice, rows of 128 * per_wave + 8 elements.
+  const int wstride = 128 * per_wave + 8;
+  uint16_t* xw = xs + wave * mrows * wstride;
+  if constexpr (XL) {
+    const int units_per_row = (ce - cb) * 16;  // 8-element units
+    const int total = mrows * units_per_row;
+    for (int i = lane; i < total; i += 64) {
+      const int r = i / units_per_row, u8 = i - r * units_per_row;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m0 + r) * K + 128 * cb + 8 * u8);
+      *reinterpret_cast<u32x4*>(xw + r * wstride + 8 * u8) = permute_x8(v);
+    }
   }
 
   u32x4 ones;
   ones.x = ones.y = ones.z = ones.w = E::ONE2;
+  // Constants of the pair-order widening, kept in VGPRs (see and_or).
+  const uint32_t nib_mask = 0x000f000fu;
+  const uint32_t nib_magic = E::MAGIC2;
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t wnext[4] = {0, 0, 0, 0};
-  if (cb < ce) load_chunk<LOADW>(wrow + 64 * cb, j, wnext);
-
-  for (int c = cb; c < ce; ++c) {
-    uint32_t w[4] = {wnext[0], wnext[1], wnext[2], wnext[3]};
-    if (c + 1 < ce) load_chunk<LOADW>(wrow + 64 * (c + 1), j, wnext);
-
-    f32x4 C[MT], Cx[MT];
+  auto load_x = [&](int c, u32x4 (&dst)[MT][4]) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int k = 128 * c + chunk_koff<LOADW>(t, j);
+        if constexpr (XL)
+          dst[mt][t] = *reinterpret_cast<const u32x4*>(xw + xr[mt] * wstride + (k - 128 * cb));
+        else
+          dst[mt][t] = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m0 + xr[mt]) * K + k);
+      }
+  };
+
+  struct Batch {
+    uint32_t w[U][4];
+    float s[U][GPC], zz[U][GPC];
+  };
+  auto load_batch = [&](int c0, Batch& bt) {
+    if constexpr (SV) {
+      // c0 % 4 == 0 and one group a chunk: groups c0..c0+3 of this row.
+      const u32x2 sv = *reinterpret_cast<const u32x2*>(srow + c0);
+      const uint32_t zv = *reinterpret_cast<const uint32_t*>(zrow + c0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t half = (u < 2 ? sv.x : sv.y) >> (16 * (u & 1));
+        bt.s[u][0] = E::to_f32(static_cast<uint16_t>(half & 0xffffu));
+        bt.zz[u][0] = E::MAGIC_VALUE + static_cast<float>((zv >> (8 * u)) & 0xffu);
+      }
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const u32x4 b = nibbles_to_magic<DT>(w[t]);
-      const int k = 128 * c + chunk_koff<LOADW>(t, j);
+    for (int u = 0; u < U; ++u) {
+      const int c = min(c0 + u, ce - 1);  // past the end: re-read the last chunk, unused
+      load_chunk<LOADW>(wrow + 64 * c, j, bt.w[u]);
+      if constexpr (!SV) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        u32x4 a = *reinterpret_cast<const u32x4*>(xrow[mt] + k);
-        if (!mok[mt]) a = u32x4{0u, 0u, 0u, 0u};
-        C[mt] = mfma16x16x32<DT>(a, b, C[mt]);
-        Cx[mt] = mfma16x16x32<DT>(a, ones, Cx[mt]);
-      }
-      if ((t + 1) % tpg == 0) {
-        const int g = (128 * c + chunk_koff<LOADW>(t, 0)) / G;
-        const float s = E::to_f32(srow[g]);
-        const float zz = E::MAGIC_VALUE + static_cast<float>(zrow[g]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float d = fmaf(-zz, Cx[mt][r], C[mt][r]);
-            acc[mt][r] = fmaf(s, d, acc[mt][r]);
-          }
-          C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-          Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < GPC; ++q) {
+          const int g = (128 * c + chunk_koff<LOADW>(q * tpg, 0)) / G;
+          bt.s[u][q] = E::to_f32(srow[g]);
+          bt.zz[u][q] = E::MAGIC_VALUE + static_cast<float>(zrow[g]);
         }
       }
     }
+  };
+  auto run_batch = [&](int c0, const Batch& bt) {
+    u32x4 xa[PD + 1][MT][4];
+#pragma unroll
+    for (int d = 0; d < PD; ++d)
+      if (c0 + d < ce) load_x(c0 + d, xa[d]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u;
+      if (c >= ce) break;
+      if (u + PD < U && c + PD < ce) load_x(c + PD, xa[(u + PD) % (PD + 1)]);
+      f32x4 C[MT], Cx[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4 b = XL ? nibbles_to_magic_paired<DT>(bt.w[u][t], nib_mask, nib_magic) : nibbles_to_magic<DT>(bt.w[u][t]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4 a = xa[u % (PD + 1)][mt][t];
+          C[mt] = mfma16x16x32<DT>(a, b, C[mt]);
+          Cx[mt] = mfma16x16x32<DT>(a, ones, Cx[mt]);
+        }
+        if ((t + 1) % tpg == 0) {
+          const int q = t / tpg;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float d = fmaf(-bt.zz[u][q], Cx[mt][r], C[mt][r]);
+              acc[mt][r] = fmaf(bt.s[u][q], d, acc[mt][r]);
+            }
+            C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+    }
+  };
+
+  Batch even, odd;
+  if (cb < ce) load_batch(cb, even);
+  // The staged slice is read only by this wave; LDS requests of a wave are served
+  // in order, and the fence keeps the compiler from moving reads above writes.
+  if constexpr (XL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  for (int c0 = cb; c0 < ce; c0 += 2 * U) {
+    if (c0 + U < ce) load_batch(c0 + U, odd);
+    run_batch(c0, even);
+    if (c0 + U >= ce) break;
+    if (c0 + 2 * U < ce) load_batch(c0 + 2 * U, even);
+    run_batch(c0 + U, odd);
   }
 
 #pragma unroll
@@ -305,6 +392,38 @@ __global__ __launch_bounds__(256) void int4_unpack_kernel(const uint8_t* __restr
 
 // ============================================================ launch helpers
 
+// LDS bytes a workgroup may spend on its rows of x (decode shapes fit).
+constexpr int kXLdsBudget = 48 * 1024;
+
+template <int DT, int LOADW, int MT>
+static void launch_skinny_mt(const uint16_t* xs, const uint8_t* packed, const uint16_t* ss,
+                             const uint8_t* zero, const uint16_t* bs, uint16_t* ys, int M, int N,
+                             int K, int G, hipStream_t stream) {
+  const dim3 grid((N + 15) / 16, (M + 16 * MT - 1) / (16 * MT)), block(256);
+  const int rows = min(M, 16 * MT);
+  const int per_wave = ((K >> 7) + 3) >> 2;
+  const size_t lds = 4 * static_cast<size_t>(rows) * (128 * per_wave + 8) * 2;
+  // Vector scale loads: group 128, batches of 4 chunks aligned (chunks % 16 == 0
+  // makes every wave's first chunk a multiple of 4), aligned scale / zero rows.
+  const bool sv = LOADW == 16 && G == 128 && (K / G) % 4 == 0 && (K >> 7) % 16 == 0 &&
+                  aligned(ss, 8) && aligned(zero, 4);
+  if (lds <= kXLdsBudget) {
+    if (sv)
+      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, true, true>), grid, block, lds, stream,
+                         xs, packed, ss, zero, bs, ys, M, N, K, G);
+    else
+      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, true, false>), grid, block, lds, stream,
+                         xs, packed, ss, zero, bs, ys, M, N, K, G);
+  } else {
+    if (sv)
+      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, false, true>), grid, block, 0, stream,
+                         xs, packed, ss, zero, bs, ys, M, N, K, G);
+    else
+      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, false, false>), grid, block, 0, stream,
+                         xs, packed, ss, zero, bs, ys, M, N, K, G);
+  }
+}
+
 template <int DT, int LOADW>
 static LnqStatus launch_skinny_lw(const void* x, const uint8_t* packed, const void* scale,
                                   const uint8_t* zero, const void* bias, void* y, int M, int N,
@@ -313,20 +432,12 @@ static LnqStatus launch_skinny_lw(const void* x, const uint8_t* packed, const vo
   const auto* ss = static_cast<const uint16_t*>(scale);
   const auto* bs = static_cast<const uint16_t*>(bias);
   auto* ys = static_cast<uint16_t*>(y);
-  const dim3 block(256);
-  if (M <= 16) {
-    const dim3 grid((N + 15) / 16, 1);
-    hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, 1>), grid, block, 0, stream, xs, packed,
-                       ss, zero, bs, ys, M, N, K, G);
-  } else if (M <= 32) {
-    const dim3 grid((N + 15) / 16, 1);
-    hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, 2>), grid, block, 0, stream, xs, packed,
-                       ss, zero, bs, ys, M, N, K, G);
-  } else {
-    const dim3 grid((N + 15) / 16, (M + 63) / 64);
-    hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, 4>), grid, block, 0, stream, xs, packed,
-                       ss, zero, bs, ys, M, N, K, G);
-  }
+  if (M <= 16)
+    launch_skinny_mt<DT, LOADW, 1>(xs, packed, ss, zero, bs, ys, M, N, K, G, stream);
+  else if (M <= 32)
+    launch_skinny_mt<DT, LOADW, 2>(xs, packed, ss, zero, bs, ys, M, N, K, G, stream);
+  else
+    launch_skinny_mt<DT, LOADW, 4>(xs, packed, ss, zero, bs, ys, M, N, K, G, stream);
   return launched("int4_skinny");
 }
 
