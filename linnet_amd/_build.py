@@ -39,6 +39,11 @@ FLAGS = [
 ]
 
 
+# Per-source extra flags. The skinny kernels feed every MFMA result straight to
+# VALU epilogue math, so their accumulators belong in VGPRs (no accvgpr moves).
+EXTRA = {"int4.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(found).exists():
@@ -53,7 +58,7 @@ def sources() -> list[Path]:
 def _compile(source: Path, objdir: Path) -> Path:
     obj = objdir / (source.stem + ".o")
     lang = ["-x", "hip"] if source.suffix in (".hip", ".cpp") else []
-    cmd = [hipcc(), *FLAGS, f"-I{INCLUDE}", *lang, "-c", str(source), "-o", str(obj)]
+    cmd = [hipcc(), *FLAGS, *EXTRA.get(source.name, []), f"-I{INCLUDE}", *lang, "-c", str(source), "-o", str(obj)]
     done = subprocess.run(cmd, capture_output=True, text=True)
     if done.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source.name}:\n{done.stdout}\n{done.stderr}")

@@ -35,6 +35,17 @@ namespace lnq {
 //   LOADW 8  (group 64):         two 8-byte loads; k = 64(t/2) + 16j + 8(t%2)
 //   LOADW 4  (group 32):         four 4-byte loads; k = 32t + 8j
 
+// A raw buffer descriptor (stride 0) over `bytes` bytes: lanes out of range read 0.
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// Chunks each of nw waves takes: K split evenly, rounded up to whole batches of
+// 4 chunks (so a wave's batches, and its scale / zero loads, stay aligned).
+__host__ __device__ inline int skinny_per_wave(int chunks, int nw) {
+  return (((chunks + nw - 1) / nw) + 3) & ~3;
+}
+
 template <int LOADW>
 __device__ inline int chunk_koff(int t, int j) {
   if constexpr (LOADW == 16) return 32 * j + 8 * t;
@@ -65,25 +76,29 @@ __device__ inline void load_chunk(const uint8_t* __restrict__ chunk, int j, uint
 // each 8 elements 0,4,1,5,2,6,3,7 so that the codes widen in pair order (one
 // v_and_or per dword), and issues those loads BEFORE its weight loads: loads
 // retire in order, so a chunk's math then waits only for that chunk's weights.
-// The weights stream in batches of U chunks, double-buffered: batch b + 1 is
-// requested before batch b is multiplied.
-//
 // Otherwise x is read from global memory PD chunks ahead, in element order,
 // and the codes widen in element order (v_perm + or).
-// SV: the scales and zero points of a batch's 4 chunks (4 groups of 128) come in
-// one 8-byte and one 4-byte load per lane (aligned shapes, group 128).
-template <int DT, int LOADW, int MT, bool XL, bool SV>
-__global__ __launch_bounds__(256) void int4_skinny_kernel(
+//
+// The weights stream in batches of U chunks, double-buffered: batch b + 1 is
+// requested before batch b is multiplied. With one group a chunk (group % 128
+// == 0) a chunk's epilogue runs after the next chunk's MFMAs are issued, so the
+// MFMA latency is hidden. NW waves split K; ONE: M == 1, whose one output row
+// sits in register 0 of lanes 0..15, so the epilogue computes that alone.
+// SV: the scales and zero points of a batch's 4 chunks (4 groups of 128) come
+// in one 8-byte and one 4-byte load per lane (aligned shapes, group 128).
+template <int DT, int LOADW, int MT, bool XL, bool SV, int NW, bool ONE>
+__global__ __launch_bounds__(64 * NW) void int4_skinny_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G) {
   using E = Elem<DT>;
   // MFMAs t = 0..3 of a chunk; a group closes after every `tpg` of them.
   constexpr int tpg = LOADW == 16 ? 4 : (LOADW == 8 ? 2 : 1);
-  constexpr int GPC = 4 / tpg;  // groups a chunk spans
-  constexpr int U = 4;          // chunks of weight a batch
-  constexpr int PD = XL ? 1 : 2;  // chunks of x in flight ahead of use
-  __shared__ f32x4 red[4][MT][64];
+  constexpr int GPC = 4 / tpg;      // groups a chunk spans
+  constexpr int U = 4;              // chunks of weight a batch
+  constexpr int PD = XL ? 1 : 2;    // chunks of x in flight ahead of use
+  constexpr int RR = ONE ? 1 : 4;   // accumulator registers that hold live rows
+  __shared__ f32x4 red[NW][MT][64];
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
 
   const int lane = threadIdx.x & 63;
@@ -95,7 +110,7 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
   const int mrows = min(M - m0, 16 * MT);  // rows of x this workgroup reads
   const int nrow = min(n0 + col, N - 1);   // rows past N read row N-1, never stored
   const int chunks = K >> 7;
-  const int per_wave = (chunks + 3) >> 2;
+  const int per_wave = skinny_per_wave(chunks, NW);
   const int cb = min(chunks, wave * per_wave);
   const int ce = min(chunks, cb + per_wave);
   const int groups = K / G;
@@ -103,6 +118,14 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
   const uint8_t* wrow = packed + static_cast<size_t>(nrow) * (K >> 1);
   const uint16_t* srow = scale + static_cast<size_t>(nrow) * groups;
   const uint8_t* zrow = zero + static_cast<size_t>(nrow) * groups;
+  // Buffer descriptors (SGPRs) with 32-bit lane offsets: a chunk's offset is an
+  // SGPR / immediate, so the loads need no per-lane 64-bit address arithmetic.
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * (K >> 1)));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
+  const int vw = nrow * (K >> 1) + 16 * j;
+  const int vs = nrow * groups * 2;
+  const int vz = nrow * groups;
 
   // Row of x behind A-operand row `col` of m-tile mt; rows past M read a valid
   // row and only pollute output rows that are never stored.
@@ -113,13 +136,32 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
   // XL: this wave's LDS slice, rows of 128 * per_wave + 8 elements.
   const int wstride = 128 * per_wave + 8;
   uint16_t* xw = xs + wave * mrows * wstride;
+  // A wave copies mrows x (ce - cb) chunks of x, 16 units (8 elements) a chunk
+  // per row. With K % 512 == 0 every wave's chunk count is a multiple of 4, so
+  // each lane copies P = (ce - cb) / 4 units of every row: unit q of a lane is
+  // row q / P, unit lane + 64 * (q % P) -- scalar arithmetic only. The first XU
+  // are requested before the weights (waiting for them then does not wait for
+  // the weights) and stored after; the loads use clamped indices so the
+  // compiler can count them.
+  const int P = (ce - cb) >> 2;
+  const int xq = XL ? mrows * P : 0;  // units this lane copies
+  const int cbx = min(cb, chunks - 1);
+  auto x_src = [&](int q) -> const u32x4* {
+    const int qq = min(q, max(xq, 1) - 1);
+    const int r = qq / P, u8 = lane + 64 * (qq - r * P);
+    return reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m0 + r) * K + 128 * cbx + 8 * u8);
+  };
+  auto x_store = [&](int q, u32x4 v) {
+    const int qq = min(q, max(xq, 1) - 1);
+    const int r = qq / P, u8 = lane + 64 * (qq - r * P);
+    *reinterpret_cast<u32x4*>(xw + r * wstride + 8 * u8) = permute_x8(v);
+  };
+  constexpr int XU = 4;
+  u32x4 xv[XU];
   if constexpr (XL) {
-    const int units_per_row = (ce - cb) * 16;  // 8-element units
-    const int total = mrows * units_per_row;
-    for (int i = lane; i < total; i += 64) {
-      const int r = i / units_per_row, u8 = i - r * units_per_row;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m0 + r) * K + 128 * cb + 8 * u8);
-      *reinterpret_cast<u32x4*>(xw + r * wstride + 8 * u8) = permute_x8(v);
+    if (xq > 0) {
+#pragma unroll
+      for (int q = 0; q < XU; ++q) xv[q] = *x_src(q);
     }
   }
 
@@ -151,9 +193,11 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
   };
   auto load_batch = [&](int c0, Batch& bt) {
     if constexpr (SV) {
-      // c0 % 4 == 0 and one group a chunk: groups c0..c0+3 of this row.
-      const u32x2 sv = *reinterpret_cast<const u32x2*>(srow + c0);
-      const uint32_t zv = *reinterpret_cast<const uint32_t*>(zrow + c0);
+      // c0 % 4 == 0 and one group a chunk: groups c0..c0+3 of this row (an
+      // idle wave's c0 == chunks reads the row's last 4, unused).
+      const int g0 = min(c0, chunks - 4);
+      const u32x2 sv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs, 2 * g0, 0));
+      const uint32_t zv = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rz, vz, g0, 0));
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const uint32_t half = (u < 2 ? sv.x : sv.y) >> (16 * (u & 1));
@@ -163,8 +207,13 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = min(c0 + u, ce - 1);  // past the end: re-read the last chunk, unused
-      load_chunk<LOADW>(wrow + 64 * c, j, bt.w[u]);
+      const int c = max(min(c0 + u, ce - 1), 0);  // past the end: re-read the last chunk, unused
+      if constexpr (LOADW == 16) {
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw, 64 * c, 0));
+        bt.w[u][0] = v.x; bt.w[u][1] = v.y; bt.w[u][2] = v.z; bt.w[u][3] = v.w;
+      } else {
+        load_chunk<LOADW>(wrow + 64 * c, j, bt.w[u]);
+      }
       if constexpr (!SV) {
 #pragma unroll
         for (int q = 0; q < GPC; ++q) {
@@ -175,42 +224,85 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
       }
     }
   };
+
+  auto widen = [&](uint32_t w) -> u32x4 {
+    if constexpr (XL) return nibbles_to_magic_paired<DT>(w, nib_mask, nib_magic);
+    else return nibbles_to_magic<DT>(w);
+  };
+  auto fold = [&](const f32x4& C, const f32x4& Cx, float s, float zz, f32x4& a) {
+#pragma unroll
+    for (int r = 0; r < RR; ++r) a[r] = fmaf(s, fmaf(-zz, Cx[r], C[r]), a[r]);
+  };
+
   auto run_batch = [&](int c0, const Batch& bt) {
     u32x4 xa[PD + 1][MT][4];
 #pragma unroll
     for (int d = 0; d < PD; ++d)
       if (c0 + d < ce) load_x(c0 + d, xa[d]);
+    if constexpr (tpg == 4) {
+      // One group a chunk: chunk u's MFMAs, then chunk u-1's epilogue.
+      f32x4 C[2][MT], Cx[2][MT];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + u;
-      if (c >= ce) break;
-      if (u + PD < U && c + PD < ce) load_x(c + PD, xa[(u + PD) % (PD + 1)]);
-      f32x4 C[MT], Cx[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const u32x4 b = XL ? nibbles_to_magic_paired<DT>(bt.w[u][t], nib_mask, nib_magic) : nibbles_to_magic<DT>(bt.w[u][t]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const u32x4 a = xa[u % (PD + 1)][mt][t];
-          C[mt] = mfma16x16x32<DT>(a, b, C[mt]);
-          Cx[mt] = mfma16x16x32<DT>(a, ones, Cx[mt]);
-        }
-        if ((t + 1) % tpg == 0) {
-          const int q = t / tpg;
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u;
+        if (c < ce) {
+          if (u + PD < U && c + PD < ce) load_x(c + PD, xa[(u + PD) % (PD + 1)]);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
+            C[u & 1][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            Cx[u & 1][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float d = fmaf(-bt.zz[u][q], Cx[mt][r], C[mt][r]);
-              acc[mt][r] = fmaf(bt.s[u][q], d, acc[mt][r]);
+          for (int t = 0; t < 4; ++t) {
+            const u32x4 b = widen(bt.w[u][t]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const u32x4 a = xa[u % (PD + 1)][mt][t];
+              C[u & 1][mt] = mfma16x16x32<DT>(a, b, C[u & 1][mt]);
+              Cx[u & 1][mt] = mfma16x16x32<DT>(a, ones, Cx[u & 1][mt]);
             }
-            C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+        if (u > 0 && c - 1 < ce) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            fold(C[(u - 1) & 1][mt], Cx[(u - 1) & 1][mt], bt.s[u - 1][0], bt.zz[u - 1][0], acc[mt]);
+        }
+      }
+      if (c0 + U - 1 < ce) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          fold(C[(U - 1) & 1][mt], Cx[(U - 1) & 1][mt], bt.s[U - 1][0], bt.zz[U - 1][0], acc[mt]);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u;
+        if (c >= ce) break;
+        if (u + PD < U && c + PD < ce) load_x(c + PD, xa[(u + PD) % (PD + 1)]);
+        f32x4 C[MT], Cx[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 b = widen(bt.w[u][t]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const u32x4 a = xa[u % (PD + 1)][mt][t];
+            C[mt] = mfma16x16x32<DT>(a, b, C[mt]);
+            Cx[mt] = mfma16x16x32<DT>(a, ones, Cx[mt]);
+          }
+          if ((t + 1) % tpg == 0) {
+            const int q = t / tpg;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              fold(C[mt], Cx[mt], bt.s[u][q], bt.zz[u][q], acc[mt]);
+              C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+              Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
           }
         }
       }
@@ -218,10 +310,19 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
   };
 
   Batch even, odd;
-  if (cb < ce) load_batch(cb, even);
-  // The staged slice is read only by this wave; LDS requests of a wave are served
-  // in order, and the fence keeps the compiler from moving reads above writes.
-  if constexpr (XL) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // Unconditional (addresses clamped for an idle wave) so the compiler can count
+  // the loads in flight when it waits for x below.
+  load_batch(cb, even);
+  if constexpr (XL) {
+    if (xq > 0) {
+#pragma unroll
+      for (int q = 0; q < XU; ++q) x_store(q, xv[q]);  // past xq: a repeat of the last unit
+      for (int q = XU; q < xq; ++q) x_store(q, *x_src(q));
+    }
+    // The slice is read only by this wave; a wave's LDS requests are served in
+    // order, and the fence keeps the compiler from moving reads above writes.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  }
   for (int c0 = cb; c0 < ce; c0 += 2 * U) {
     if (c0 + U < ce) load_batch(c0 + U, odd);
     run_batch(c0, even);
@@ -234,19 +335,22 @@ __global__ __launch_bounds__(256) void int4_skinny_kernel(
   for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
   __syncthreads();
 
-  // 256 threads, one output each per m-tile: (lane, r) of the 16x16 tile.
-  const int olane = threadIdx.x & 63;
-  const int r = threadIdx.x >> 6;
-  const int n = n0 + (olane & 15);
+  // One output per thread per m-tile: (lane, r) of the 16x16 tile, r < 4.
+  if (threadIdx.x < 256) {
+    const int olane = threadIdx.x & 63;
+    const int r = threadIdx.x >> 6;
+    const int n = n0 + (olane & 15);
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = m0 + 16 * mt + 4 * (olane >> 4) + r;
-    const float v = red[0][mt][olane][r] + red[1][mt][olane][r] + red[2][mt][olane][r] +
-                    red[3][mt][olane][r];
-    if (m < M && n < N) {
-      uint16_t out = E::from_f32(v);
-      if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
-      y[static_cast<size_t>(m) * N + n] = out;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + 16 * mt + 4 * (olane >> 4) + r;
+      if (m < M && n < N) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w][mt][olane][r];
+        uint16_t out = E::from_f32(v);
+        if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
+        y[static_cast<size_t>(m) * N + n] = out;
+      }
     }
   }
 }
@@ -392,6 +496,30 @@ __global__ __launch_bounds__(256) void int4_unpack_kernel(const uint8_t* __restr
 
 // ============================================================ launch helpers
 
+template <int DT, int LOADW, int MT, bool XL, bool SV>
+static void launch_skinny_v(const uint16_t* xs, const uint8_t* packed, const uint16_t* ss,
+                            const uint8_t* zero, const uint16_t* bs, uint16_t* ys, int M, int N,
+                            int K, int G, hipStream_t stream) {
+  // Eight waves split K when each still gets at least one batch of chunks.
+  const int chunks = K >> 7;
+  const bool eight = chunks >= 64;
+  const int nw = eight ? 8 : 4;
+  const dim3 grid((N + 15) / 16, (M + 16 * MT - 1) / (16 * MT)), block(64 * nw);
+  const int rows = min(M, 16 * MT);
+  const int per_wave = skinny_per_wave(chunks, nw);
+  const size_t lds = XL ? static_cast<size_t>(nw) * rows * (128 * per_wave + 8) * 2 : 0;
+  const bool one = M == 1;
+#define LNQ_SKINNY(NW, ONE)                                                                        \
+  hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, XL, SV, NW, ONE>), grid, block, lds, stream, \
+                     xs, packed, ss, zero, bs, ys, M, N, K, G)
+  if (eight) {
+    if (one && MT == 1) LNQ_SKINNY(8, true); else LNQ_SKINNY(8, false);
+  } else {
+    if (one && MT == 1) LNQ_SKINNY(4, true); else LNQ_SKINNY(4, false);
+  }
+#undef LNQ_SKINNY
+}
+
 // LDS bytes a workgroup may spend on its rows of x (decode shapes fit).
 constexpr int kXLdsBudget = 48 * 1024;
 
@@ -399,28 +527,19 @@ template <int DT, int LOADW, int MT>
 static void launch_skinny_mt(const uint16_t* xs, const uint8_t* packed, const uint16_t* ss,
                              const uint8_t* zero, const uint16_t* bs, uint16_t* ys, int M, int N,
                              int K, int G, hipStream_t stream) {
-  const dim3 grid((N + 15) / 16, (M + 16 * MT - 1) / (16 * MT)), block(256);
   const int rows = min(M, 16 * MT);
-  const int per_wave = ((K >> 7) + 3) >> 2;
-  const size_t lds = 4 * static_cast<size_t>(rows) * (128 * per_wave + 8) * 2;
-  // Vector scale loads: group 128, batches of 4 chunks aligned (chunks % 16 == 0
-  // makes every wave's first chunk a multiple of 4), aligned scale / zero rows.
-  const bool sv = LOADW == 16 && G == 128 && (K / G) % 4 == 0 && (K >> 7) % 16 == 0 &&
-                  aligned(ss, 8) && aligned(zero, 4);
-  if (lds <= kXLdsBudget) {
-    if (sv)
-      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, true, true>), grid, block, lds, stream,
-                         xs, packed, ss, zero, bs, ys, M, N, K, G);
-    else
-      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, true, false>), grid, block, lds, stream,
-                         xs, packed, ss, zero, bs, ys, M, N, K, G);
+  // Upper bound of what launch_skinny_v asks for (any NW): 8 padded slices.
+  const size_t lds = static_cast<size_t>(rows) * (128 * 8 * skinny_per_wave(K >> 7, 8) + 8 * 8) * 2;
+  // Vector scale loads: group 128 and rows of a multiple of 4 groups (every
+  // wave's first chunk is a multiple of 4), aligned scale / zero rows.
+  const bool sv = LOADW == 16 && G == 128 && (K / G) % 4 == 0 && aligned(ss, 8) && aligned(zero, 4) &&
+                  static_cast<size_t>(N) * (K >> 1) < (1ull << 31);
+  if (lds <= kXLdsBudget && K % 512 == 0 && static_cast<size_t>(N) * (K >> 1) < (1ull << 31)) {
+    if (sv) launch_skinny_v<DT, LOADW, MT, true, true>(xs, packed, ss, zero, bs, ys, M, N, K, G, stream);
+    else launch_skinny_v<DT, LOADW, MT, true, false>(xs, packed, ss, zero, bs, ys, M, N, K, G, stream);
   } else {
-    if (sv)
-      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, false, true>), grid, block, 0, stream,
-                         xs, packed, ss, zero, bs, ys, M, N, K, G);
-    else
-      hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, false, false>), grid, block, 0, stream,
-                         xs, packed, ss, zero, bs, ys, M, N, K, G);
+    if (sv) launch_skinny_v<DT, LOADW, MT, false, true>(xs, packed, ss, zero, bs, ys, M, N, K, G, stream);
+    else launch_skinny_v<DT, LOADW, MT, false, false>(xs, packed, ss, zero, bs, ys, M, N, K, G, stream);
   }
 }
 
