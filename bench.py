@@ -66,26 +66,26 @@ def main() -> int:
     stream = torch.cuda.current_stream(dev)
 
     def timed_graph(launches: list, steps: int, warmup: int) -> float:
-        """Seconds per launch: the launches recorded once into a HIP graph,
-        replayed until `steps` launches ran, timed by HIP events on the stream."""
-        for f in launches:
-            f()
+        """Seconds per call over exactly `steps` calls, cycling through
+        `launches`: `warmup` untimed eager calls, then the `steps` calls recorded
+        into one HIP graph, replayed once untimed and once between HIP events on
+        the stream the kernels run on (synchronized on both sides)."""
+        for i in range(max(warmup, len(launches))):
+            launches[i % len(launches)]()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for f in launches:
-                f()
-        reps = max(1, -(-steps // len(launches)))
-        for _ in range(max(1, warmup // len(launches))):
-            graph.replay()
+            for i in range(steps):
+                launches[i % len(launches)]()
+        graph.replay()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for _ in range(reps):
-            graph.replay()
+        graph.replay()
         end.record(stream)
         torch.cuda.synchronize()
-        return start.elapsed_time(end) / 1e3 / (reps * len(launches))
+        del graph
+        return start.elapsed_time(end) / 1e3 / steps
 
     def int4_layers(n: int, k: int, copies: int, seed: int = 0):
         g = torch.Generator(device=dev).manual_seed(seed)

@@ -64,12 +64,18 @@ __host__ __device__ inline float bf16_bits_to_f32(uint32_t bits) {
   return __builtin_bit_cast(float, bits << 16);
 }
 
-// f32 -> bf16 bits, round to nearest even (NaN kept NaN).
-__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// f32 -> bf16 bits, round to nearest even: gfx950's v_cvt_pk_bf16_f32.
+__device__ inline uint16_t f32_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two f32 values as a packed bf16 pair (low = a), one v_cvt_pk_bf16_f32.
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 __device__ inline float f16_bits_to_f32(uint32_t bits) {
@@ -83,6 +89,12 @@ __device__ inline float f16_bits_to_f32(uint32_t bits) {
 __device__ inline uint16_t f32_to_f16_bits(float f) {
   __asm__ volatile("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Two f32 values exact in f16 (or whose double rounding does not matter) as a
+// packed f16 pair (low = a), one v_cvt_pk_f16_f32.
+__device__ inline uint32_t pack_f16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
 }
 
 // Element type of activations / scales / outputs, as a compile-time tag.
@@ -183,6 +195,19 @@ __device__ inline u32x4 permute_x8(u32x4 v) {
   out.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
   out.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
   return out;
+}
+
+// `v` with every bit unknown to the compiler: keeps it from folding a preceding
+// mask into each later byte extraction (v_bfe + v_cvt_f32_ubyte0 per byte
+// instead of one v_cvt_f32_ubyteN).
+__device__ inline uint32_t opaque(uint32_t v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+
+// A raw buffer descriptor (stride 0) over `bytes` bytes: lanes out of range read 0.
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
 }
 
 // Wave-wide reductions (64 lanes).

@@ -35,11 +35,6 @@ namespace lnq {
 //   LOADW 8  (group 64):         two 8-byte loads; k = 64(t/2) + 16j + 8(t%2)
 //   LOADW 4  (group 32):         four 4-byte loads; k = 32t + 8j
 
-// A raw buffer descriptor (stride 0) over `bytes` bytes: lanes out of range read 0.
-__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
-}
-
 // Chunks each of nw waves takes: K split evenly, rounded up to whole batches of
 // 4 chunks (so a wave's batches, and its scale / zero loads, stay aligned).
 __host__ __device__ inline int skinny_per_wave(int chunks, int nw) {
@@ -361,51 +356,56 @@ __global__ __launch_bounds__(64 * NW) void int4_skinny_kernel(
 // `(q.to(T) - z.to(T)) * s` both give, (q - z) * s being exact in f32 for
 // bf16 / f16 scales.
 
-// 16 packed bytes (32 elements of one group) per thread; K % 32 == 0, G % 32 == 0.
+// 4 packed bytes (8 elements of one group) per thread, consecutive threads on
+// consecutive bytes: each wave reads 256 contiguous bytes and writes 1 KB (2 KB
+// for f32) contiguous. K % 8 == 0, G % 8 == 0. Grid: x over a row's 8-element
+// units, y over rows (no division).
 template <int DT>
 __global__ __launch_bounds__(256) void int4_dequant_fast(
     const uint8_t* __restrict__ packed, const typename Elem<DT>::storage* __restrict__ scale,
-    const uint8_t* __restrict__ zero, typename Elem<DT>::storage* __restrict__ out,
-    int64_t units, int K, int G) {
+    const uint8_t* __restrict__ zero, typename Elem<DT>::storage* __restrict__ out, int K, int gshift,
+    int G) {
   using E = Elem<DT>;
   using S = typename E::storage;
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (u >= units) return;
-  const int64_t per_row = K >> 5;  // 32-element units a row
-  const int64_t n = u / per_row;
-  const int k0 = static_cast<int>(u - n * per_row) << 5;
+  const int per_row = K >> 3;
+  const int unit = blockIdx.x * blockDim.x + threadIdx.x;
+  if (unit >= per_row) return;
+  const int64_t n = blockIdx.y;
+  const int k0 = unit << 3;
   const int groups = K / G;
-  const int g = k0 / G;
+  const int g = gshift >= 0 ? k0 >> gshift : k0 / G;
   const float s = E::load(scale + n * groups + g);
-  const float z = static_cast<float>(zero[n * groups + g]);
-  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + (u << 4)));
-  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-  S vals[32];
+  const float zf = static_cast<float>(zero[n * groups + g]);
+  // z * s is exact for a 16-bit scale (4 bits times at most 11), not for an f32 one.
+  const float zs = zf * s;
+  const uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(packed + n * (K >> 1)) + unit);
+  // 16-bit scale: (q - z) * s = fma(q, s, -z*s), exact in f32, then one
+  // rounding to the output type. f32 scale: (q - z) * s, one f32 rounding.
+  const uint32_t lo = opaque(w & 0x0f0f0f0fu);
+  const uint32_t hi = opaque((w >> 4) & 0x0f0f0f0fu);
+  float v[8];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float q = static_cast<float>((words[d] >> (4 * i)) & 15u);
-      vals[8 * d + i] = E::from_f32((q - z) * s);
+  for (int b = 0; b < 4; ++b) {
+    const float q0 = static_cast<float>((lo >> (8 * b)) & 0xffu);
+    const float q1 = static_cast<float>((hi >> (8 * b)) & 0xffu);
+    if constexpr (DT == LNQ_F32) {
+      v[2 * b] = (q0 - zf) * s;
+      v[2 * b + 1] = (q1 - zf) * s;
+    } else {
+      v[2 * b] = fmaf(q0, s, -zs);
+      v[2 * b + 1] = fmaf(q1, s, -zs);
     }
   }
   S* dst = out + n * K + k0;
-  if constexpr (sizeof(S) == 2) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      u32x4 o;
-      o.x = static_cast<uint32_t>(vals[8 * v + 0]) | (static_cast<uint32_t>(vals[8 * v + 1]) << 16);
-      o.y = static_cast<uint32_t>(vals[8 * v + 2]) | (static_cast<uint32_t>(vals[8 * v + 3]) << 16);
-      o.z = static_cast<uint32_t>(vals[8 * v + 4]) | (static_cast<uint32_t>(vals[8 * v + 5]) << 16);
-      o.w = static_cast<uint32_t>(vals[8 * v + 6]) | (static_cast<uint32_t>(vals[8 * v + 7]) << 16);
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst) + v);
-    }
+  if constexpr (DT == LNQ_BF16) {
+    *reinterpret_cast<u32x4*>(dst) = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                           pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+  } else if constexpr (DT == LNQ_F16) {
+    *reinterpret_cast<u32x4*>(dst) = u32x4{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3]),
+                                           pack_f16x2(v[4], v[5]), pack_f16x2(v[6], v[7])};
   } else {
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      f32x4 o = {vals[4 * v], vals[4 * v + 1], vals[4 * v + 2], vals[4 * v + 3]};
-      __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(dst) + v);
-    }
+    reinterpret_cast<f32x4*>(dst)[0] = f32x4{v[0], v[1], v[2], v[3]};
+    reinterpret_cast<f32x4*>(dst)[1] = f32x4{v[4], v[5], v[6], v[7]};
   }
 }
 
@@ -643,22 +643,23 @@ LNQ_API LnqStatus lnq_int4_dequantize(const uint8_t* packed, const void* scale,
   LNQ_REQUIRE(packed && scale && zero && out, "lnq_int4_dequantize: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int K = static_cast<int>(in_features), G = static_cast<int>(group);
-  const bool fast = K % 32 == 0 && G % 32 == 0 && aligned(packed, 16) && aligned(out, 16);
-  if (fast) {
-    const int64_t units = out_features * (K / 32);
-    const dim3 grid(static_cast<unsigned>((units + 255) / 256));
+  const bool fast = K % 8 == 0 && G % 8 == 0 && aligned(packed, 4) && aligned(out, 16);
+  if (fast && out_features <= 65535) {
+    const int per_row = K / 8;
+    const int gshift = (G & (G - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(G)) : -1;
+    const dim3 grid(static_cast<unsigned>((per_row + 255) / 256), static_cast<unsigned>(out_features));
     if (dtype == LNQ_BF16)
       hipLaunchKernelGGL((int4_dequant_fast<LNQ_BF16>), grid, dim3(256), 0, s, packed,
-                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out),
-                         units, K, G);
+                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out), K,
+                         gshift, G);
     else if (dtype == LNQ_F16)
       hipLaunchKernelGGL((int4_dequant_fast<LNQ_F16>), grid, dim3(256), 0, s, packed,
-                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out),
-                         units, K, G);
+                         static_cast<const uint16_t*>(scale), zero, static_cast<uint16_t*>(out), K,
+                         gshift, G);
     else
       hipLaunchKernelGGL((int4_dequant_fast<LNQ_F32>), grid, dim3(256), 0, s, packed,
-                         static_cast<const float*>(scale), zero, static_cast<float*>(out), units,
-                         K, G);
+                         static_cast<const float*>(scale), zero, static_cast<float*>(out), K, gshift,
+                         G);
   } else {
     const int64_t bytes = out_features * (K / 2);
     const dim3 grid(static_cast<unsigned>((bytes + 255) / 256));
