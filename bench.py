@@ -4,7 +4,7 @@ Headline (BASELINE.json `metric`, config 2): the W4A16 group-128 decode GEMV,
 M=1, K=4096, N=14336 (Llama-3-8B MLP up/gate), as GB/s of algorithmic bytes
 (packed weight + bf16 scales + u8 zeros + x + y) against HBM peak. A "step" is
 one `lnq_int4_linear` call over one batch (one token) with every operand
-resident in HBM; the steps rotate over enough distinct weight copies (> 256 MB,
+resident in HBM (the output too: a preallocated tensor written each call); the steps rotate over enough distinct weight copies (> 256 MB,
 the Infinity Cache) that each call streams its weight from HBM. Launches are
 recorded in a HIP graph and replayed, and the timed region is bracketed by HIP
 events on the stream the kernels run on.
@@ -118,7 +118,8 @@ def main() -> int:
         g = torch.Generator(device=dev).manual_seed(1)
         for m in (1, 4, 16):
             x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
-            launches = [lambda l=l, x=x: kernels.int4_linear(x, *l) for l in layers]
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)  # resident output, written each call
+            launches = [lambda l=l, x=x, y=y: kernels.int4_linear(x, *l, out=y) for l in layers]
             sec = timed_graph(launches, args.steps, args.warmup)
             gbps = gemv_bytes(m, k, n) / sec / 1e9
             gemv[f"M{m}"] = {"us": round(sec * 1e6, 3), "gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
@@ -174,8 +175,8 @@ def main() -> int:
         config = {"workload": "int4 g128 W4A16 decode GEMV (linear_int4_groups)", "M": 1, "K": k, "N": n,
                   "group": 128, "dtype": "bf16 activations, bf16 scales, u8 zeros", "baseline_config": 2}
         roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic_from_profiles("int4_skinny_M1"),
-                    "kernel": "int4_skinny_kernel<bf16,16,1>", "bytes_per_launch": gemv_bytes(1, k, n)}
+                    "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic_from_profiles("int4_gemv_M1"),
+                    "kernel": "int4_gemv_kernel<bf16,7,group128>", "bytes_per_launch": gemv_bytes(1, k, n)}
     else:
         key = next(iter(gemm))
         entry = gemm[key]

@@ -40,7 +40,8 @@ FLAGS = [
 
 
 # Per-source extra flags. The skinny kernels feed every MFMA result straight to
-# VALU epilogue math, so their accumulators belong in VGPRs (no accvgpr moves).
+# VALU epilogue math, so their accumulators belong in VGPRs (no accvgpr moves);
+# int4_gemv.hip's kernel asks for AGPR accumulators itself (LNQ_MFMA_IN_AGPRS).
 EXTRA = {"int4.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 

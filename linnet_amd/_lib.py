@@ -21,7 +21,7 @@ ABI_VERSION = 1
 
 LNQ_OK, LNQ_ERROR, LNQ_UNAVAILABLE = 0, 1, 2
 BF16, F16, F32 = 0, 1, 2
-KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED = 0, 1, 2
+KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV = 0, 1, 2, 3
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64

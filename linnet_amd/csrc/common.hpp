@@ -210,6 +210,43 @@ __device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t byt
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
 }
 
+
+// LDS address space pointer, the destination type of buffer_load ... lds.
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still in
+// flight. Loads retire in issue order, so this waits for all but the N most
+// recently issued.
+template <int N>
+__device__ inline void wait_vm() {
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait_vm with a count known only after unrolling (folds to one s_waitcnt).
+__device__ inline void wait_vm_rt(int n) {
+  switch (n) {
+#define LNQ_WAIT_CASE(i) \
+  case i:                \
+    wait_vm<i>();        \
+    break;
+    LNQ_WAIT_CASE(0) LNQ_WAIT_CASE(1) LNQ_WAIT_CASE(2) LNQ_WAIT_CASE(3) LNQ_WAIT_CASE(4)
+    LNQ_WAIT_CASE(5) LNQ_WAIT_CASE(6) LNQ_WAIT_CASE(7) LNQ_WAIT_CASE(8) LNQ_WAIT_CASE(9)
+    LNQ_WAIT_CASE(10) LNQ_WAIT_CASE(11) LNQ_WAIT_CASE(12) LNQ_WAIT_CASE(13) LNQ_WAIT_CASE(14)
+    LNQ_WAIT_CASE(15) LNQ_WAIT_CASE(16) LNQ_WAIT_CASE(17) LNQ_WAIT_CASE(18) LNQ_WAIT_CASE(19)
+#undef LNQ_WAIT_CASE
+    default:
+      wait_vm<0>();
+      break;
+  }
+}
+
+// MFMA accumulators in AGPRs. When the compiler keeps MFMA results in VGPRs
+// (it does so on its own when a kernel touches no AGPR), gfx950 code built by
+// this toolchain was seen to let VALU instructions write registers of an MFMA
+// destination still in flight, which corrupts results. Naming an AGPR in an
+// asm clobber makes the compiler allocate MFMA destinations in AGPRs.
+#define LNQ_MFMA_IN_AGPRS() __asm__ volatile("" ::: "a0")
+
 // Wave-wide reductions (64 lanes).
 __device__ inline float wave_max(float v) {
 #pragma unroll

@@ -508,7 +508,10 @@ static void launch_skinny_v(const uint16_t* xs, const uint8_t* packed, const uin
   const int rows = min(M, 16 * MT);
   const int per_wave = skinny_per_wave(chunks, nw);
   const size_t lds = XL ? static_cast<size_t>(nw) * rows * (128 * per_wave + 8) * 2 : 0;
-  const bool one = M == 1;
+  // The one-row specialization (ONE) is not used: with its fewer live registers
+  // the compiler reuses MFMA operand registers early, and one row with group 32
+  // came out wrong on gfx950; the four-row epilogue is correct for one row too.
+  const bool one = false;
 #define LNQ_SKINNY(NW, ONE)                                                                        \
   hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, XL, SV, NW, ONE>), grid, block, lds, stream, \
                      xs, packed, ss, zero, bs, ys, M, N, K, G)
@@ -576,6 +579,12 @@ LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* sc
                             int G, int dtype, hipStream_t stream);
 bool int4_tiled_supports(int M, int N, int K, int G, int dtype);
 
+// Defined in int4_gemv.hip: the one-token dequant-GEMV.
+bool int4_gemv_supports(int N, int K, int G, const void* x, const void* packed, const void* scale,
+                        const void* zero);
+LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                           const void* bias, void* y, int N, int K, int G, int dtype, hipStream_t stream);
+
 }  // namespace lnq
 
 using namespace lnq;
@@ -601,7 +610,7 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
   LNQ_REQUIRE(x && packed && scale && zero && y, "lnq_int4_linear: null pointer");
   LNQ_REQUIRE(aligned(x, 16) && aligned(packed, 16),
               "lnq_int4_linear: x and packed must be 16-byte aligned");
-  LNQ_REQUIRE(kernel >= LNQ_KERNEL_AUTO && kernel <= LNQ_KERNEL_TILED,
+  LNQ_REQUIRE(kernel >= LNQ_KERNEL_AUTO && kernel <= LNQ_KERNEL_GEMV,
               "lnq_int4_linear: unknown kernel %d", kernel);
   if (rows == 0) {
     clear_error();
@@ -610,6 +619,12 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
   const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
   const int K = static_cast<int>(in_features), G = static_cast<int>(group);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool gemv_ok = M == 1 && int4_gemv_supports(N, K, G, x, packed, scale, zero);
+  if (kernel == LNQ_KERNEL_GEMV) {
+    LNQ_REQUIRE(gemv_ok, "lnq_int4_linear: the one-token kernel does not take rows=%d N=%d K=%d group=%d", M, N, K, G);
+  }
+  if (kernel == LNQ_KERNEL_GEMV || (kernel == LNQ_KERNEL_AUTO && gemv_ok))
+    return launch_int4_gemv(x, packed, scale, zero, bias, y, N, K, G, dtype, s);
   bool tiled = kernel == LNQ_KERNEL_TILED;
   if (kernel == LNQ_KERNEL_AUTO) tiled = M > 64 && int4_tiled_supports(M, N, K, G, dtype);
   if (tiled) {

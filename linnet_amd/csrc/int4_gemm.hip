@@ -110,8 +110,6 @@ __device__ inline void interleave() {
   if constexpr (WRITES > 0) __builtin_amdgcn_sched_group_barrier(0x200, WRITES, 0);  // DS write
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr;
-
 template <int DT>
 __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,

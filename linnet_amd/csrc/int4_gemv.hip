@@ -1,0 +1,292 @@
+// The one-token (M == 1) int4 group-wise dequant-GEMV on gfx950: y = x @ W^T,
+// W[n, k] = (q[n, k] - z[n, k/G]) * s[n, k/G], the decode shape of
+// std.quant::linear_int4_groups (stdlib/quant.linnet:132-140) as the reference
+// launches it per token (linnet/torch/kernels.py:212-323; tinygemm below 8 rows).
+//
+// The path is bound by HBM: every packed byte is read once. The kernel is
+// shaped around what one launch of ~30 MB can reach on MI355X:
+//
+// * Exact balance: one workgroup per CU. N rows are split into R = 8 * U8 rows
+//   per workgroup with U8 = ceil(N / 2048) (14336 rows: 56 each, 256
+//   workgroups), so every CU streams the same bytes.
+// * Wide, contiguous weight reads: each wave owns R rows x 256 inputs; its
+//   weights move HBM -> LDS with buffer_load ... lds, one instruction per
+//   8 rows x 128 contiguous bytes (reads of 16 rows x 64 bytes, the footprint a
+//   register load in MFMA operand order would have, stream ~20% slower). The
+//   16-byte piece each lane fetches is chosen so that the reads in MFMA operand
+//   order hit 16 distinct bank groups.
+// * Few memory instructions per CU: a wave issues one x load, U8 weight loads
+//   and one scale and one zero load, about 160 per CU for 14336 x 4096.
+// * x first: each wave's slice of x is loaded first, staged in its own LDS
+//   array (a separate array, so the compiler can see the weight loads do not
+//   touch it and adds no wait for them) and turned into MFMA A operands; each
+//   8-row pair of loads is multiplied as soon as it lands (explicit vmcnt
+//   waits; loads retire in order).
+// * Zero point and scale at the end: per tile and 128-input half the MFMA sums
+//   C = sum x * (MAGIC + q) ((MAGIC | q) read as bf16 is 128 + q, f16 1024 + q)
+//   and the wave folds acc = s * (C - (MAGIC + z) * sum x) after its scale and
+//   zero loads (issued last) arrive; one barrier, then the 16 waves' partial
+//   sums are added in a fixed order.
+// * An odd U8 leaves a last tile of 8 rows: its two 128-input halves run as
+//   one MFMA chain, half 0 in A row 0 / B columns 0-7 and half 1 in A row 1 /
+//   B columns 8-15 (only row 0 of A carries x otherwise).
+#include "common.hpp"
+
+namespace lnq {
+
+namespace gemv {
+constexpr int MAX_WAVES = 16;  // K <= 4096
+constexpr int MAX_U8 = 8;      // R <= 64 rows per workgroup
+}  // namespace gemv
+
+// The widened B operands of two packed dwords (16 codes): (MAGIC | q) pairs in
+// pair order (dword s holds elements s and s + 4 of its 8). The three shifts of
+// each dword are shared between the two as 64-bit funnel shifts; bits shifted
+// in from the high dword land outside the 0x000f000f mask.
+template <int DT>
+__device__ inline void widen_pair(uint32_t lo, uint32_t hi, uint32_t mask, uint32_t magic, u32x4& b0, u32x4& b1) {
+  const uint64_t v = (static_cast<uint64_t>(hi) << 32) | lo;
+  const uint64_t v4 = v >> 4, v8 = v >> 8, v12 = v >> 12;
+  b0 = u32x4{and_or(lo, mask, magic), and_or(static_cast<uint32_t>(v4), mask, magic),
+             and_or(static_cast<uint32_t>(v8), mask, magic), and_or(static_cast<uint32_t>(v12), mask, magic)};
+  b1 = u32x4{and_or(hi, mask, magic), and_or(static_cast<uint32_t>(v4 >> 32), mask, magic),
+             and_or(static_cast<uint32_t>(v8 >> 32), mask, magic), and_or(static_cast<uint32_t>(v12 >> 32), mask, magic)};
+}
+
+// Workgroup: NW = K / 256 waves, R = 8 * U8 rows. G128: group 128 (a wave's two
+// halves have consecutive groups, scales loaded as one dword); otherwise G is
+// a multiple of 256 (both halves share one group).
+template <int DT, int U8, bool G128>
+__global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G) {
+  using E = Elem<DT>;
+  LNQ_MFMA_IN_AGPRS();
+  constexpr int R = 8 * U8;
+  constexpr int NF = U8 / 2;            // full 16-row tiles
+  constexpr bool HALF = (U8 & 1) != 0;  // a last tile of 8 rows
+  __shared__ __attribute__((aligned(16))) uint8_t Wsm[gemv::MAX_WAVES][U8 * 1024];
+  __shared__ __attribute__((aligned(16))) uint16_t Xsm[gemv::MAX_WAVES][256];
+  __shared__ float Rsm[R][gemv::MAX_WAVES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int col = lane & 15, j = lane >> 4;
+  const int n0 = blockIdx.x * R;
+  const int k0 = wave * 256;
+  const int rowb = K >> 1;
+  const int groups = K / G;
+  uint8_t* Wl = Wsm[wave];
+  uint16_t* Xw = Xsm[wave];
+  // Buffer descriptors: rows past N read zeros through the range check.
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * rowb));
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint32_t>(K * 2));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
+
+  // ---- loads: x slice (lanes 0..31, 8 inputs each), weights, scales, zeros.
+  const u32x4 xv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (k0 + 8 * (lane & 31)) * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    // Load u: rows n0 + 8u + (lane & 7) at 16-byte piece sigma of the wave's 128
+    // bytes; sigma = 2 (lane / 16) + ((lane / 8) % 2 ^ u % 2) puts piece sigma of
+    // row r at LDS slot 16 (sigma / 2) + 8 (sigma % 2 ^ u % 2) + r.
+    const int a = lane >> 4, b = lane & 15;
+#pragma unroll
+    for (int u = 0; u < U8; ++u) {
+      const int sigma = 2 * a + ((b >> 3) ^ (u & 1));
+      const int row = n0 + 8 * u + (b & 7);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(Wl + 1024 * u), 16, row * rowb + (k0 >> 1) + 16 * sigma,
+                                               0, 0, 2 /* non-temporal */);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Lane r < R: row n0 + r's scales and zero points of this wave's groups.
+  const int srow = n0 + (lane < R ? lane : R - 1);
+  const int g0 = k0 / G;
+  uint32_t sv;
+  uint16_t zv16;
+  if constexpr (G128) {
+    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);  // s[g0] | s[g0 + 1] << 16
+    zv16 = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);      // z[g0] | z[g0 + 1] << 8
+  } else {
+    sv = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
+    zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- x: wait for it alone, stage it in pair order, sums of both halves.
+  wait_vm<U8 + 2>();
+  __builtin_amdgcn_sched_barrier(0);
+  if (lane < 32) *reinterpret_cast<u32x4*>(Xw + 8 * lane) = permute_x8(xv);
+  float sum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t d = xv[e];
+    sum += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
+  }
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  sum += __shfl_xor(sum, 4, 64);
+  sum += __shfl_xor(sum, 8, 64);
+  const float xs0 = __shfl(sum, 0, 64), xs1 = __shfl(sum, 16, 64);
+  // A operands: half H, MFMA t of lane (., j) = x[k0 + 128 H + 32 j + 8 t ..] (pair
+  // order); ac: the 8-row tile's, half 1 in A row 1 (lanes col == 1).
+  u32x4 xa[2][4], ac[4];
+#pragma unroll
+  for (int H = 0; H < 2; ++H)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xa[H][t] = *reinterpret_cast<const u32x4*>(Xw + 128 * H + 32 * j + 8 * t);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) ac[t] = *reinterpret_cast<const u32x4*>(Xw + (col == 1 ? 128 : 0) + 32 * j + 8 * t);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const uint32_t nib_mask = 0x000f000fu, nib_magic = E::MAGIC2;
+  const int r7 = col & 7;
+  // One MFMA chain over a lane's 16 bytes of weights; returns output register
+  // `reg`. The operand registers are kept allocated until the result has been
+  // read (which waits for the chain): code built by this toolchain for gfx950
+  // was seen to overwrite an MFMA's A / B registers while it was still in
+  // flight once they were otherwise dead.
+  auto chain = [&](const u32x4 (&a)[4], const u32x4 w, int reg) -> float {
+    u32x4 b0, b1, b2, b3;
+    widen_pair<DT>(w.x, w.y, nib_mask, nib_magic, b0, b1);
+    widen_pair<DT>(w.z, w.w, nib_mask, nib_magic, b2, b3);
+    f32x4 C = f32x4{0.f, 0.f, 0.f, 0.f};
+    C = mfma16x16x32<DT>(a[0], b0, C);
+    C = mfma16x16x32<DT>(a[1], b1, C);
+    C = mfma16x16x32<DT>(a[2], b2, C);
+    C = mfma16x16x32<DT>(a[3], b3, C);
+    float c = reg == 0 ? C[0] : C[1];
+    __asm__ volatile("" : "+v"(c) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
+    return c;
+  };
+  // ---- tiles as their loads land (the scale / zero loads are the last 2).
+  float cf[NF + 1][2];
+#pragma unroll
+  for (int T = 0; T < NF; ++T) {
+    // No LDS load below may be issued before the previous tile's MFMAs have read
+    // their operands: the fences keep each tile's reads after the prior tile.
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_rt(U8 - 1 - (2 * T + 1) + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    const int h = col >> 3;
+    const int u = 2 * T + h;
+    const int p0 = 16 * (j >> 1) + 8 * ((j & 1) ^ h) + r7;        // piece j      (half 0)
+    const int p1 = 16 * (2 + (j >> 1)) + 8 * ((j & 1) ^ h) + r7;  // piece 4 + j  (half 1)
+    const u32x4 w0 = *reinterpret_cast<const u32x4*>(Wl + 1024 * u + 16 * p0);
+    const u32x4 w1 = *reinterpret_cast<const u32x4*>(Wl + 1024 * u + 16 * p1);
+    cf[T][0] = chain(xa[0], w0, 0);
+    cf[T][1] = chain(xa[1], w1, 0);
+  }
+  if constexpr (HALF) {
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm<2>();
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int u = U8 - 1;
+    const int H = col >> 3;
+    const int sigma = 4 * H + j;
+    const int pp = 16 * (sigma >> 1) + 8 * (sigma & 1) + r7;
+    const u32x4 w = *reinterpret_cast<const u32x4*>(Wl + 1024 * u + 16 * pp);
+    cf[NF][0] = chain(ac, w, H);
+  }
+  // ---- scales / zeros, the fold, the cross-wave sum.
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm<0>();
+  __builtin_amdgcn_sched_barrier(0);
+  __asm__ volatile("" : "+v"(sv), "+v"(zv16));  // no use of these loads before the wait
+  uint32_t zv = zv16;
+  if constexpr (!G128) {
+    sv = (sv & 0xffffu) | (sv << 16);
+    zv = (zv & 0xffu) | (zv << 8);
+  }
+  auto sz_of = [&](int n, float& s0, float& s1, float& z0, float& z1) {
+    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(sv)));
+    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(zv)));
+    s0 = E::to_f32(static_cast<uint16_t>(sp & 0xffffu));
+    s1 = E::to_f32(static_cast<uint16_t>(sp >> 16));
+    z0 = E::MAGIC_VALUE + static_cast<float>(zp & 0xffu);
+    z1 = E::MAGIC_VALUE + static_cast<float>((zp >> 8) & 0xffu);
+  };
+#pragma unroll
+  for (int T = 0; T < NF; ++T) {
+    float s0, s1, z0, z1;
+    sz_of(8 * (2 * T + (col >> 3)) + r7, s0, s1, z0, z1);
+    const float acc = fmaf(s0, fmaf(-z0, xs0, cf[T][0]), s1 * fmaf(-z1, xs1, cf[T][1]));
+    if (lane < 16) Rsm[16 * T + lane][wave] = acc;
+  }
+  if constexpr (HALF) {
+    const int H = col >> 3;
+    float s0, s1, z0, z1;
+    sz_of(8 * (U8 - 1) + r7, s0, s1, z0, z1);
+    const float part = H == 0 ? s0 * fmaf(-z0, xs0, cf[NF][0]) : s1 * fmaf(-z1, xs1, cf[NF][0]);
+    const float acc = part + __shfl_xor(part, 8, 64);
+    if (lane < 8) Rsm[16 * NF + lane][wave] = acc;
+  }
+  __syncthreads();
+  if (threadIdx.x < R) {
+    const int n = n0 + threadIdx.x;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < gemv::MAX_WAVES; ++w)
+      if (w < nw) v += Rsm[threadIdx.x][w];
+    if (n < N) {
+      uint16_t out = E::from_f32(v);
+      if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
+      y[n] = out;
+    }
+  }
+}
+
+// Whether the one-token kernel takes this shape (else the caller uses the
+// general skinny kernel).
+bool int4_gemv_supports(int N, int K, int G, const void* x, const void* packed, const void* scale,
+                        const void* zero) {
+  if (K % 256 != 0 || K < 256 || K > 256 * gemv::MAX_WAVES) return false;
+  if (!(G == 128 || G % 256 == 0) || K % G != 0) return false;
+  const int u8 = (N + 2047) / 2048;
+  if (N <= 0 || u8 > gemv::MAX_U8) return false;
+  if (static_cast<size_t>(N) * (K / 2) >= (1ull << 31)) return false;
+  // 16-byte x and weight loads; scale pairs as dwords (group 128).
+  return aligned(x, 16) && aligned(packed, 16) && (G != 128 || aligned(scale, 4)) && (G != 128 || aligned(zero, 2));
+}
+
+template <int DT, int U8>
+static void launch_gemv_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                           const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+  const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / 256));
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* ys = static_cast<uint16_t*>(y);
+  if (G == 128)
+    hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K, G);
+  else
+    hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, false>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K, G);
+}
+
+template <int DT>
+static void launch_gemv_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                           const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+  switch ((N + 2047) / 2048) {
+    case 1: launch_gemv_u8<DT, 1>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    case 2: launch_gemv_u8<DT, 2>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    case 3: launch_gemv_u8<DT, 3>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    case 4: launch_gemv_u8<DT, 4>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    case 5: launch_gemv_u8<DT, 5>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    case 6: launch_gemv_u8<DT, 6>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    case 7: launch_gemv_u8<DT, 7>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    default: launch_gemv_u8<DT, 8>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+  }
+}
+
+LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                           const void* bias, void* y, int N, int K, int G, int dtype, hipStream_t stream) {
+  if (dtype == LNQ_BF16) launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+  else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+  return launched("int4_gemv");
+}
+
+}  // namespace lnq

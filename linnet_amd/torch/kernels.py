@@ -19,7 +19,7 @@ from ..errors import LinnetError
 
 _CODES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
 _HALF = (torch.bfloat16, torch.float16)
-KERNELS = {"auto": _lib.KERNEL_AUTO, "skinny": _lib.KERNEL_SKINNY, "tiled": _lib.KERNEL_TILED}
+KERNELS = {"auto": _lib.KERNEL_AUTO, "skinny": _lib.KERNEL_SKINNY, "tiled": _lib.KERNEL_TILED, "gemv": _lib.KERNEL_GEMV}
 
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
@@ -61,13 +61,17 @@ def int4_linear(
     zero: torch.Tensor,
     bias: torch.Tensor | None = None,
     kernel: str = "auto",
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """`F.linear(x, W) (+ bias)` for `x` [rows, In] (bf16 or f16) and the group-wise
     4-bit weight of `std.quant::linear_int4_groups` -- `packed` ([Out, Groups,
     Group/2] u8, the even value low), `scale` ([Out, Groups], x's dtype) and `zero`
-    ([Out, Groups] u8) -- read once from HBM as they are stored. Few rows run the
+    ([Out, Groups] u8) -- read once from HBM as they are stored. One row runs the
+    one-token GEMV (one workgroup per CU) where its shape limits allow, few rows the
     skinny MFMA kernel, many the LDS-tiled dequant-GEMM (`kernel` may force one).
-    In is a multiple of 128; the group is 32, 64 or a multiple of 128.
+    In is a multiple of 128; the group is 32, 64 or a multiple of 128. `out`, if
+    given, is a contiguous [rows, Out] tensor of x's dtype on x's device that
+    receives the result (and is returned) instead of a new one.
 
     Replaces `kernels.py:277-323` (`int4_linear`) and tinygemm's
     `aten._weight_int4pack_mm` (`src/backend/torch_source.cpp:1556-1558`)."""
@@ -93,7 +97,12 @@ def int4_linear(
     x = x.contiguous()
     packed, scale, zero = packed.contiguous(), scale.contiguous(), zero.contiguous()
     bias = None if bias is None else bias.contiguous()
-    y = torch.empty(rows, width, dtype=x.dtype, device=device)
+    if out is None:
+        y = torch.empty(rows, width, dtype=x.dtype, device=device)
+    else:
+        if tuple(out.shape) != (rows, width) or out.dtype != x.dtype or out.device != device or not out.is_contiguous():
+            raise LinnetError(f"int4_linear: out is a contiguous [{rows}, {width}] {x.dtype} tensor on {device}")
+        y = out
     with torch.cuda.device(device):
         _lib.call(
             "lnq_int4_linear", _ptr(x), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),

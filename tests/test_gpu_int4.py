@@ -182,6 +182,74 @@ def test_unsupported_groups_fall_back_to_the_dequantized_weight() -> None:
     _check_linear(x, packed, scale, zero, y)
 
 
+# ------------------------------------------------------------- one-token GEMV
+
+
+@pytest.mark.parametrize(
+    ("out", "width", "group", "dtype"),
+    [
+        (56, 4096, 128, torch.bfloat16),  # one 56-row workgroup (the 14336-row split)
+        (100, 4096, 128, torch.bfloat16),  # ragged last workgroup
+        (5, 256, 128, torch.bfloat16),  # one wave, 5 of 8 rows
+        (2049, 1024, 128, torch.float16),  # 16 rows a workgroup, one row over
+        (1024, 512, 256, torch.bfloat16),  # group 256: both halves share a group
+        (300, 2048, 512, torch.float16),
+        (4000, 768, 128, torch.bfloat16),  # 3 waves, 16 rows a workgroup
+        (9000, 4096, 128, torch.bfloat16),  # 40 rows a workgroup (U8 = 5)
+        (16384, 256, 128, torch.bfloat16),  # 64 rows a workgroup (U8 = 8)
+        (6144, 1280, 128, torch.float16),  # 24 rows a workgroup (U8 = 3)
+        (12288, 512, 128, torch.bfloat16),  # U8 = 6
+        (8192, 256, 256, torch.bfloat16),  # U8 = 4
+    ],
+)
+def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, group: int, dtype: torch.dtype) -> None:
+    packed, scale, zero = _layer(out, width, group, seed=out + width, dtype=dtype)
+    x = torch.randn(1, width, generator=torch.Generator().manual_seed(width)).to(dtype)
+    args = (packed.to(DEV), scale.to(DEV), zero.to(DEV))
+    y = kernels.int4_linear(x.to(DEV), *args, kernel="gemv")
+    assert y.shape == (1, out) and y.dtype == dtype
+    _check_linear(x, packed, scale, zero, y)
+    # the skinny kernel sums in another order: the two agree within bf16 rounding
+    other = kernels.int4_linear(x.to(DEV), *args, kernel="skinny").float()
+    assert (y.float() - other).abs().max().item() <= 1e-2 * other.abs().max().item()
+
+
+def test_out_receives_the_product() -> None:
+    packed, scale, zero = _layer(96, 512, 128, seed=8)
+    args = (packed.to(DEV), scale.to(DEV), zero.to(DEV))
+    for rows in (1, 3, 80):
+        x = torch.randn(rows, 512, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16).to(DEV)
+        out = torch.full((rows, 96), float("nan"), dtype=torch.bfloat16, device=DEV)
+        got = kernels.int4_linear(x, *args, out=out)
+        assert got.data_ptr() == out.data_ptr()
+        assert torch.equal(out, kernels.int4_linear(x, *args))
+
+
+def test_one_token_gemv_bias_is_added_after_the_rounded_product() -> None:
+    packed, scale, zero = _layer(120, 1024, 128, seed=21)
+    bias = torch.randn(120, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
+    x = torch.randn(1, 1024, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).to(DEV)
+    args = (packed.to(DEV), scale.to(DEV), zero.to(DEV))
+    fused = kernels.int4_linear(x, *args, bias, kernel="gemv")
+    plain = kernels.int4_linear(x, *args, kernel="gemv") + bias
+    assert torch.equal(fused, plain)
+
+
+def test_one_token_gemv_is_chosen_for_one_row_and_refuses_other_shapes() -> None:
+    from linnet_amd.errors import LinnetError
+
+    packed, scale, zero = _layer(64, 512, 32, seed=2)
+    x = torch.randn(1, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
+    with pytest.raises(LinnetError, match="one-token kernel"):
+        kernels.int4_linear(x, packed.to(DEV), scale.to(DEV), zero.to(DEV), kernel="gemv")
+    # group 32 at one row: auto falls back to the skinny kernel
+    _check_linear(x.cpu(), packed, scale, zero, kernels.int4_linear(x, packed.to(DEV), scale.to(DEV), zero.to(DEV)))
+    packed, scale, zero = _layer(64, 512, 128, seed=2)
+    x2 = torch.randn(2, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
+    with pytest.raises(LinnetError, match="one-token kernel"):
+        kernels.int4_linear(x2, packed.to(DEV), scale.to(DEV), zero.to(DEV), kernel="gemv")
+
+
 # ------------------------------------------------------------ full BASELINE sizes
 
 
