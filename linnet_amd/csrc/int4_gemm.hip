@@ -5,22 +5,32 @@
 // rounding), so that every MFMA product is x * bf16(W) as in the reference's
 // dequant + BLAS path (src/backend/torch_source.cpp:1561-1566).
 //
-// Tiles: 256 x 128 outputs per workgroup of 4 waves (2 x 2), each wave a
-// 128 x 64 block of 4 x 2 MFMA 32x32x16 tiles; 64 inputs per step.
+// Tiles: 256 rows of x by BN = 256 or 128 columns of W per workgroup of 8
+// waves, two per SIMD. A wave owns a 128 x 64 (BN = 256) or 64 x 64 (BN = 128)
+// block of MFMA 32x32x16 tiles; 64 inputs per step. Two waves per SIMD is what
+// lets the matrix core run while a wave's loads and dequantization issue: on
+// gfx950 an MFMA 32x32x16 holds its wave's issue for about 20 of its 32
+// cycles, and a buffer load issued beside MFMA and VALU work stalls the wave
+// for tens of cycles; the other wave of the SIMD covers both.
 //
-// Pipeline, per step ks:
+// Pipeline, per step ks (each wave):
 //   * x moves HBM/L2 -> LDS without registers (buffer_load ... lds), two steps
 //     ahead, into a ring of three 32 KB stages;
-//   * the packed weights (16 bytes per thread), scale and zero point of step
-//     ks + 2 are requested into one of two register sets;
-//   * while step ks's MFMAs run, the register set of step ks + 1 is
-//     dequantized into the other of two 16 KB W stages;
-//   * each wave waits for its own x loads of step ks + 1 (an explicit vmcnt
-//     that leaves step ks + 2's loads in flight), then one barrier.
-// The barriers are bare s_barrier with explicit waits: __syncthreads()'s fence
+//   * the packed weights, scale and zero point of step ks + 3 are requested
+//     into one of three register sets;
+//   * the weights of the next step are dequantized into one of two W stages:
+//     (q - z) * s = fma(q, s, -z * s) in f32 (exact), one rounding to the
+//     16-bit type. The work of a step's weights is spread evenly over the 4 *
+//     NMF MFMA slots from the last kk of step ks - 1 through kk = 2 of step ks
+//     (about three VALU instructions per MFMA); each slot is its own
+//     scheduling region (sched_barrier), which pins that interleave;
+//   * one barrier, after kk = 2: every wave's x of step ks + 1 has landed and
+//     its W stores are done; kk = 3 then runs while step ks + 1's kk = 0
+//     operands are read and the dequantization of step ks + 2 begins in the W
+//     stage step ks has finished with.
+// The barrier is a bare s_barrier with explicit waits: __syncthreads()'s fence
 // would wait for every outstanding load, including the ones two steps ahead.
-// Stage indices are compile-time (the loop is unrolled by 6 = lcm(3, 2)) so
-// that the compiler can tell the stages' LDS accesses apart.
+// Stage indices are compile-time (the loop is unrolled by 6 = lcm(3, 2)).
 //
 // Rows of 64 elements are stored with their 16-byte columns XOR-swizzled by
 // bits 1..3 of the row, so the MFMA operand reads hit distinct banks; the x
@@ -36,26 +46,35 @@ namespace lnq {
 
 namespace gemm {
 constexpr int BM = 256;
-constexpr int BN = 128;
 constexpr int BK = 64;
-constexpr int THREADS = 256;
+constexpr int THREADS = 512;
 constexpr int GROUP_M = 4;
 constexpr int XCDS = 8;
+
+template <int BN>
+struct Cfg;
+template <>
+struct Cfg<256> {
+  static constexpr int WAVES_N = 4;  // waves of 128 x 64, 2 x 4
+  static constexpr int FA = 4;       // 32-row fragments of a wave
+  static constexpr int FB = 2;       // 32-column fragments of a wave
+};
+template <>
+struct Cfg<128> {
+  static constexpr int WAVES_N = 2;  // waves of 64 x 64, 4 x 2
+  static constexpr int FA = 2;
+  static constexpr int FB = 2;
+};
 }  // namespace gemm
 
 template <int DT>
-__device__ inline f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c);
-
-template <>
-__device__ inline f32x16 mfma32x32x16<LNQ_BF16>(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-template <>
-__device__ inline f32x16 mfma32x32x16<LNQ_F16>(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+__device__ inline f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == LNQ_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
 }
 
 // Two exact f32 products rounded to the 16-bit type and packed (low = a): one
@@ -68,7 +87,7 @@ __device__ inline uint32_t pack2(float a, float b) {
 
 // Element offset of 16-byte column c16 of row `row` in a swizzled 64-wide tile
 // (rows of 128 bytes). The 16-byte columns are XOR-swizzled by bits 1..3 of the
-// row: an MFMA operand read takes 16 consecutive rows at one column, and rows
+// row: an MFMA operand read takes 32 consecutive rows at one column, and rows
 // 2i and 2i+1 share a 256-byte bank line in opposite halves, so the XOR must
 // separate row pairs, not single rows.
 __device__ inline int swz(int row, int c16) { return row * gemm::BK + ((c16 ^ ((row >> 1) & 7)) << 3); }
@@ -80,8 +99,8 @@ __device__ inline void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn
   const int xcd = b % gemm::XCDS;
   const int local = b / gemm::XCDS;
   int logical = xcd * per_xcd + local;
-  // The last XCDs may own fewer tiles when total % 8 != 0: the excess
-  // logical ids fold back onto the tail workgroups' slots.
+  // The last XCDs own one tile fewer when total % 8 != 0: the excess logical
+  // ids fold back onto the tail workgroups' slots.
   const int full = total - (per_xcd - 1) * gemm::XCDS;  // XCDs owning per_xcd tiles
   if (total % gemm::XCDS != 0) {
     logical = xcd < full ? xcd * per_xcd + local : full * per_xcd + (xcd - full) * (per_xcd - 1) + local;
@@ -93,42 +112,31 @@ __device__ inline void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn
   tn = (logical % per_group) / rows;
 }
 
-// The issue order the scheduler is asked for within one kk: each of the 8
-// MFMAs followed by one operand read (of the next kk) and VALU instructions of
-// the dequantization, then the W tile writes, so that the matrix core is fed
-// while the rest of the step's work issues beside it.
-template <bool READS, int VALU, int WRITES>
-__device__ inline void interleave() {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    if constexpr (READS) {
-      if (i < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    }
-    if constexpr (VALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);
-  }
-  if constexpr (WRITES > 0) __builtin_amdgcn_sched_group_barrier(0x200, WRITES, 0);  // DS write
-}
-
-template <int DT>
+template <int DT, int BN>
 __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
-    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G,
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint8_t* __restrict__ zero, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
     int gshift) {
   using namespace gemm;
   using E = Elem<DT>;
+  constexpr int FA = Cfg<BN>::FA, FB = Cfg<BN>::FB, WAVES_N = Cfg<BN>::WAVES_N;
+  constexpr int NMF = FA * FB;   // MFMA slots of one kk
+  constexpr int TPR = THREADS / BN;  // threads per W row
+  constexpr int KPT = BK / TPR;  // inputs of a thread per step
+  constexpr int DW = KPT / 8;    // packed dwords of a thread per step
+  static_assert(DW * 8 == 4 * NMF, "one packed dword of dequantization per 8 MFMA slots");
   __shared__ __attribute__((aligned(16))) uint16_t X0[BM * BK];
   __shared__ __attribute__((aligned(16))) uint16_t X1[BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t X2[BM * BK];
   __shared__ __attribute__((aligned(16))) uint16_t W0[BN * BK];
   __shared__ __attribute__((aligned(16))) uint16_t W1[BN * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t X2[BM * BK];
+  LNQ_MFMA_IN_AGPRS();
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1;  // 0..1: 128-row half
-  const int wn = wave & 1;   // 0..1: 64-column half
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   int tm, tn;
@@ -136,7 +144,7 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   if (tm >= tiles_m || tn >= tiles_n) return;
   const int m0 = tm * BM;
   const int n0 = tn * BN;
-  const int groups = K / G;
+  const int groups = K >> gshift;
   const int steps = K / BK;
 
   // Operands through buffer descriptors: 32-bit lane offsets, the step's offset
@@ -149,172 +157,219 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   // and the same number of loads in flight as any other step.
   const __amdgpu_buffer_rsrc_t rnull = buffer_rsrc(packed, 0);
 
-  // x: load i of wave w writes LDS rows 32 i + 8 w .. + 7 (1 KB, lane l at byte
-  // 16 l: row 32 i + 8 w + l / 8, stored column l % 8). The stored column holds
-  // source column (l % 8) ^ key(row); key = (row >> 1) & 7 = (4 w + l / 16) & 7
-  // does not depend on i, so the 8 loads differ only by a uniform offset.
+  // x: load i (0..3) of wave w writes LDS rows 64 i + 8 w .. + 7 (1 KB, lane l
+  // at byte 16 l: row 64 i + 8 w + l / 8, stored column l % 8). The stored
+  // column holds source column (l % 8) ^ key(row); key = (row >> 1) & 7 =
+  // (4 w + l / 16) & 7 does not depend on i, so the 4 loads differ only by a
+  // uniform offset.
   const int xrow = 8 * wave + (lane >> 3);
   const int xcol = (lane & 7) ^ ((xrow >> 1) & 7);
   const int xoff = (m0 + xrow) * K * 2 + xcol * 16;
   const int xlds = wave * 512;  // elements
-  auto load_x = [&](uint16_t* dst, int ks) {
-    const bool in = ks < steps;
-    const int k0 = in ? ks * BK : 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(in ? rx : rnull, (lds_ptr)(dst + xlds + i * 32 * BK), 16, xoff,
-                                                2 * k0 + i * 64 * K, 0, 0);
+  auto load_x = [&](uint16_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + xlds + i * 64 * BK), 16, xoff, 2 * k0 + i * 128 * K, 0,
+                                              0);
   };
 
-  // W: thread -> row n0 + tid / 2, 32 weights (16 packed bytes) at k offset 32 * (tid % 2).
-  const int brow = tid >> 1;
-  const int bhalf = tid & 1;
+  // W: thread -> row n0 + tid / TPR, KPT weights (KPT / 2 packed bytes) at k
+  // offset KPT * (tid % TPR), within one group (G is a power of two >= 32).
+  const int brow = tid / TPR;
+  const int bpart = tid % TPR;
   const int nsrc = n0 + brow;
-  const int woff = nsrc * (K >> 1) + bhalf * 16;
+  const int woff = nsrc * (K >> 1) + bpart * (KPT / 2);
   const int soff = nsrc * groups * 2;
   const int zoff = nsrc * groups;
   struct WRegs {
-    u32x4 w;
+    uint32_t w[DW];
     uint32_t s, z;
   };
   auto load_w = [&](WRegs& r, int ks) {
     const bool in = ks < steps;
     const int k0 = in ? ks * BK : 0;
-    const int g = gshift >= 0 ? (k0 + 32 * bhalf) >> gshift : (k0 + 32 * bhalf) / G;
-    r.s = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(in ? rs : rnull, soff + 2 * g, 0, 0));
-    r.z = __builtin_amdgcn_raw_buffer_load_b8(in ? rz : rnull, zoff + g, 0, 0);
-    r.w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(in ? rw : rnull, woff, k0 >> 1, 0));
-  };
-  // Dequantize packed dword d (elements 8d..8d+7 of the thread's 32) into one
-  // 16-byte column of the W tile: (q - z) * s = fma(q, s, -z*s), exact in f32
-  // (z * s: 4 bits times a 16-bit float), then one rounding to the 16-bit type.
-  float sreg = 0.f, zsreg = 0.f;
-  auto store_w = [&](uint16_t* dst, int d, const WRegs& r) {
-    if (d == 0) {
-      sreg = E::to_f32(static_cast<uint16_t>(r.s));
-      zsreg = static_cast<float>(r.z & 0xffu) * sreg;
+    const int g = (k0 + KPT * bpart) >> gshift;
+    const __amdgpu_buffer_rsrc_t qs = in ? rs : rnull, qz = in ? rz : rnull, qw = in ? rw : rnull;
+    r.s = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(qs, soff + 2 * g, 0, 0));
+    r.z = __builtin_amdgcn_raw_buffer_load_b8(qz, zoff + g, 0, 0);
+    if constexpr (DW == 4) {
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qw, woff, k0 >> 1, 0));
+      r.w[0] = v.x;
+      r.w[1] = v.y;
+      r.w[2] = v.z;
+      r.w[3] = v.w;
+    } else {
+      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(qw, woff, k0 >> 1, 0));
+      r.w[0] = v.x;
+      r.w[1] = v.y;
     }
-    const uint32_t word = d == 0 ? r.w.x : d == 1 ? r.w.y : d == 2 ? r.w.z : r.w.w;
-    const uint32_t lo = opaque(word & 0x0f0f0f0fu);
-    const uint32_t hi = opaque((word >> 4) & 0x0f0f0f0fu);
-    float v[8];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      v[2 * b] = fmaf(static_cast<float>((lo >> (8 * b)) & 0xffu), sreg, -zsreg);
-      v[2 * b + 1] = fmaf(static_cast<float>((hi >> (8 * b)) & 0xffu), sreg, -zsreg);
-    }
-    u32x4 o;
-    o.x = pack2<DT>(v[0], v[1]);
-    o.y = pack2<DT>(v[2], v[3]);
-    o.z = pack2<DT>(v[4], v[5]);
-    o.w = pack2<DT>(v[6], v[7]);
-    *reinterpret_cast<u32x4*>(&dst[swz(brow, 4 * bhalf + d)]) = o;
   };
 
-  f32x16 acc[4][2];
+  // The dequantization of one step's weights as a stream of 4 * NMF positions,
+  // 8 per packed dword (8 weights -> one 16-byte column of row brow): position
+  // j of a dword does its share of 2 masks, 8 conversions, 8 FMAs and 4 packs.
+  struct Deq {
+    uint32_t lo, hi;
+    float f0, f1, v0, v1;
+    u32x4 o;
+  };
+  Deq q;
+  float sv = 0.f, nzs = 0.f;  // scale and -zero * scale of the weights being dequantized
+  auto cvtb = [](uint32_t v, int byte) -> float { return static_cast<float>((v >> (8 * byte)) & 0xffu); };
+  auto set_scale = [&](const WRegs& r) {
+    sv = E::to_f32(static_cast<uint16_t>(r.s));
+    nzs = -static_cast<float>(r.z & 0xffu) * sv;
+  };
+  auto deq_slot = [&](const WRegs& r, int pos, uint16_t* dst) {
+    const int d = pos >> 3;
+    switch (pos & 7) {
+      case 0:
+        q.lo = opaque(r.w[d] & 0x0f0f0f0fu);
+        q.hi = opaque((r.w[d] >> 4) & 0x0f0f0f0fu);
+        break;
+      case 1: q.f0 = cvtb(q.lo, 0); q.f1 = cvtb(q.hi, 0); q.v0 = fmaf(q.f0, sv, nzs); break;
+      case 2: q.v1 = fmaf(q.f1, sv, nzs); q.o.x = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 1); break;
+      case 3: q.f1 = cvtb(q.hi, 1); q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); break;
+      case 4: q.o.y = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 2); q.f1 = cvtb(q.hi, 2); break;
+      case 5: q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); q.o.z = pack2<DT>(q.v0, q.v1); break;
+      case 6: q.f0 = cvtb(q.lo, 3); q.f1 = cvtb(q.hi, 3); q.v0 = fmaf(q.f0, sv, nzs); break;
+      default:
+        q.v1 = fmaf(q.f1, sv, nzs);
+        q.o.w = pack2<DT>(q.v0, q.v1);
+        *reinterpret_cast<u32x4*>(&dst[swz(brow, DW * bpart + d)]) = q.o;
+        break;
+    }
+  };
+
+  f32x16 acc[FA][FB];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < FA; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < FB; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
   const int lrow = lane & 31;
   const int lk = lane >> 5;  // which 8 of an MFMA's 16 inputs
-  // Operand fragments: f0 holds even kk, f1 odd kk. kk + 1's are read from LDS
-  // while kk's MFMAs run; step ks + 1's kk = 0 is read right after the barrier,
-  // under step ks's last MFMAs.
-  u32x4 af0[4], bf0[2], af1[4], bf1[2];
-  auto read = [&](const uint16_t* xs, const uint16_t* ws, int kk, u32x4* a_, u32x4* b_) {
-    const int c16 = 2 * kk + lk;
+  // Operand byte offsets within a stage, per kk. The fragments of one kk are
+  // 32 rows (4096 bytes) apart and share the swizzle key (row >> 1) & 7, so
+  // one offset register per kk serves them all through the immediate field.
+  uint32_t aoff[4], boff[4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) a_[a] = *reinterpret_cast<const u32x4*>(&xs[swz(wm * 128 + a * 32 + lrow, c16)]);
-#pragma unroll
-    for (int b = 0; b < 2; ++b) b_[b] = *reinterpret_cast<const u32x4*>(&ws[swz(wn * 64 + b * 32 + lrow, c16)]);
+  for (int kk = 0; kk < 4; ++kk) {
+    const uint32_t col = static_cast<uint32_t>(((2 * kk + lk) ^ ((lrow >> 1) & 7)) << 4);
+    aoff[kk] = static_cast<uint32_t>((wm * FA * 32 + lrow) * 128) + col;
+    boff[kk] = static_cast<uint32_t>((wn * FB * 32 + lrow) * 128) + col;
+  }
+  auto rd = [&](const uint16_t* stage, uint32_t off, int frag) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(stage) + off + frag * 4096);
   };
-  auto mfmas = [&](const u32x4* a_, const u32x4* b_) {
+  // Operand fragments: f0 holds even kk, f1 odd kk; kk + 1's are read while
+  // kk's MFMAs run.
+  u32x4 af0[FA], bf0[FB], af1[FA], bf1[FB];
+
+  // One kk: NMF MFMA slots on (ca, cb). The first FA + FB slots read the next
+  // kk's operands from (rxs, rws); slot s also carries dequantization position
+  // pos0 + s of `deq` (into wd) and the loads vm(s).
+  auto region = [&](const u32x4* ca, const u32x4* cb, u32x4* na, u32x4* nb, const uint16_t* rxs,
+                    const uint16_t* rws, int nkk, const WRegs& deq, uint16_t* wd, int pos0, auto&& vm) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b) acc[a][b] = mfma32x32x16<DT>(a_[a], b_[b], acc[a][b]);
+    for (int s = 0; s < NMF; ++s) {
+      acc[s / FB][s % FB] = mfma32x32x16<DT>(ca[s / FB], cb[s % FB], acc[s / FB][s % FB]);
+      if (s < FA) na[s] = rd(rxs, aoff[nkk], s);
+      else if (s < FA + FB) nb[s - FA] = rd(rws, boff[nkk], s - FA);
+      deq_slot(deq, pos0 + s, wd);
+      vm(s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  // One step: MFMAs on (xc, wcur) with kk = 0 already in f0; step ks + 2
-  // requested into (xn2, later); step ks + 1's weights (next) dequantized into
-  // wnext, which with xn1 holds step ks + 1's operands after the barrier.
-  auto step = [&](int ks, const uint16_t* xc, const uint16_t* xn1, uint16_t* xn2, const uint16_t* wcur,
-                  uint16_t* wnext, const WRegs& next, WRegs& later) {
-    load_w(later, ks + 2);
-    load_x(xn2, ks + 2);
-    read(xc, wcur, 1, af1, bf1);
-    mfmas(af0, bf0);
-    store_w(wnext, 0, next);
-    interleave<true, 3, 1>();
-    read(xc, wcur, 2, af0, bf0);
-    mfmas(af1, bf1);
-    store_w(wnext, 1, next);
-    interleave<true, 3, 1>();
-    read(xc, wcur, 3, af1, bf1);
-    mfmas(af0, bf0);
-    store_w(wnext, 2, next);
-    store_w(wnext, 3, next);
-    interleave<true, 6, 2>();
-    // This wave's x loads of step ks + 1 are done once at most the 11 loads
-    // issued after them (step ks + 2's 3 weight loads and 8 x loads) remain;
-    // its W stores and kk = 3 reads are done at lgkmcnt(0). Past the barrier
-    // every wave's are: step ks + 1's operands are in LDS, and no wave reads
-    // step ks's stages again, so the next step's loads may overwrite them.
-    __asm__ volatile("s_waitcnt vmcnt(11)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+
+  // Step ks: MFMAs on (xc, wc) with kk = 0 already in f0. Regions kk = 0..2
+  // also DMA x of step ks + 2 into xn2, dequantize positions NMF.. of step
+  // ks + 1's weights (registers d1) into wn, and request step ks + 3's weights
+  // into req. After the barrier, kk = 3 reads step ks + 1's kk = 0 operands
+  // from (xn1, wn) and starts step ks + 2's weights (registers d2) in wc,
+  // which no wave reads any more.
+  auto step = [&](int ks, const uint16_t* xc, const uint16_t* xn1, uint16_t* xn2, uint16_t* wc, uint16_t* wn,
+                  const WRegs& d1, const WRegs& d2, WRegs& req) {
+    const bool xin = ks + 2 < steps;
+    const __amdgpu_buffer_rsrc_t xr = xin ? rx : rnull;
+    const int xk0 = xin ? (ks + 2) * BK : 0;
+    constexpr int XGAP = NMF / 4 + 1;  // slots between the 4 x loads
+    auto vm = [&](int r, int s) {
+      const int p = r * NMF + s;
+      if (p == 1) load_w(req, ks + 3);
+      if (p >= 3 && (p - 3) % XGAP == 0 && (p - 3) / XGAP < 4) load_x(xn2, xr, xk0, (p - 3) / XGAP);
+    };
+    region(af0, bf0, af1, bf1, xc, wc, 1, d1, wn, NMF, [&](int s) { vm(0, s); });
+    region(af1, bf1, af0, bf0, xc, wc, 2, d1, wn, 2 * NMF, [&](int s) { vm(1, s); });
+    region(af0, bf0, af1, bf1, xc, wc, 3, d1, wn, 3 * NMF, [&](int s) { vm(2, s); });
+    // This wave's x of step ks + 1 has arrived once at most the 7 loads issued
+    // after it (this step's 3 weight loads and 4 x loads) remain; its W stores
+    // are done at lgkmcnt(0). Past the barrier every wave's are, and no wave
+    // reads step ks's stages again.
+    __asm__ volatile("s_waitcnt vmcnt(7)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    read(xn1, wnext, 0, af0, bf0);
-    mfmas(af1, bf1);
-    interleave<true, 0, 0>();
-    __builtin_amdgcn_sched_barrier(0);
+    set_scale(d2);
+    region(af1, bf1, af0, bf0, xn1, wn, 0, d2, wc, 0, [&](int) {});
   };
 
-  WRegs ra, rb;
+  // Prologue: registers of steps 0..2 requested, x of steps 0 and 1 DMA'd;
+  // step 0's weights dequantized into W0 and the first NMF positions of step
+  // 1's into W1 (where the steady state's last region would have put them).
+  WRegs ra, rb, rc;
   load_w(ra, 0);
-  load_x(X0, 0);
-  load_w(rb, 1);
-  load_x(X1, 1);
 #pragma unroll
-  for (int d = 0; d < 4; ++d) store_w(W0, d, ra);
-  __asm__ volatile("s_waitcnt vmcnt(11)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+  for (int i = 0; i < 4; ++i) load_x(X0, rx, 0, i);
+  load_w(rb, 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) load_x(X1, steps > 1 ? rx : rnull, steps > 1 ? BK : 0, i);
+  load_w(rc, 2);
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  set_scale(ra);
+#pragma unroll
+  for (int p = 0; p < 4 * NMF; ++p) deq_slot(ra, p, W0);
+  set_scale(rb);
+#pragma unroll
+  for (int p = 0; p < NMF; ++p) deq_slot(rb, p, W1);
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
-  read(X0, W0, 0, af0, bf0);
+#pragma unroll
+  for (int a = 0; a < FA; ++a) af0[a] = rd(X0, aoff[0], a);
+#pragma unroll
+  for (int b = 0; b < FB; ++b) bf0[b] = rd(W0, boff[0], b);
 
-  // Stages: x step j in X[j % 3], W step j in W[j % 2], registers of step j in
-  // (ra, rb)[j % 2].
+  // x of step j in X[j % 3]; W of step j in W[j % 2]; registers of step j in
+  // (ra, rb, rc)[j % 3].
   int ks = 0;
   for (; ks + 6 <= steps; ks += 6) {
-    step(ks, X0, X1, X2, W0, W1, rb, ra);
-    step(ks + 1, X1, X2, X0, W1, W0, ra, rb);
-    step(ks + 2, X2, X0, X1, W0, W1, rb, ra);
-    step(ks + 3, X0, X1, X2, W1, W0, ra, rb);
-    step(ks + 4, X1, X2, X0, W0, W1, rb, ra);
-    step(ks + 5, X2, X0, X1, W1, W0, ra, rb);
+    step(ks + 0, X0, X1, X2, W0, W1, rb, rc, ra);
+    step(ks + 1, X1, X2, X0, W1, W0, rc, ra, rb);
+    step(ks + 2, X2, X0, X1, W0, W1, ra, rb, rc);
+    step(ks + 3, X0, X1, X2, W1, W0, rb, rc, ra);
+    step(ks + 4, X1, X2, X0, W0, W1, rc, ra, rb);
+    step(ks + 5, X2, X0, X1, W1, W0, ra, rb, rc);
   }
   // The last steps % 6 steps continue the same stage sequence.
   const int rest = steps - ks;
-  if (rest > 0) step(ks, X0, X1, X2, W0, W1, rb, ra);
-  if (rest > 1) step(ks + 1, X1, X2, X0, W1, W0, ra, rb);
-  if (rest > 2) step(ks + 2, X2, X0, X1, W0, W1, rb, ra);
-  if (rest > 3) step(ks + 3, X0, X1, X2, W1, W0, ra, rb);
-  if (rest > 4) step(ks + 4, X1, X2, X0, W0, W1, rb, ra);
-  // Loads of the two steps past the end (zeros through rnull) may be in flight.
+  if (rest > 0) step(ks + 0, X0, X1, X2, W0, W1, rb, rc, ra);
+  if (rest > 1) step(ks + 1, X1, X2, X0, W1, W0, rc, ra, rb);
+  if (rest > 2) step(ks + 2, X2, X0, X1, W0, W1, ra, rb, rc);
+  if (rest > 3) step(ks + 3, X0, X1, X2, W1, W0, rb, rc, ra);
+  if (rest > 4) step(ks + 4, X1, X2, X0, W0, W1, rc, ra, rb);
+  // Loads of the steps past the end (zeros through rnull) may be in flight.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Epilogue. MFMA 32x32 output: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4,
-  // column l%32.
+  // Epilogue. MFMA 32x32 output: lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4,
+  // column l % 32.
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
+  for (int a = 0; a < FA; ++a) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int n = n0 + wn * 64 + b * 32 + (lane & 31);
+    for (int b = 0; b < FB; ++b) {
+      const int n = n0 + wn * FB * 32 + b * 32 + (lane & 31);
       if (n >= N) continue;
       const float bv = bias != nullptr ? E::to_f32(bias[n]) : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 128 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int m = m0 + wm * FA * 32 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m < M) {
           uint16_t out = E::from_f32(acc[a][b][r]);
           if (bias != nullptr) out = E::from_f32(E::to_f32(out) + bv);
@@ -326,28 +381,50 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
 }
 
 bool int4_tiled_supports(int M, int N, int K, int G, int dtype) {
-  // Buffer offsets are 32-bit: x and the packed weight stay under 2 GiB.
-  return (dtype == LNQ_BF16 || dtype == LNQ_F16) && M > 0 && N > 0 && K % gemm::BK == 0 &&
-         K >= gemm::BK && G % 32 == 0 && K % G == 0 &&
-         static_cast<size_t>(M) * K * 2 < (1ull << 31) && static_cast<size_t>(N) * (K >> 1) < (1ull << 31);
+  // Buffer offsets are 32-bit: x and the packed weight stay under 2 GiB. A
+  // thread's 16 or 32 weights of a step lie in one group: G is a power of two
+  // of at least 32.
+  return (dtype == LNQ_BF16 || dtype == LNQ_F16) && M > 0 && N > 0 && K % gemm::BK == 0 && K >= gemm::BK &&
+         G >= 32 && (G & (G - 1)) == 0 && K % G == 0 && static_cast<size_t>(M) * K * 2 < (1ull << 31) &&
+         static_cast<size_t>(N) * (K >> 1) < (1ull << 31);
 }
 
-LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale,
-                            const uint8_t* zero, const void* bias, void* y, int M, int N, int K,
-                            int G, int dtype, hipStream_t stream) {
-  const int tiles = ((M + gemm::BM - 1) / gemm::BM) * ((N + gemm::BN - 1) / gemm::BN);
-  const dim3 grid(tiles), block(gemm::THREADS);
-  const int gshift = (G & (G - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(G)) : -1;
-  const auto* xs = static_cast<const uint16_t*>(x);
-  const auto* ss = static_cast<const uint16_t*>(scale);
-  const auto* bs = static_cast<const uint16_t*>(bias);
-  auto* ys = static_cast<uint16_t*>(y);
-  if (dtype == LNQ_BF16)
-    hipLaunchKernelGGL((int4_tiled_kernel<LNQ_BF16>), grid, block, 0, stream, xs, packed, ss, zero,
-                       bs, ys, M, N, K, G, gshift);
-  else
-    hipLaunchKernelGGL((int4_tiled_kernel<LNQ_F16>), grid, block, 0, stream, xs, packed, ss, zero,
-                       bs, ys, M, N, K, G, gshift);
+// Compute units of the current device, cached per device.
+static int compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+template <int DT, int BN>
+static void launch_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                         const void* bias, void* y, int M, int N, int K, int gshift, hipStream_t stream) {
+  const int tiles = ((M + gemm::BM - 1) / gemm::BM) * ((N + BN - 1) / BN);
+  hipLaunchKernelGGL((int4_tiled_kernel<DT, BN>), dim3(tiles), dim3(gemm::THREADS), 0, stream,
+                     static_cast<const uint16_t*>(x), packed, static_cast<const uint16_t*>(scale), zero,
+                     static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, K, gshift);
+}
+
+LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                            const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream) {
+  const int gshift = __builtin_ctz(static_cast<unsigned>(G));
+  // 256-column tiles read half the x bytes per FLOP of 128-column ones, but
+  // only pay while they still give every compute unit a tile.
+  const long tiles256 = static_cast<long>((M + gemm::BM - 1) / gemm::BM) * ((N + 255) / 256);
+  const bool wide = tiles256 >= compute_units();
+  if (dtype == LNQ_BF16) {
+    if (wide) launch_tiled<LNQ_BF16, 256>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
+    else launch_tiled<LNQ_BF16, 128>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
+  } else {
+    if (wide) launch_tiled<LNQ_F16, 256>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
+    else launch_tiled<LNQ_F16, 128>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
+  }
   return launched("int4_tiled");
 }
 
