@@ -9,6 +9,8 @@
 //   - int8_quantize: symmetric group-wise int8 rounding, bit-exact with numpy.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace lnq {
 
 // ------------------------------------------------------------------ helpers
@@ -249,20 +251,48 @@ __global__ __launch_bounds__(256) void rows8_kernel(const typename Elem<DT>::sto
 }
 
 // ======================================================================= mm8
-// 128 x 128 outputs per workgroup of 4 waves (2 x 2, each 64 x 64 = 2 x 2 MFMA
-// 32x32 tiles); 128 input bytes per step, double-buffered in LDS with 16-byte
-// columns XOR-swizzled by (row & 7). FP8: v_mfma_scale_f32_32x32x64_f8f6f4
-// (unit E8M0 scales); int8: v_mfma_i32_32x32x32_i8.
+// 8-bit x 8-bit products on gfx950 MFMA: FP8 E4M3 rows times FP8 weights
+// (v_mfma_scale_f32_32x32x64_f8f6f4 with unit E8M0 scales, f32 sums) or int8
+// rows times int8 weights (v_mfma_i32_32x32x32_i8, exact int32 sums); the
+// per-row and per-column scales are applied in f32 at the end.
+//
+// Tiles: 256 rows by BN = 256 or 128 columns per workgroup of 8 waves, two
+// per SIMD (the other wave of a SIMD covers the issue stalls of a wave's
+// loads); a wave owns 128 x 64 (BN = 256) or 64 x 64 (BN = 128) outputs as
+// MFMA 32x32 tiles. 128 input bytes per step, moved HBM/L2 -> LDS without
+// registers (buffer_load ... lds) one step ahead into two stages per operand,
+// rows of 128 bytes with 16-byte columns XOR-swizzled by bits 1..3 of the row.
+// A step's kk sub-steps are scheduling regions of one MFMA per slot
+// (sched_barrier), each slot carrying its share of the next kk's operand
+// reads; the one barrier per step sits before the last kk, whose MFMAs run
+// while the next step's first operands are read.
 namespace mm8 {
-constexpr int BM = 128;
-constexpr int BN = 128;
+constexpr int BM = 256;
 constexpr int BK = 128;  // bytes (= elements) per step
-constexpr int THREADS = 256;
+constexpr int THREADS = 512;
 constexpr int GROUP_M = 4;
 constexpr int XCDS = 8;
+
+template <int BN>
+struct Cfg;
+template <>
+struct Cfg<256> {
+  static constexpr int WAVES_N = 4;  // waves of 128 x 64, 2 x 4
+  static constexpr int FA = 4;
+  static constexpr int FB = 2;
+};
+template <>
+struct Cfg<128> {
+  static constexpr int WAVES_N = 2;  // waves of 64 x 64, 4 x 2
+  static constexpr int FA = 2;
+  static constexpr int FB = 2;
+};
 }  // namespace mm8
 
-__device__ inline int swz8(int row, int c16) { return row * mm8::BK + ((c16 ^ (row & 7)) << 4); }
+// Byte offset of 16-byte column c16 of row `row` in a swizzled stage (rows of
+// 128 bytes; rows 2i and 2i+1 share a 256-byte bank line, so the XOR key is
+// bits 1..3 of the row).
+__device__ inline int swz8(int row, int c16) { return row * mm8::BK + ((c16 ^ ((row >> 1) & 7)) << 4); }
 
 __device__ inline void mm8_tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
@@ -281,19 +311,39 @@ __device__ inline void mm8_tile_of(int b, int tiles_m, int tiles_n, int& tm, int
   tn = (logical % per_group) / rows;
 }
 
-template <int DT, int FP8>
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+template <int DT, int FP8, int BN>
 __global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
     const uint8_t* __restrict__ qx, const uint8_t* __restrict__ weight,
     const float* __restrict__ x_scale, const float* __restrict__ scale,
     uint16_t* __restrict__ y, int M, int N, int K) {
   using namespace mm8;
   using E = Elem<DT>;
-  __shared__ __attribute__((aligned(16))) uint8_t As[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * BK];
+  constexpr int FA = Cfg<BN>::FA, FB = Cfg<BN>::FB, WAVES_N = Cfg<BN>::WAVES_N;
+  constexpr int NMF = FA * FB;           // MFMA slots of one kk
+  constexpr int KPM = FP8 ? 64 : 32;     // inputs per MFMA
+  constexpr int KK = BK / KPM;           // kk sub-steps per step
+  constexpr int CPL = KPM / 32;          // 16-byte columns of an operand per lane
+  constexpr int BLOADS = BN / 64;        // weight loads of a wave per step
+  using Op = typename std::conditional<FP8, i32x8, i32x4>::type;
+  using Acc = typename std::conditional<FP8, f32x16, i32x16>::type;
+  // Stages per operand: three (loads two steps ahead) where they fit in LDS.
+  constexpr int S = BN == 256 ? 2 : 3;
+  constexpr int LPW = 4 + BLOADS;  // loads of a wave per step
+  __shared__ __attribute__((aligned(16))) uint8_t A0[BM * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t A1[BM * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t A2[S > 2 ? BM * BK : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t B0[BN * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t B1[BN * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t B2[S > 2 ? BN * BK : 16];
+  LNQ_MFMA_IN_AGPRS();
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   int tm, tn;
@@ -302,118 +352,170 @@ __global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
   const int m0 = tm * BM, n0 = tn * BN;
   const int steps = K / BK;
 
-  // Loads: 128 rows x 8 columns of 16 bytes per operand = 4 per thread each.
-  const uint8_t* asrc[4];
-  const uint8_t* bsrc[4];
-  int dst[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int id = tid + THREADS * i;
-    const int row = id >> 3, c16 = id & 7;
-    asrc[i] = qx + static_cast<size_t>(min(m0 + row, M - 1)) * K + 16 * c16;
-    bsrc[i] = weight + static_cast<size_t>(min(n0 + row, N - 1)) * K + 16 * c16;
-    dst[i] = swz8(row, c16);
-  }
-  u32x4 areg[4], breg[4];
-  auto load_step = [&](int ks) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      areg[i] = *reinterpret_cast<const u32x4*>(asrc[i] + ks * BK);
-      breg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bsrc[i] + ks * BK));
-    }
+  // Rows past M (N) read zeros through the descriptors' range checks; a step
+  // past the end reads through a 0-byte descriptor.
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(qx, static_cast<uint32_t>(static_cast<size_t>(M) * K));
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(weight, static_cast<uint32_t>(static_cast<size_t>(N) * K));
+  const __amdgpu_buffer_rsrc_t rnull = buffer_rsrc(weight, 0);
+
+  // Load i of wave w writes stage rows 64 i + 8 w .. + 7 (1 KB; lane l at byte
+  // 16 l: row 64 i + 8 w + l / 8, stored column l % 8 holding source column
+  // (l % 8) ^ key(row), key = (row >> 1) & 7, the same for every i).
+  const int lrow8 = 8 * wave + (lane >> 3);
+  const int lcol = (lane & 7) ^ ((lrow8 >> 1) & 7);
+  const int aoff_g = (m0 + lrow8) * K + lcol * 16;
+  const int boff_g = (n0 + lrow8) * K + lcol * 16;
+  const int lds_w = wave * 1024;
+  auto load_a = [&](uint8_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 64 * BK), 16, aoff_g, k0 + i * 64 * K, 0, 0);
   };
-  auto store_step = [&](int stage) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u32x4*>(&As[stage][dst[i]]) = areg[i];
-      *reinterpret_cast<u32x4*>(&Bs[stage][dst[i]]) = breg[i];
-    }
+  auto load_b = [&](uint8_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 64 * BK), 16, boff_g, k0 + i * 64 * K, 0, 0);
   };
 
-  typedef int i32x16 __attribute__((ext_vector_type(16)));
-  f32x16 facc[2][2];
-  i32x16 iacc[2][2];
+  Acc acc[FA][FB];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < FA; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < FB; ++b)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        facc[a][b][r] = 0.f;
-        iacc[a][b][r] = 0;
-      }
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
 
-  load_step(0);
-  store_step(0);
-  __syncthreads();
   const int lrow = lane & 31;
   const int lk = lane >> 5;
-  for (int ks = 0; ks < steps; ++ks) {
-    const int stage = ks & 1;
-    if (ks + 1 < steps) load_step(ks + 1);
-    const uint8_t* as = As[stage];
-    const uint8_t* bs = Bs[stage];
-    if constexpr (FP8) {
-      // 2 sub-steps of 64 inputs; a lane holds 32 bytes: columns 4kk + 2lk, +1.
+  // Operand byte offsets within a stage per (kk, column j of the lane): the
+  // fragments of one kk are 32 rows (4096 bytes) apart with the same key.
+  uint32_t aoff[KK][CPL], boff[KK][CPL];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        i32x8 af[2], bf[2];
+  for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-          const int row = wm * 64 + a * 32 + lrow;
-          const u32x4 lo = *reinterpret_cast<const u32x4*>(&as[swz8(row, 4 * kk + 2 * lk)]);
-          const u32x4 hi = *reinterpret_cast<const u32x4*>(&as[swz8(row, 4 * kk + 2 * lk + 1)]);
-          af[a] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const int row = wn * 64 + b * 32 + lrow;
-          const u32x4 lo = *reinterpret_cast<const u32x4*>(&bs[swz8(row, 4 * kk + 2 * lk)]);
-          const u32x4 hi = *reinterpret_cast<const u32x4*>(&bs[swz8(row, 4 * kk + 2 * lk + 1)]);
-          bf[b] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int b = 0; b < 2; ++b)
-            facc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                af[a], bf[b], facc[a][b], 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
-      }
-    } else {
-      // 4 sub-steps of 32 inputs; a lane holds 16 bytes: column 2kk + lk.
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        i32x4 af[2], bf[2];
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-          af[a] = *reinterpret_cast<const i32x4*>(&as[swz8(wm * 64 + a * 32 + lrow, 2 * kk + lk)]);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          bf[b] = *reinterpret_cast<const i32x4*>(&bs[swz8(wn * 64 + b * 32 + lrow, 2 * kk + lk)]);
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int b = 0; b < 2; ++b)
-            iacc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], iacc[a][b], 0, 0, 0);
-      }
+    for (int j = 0; j < CPL; ++j) {
+      const int c16 = kk * 2 * CPL + lk * CPL + j;
+      const uint32_t col = static_cast<uint32_t>((c16 ^ ((lrow >> 1) & 7)) << 4);
+      aoff[kk][j] = static_cast<uint32_t>((wm * FA * 32 + lrow) * BK) + col;
+      boff[kk][j] = static_cast<uint32_t>((wn * FB * 32 + lrow) * BK) + col;
     }
-    if (ks + 1 < steps) store_step(stage ^ 1);
-    __syncthreads();
-  }
+  auto rd = [&](const uint8_t* stage, uint32_t off, int frag) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(stage + off + frag * 4096);
+  };
+  auto set_op = [](Op& o, int j, u32x4 v) {
+    if constexpr (FP8) {
+      o[4 * j + 0] = (int)v.x;
+      o[4 * j + 1] = (int)v.y;
+      o[4 * j + 2] = (int)v.z;
+      o[4 * j + 3] = (int)v.w;
+    } else {
+      o = __builtin_bit_cast(i32x4, v);
+    }
+  };
+  auto mma = [](const Op& a, const Op& b, Acc c) -> Acc {
+    if constexpr (FP8)
+      return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+    else
+      return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  };
+  // Operand fragments: set 0 holds even kk, set 1 odd kk.
+  Op af[2][FA], bf[2][FB];
+  constexpr int READS = (FA + FB) * CPL;
+  // Read number r of a kk: fragment r / CPL (A first, then B), column r % CPL.
+  auto read_one = [&](int set, const uint8_t* as, const uint8_t* bs, int kk, int r) {
+    const int f = r / CPL, j = r % CPL;
+    if (f < FA) set_op(af[set][f], j, rd(as, aoff[kk][j], f));
+    else set_op(bf[set][f - FA], j, rd(bs, boff[kk][j], f - FA));
+  };
 
+  // One kk on operand set `cur`: NMF MFMA slots; the slots read the next kk's
+  // operands (set cur ^ 1) from (as, bs) at nkk, READS spread over the NMF
+  // slots, and issue vm(slot).
+  auto region = [&](int cur, const uint8_t* as, const uint8_t* bs, int nkk, auto&& vm) {
 #pragma unroll
-  for (int a = 0; a < 2; ++a) {
+    for (int s = 0; s < NMF; ++s) {
+      acc[s / FB][s % FB] = mma(af[cur][s / FB], bf[cur][s % FB], acc[s / FB][s % FB]);
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int n = n0 + wn * 64 + b * 32 + (lane & 31);
+      for (int r = s * READS / NMF; r < (s + 1) * READS / NMF; ++r) read_one(cur ^ 1, as, bs, nkk, r);
+      vm(s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Step ks on stage (ac, bc): the loads of step ks + S - 1 go into (al, bl)
+  // over the first kk (that stage was last read before the previous barrier).
+  // After kk = KK - 2, this wave's loads of step ks + 1 have landed (at most
+  // the (S - 2) * LPW loads issued after them remain) and its reads are done
+  // (lgkmcnt(0)); past the barrier every wave's are, and the last kk's MFMAs
+  // run while the next step's kk = 0 operands are read from (an, bn).
+  auto step = [&](int ks, const uint8_t* ac, const uint8_t* bc, const uint8_t* an, const uint8_t* bn, uint8_t* al,
+                  uint8_t* bl) {
+    const bool in = ks + S - 1 < steps;
+    const __amdgpu_buffer_rsrc_t qa = in ? ra : rnull, qb = in ? rb : rnull;
+    const int k0 = in ? (ks + S - 1) * BK : 0;
+    auto vm = [&](int kk, int s) {
+      if (kk != 0) return;
+      for (int i = 0; i < LPW; ++i)
+        if (s == (i * NMF) / LPW) {
+          if (i < 4) load_a(al, qa, k0, i);
+          else load_b(bl, qb, k0, i - 4);
+        }
+    };
+#pragma unroll
+    for (int kk = 0; kk + 1 < KK; ++kk)
+      region(kk & 1, ac, bc, kk + 1, [&](int s) { vm(kk, s); });
+    if constexpr (S == 2) __asm__ volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"((S - 2) * LPW) : "memory");
+    __builtin_amdgcn_s_barrier();
+    region((KK - 1) & 1, an, bn, 0, [&](int) {});
+  };
+
+  // Prologue: steps 0 .. S - 2 requested; step 0 waited for.
+#pragma unroll
+  for (int j = 0; j < S - 1; ++j) {
+    uint8_t* a = j == 0 ? A0 : A1;
+    uint8_t* b = j == 0 ? B0 : B1;
+    const bool in = j < steps;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_a(a, in ? ra : rnull, in ? j * BK : 0, i);
+#pragma unroll
+    for (int i = 0; i < BLOADS; ++i) load_b(b, in ? rb : rnull, in ? j * BK : 0, i);
+  }
+  if constexpr (S == 2) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 2) * LPW) : "memory");
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int r = 0; r < READS; ++r) read_one(0, A0, B0, 0, r);
+
+  // Step j on stage j % S.
+  int ks = 0;
+  if constexpr (S == 2) {
+    for (; ks + 2 <= steps; ks += 2) {
+      step(ks, A0, B0, A1, B1, A1, B1);
+      step(ks + 1, A1, B1, A0, B0, A0, B0);
+    }
+    if (ks < steps) step(ks, A0, B0, A1, B1, A1, B1);
+  } else {
+    for (; ks + 3 <= steps; ks += 3) {
+      step(ks, A0, B0, A1, B1, A2, B2);
+      step(ks + 1, A1, B1, A2, B2, A0, B0);
+      step(ks + 2, A2, B2, A0, B0, A1, B1);
+    }
+    if (ks < steps) step(ks, A0, B0, A1, B1, A2, B2);
+    if (ks + 1 < steps) step(ks + 1, A1, B1, A2, B2, A0, B0);
+  }
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Epilogue. MFMA 32x32 output: lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+#pragma unroll
+  for (int a = 0; a < FA; ++a) {
+#pragma unroll
+    for (int b = 0; b < FB; ++b) {
+      const int n = n0 + wn * FB * 32 + b * 32 + (lane & 31);
       if (n >= N) continue;
       const float ws = scale[n];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int m = m0 + wm * FA * 32 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m < M) {
-          const float acc = FP8 ? facc[a][b][r] : static_cast<float>(iacc[a][b][r]);
-          y[static_cast<size_t>(m) * N + n] = E::from_f32(acc * x_scale[m] * ws);
+          const float v = FP8 ? static_cast<float>(acc[a][b][r]) : static_cast<float>(acc[a][b][r]);
+          y[static_cast<size_t>(m) * N + n] = E::from_f32(v * x_scale[m] * ws);
         }
       }
     }
@@ -606,14 +708,29 @@ LNQ_API LnqStatus lnq_mm8(const uint8_t* qx, const uint8_t* weight, const float*
     return LNQ_OK;
   }
   const int M = (int)rows, N = (int)out_features, K = (int)in_features;
-  const int tiles = ((M + mm8::BM - 1) / mm8::BM) * ((N + mm8::BN - 1) / mm8::BN);
+  LNQ_REQUIRE(static_cast<size_t>(M) * K < (1ull << 31) && static_cast<size_t>(N) * K < (1ull << 31),
+              "lnq_mm8: operands exceed the 2 GiB buffer range");
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto* ys = static_cast<uint16_t*>(y);
-#define LNQ_MM8(DT, F)                                                                            \
-  hipLaunchKernelGGL((mm8_kernel<DT, F>), dim3(tiles), dim3(mm8::THREADS), 0, s, qx, weight,     \
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+  }
+  // 256-column tiles read half the bytes per FLOP of 128-column ones, but only
+  // pay while they still give every compute unit a tile.
+  const long tiles256 = static_cast<long>((M + mm8::BM - 1) / mm8::BM) * ((N + 255) / 256);
+  const bool wide = tiles256 >= cus;
+  const int bn = wide ? 256 : 128;
+  const int tiles = ((M + mm8::BM - 1) / mm8::BM) * ((N + bn - 1) / bn);
+#define LNQ_MM8(DT, F, BN)                                                                          \
+  hipLaunchKernelGGL((mm8_kernel<DT, F, BN>), dim3(tiles), dim3(mm8::THREADS), 0, s, qx, weight,   \
                      x_scale, scale, ys, M, N, K)
-  if (dtype == LNQ_BF16) { if (fp8) LNQ_MM8(LNQ_BF16, 1); else LNQ_MM8(LNQ_BF16, 0); }
-  else { if (fp8) LNQ_MM8(LNQ_F16, 1); else LNQ_MM8(LNQ_F16, 0); }
+#define LNQ_MM8_BN(DT, F) \
+  if (wide) LNQ_MM8(DT, F, 256); else LNQ_MM8(DT, F, 128)
+  if (dtype == LNQ_BF16) { if (fp8) { LNQ_MM8_BN(LNQ_BF16, 1); } else { LNQ_MM8_BN(LNQ_BF16, 0); } }
+  else { if (fp8) { LNQ_MM8_BN(LNQ_F16, 1); } else { LNQ_MM8_BN(LNQ_F16, 0); } }
+#undef LNQ_MM8_BN
 #undef LNQ_MM8
   return launched("mm8");
 }
