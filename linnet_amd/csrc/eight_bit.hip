@@ -65,14 +65,18 @@ __device__ inline void widen4(uint32_t w, uint32_t& d0, uint32_t& d1) {
 // feeds MFMA t (t = 0, 1) elements 8t..8t+7 of them. A group (of `group`
 // inputs, or the whole row when the scale is per row) closes with
 //   acc += s * (C - offset * Cx),  Cx = sum of x over the group (B = ones).
-template <int DT, int FP8, int MT>
+// ONE (one row of x, MT = 1): x is staged in LDS once (dynamic shared memory
+// of K 16-bit values) and the ring holds only weight bytes, 16 chunks deep.
+template <int DT, int FP8, int MT, bool ONE = false>
 __global__ __launch_bounds__(256) void w8_skinny_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ weight,
     const float* __restrict__ scale, uint16_t* __restrict__ y, int M, int N, int K, int G,
     int row_block, int scale_cols) {
   using E = Elem<DT>;
   constexpr float offset = FP8 ? 0.0f : 128.0f;
+  static_assert(!ONE || MT == 1, "the one-row form has one x tile");
   __shared__ f32x4 red[4][MT][64];
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -109,41 +113,76 @@ __global__ __launch_bounds__(256) void w8_skinny_kernel(
     Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  u32x4 wnext = {0u, 0u, 0u, 0u};
-  if (cb < ce)
-    wnext = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 64 * cb + 16 * j));
-  for (int c = cb; c < ce; ++c) {
-    const u32x4 w = wnext;
-    if (c + 1 < ce)
-      wnext = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 64 * (c + 1) + 16 * j));
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+  // A ring of D chunks in flight per wave: the weight bytes (streamed once,
+  // non-temporal) and the x values they meet, requested D chunks ahead so the
+  // wave keeps D loads of each in flight instead of waiting on every chunk.
+  constexpr int D = ONE ? 16 : MT == 1 ? 8 : MT == 2 ? 4 : 2;
+  u32x4 rw[D];
+  u32x4 rx[ONE ? 1 : D][MT][2];
+  auto fetch = [&](int slot, int c) {
+    rw[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 64 * c + 16 * j));
+    if constexpr (!ONE) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      uint32_t b0, b1, b2, b3;
-      widen4<DT, FP8>(words[2 * t], b0, b1);
-      widen4<DT, FP8>(words[2 * t + 1], b2, b3);
-      const u32x4 b = {b0, b1, b2, b3};
-      const int k = 64 * c + 16 * j + 8 * t;
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        u32x4 a = *reinterpret_cast<const u32x4*>(xrow[mt] + k);
-        if (!mok[mt]) a = u32x4{0u, 0u, 0u, 0u};
-        C[mt] = mfma16x16x32<DT>(a, b, C[mt]);
-        if constexpr (!FP8) Cx[mt] = mfma16x16x32<DT>(a, ones, Cx[mt]);
-      }
+        for (int t = 0; t < 2; ++t)
+          rx[slot][mt][t] = *reinterpret_cast<const u32x4*>(xrow[mt] + 64 * c + 16 * j + 8 * t);
     }
-    const bool closes = ((c + 1) % chunks_per_group == 0) || (c + 1 == ce);
-    if (closes) {
-      const float s = srow[c / chunks_per_group];
+  };
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+  for (int i = 0; i < D; ++i)
+    if (cb + i < ce) fetch(i, cb + i);
+  if constexpr (ONE) {
+    // Staged while the first D weight chunks are in flight.
+    for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
+      *reinterpret_cast<u32x4*>(&xl[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
+    __syncthreads();
+  }
+  for (int c0 = cb; c0 < ce; c0 += D) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float d = FP8 ? C[mt][r] : fmaf(-offset, Cx[mt][r], C[mt][r]);
-          acc[mt][r] = fmaf(s, d, acc[mt][r]);
+    for (int i = 0; i < D; ++i) {
+      const int c = c0 + i;
+      if (c >= ce) break;
+      const u32x4 w = rw[i];
+      u32x4 xa[MT][2];
+      if constexpr (ONE) {
+        // Every lane takes row 0: the 15 copies of it land in output rows
+        // past M, which are not stored.
+#pragma unroll
+        for (int t = 0; t < 2; ++t) xa[0][t] = *reinterpret_cast<const u32x4*>(&xl[64 * c + 16 * j + 8 * t]);
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) xa[mt][t] = mok[mt] ? rx[i][mt][t] : u32x4{0u, 0u, 0u, 0u};
+      }
+      if (c + D < ce) fetch(i, c + D);
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        uint32_t b0, b1, b2, b3;
+        widen4<DT, FP8>(words[2 * t], b0, b1);
+        widen4<DT, FP8>(words[2 * t + 1], b2, b3);
+        const u32x4 b = {b0, b1, b2, b3};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          C[mt] = mfma16x16x32<DT>(xa[mt][t], b, C[mt]);
+          if constexpr (!FP8) Cx[mt] = mfma16x16x32<DT>(xa[mt][t], ones, Cx[mt]);
         }
-        C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      const bool closes = ((c + 1) % chunks_per_group == 0) || (c + 1 == ce);
+      if (closes) {
+        const float s = srow[c / chunks_per_group];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float d = FP8 ? C[mt][r] : fmaf(-offset, Cx[mt][r], C[mt][r]);
+            acc[mt][r] = fmaf(s, d, acc[mt][r]);
+          }
+          C[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          Cx[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
   }
@@ -558,7 +597,10 @@ static void launch_w8_skinny(const void* x, const uint8_t* w, const float* s, vo
                              int N, int K, int G, int rb, int cols, hipStream_t stream) {
   const auto* xs = static_cast<const uint16_t*>(x);
   auto* ys = static_cast<uint16_t*>(y);
-  if (M <= 16)
+  if (M == 1 && K <= 32768)
+    hipLaunchKernelGGL((w8_skinny_kernel<DT, FP8, 1, true>), dim3((N + 15) / 16, 1), dim3(256), K * 2, stream,
+                       xs, w, s, ys, M, N, K, G, rb, cols);
+  else if (M <= 16)
     hipLaunchKernelGGL((w8_skinny_kernel<DT, FP8, 1>), dim3((N + 15) / 16, 1), dim3(256), 0, stream,
                        xs, w, s, ys, M, N, K, G, rb, cols);
   else if (M <= 32)
