@@ -11,10 +11,13 @@ events on the stream the kernels run on.
 
 Also reported (extra keys): M=4 and M=16 GEMV, the prefill dequant-GEMM
 (config 3: M=2048 over three (K, N)) in TFLOP/s against bf16 MFMA peak beside
-the reference's own prefill strategy (HIP dequantize + hipBLASLt), a measured
-copy-bandwidth ceiling, and the reference's CPU path timed on the host cores.
+the reference's own prefill strategy (HIP dequantize + hipBLASLt), the 8-bit
+paths (config 1: int8 per-row weight-only GEMV 4096x4096; config 4: FP8 weight
+with per-token FP8 activations, K=8192 N=28672 at M=1/256/4096, against HBM
+and fp8 MFMA peaks), a measured copy-bandwidth ceiling, and the reference's
+CPU path timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|8bit|all]
 """
 
 from __future__ import annotations
@@ -29,6 +32,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 MFMA, published
 L3_BYTES = 256 << 20  # Infinity Cache
 
 
@@ -43,7 +47,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=("gemv", "gemm", "all"), default="all")
+    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "all"), default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
@@ -163,6 +167,10 @@ def main() -> int:
         extra["gemm_M2048"] = gemm
     torch.cuda.synchronize()
 
+    if args.only in ("8bit", "all"):
+        extra.update(eight_bit(torch, dev, timed_graph, args.steps))
+    torch.cuda.synchronize()
+
     # --- CPU baseline: the reference's CPU path (generated source: the weight
     # dequantized once at prepare, then bf16 F.linear per call), on host cores.
     cpu = None
@@ -177,13 +185,19 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic_from_profiles("int4_gemv_M1"),
                     "kernel": "int4_gemv_kernel<bf16,7,group128>", "bytes_per_launch": gemv_bytes(1, k, n)}
-    else:
+    elif gemm:
         key = next(iter(gemm))
         entry = gemm[key]
         metric_value, unit, ms = entry["tflops"], "TFLOP/s", entry["us"] / 1e3
         config = {"workload": f"int4 g128 prefill dequant-GEMM M=2048 {key}", "baseline_config": 3}
         roofline = {"bound": "mfma", "achieved": entry["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": entry["frac_bf16_peak"], "traffic": None}
+    else:
+        entry = extra["fp8_C4_K8192_N28672"]["M4096"]
+        metric_value, unit, ms = entry["tflops"], "TFLOP/s", entry["us"] / 1e3
+        config = {"workload": "FP8 weight x per-token FP8 rows, M=4096 K=8192 N=28672", "baseline_config": 4}
+        roofline = {"bound": "mfma", "achieved": entry["tflops"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": entry["frac_fp8_peak"], "traffic": None}
     result = {
         "metric": "W4A16 decode GEMV GB/s (% HBM peak); prefill qGEMM TFLOP/s (% MFMA peak)",
         "value": round(float(metric_value), 2),
@@ -205,6 +219,56 @@ def main() -> int:
     }
     print(json.dumps(result))
     return 0
+
+
+def eight_bit(torch, dev, timed_graph, steps: int) -> dict[str, object]:
+    """Configs 1 and 4 through the `linnet.torch.quantized` operands/linear entry
+    points (`quantized.py:113-194`), weights rotated past the Infinity Cache.
+    Config 1: int8 per-row symmetric W [4096, 4096] ~ N(0, 0.02), one bf16 token
+    (weight-only GEMV). Config 4: FP8 E4M3 W [28672, 8192] ~ N(0, 0.02) with
+    the per-tensor scale max|W| / 448 broadcast per row, x ~ N(0, 1) bf16 with
+    dynamic per-token FP8 quantization (`rounded`): M = 1 streams the weight
+    (weight-only GEMV), M = 256 and 4096 run the per-token quantize + FP8 MFMA
+    product. Bytes are algorithmic (weight + scales + x + y)."""
+    from linnet_amd.torch import kernels, quantized
+
+    out: dict[str, object] = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+    k = n = 4096
+    w = torch.randn(n, k, generator=g, device=dev) * 0.02
+    q, s = kernels.quantize_int8(w, k, "f32")
+    del w
+    copies = -(-(L3_BYTES + (64 << 20)) // (n * k))
+    ops = [quantized.int8_operands(q.clone(), s.clone(), 0) for _ in range(copies)]
+    x = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
+    sec = timed_graph([lambda o=o: quantized.int8_linear(x, o, None) for o in ops], steps, 4)
+    nbytes = n * k + n * 4 + k * 2 + n * 2
+    out["int8_gemv_C1"] = {"us": round(sec * 1e6, 3), "gbps": round(nbytes / sec / 1e9, 1),
+                           "frac_hbm_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4)}
+    del ops, q, s
+
+    n, k = 28672, 8192
+    w = torch.randn(n, k, generator=g, device=dev) * 0.02
+    per_tensor = w.abs().max() / 448
+    wq = (w / per_tensor).to(torch.float8_e4m3fn)
+    del w
+    scale = per_tensor.reshape(1, 1).expand(n, 1).to(torch.bfloat16).contiguous()
+    ops = [quantized.fp8_operands(wq, scale, 1), quantized.fp8_operands(wq.clone(), scale.clone(), 1)]
+    fp8: dict[str, object] = {}
+    for m in (1, 256, 4096):
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        calls = max(4, steps // 5) if m < 4096 else 10
+        sec = timed_graph([lambda o=o, x=x: quantized.fp8_linear(x, o, None) for o in ops], calls, 2)
+        nbytes = n * k + n * 2 + m * k * 2 + m * n * 2
+        flops = 2 * m * n * k
+        fp8[f"M{m}"] = {"us": round(sec * 1e6, 2), "gbps": round(nbytes / sec / 1e9, 1),
+                        "frac_hbm_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
+                        "tflops": round(flops / sec / 1e12, 1),
+                        "frac_fp8_peak": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4)}
+        del x
+    out["fp8_C4_K8192_N28672"] = fp8
+    del ops, wq
+    return out
 
 
 def traffic_from_profiles(name: str) -> float | None:
