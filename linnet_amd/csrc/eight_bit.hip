@@ -289,6 +289,75 @@ __global__ __launch_bounds__(256) void rows8_kernel(const typename Elem<DT>::sto
   if (threadIdx.x == 0) x_scale[row] = s;
 }
 
+// The same per row with 16-byte loads and VEC-byte stores (K % VEC == 0 and
+// 16-byte aligned rows): a pass for max|x|, then a pass that quantizes from a
+// second read of the row (an L2 hit). Same arithmetic as rows8_kernel.
+template <int DT, int FP8>
+__global__ __launch_bounds__(256) void rows8_vec_kernel(const typename Elem<DT>::storage* __restrict__ x,
+                                                        uint8_t* __restrict__ q, float* __restrict__ x_scale, int K) {
+  using E = Elem<DT>;
+  constexpr int VEC = 16 / static_cast<int>(sizeof(typename E::storage));  // elements per 16 bytes
+  __shared__ float partial[4];
+  const int64_t row = blockIdx.x;
+  const typename E::storage* src = x + row * K;
+  // (f32 rows load as a float vector: this toolchain folds __builtin_bit_cast
+  // of an ext_vector element to element 0.)
+  auto load = [&](int i, float (&v)[VEC]) {
+    if constexpr (VEC == 8) {
+      const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + i));
+      const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = E::to_f32(static_cast<uint16_t>(d[j] & 0xffffu));
+        v[2 * j + 1] = E::to_f32(static_cast<uint16_t>(d[j] >> 16));
+      }
+    } else {
+      const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + i));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = w[j];
+    }
+  };
+  float top = 0.0f;
+  for (int i = VEC * threadIdx.x; i < K; i += VEC * 256) {
+    float v[VEC];
+    load(i, v);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) top = fmaxf(top, fabsf(v[j]));
+  }
+  top = wave_max(top);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = top;
+  __syncthreads();
+  top = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
+  const float largest = FP8 ? 448.0f : 127.0f;
+  const float s = fmaxf(top, 1e-12f) / largest;
+  uint8_t* dst = q + row * K;
+  for (int i = VEC * threadIdx.x; i < K; i += VEC * 256) {
+    float v[VEC];
+    load(i, v);
+    uint32_t b[VEC / 4];
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) b[j] = 0;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float t = v[j] / s;
+      uint32_t code;
+      if constexpr (FP8) {
+        code = f32_to_e4m3(fminf(fmaxf(t, -448.0f), 448.0f));
+      } else {
+        const float h = t >= 0.0f ? __fadd_rn(t, 0.5f) : __fsub_rn(t, 0.5f);
+        code = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(fminf(fmaxf(truncf(h), -127.0f), 127.0f))));
+      }
+      b[j / 4] |= code << (8 * (j % 4));
+    }
+    if constexpr (VEC == 8) {
+      *reinterpret_cast<u32x2*>(dst + i) = u32x2{b[0], b[1]};
+    } else {
+      *reinterpret_cast<uint32_t*>(dst + i) = b[0];
+    }
+  }
+  if (threadIdx.x == 0) x_scale[row] = s;
+}
+
 // ======================================================================= mm8
 // 8-bit x 8-bit products on gfx950 MFMA: FP8 E4M3 rows times FP8 weights
 // (v_mfma_scale_f32_32x32x64_f8f6f4 with unit E8M0 scales, f32 sums) or int8
@@ -724,12 +793,18 @@ LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t r
   const dim3 grid(static_cast<unsigned>(rows));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int K = (int)in_features;
+  const int esize = dtype == LNQ_F32 ? 4 : 2;
+  const bool vec = (K % (16 / esize)) == 0 && aligned(x, 16) && aligned(q, 8) && (static_cast<size_t>(K) * esize) % 16 == 0;
 #define LNQ_R8(DT, F)                                                                              \
-  hipLaunchKernelGGL((rows8_kernel<DT, F>), grid, dim3(256), 0, s,                                \
-                     static_cast<const typename Elem<DT>::storage*>(x), q, x_scale, K)
-  if (dtype == LNQ_BF16) { if (fp8) LNQ_R8(LNQ_BF16, 1); else LNQ_R8(LNQ_BF16, 0); }
-  else if (dtype == LNQ_F16) { if (fp8) LNQ_R8(LNQ_F16, 1); else LNQ_R8(LNQ_F16, 0); }
-  else { if (fp8) LNQ_R8(LNQ_F32, 1); else LNQ_R8(LNQ_F32, 0); }
+  if (vec)                                                                                         \
+    hipLaunchKernelGGL((rows8_vec_kernel<DT, F>), grid, dim3(256), 0, s,                          \
+                       static_cast<const typename Elem<DT>::storage*>(x), q, x_scale, K);          \
+  else                                                                                             \
+    hipLaunchKernelGGL((rows8_kernel<DT, F>), grid, dim3(256), 0, s,                              \
+                       static_cast<const typename Elem<DT>::storage*>(x), q, x_scale, K)
+  if (dtype == LNQ_BF16) { if (fp8) { LNQ_R8(LNQ_BF16, 1); } else { LNQ_R8(LNQ_BF16, 0); } }
+  else if (dtype == LNQ_F16) { if (fp8) { LNQ_R8(LNQ_F16, 1); } else { LNQ_R8(LNQ_F16, 0); } }
+  else { if (fp8) { LNQ_R8(LNQ_F32, 1); } else { LNQ_R8(LNQ_F32, 0); } }
 #undef LNQ_R8
   return launched("rows8");
 }
