@@ -538,7 +538,7 @@ __global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
   auto region = [&](int cur, const uint8_t* as, const uint8_t* bs, int nkk, auto&& vm) {
 #pragma unroll
     for (int s = 0; s < NMF; ++s) {
-      acc[s / FB][s % FB] = mma(af[cur][s / FB], bf[cur][s % FB], acc[s / FB][s % FB]);
+      acc[s / FB][s % FB] = mma(bf[cur][s % FB], af[cur][s / FB], acc[s / FB][s % FB]);
 #pragma unroll
       for (int r = s * READS / NMF; r < (s + 1) * READS / NMF; ++r) read_one(cur ^ 1, as, bs, nkk, r);
       vm(s);
@@ -610,20 +610,36 @@ __global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
   }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Epilogue. MFMA 32x32 output: lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+  // Epilogue. The MFMAs compute the transposed tile (the weight as the A
+  // operand): lane l, register r holds row m = l % 32 and output feature
+  // 8 (r / 4) + 4 (l / 32) + r % 4 of its 32x32 tile; registers 4q..4q+3 are
+  // four consecutive features of one row of y, stored as 8 bytes when N % 4 == 0.
+  const bool vec_out = (N & 3) == 0;
 #pragma unroll
   for (int a = 0; a < FA; ++a) {
+    const int m = m0 + wm * FA * 32 + a * 32 + (lane & 31);
+    if (m >= M) continue;
+    const float xs = x_scale[m];
+    uint16_t* yrow = y + static_cast<size_t>(m) * N;
 #pragma unroll
     for (int b = 0; b < FB; ++b) {
-      const int n = n0 + wn * FB * 32 + b * 32 + (lane & 31);
-      if (n >= N) continue;
-      const float ws = scale[n];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * FA * 32 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < M) {
-          const float v = FP8 ? static_cast<float>(acc[a][b][r]) : static_cast<float>(acc[a][b][r]);
-          y[static_cast<size_t>(m) * N + n] = E::from_f32(v * x_scale[m] * ws);
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int n = n0 + wn * FB * 32 + b * 32 + 8 * q4 + 4 * (lane >> 5);
+        uint16_t out[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float ws = n + i < N ? scale[n + i] : 0.f;
+          out[i] = E::from_f32(static_cast<float>(acc[a][b][4 * q4 + i]) * xs * ws);
+        }
+        if (vec_out && n + 3 < N) {
+          *reinterpret_cast<u32x2*>(yrow + n) =
+              u32x2{static_cast<uint32_t>(out[0]) | (static_cast<uint32_t>(out[1]) << 16),
+                    static_cast<uint32_t>(out[2]) | (static_cast<uint32_t>(out[3]) << 16)};
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < N) yrow[n + i] = out[i];
         }
       }
     }

@@ -273,7 +273,7 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
                     const uint16_t* rws, int nkk, const WRegs& deq, uint16_t* wd, int pos0, auto&& vm) {
 #pragma unroll
     for (int s = 0; s < NMF; ++s) {
-      acc[s / FB][s % FB] = mfma32x32x16<DT>(ca[s / FB], cb[s % FB], acc[s / FB][s % FB]);
+      acc[s / FB][s % FB] = mfma32x32x16<DT>(cb[s % FB], ca[s / FB], acc[s / FB][s % FB]);
       if (s < FA) na[s] = rd(rxs, aoff[nkk], s);
       else if (s < FA + FB) nb[s - FA] = rd(rws, boff[nkk], s - FA);
       deq_slot(deq, pos0 + s, wd);
@@ -358,22 +358,35 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   // Loads of the steps past the end (zeros through rnull) may be in flight.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Epilogue. MFMA 32x32 output: lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4,
-  // column l % 32.
+  // Epilogue. The MFMAs compute the transposed tile (W as the A operand): lane
+  // l, register r holds token m = l % 32 and output feature 8 (r / 4) + 4 (l /
+  // 32) + r % 4 of its 32x32 tile, so registers 4q..4q+3 are four consecutive
+  // features of one row of y: one 8-byte store (N % 4 == 0), else four.
+  const bool vec_out = (N & 3) == 0;
 #pragma unroll
   for (int a = 0; a < FA; ++a) {
+    const int m = m0 + wm * FA * 32 + a * 32 + (lane & 31);
+    if (m >= M) continue;
+    uint16_t* yrow = y + static_cast<size_t>(m) * N;
 #pragma unroll
     for (int b = 0; b < FB; ++b) {
-      const int n = n0 + wn * FB * 32 + b * 32 + (lane & 31);
-      if (n >= N) continue;
-      const float bv = bias != nullptr ? E::to_f32(bias[n]) : 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * FA * 32 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < M) {
-          uint16_t out = E::from_f32(acc[a][b][r]);
-          if (bias != nullptr) out = E::from_f32(E::to_f32(out) + bv);
-          y[static_cast<size_t>(m) * N + n] = out;
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int n = n0 + wn * FB * 32 + b * 32 + 8 * q4 + 4 * (lane >> 5);
+        uint16_t out[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          out[i] = E::from_f32(acc[a][b][4 * q4 + i]);
+          if (bias != nullptr && n + i < N) out[i] = E::from_f32(E::to_f32(out[i]) + E::to_f32(bias[n + i]));
+        }
+        if (vec_out && n + 3 < N) {
+          *reinterpret_cast<u32x2*>(yrow + n) =
+              u32x2{static_cast<uint32_t>(out[0]) | (static_cast<uint32_t>(out[1]) << 16),
+                    static_cast<uint32_t>(out[2]) | (static_cast<uint32_t>(out[3]) << 16)};
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < N) yrow[n + i] = out[i];
         }
       }
     }
