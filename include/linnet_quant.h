@@ -44,7 +44,7 @@ typedef int32_t LnqStatus;
 #define LNQ_KERNEL_AUTO 0
 #define LNQ_KERNEL_SKINNY 1 /* dequant-GEMV/skinny GEMM on MFMA, rows <= 64 */
 #define LNQ_KERNEL_TILED 2  /* prefill dequant-GEMM, LDS-staged bf16 tiles on MFMA */
-#define LNQ_KERNEL_GEMV 3   /* one-token dequant-GEMV, one workgroup per CU (rows == 1;
+#define LNQ_KERNEL_GEMV 3   /* few-token dequant-GEMV, one workgroup per CU (rows 1..16;
                                in % 256 == 0 and <= 4096, group 128 or a multiple of 256,
                                out <= 16384) */
 

@@ -39,10 +39,11 @@ FLAGS = [
 ]
 
 
-# Per-source extra flags. The skinny kernels feed every MFMA result straight to
-# VALU epilogue math, so their accumulators belong in VGPRs (no accvgpr moves);
-# int4_gemv.hip's kernel asks for AGPR accumulators itself (LNQ_MFMA_IN_AGPRS).
-EXTRA = {"int4.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source extra flags. The skinny and GEMV kernels feed every MFMA result
+# straight to VALU math, so their accumulators belong in VGPRs (no accvgpr
+# moves). A kernel without AGPRs also gets the whole register budget as VGPRs;
+# one with AGPRs has it split in half, and the GEMV kernels then spill.
+EXTRA = {name: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for name in ("int4.hip", "int4_gemv.hip")}
 
 
 def hipcc() -> str:

@@ -167,14 +167,17 @@ __device__ inline u32x4 nibbles_to_magic(uint32_t w) {
 // 8 packed 4-bit codes as MAGIC + q, pair order: dword s holds elements s (low)
 // and s + 4 (high) -- one v_and_or per dword after a shift. The A operand must
 // then hold x in the order 0,4,1,5,2,6,3,7 of each 8 (see permute_x8).
-// (a & b) | c in one v_and_or_b32. The operands are VGPRs: a VOP3 instruction
-// on gfx950 takes no literal constants and at most one SGPR, so the compiler
-// would otherwise split it into v_and + v_or with literals.
-__device__ inline uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
-  uint32_t d;
-  __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
+// (a & b) | c, selected as one v_and_or_b32 when the caller has hidden the
+// constants b and c behind hide_in_vgpr (a gfx950 VOP3 instruction takes no
+// literal constant, so the compiler would otherwise split it into v_and + v_or
+// with literals). Plain code, not an asm statement: the hazard recognizer does
+// not count an asm statement as a VALU write, so an MFMA that reads its result
+// right after it gets no wait states and can read the register's old value.
+__device__ inline uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) { return (a & b) | c; }
+
+// Makes v an opaque VGPR value (no instruction): the compiler then cannot fold
+// it into a literal operand.
+__device__ inline void hide_in_vgpr(uint32_t& v) { __asm__ volatile("" : "+v"(v)); }
 
 // `mask` and `magic` are 0x000f000f and Elem<DT>::MAGIC2, held in VGPRs by the caller.
 template <int DT>

@@ -583,7 +583,7 @@ bool int4_tiled_supports(int M, int N, int K, int G, int dtype);
 bool int4_gemv_supports(int N, int K, int G, const void* x, const void* packed, const void* scale,
                         const void* zero);
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int N, int K, int G, int dtype, hipStream_t stream);
+                           const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream);
 
 }  // namespace lnq
 
@@ -619,12 +619,14 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
   const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
   const int K = static_cast<int>(in_features), G = static_cast<int>(group);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool gemv_ok = M == 1 && int4_gemv_supports(N, K, G, x, packed, scale, zero);
+  // The one-workgroup-per-CU GEMV takes 1..16 rows (1: one x row broadcast; 2..16:
+  // x row m in MFMA A row m).
+  const bool gemv_ok = M >= 1 && M <= 16 && int4_gemv_supports(N, K, G, x, packed, scale, zero);
   if (kernel == LNQ_KERNEL_GEMV) {
     LNQ_REQUIRE(gemv_ok, "lnq_int4_linear: the one-token kernel does not take rows=%d N=%d K=%d group=%d", M, N, K, G);
   }
   if (kernel == LNQ_KERNEL_GEMV || (kernel == LNQ_KERNEL_AUTO && gemv_ok))
-    return launch_int4_gemv(x, packed, scale, zero, bias, y, N, K, G, dtype, s);
+    return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
   bool tiled = kernel == LNQ_KERNEL_TILED;
   if (kernel == LNQ_KERNEL_AUTO) tiled = M > 64 && int4_tiled_supports(M, N, K, G, dtype);
   if (tiled) {

@@ -37,7 +37,28 @@ namespace lnq {
 namespace gemv {
 constexpr int MAX_WAVES = 16;  // K <= 4096
 constexpr int MAX_U8 = 8;      // R <= 64 rows per workgroup
+
+// Weight tile T (loads 2T and 2T + 1, 1 KB each per wave) has an LDS array of
+// its own. The compiler tracks buffer_load ... lds writes per LDS variable, so a
+// tile's reads wait for that tile's two loads only; with one array for all
+// loads it waits for every load before the first tile. Per-wave bytes of tile
+// T, and the array's bytes (a 16-byte placeholder past the last tile):
+constexpr int tile_wave_bytes(int u8, int t) { return 2 * t + 1 < u8 ? 2048 : 1024; }
+constexpr int tile_bytes(int u8, int t) { return 2 * t < u8 ? tile_wave_bytes(u8, t) * MAX_WAVES : 16; }
 }  // namespace gemv
+
+// The tile arrays of a kernel with U8 loads, and tile_lds(T, wave): wave's part
+// of tile T (T a constant after unrolling).
+#define LNQ_GEMV_TILE_ARRAYS(U8)                                                             \
+  __shared__ __attribute__((aligned(16))) uint8_t L0[gemv::tile_bytes(U8, 0)];              \
+  __shared__ __attribute__((aligned(16))) uint8_t L1[gemv::tile_bytes(U8, 1)];              \
+  __shared__ __attribute__((aligned(16))) uint8_t L2[gemv::tile_bytes(U8, 2)];              \
+  __shared__ __attribute__((aligned(16))) uint8_t L3[gemv::tile_bytes(U8, 3)];              \
+  static_assert(U8 <= 8, "four tile arrays");                                                \
+  auto tile_lds = [&](int T, int w) -> uint8_t* {                                            \
+    uint8_t* base = T == 0 ? L0 : T == 1 ? L1 : T == 2 ? L2 : L3;                            \
+    return base + w * gemv::tile_wave_bytes(U8, T);                                          \
+  }
 
 // The widened B operands of two packed dwords (16 codes): (MAGIC | q) pairs in
 // pair order (dword s holds elements s and s + 4 of its 8). The three shifts of
@@ -62,13 +83,12 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G) {
   using E = Elem<DT>;
-  LNQ_MFMA_IN_AGPRS();
   constexpr int R = 8 * U8;
   constexpr int NF = U8 / 2;            // full 16-row tiles
   constexpr bool HALF = (U8 & 1) != 0;  // a last tile of 8 rows
-  __shared__ __attribute__((aligned(16))) uint8_t Wsm[gemv::MAX_WAVES][U8 * 1024];
+  LNQ_GEMV_TILE_ARRAYS(U8);
   __shared__ __attribute__((aligned(16))) uint16_t Xsm[gemv::MAX_WAVES][256];
-  __shared__ float Rsm[R][gemv::MAX_WAVES];
+  __shared__ float Rsm[gemv::MAX_WAVES][R];  // wave-major: consecutive lanes, consecutive dwords
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -78,7 +98,6 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   const int k0 = wave * 256;
   const int rowb = K >> 1;
   const int groups = K / G;
-  uint8_t* Wl = Wsm[wave];
   uint16_t* Xw = Xsm[wave];
   // Buffer descriptors: rows past N read zeros through the range check.
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * rowb));
@@ -98,8 +117,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     for (int u = 0; u < U8; ++u) {
       const int sigma = 2 * a + ((b >> 3) ^ (u & 1));
       const int row = n0 + 8 * u + (b & 7);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(Wl + 1024 * u), 16, row * rowb + (k0 >> 1) + 16 * sigma,
-                                               0, 0, 2 /* non-temporal */);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(tile_lds(u >> 1, wave) + 1024 * (u & 1)), 16,
+                                               row * rowb + (k0 >> 1) + 16 * sigma, 0, 0, 2 /* non-temporal */);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -143,7 +162,9 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   for (int t = 0; t < 4; ++t) ac[t] = *reinterpret_cast<const u32x4*>(Xw + (col == 1 ? 128 : 0) + 32 * j + 8 * t);
   __builtin_amdgcn_sched_barrier(0);
 
-  const uint32_t nib_mask = 0x000f000fu, nib_magic = E::MAGIC2;
+  uint32_t nib_mask = 0x000f000fu, nib_magic = E::MAGIC2;
+  hide_in_vgpr(nib_mask);
+  hide_in_vgpr(nib_magic);
   const int r7 = col & 7;
   // One MFMA chain over a lane's 16 bytes of weights; returns output register
   // `reg`. The operand registers are kept allocated until the result has been
@@ -176,8 +197,9 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const int u = 2 * T + h;
     const int p0 = 16 * (j >> 1) + 8 * ((j & 1) ^ h) + r7;        // piece j      (half 0)
     const int p1 = 16 * (2 + (j >> 1)) + 8 * ((j & 1) ^ h) + r7;  // piece 4 + j  (half 1)
-    const u32x4 w0 = *reinterpret_cast<const u32x4*>(Wl + 1024 * u + 16 * p0);
-    const u32x4 w1 = *reinterpret_cast<const u32x4*>(Wl + 1024 * u + 16 * p1);
+    const uint8_t* Wt = tile_lds(T, wave) + 1024 * h;  // load u
+    const u32x4 w0 = *reinterpret_cast<const u32x4*>(Wt + 16 * p0);
+    const u32x4 w1 = *reinterpret_cast<const u32x4*>(Wt + 16 * p1);
     cf[T][0] = chain(xa[0], w0, 0);
     cf[T][1] = chain(xa[1], w1, 0);
   }
@@ -189,7 +211,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const int H = col >> 3;
     const int sigma = 4 * H + j;
     const int pp = 16 * (sigma >> 1) + 8 * (sigma & 1) + r7;
-    const u32x4 w = *reinterpret_cast<const u32x4*>(Wl + 1024 * u + 16 * pp);
+    static_assert((u & 1) == 0, "the last load of an odd U8 is the first of its tile");
+    const u32x4 w = *reinterpret_cast<const u32x4*>(tile_lds(NF, wave) + 16 * pp);
     cf[NF][0] = chain(ac, w, H);
   }
   // ---- scales / zeros, the fold, the cross-wave sum.
@@ -215,7 +238,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     float s0, s1, z0, z1;
     sz_of(8 * (2 * T + (col >> 3)) + r7, s0, s1, z0, z1);
     const float acc = fmaf(s0, fmaf(-z0, xs0, cf[T][0]), s1 * fmaf(-z1, xs1, cf[T][1]));
-    if (lane < 16) Rsm[16 * T + lane][wave] = acc;
+    if (lane < 16) Rsm[wave][16 * T + lane] = acc;
   }
   if constexpr (HALF) {
     const int H = col >> 3;
@@ -223,7 +246,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     sz_of(8 * (U8 - 1) + r7, s0, s1, z0, z1);
     const float part = H == 0 ? s0 * fmaf(-z0, xs0, cf[NF][0]) : s1 * fmaf(-z1, xs1, cf[NF][0]);
     const float acc = part + __shfl_xor(part, 8, 64);
-    if (lane < 8) Rsm[16 * NF + lane][wave] = acc;
+    if (lane < 8) Rsm[wave][16 * NF + lane] = acc;
   }
   __syncthreads();
   if (threadIdx.x < R) {
@@ -231,11 +254,206 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < gemv::MAX_WAVES; ++w)
-      if (w < nw) v += Rsm[threadIdx.x][w];
+      if (w < nw) v += Rsm[w][threadIdx.x];
     if (n < N) {
       uint16_t out = E::from_f32(v);
       if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
       y[n] = out;
+    }
+  }
+}
+
+// A few tokens (2..MX rows, MX = 4 or 16): the one-token kernel's workgroup
+// shape and weight streams, with A-operand row m of every MFMA holding x row m
+// (lane col = m). Each lane loads its own 128 bytes of x (its row, its 32-input
+// slices of both halves) straight into registers, in pair order; the whole x
+// is read once per CU. The output registers of a tile then hold rows
+// 4 (lane / 16) + i; the fold takes each row's sum of x from the lane that
+// loaded it, and after a barrier the 16 waves' partial sums are added through
+// LDS (the weight buffers, no longer read).
+template <int DT, int U8, bool G128, int MX>
+__global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G) {
+  using E = Elem<DT>;
+  constexpr int R = 8 * U8;
+  constexpr int NT = (U8 + 1) / 2;  // 16-row tiles (an odd U8: the last one has 8 rows)
+  LNQ_GEMV_TILE_ARRAYS(U8);
+  // After the barrier, tile T's array holds the waves' partial sums of its 16
+  // output rows in output-register order, red[wave][i][lane] (x row 4 (lane / 16)
+  // + i, output row 16 T + lane % 16): each store and each read of the final sum
+  // touches consecutive dwords (a stride of 16 dwords would put 16 lanes on one
+  // bank).
+  static_assert(gemv::MAX_WAVES * 256 * 4 <= gemv::tile_bytes(U8, NT - 1), "partial sums fit a tile array");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int col = lane & 15, j = lane >> 4;
+  const int n0 = blockIdx.x * R;
+  const int k0 = wave * 256;
+  const int rowb = K >> 1;
+  const int groups = K / G;
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * rowb));
+  // Rows of x past M read zeros through the range check.
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint32_t>(static_cast<size_t>(M) * K * 2));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
+
+  // ---- loads: scales and zeros (first: they are few, and the compiler may copy
+  // them out of their registers early), x (row col, inputs k0 + 128 H + 32 j +
+  // 8 t), weights.
+  const int srow = n0 + (lane < R ? lane : R - 1);
+  const int g0 = k0 / G;
+  uint32_t sv;
+  uint16_t zv16;
+  if constexpr (G128) {
+    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);
+    zv16 = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);
+  } else {
+    sv = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
+    zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Lane row col: rows M .. 15 read zeros through the range check.
+  u32x4 xr[2][4];
+#pragma unroll
+  for (int H = 0; H < 2; ++H)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      xr[H][t] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (col * K + k0 + 128 * H + 32 * j + 8 * t) * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    const int a = lane >> 4, b = lane & 15;
+#pragma unroll
+    for (int u = 0; u < U8; ++u) {
+      const int sigma = 2 * a + ((b >> 3) ^ (u & 1));
+      const int row = n0 + 8 * u + (b & 7);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(tile_lds(u >> 1, wave) + 1024 * (u & 1)), 16,
+                                               row * rowb + (k0 >> 1) + 16 * sigma, 0, 0, 2 /* non-temporal */);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- x: wait for it (and the scales) alone; pair order; the sums of x row col
+  // over both halves.
+  wait_vm<U8>();
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 xa[2][4];
+  float xsum[2];
+#pragma unroll
+  for (int H = 0; H < 2; ++H) {
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4 v = xr[H][t];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t d = v[e];
+        sum += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
+      }
+      xa[H][t] = permute_x8(v);
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    xsum[H] = sum;  // sum of x row col over half H of this wave's inputs
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t nib_mask = 0x000f000fu, nib_magic = E::MAGIC2;
+  hide_in_vgpr(nib_mask);
+  hide_in_vgpr(nib_magic);
+  const int r7 = col & 7;
+  // One MFMA chain over a lane's 16 bytes of weights; the operand registers stay
+  // allocated until the result has been read.
+  auto chain = [&](const u32x4 (&a)[4], const u32x4 w) -> f32x4 {
+    u32x4 b0, b1, b2, b3;
+    widen_pair<DT>(w.x, w.y, nib_mask, nib_magic, b0, b1);
+    widen_pair<DT>(w.z, w.w, nib_mask, nib_magic, b2, b3);
+    f32x4 C = f32x4{0.f, 0.f, 0.f, 0.f};
+    C = mfma16x16x32<DT>(a[0], b0, C);
+    C = mfma16x16x32<DT>(a[1], b1, C);
+    C = mfma16x16x32<DT>(a[2], b2, C);
+    C = mfma16x16x32<DT>(a[3], b3, C);
+    __asm__ volatile("" : "+v"(C) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
+    return C;
+  };
+  // ---- tiles as their loads land; tile T covers rows 16 T .. 16 T + 15 (the
+  // last of an odd U8 only its first 8, the other 8 columns read again and dropped).
+  f32x4 cf[NT][2];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (2 * T + 1 < U8) wait_vm_rt(U8 - 1 - (2 * T + 1));
+    else wait_vm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    const int h = col >> 3;
+    const int u = min(2 * T + h, U8 - 1);
+    const int hh = u & 1;  // the piece order of load u (and its half of the tile array)
+    const int p0 = 16 * (j >> 1) + 8 * ((j & 1) ^ hh) + r7;
+    const int p1 = 16 * (2 + (j >> 1)) + 8 * ((j & 1) ^ hh) + r7;
+    const uint8_t* Wt = tile_lds(T, wave) + 1024 * hh;
+    const u32x4 w0 = *reinterpret_cast<const u32x4*>(Wt + 16 * p0);
+    const u32x4 w1 = *reinterpret_cast<const u32x4*>(Wt + 16 * p1);
+    cf[T][0] = chain(xa[0], w0);
+    cf[T][1] = chain(xa[1], w1);
+  }
+  // ---- scales / zeros (landed before x), the fold.
+  __builtin_amdgcn_sched_barrier(0);
+  __asm__ volatile("" : "+v"(sv), "+v"(zv16));
+  uint32_t zv = zv16;
+  if constexpr (!G128) {
+    sv = (sv & 0xffffu) | (sv << 16);
+    zv = (zv & 0xffu) | (zv << 8);
+  }
+  // Sums of x rows 4 j + i (i = 0..3), the rows this lane's output registers hold.
+  float xs[2][4];
+#pragma unroll
+  for (int H = 0; H < 2; ++H)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[H][i] = __shfl(xsum[H], 4 * j + i, 64);
+  float acc[NT][4];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const int n = 16 * T + col;  // output row within the workgroup (lane's column)
+    const int src = n < R ? n : R - 1;
+    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(sv)));
+    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(zv)));
+    const float s0 = E::to_f32(static_cast<uint16_t>(sp & 0xffffu)), s1 = E::to_f32(static_cast<uint16_t>(sp >> 16));
+    const float z0 = E::MAGIC_VALUE + static_cast<float>(zp & 0xffu);
+    const float z1 = E::MAGIC_VALUE + static_cast<float>((zp >> 8) & 0xffu);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc[T][i] = fmaf(s0, fmaf(-z0, xs[0][i], cf[T][0][i]), s1 * fmaf(-z1, xs[1][i], cf[T][1][i]));
+  }
+  // ---- the cross-wave sum through the (now unread) tile arrays.
+  __syncthreads();
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    float* red = reinterpret_cast<float*>(tile_lds(T, 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * j + i;
+      if (m < MX) red[wave * 256 + i * 64 + lane] = acc[T][i];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const float* red = reinterpret_cast<const float*>(tile_lds(T, 0));
+    for (int o = threadIdx.x; o < M * 16; o += blockDim.x) {
+      const int m = o >> 4, c = o & 15;
+      const int n = n0 + 16 * T + c;
+      if (16 * T + c >= R || n >= N) continue;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < gemv::MAX_WAVES; ++w)
+        if (w < nw) v += red[w * 256 + (m & 3) * 64 + (m >> 2) * 16 + c];
+      uint16_t out = E::from_f32(v);
+      if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
+      y[static_cast<size_t>(m) * N + n] = out;
     }
   }
 }
@@ -282,10 +500,49 @@ static void launch_gemv_dt(const void* x, const uint8_t* packed, const void* sca
   }
 }
 
+template <int DT, int U8, int MX>
+static void launch_rows_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                           const void* bias, void* y, int M, int N, int K, int G, hipStream_t stream) {
+  const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / 256));
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* ys = static_cast<uint16_t*>(y);
+  if (G == 128)
+    hipLaunchKernelGGL((int4_gemv_rows_kernel<DT, U8, true, MX>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
+                       M, N, K, G);
+  else
+    hipLaunchKernelGGL((int4_gemv_rows_kernel<DT, U8, false, MX>), grid, block, 0, stream, xs, packed, ss, zero, bs,
+                       ys, M, N, K, G);
+}
+
+template <int DT, int MX>
+static void launch_rows_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                           const void* bias, void* y, int M, int N, int K, int G, hipStream_t stream) {
+  switch ((N + 2047) / 2048) {
+    case 1: launch_rows_u8<DT, 1, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 2: launch_rows_u8<DT, 2, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 3: launch_rows_u8<DT, 3, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 4: launch_rows_u8<DT, 4, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 5: launch_rows_u8<DT, 5, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 6: launch_rows_u8<DT, 6, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 7: launch_rows_u8<DT, 7, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    default: launch_rows_u8<DT, 8, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+  }
+}
+
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int N, int K, int G, int dtype, hipStream_t stream) {
-  if (dtype == LNQ_BF16) launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, stream);
-  else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+                           const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream) {
+  if (M == 1) {
+    if (dtype == LNQ_BF16) launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+    else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+  } else if (M <= 4) {
+    if (dtype == LNQ_BF16) launch_rows_dt<LNQ_BF16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+    else launch_rows_dt<LNQ_F16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+  } else {
+    if (dtype == LNQ_BF16) launch_rows_dt<LNQ_BF16, 16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+    else launch_rows_dt<LNQ_F16, 16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+  }
   return launched("int4_gemv");
 }
 

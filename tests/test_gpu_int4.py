@@ -245,9 +245,36 @@ def test_one_token_gemv_is_chosen_for_one_row_and_refuses_other_shapes() -> None
     # group 32 at one row: auto falls back to the skinny kernel
     _check_linear(x.cpu(), packed, scale, zero, kernels.int4_linear(x, packed.to(DEV), scale.to(DEV), zero.to(DEV)))
     packed, scale, zero = _layer(64, 512, 128, seed=2)
-    x2 = torch.randn(2, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
+    x17 = torch.randn(17, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
     with pytest.raises(LinnetError, match="one-token kernel"):
-        kernels.int4_linear(x2, packed.to(DEV), scale.to(DEV), zero.to(DEV), kernel="gemv")
+        kernels.int4_linear(x17, packed.to(DEV), scale.to(DEV), zero.to(DEV), kernel="gemv")
+
+
+@pytest.mark.parametrize(
+    ("rows", "out", "width", "group", "dtype"),
+    [
+        (2, 14336, 4096, 128, torch.bfloat16),  # config 2 shape, U8 = 7 (a last 8-row tile)
+        (4, 14336, 4096, 128, torch.bfloat16),
+        (16, 14336, 4096, 128, torch.bfloat16),
+        (3, 4096, 4096, 128, torch.float16),  # U8 = 2
+        (5, 2049, 1024, 128, torch.bfloat16),  # U8 = 2, ragged last workgroup, 16-row form
+        (8, 6144, 1280, 256, torch.bfloat16),  # group 256, U8 = 3, 5 waves
+        (16, 16384, 256, 128, torch.float16),  # U8 = 8, one wave
+        (12, 100, 4096, 128, torch.bfloat16),  # one short workgroup
+    ],
+)
+def test_few_token_gemv_multiplies_the_dequantized_weight(rows: int, out: int, width: int, group: int, dtype: torch.dtype) -> None:
+    """2..16 rows through the one-workgroup-per-CU GEMV (x row m in MFMA A row m),
+    against the f64 product and against the skinny kernel on the same inputs."""
+    packed, scale, zero = _layer(out, width, group, seed=out + rows, dtype=dtype)
+    x = torch.randn(rows, width, generator=torch.Generator().manual_seed(rows)).to(dtype)
+    args = (x.to(DEV), packed.to(DEV), scale.to(DEV), zero.to(DEV))
+    y = kernels.int4_linear(*args, kernel="gemv")
+    _check_linear(x, packed, scale, zero, y)
+    skinny = kernels.int4_linear(*args, kernel="skinny").float()
+    assert (y.float() - skinny).abs().max().item() <= 1e-2 * skinny.abs().max().item()
+    bias = torch.randn(out, generator=torch.Generator().manual_seed(3)).to(dtype).to(DEV)
+    assert torch.equal(kernels.int4_linear(*args, bias, kernel="gemv"), y + bias)
 
 
 # ------------------------------------------------------------ full BASELINE sizes
