@@ -105,7 +105,22 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
 
-  // ---- loads: x slice (lanes 0..31, 8 inputs each), weights, scales, zeros.
+  // ---- loads: scales, zeros, x slice (lanes 0..31, 8 inputs each), weights.
+  // The scale and zero loads go first: scattered (a row per lane) and needed only
+  // at the end, they would otherwise return after all the weights.
+  // Lane r < R: row n0 + r's scales and zero points of this wave's groups.
+  const int srow = n0 + (lane < R ? lane : R - 1);
+  const int g0 = k0 / G;
+  uint32_t sv;
+  uint16_t zv16;
+  if constexpr (G128) {
+    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);  // s[g0] | s[g0 + 1] << 16
+    zv16 = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);      // z[g0] | z[g0 + 1] << 8
+  } else {
+    sv = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
+    zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const u32x4 xv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (k0 + 8 * (lane & 31)) * 2, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
   {
@@ -122,22 +137,9 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  // Lane r < R: row n0 + r's scales and zero points of this wave's groups.
-  const int srow = n0 + (lane < R ? lane : R - 1);
-  const int g0 = k0 / G;
-  uint32_t sv;
-  uint16_t zv16;
-  if constexpr (G128) {
-    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);  // s[g0] | s[g0 + 1] << 16
-    zv16 = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);      // z[g0] | z[g0 + 1] << 8
-  } else {
-    sv = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
-    zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
-  }
-  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- x: wait for it alone, stage it in pair order, sums of both halves.
-  wait_vm<U8 + 2>();
+  // ---- x: wait for it (and the scales), stage it in pair order, sums of both halves.
+  wait_vm<U8>();
   __builtin_amdgcn_sched_barrier(0);
   if (lane < 32) *reinterpret_cast<u32x4*>(Xw + 8 * lane) = permute_x8(xv);
   float sum = 0.f;
@@ -184,28 +186,49 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     __asm__ volatile("" : "+v"(c) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
     return c;
   };
-  // ---- tiles as their loads land (the scale / zero loads are the last 2).
-  float cf[NF + 1][2];
+  // ---- scales and zero points of each tile's rows (landed with x), so that a
+  // tile's fold follows its MFMAs at once: acc = s0 (C0 - z0 xs0) + s1 (C1 - z1 xs1).
+  uint32_t zv = zv16;
+  if constexpr (!G128) {
+    sv = (sv & 0xffffu) | (sv << 16);
+    zv = (zv & 0xffu) | (zv << 8);
+  }
+  float fs0[NF + 1], fs1[NF + 1], fz0[NF + 1], fz1[NF + 1];
+#pragma unroll
+  for (int T = 0; T <= NF; ++T) {
+    if (T == NF && !HALF) break;
+    const int n = T < NF ? 8 * (2 * T + (col >> 3)) + r7 : 8 * (U8 - 1) + r7;  // the lane's output row
+    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(sv)));
+    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(zv)));
+    fs0[T] = E::to_f32(static_cast<uint16_t>(sp & 0xffffu));
+    fs1[T] = E::to_f32(static_cast<uint16_t>(sp >> 16));
+    fz0[T] = -(E::MAGIC_VALUE + static_cast<float>(zp & 0xffu));
+    fz1[T] = -(E::MAGIC_VALUE + static_cast<float>((zp >> 8) & 0xffu));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- tiles as their loads land, each folded and stored for the cross-wave sum.
 #pragma unroll
   for (int T = 0; T < NF; ++T) {
     // No LDS load below may be issued before the previous tile's MFMAs have read
     // their operands: the fences keep each tile's reads after the prior tile.
     __builtin_amdgcn_sched_barrier(0);
-    wait_vm_rt(U8 - 1 - (2 * T + 1) + 2);
+    wait_vm_rt(U8 - 1 - (2 * T + 1));
     __builtin_amdgcn_sched_barrier(0);
     const int h = col >> 3;
-    const int u = 2 * T + h;
     const int p0 = 16 * (j >> 1) + 8 * ((j & 1) ^ h) + r7;        // piece j      (half 0)
     const int p1 = 16 * (2 + (j >> 1)) + 8 * ((j & 1) ^ h) + r7;  // piece 4 + j  (half 1)
-    const uint8_t* Wt = tile_lds(T, wave) + 1024 * h;  // load u
+    const uint8_t* Wt = tile_lds(T, wave) + 1024 * h;  // load 2 T + h
     const u32x4 w0 = *reinterpret_cast<const u32x4*>(Wt + 16 * p0);
     const u32x4 w1 = *reinterpret_cast<const u32x4*>(Wt + 16 * p1);
-    cf[T][0] = chain(xa[0], w0, 0);
-    cf[T][1] = chain(xa[1], w1, 0);
+    const float c0 = chain(xa[0], w0, 0);
+    const float c1 = chain(xa[1], w1, 0);
+    const float acc = fmaf(fs0[T], fmaf(fz0[T], xs0, c0), fs1[T] * fmaf(fz1[T], xs1, c1));
+    if (lane < 16) Rsm[wave][16 * T + lane] = acc;
   }
   if constexpr (HALF) {
     __builtin_amdgcn_sched_barrier(0);
-    wait_vm<2>();
+    wait_vm<0>();
     __builtin_amdgcn_sched_barrier(0);
     constexpr int u = U8 - 1;
     const int H = col >> 3;
@@ -213,49 +236,27 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const int pp = 16 * (sigma >> 1) + 8 * (sigma & 1) + r7;
     static_assert((u & 1) == 0, "the last load of an odd U8 is the first of its tile");
     const u32x4 w = *reinterpret_cast<const u32x4*>(tile_lds(NF, wave) + 16 * pp);
-    cf[NF][0] = chain(ac, w, H);
-  }
-  // ---- scales / zeros, the fold, the cross-wave sum.
-  __builtin_amdgcn_sched_barrier(0);
-  wait_vm<0>();
-  __builtin_amdgcn_sched_barrier(0);
-  __asm__ volatile("" : "+v"(sv), "+v"(zv16));  // no use of these loads before the wait
-  uint32_t zv = zv16;
-  if constexpr (!G128) {
-    sv = (sv & 0xffffu) | (sv << 16);
-    zv = (zv & 0xffu) | (zv << 8);
-  }
-  auto sz_of = [&](int n, float& s0, float& s1, float& z0, float& z1) {
-    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(sv)));
-    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(zv)));
-    s0 = E::to_f32(static_cast<uint16_t>(sp & 0xffffu));
-    s1 = E::to_f32(static_cast<uint16_t>(sp >> 16));
-    z0 = E::MAGIC_VALUE + static_cast<float>(zp & 0xffu);
-    z1 = E::MAGIC_VALUE + static_cast<float>((zp >> 8) & 0xffu);
-  };
-#pragma unroll
-  for (int T = 0; T < NF; ++T) {
-    float s0, s1, z0, z1;
-    sz_of(8 * (2 * T + (col >> 3)) + r7, s0, s1, z0, z1);
-    const float acc = fmaf(s0, fmaf(-z0, xs0, cf[T][0]), s1 * fmaf(-z1, xs1, cf[T][1]));
-    if (lane < 16) Rsm[wave][16 * T + lane] = acc;
-  }
-  if constexpr (HALF) {
-    const int H = col >> 3;
-    float s0, s1, z0, z1;
-    sz_of(8 * (U8 - 1) + r7, s0, s1, z0, z1);
-    const float part = H == 0 ? s0 * fmaf(-z0, xs0, cf[NF][0]) : s1 * fmaf(-z1, xs1, cf[NF][0]);
+    const float c = chain(ac, w, H);
+    const float part = H == 0 ? fs0[NF] * fmaf(fz0[NF], xs0, c) : fs1[NF] * fmaf(fz1[NF], xs1, c);
     const float acc = part + __shfl_xor(part, 8, 64);
     if (lane < 8) Rsm[wave][16 * NF + lane] = acc;
   }
   __syncthreads();
-  if (threadIdx.x < R) {
-    const int n = n0 + threadIdx.x;
+  // Four lanes per output row, each adding a quarter of the waves, then two
+  // exchanges (a fixed order: the result does not depend on timing). A group of
+  // four lanes is always active or inactive together.
+  for (int t = threadIdx.x; t < 4 * R; t += blockDim.x) {
+    const int r = t >> 2, part = t & 3;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < gemv::MAX_WAVES; ++w)
-      if (w < nw) v += Rsm[w][threadIdx.x];
-    if (n < N) {
+    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
+      const int wv = part * (gemv::MAX_WAVES / 4) + w;
+      if (wv < nw) v += Rsm[wv][r];
+    }
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    const int n = n0 + r;
+    if (part == 0 && n < N) {
       uint16_t out = E::from_f32(v);
       if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
       y[n] = out;
