@@ -243,11 +243,11 @@ __device__ inline void wait_vm_rt(int n) {
   }
 }
 
-// MFMA accumulators in AGPRs. When the compiler keeps MFMA results in VGPRs
-// (it does so on its own when a kernel touches no AGPR), gfx950 code built by
-// this toolchain was seen to let VALU instructions write registers of an MFMA
-// destination still in flight, which corrupts results. Naming an AGPR in an
-// asm clobber makes the compiler allocate MFMA destinations in AGPRs.
+// MFMA accumulators in AGPRs: naming an AGPR in an asm clobber makes the
+// compiler allocate MFMA destinations there (it uses VGPRs on its own when a
+// kernel touches no AGPR). The register budget is then split evenly between
+// VGPRs and AGPRs; the GEMM kernels keep their accumulator tiles in the AGPR
+// half and their operands in the VGPR half.
 #define LNQ_MFMA_IN_AGPRS() __asm__ volatile("" ::: "a0")
 
 // Wave-wide reductions (64 lanes).

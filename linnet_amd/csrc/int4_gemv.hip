@@ -169,10 +169,9 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   hide_in_vgpr(nib_magic);
   const int r7 = col & 7;
   // One MFMA chain over a lane's 16 bytes of weights; returns output register
-  // `reg`. The operand registers are kept allocated until the result has been
-  // read (which waits for the chain): code built by this toolchain for gfx950
-  // was seen to overwrite an MFMA's A / B registers while it was still in
-  // flight once they were otherwise dead.
+  // `reg`. The operand registers stay allocated until the result has been read
+  // (an empty asm uses them), so no later instruction reuses a register that an
+  // MFMA still in flight reads.
   auto chain = [&](const u32x4 (&a)[4], const u32x4 w, int reg) -> float {
     u32x4 b0, b1, b2, b3;
     widen_pair<DT>(w.x, w.y, nib_mask, nib_magic, b0, b1);
