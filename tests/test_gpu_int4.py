@@ -200,6 +200,9 @@ def test_unsupported_groups_fall_back_to_the_dequantized_weight() -> None:
         (6144, 1280, 128, torch.float16),  # 24 rows a workgroup (U8 = 3)
         (12288, 512, 128, torch.bfloat16),  # U8 = 6
         (8192, 256, 256, torch.bfloat16),  # U8 = 4
+        (14336, 4096, 128, torch.bfloat16),  # the decode shape: 256 workgroups of 56 rows
+        (1000, 2048, 128, torch.bfloat16),  # 8 waves, ragged last workgroup
+        (4096, 4096, 256, torch.float16),  # group 256, 16 rows a workgroup
     ],
 )
 def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, group: int, dtype: torch.dtype) -> None:
