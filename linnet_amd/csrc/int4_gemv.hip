@@ -123,6 +123,12 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   __builtin_amdgcn_sched_barrier(0);
   const u32x4 xv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (k0 + 8 * (lane & 31)) * 2, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
+  // Every wave's small loads enter the CU's memory pipeline before any weight
+  // load: without this barrier the waves that reach their first load last find
+  // it queued behind the other waves' weights (~100 KB), their x and scales land
+  // late and their tiles are all multiplied after the stream has ended.
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   {
     // Load u: rows n0 + 8u + (lane & 7) at 16-byte piece sigma of the wave's 128
     // bytes; sigma = 2 (lane / 16) + ((lane / 8) % 2 ^ u % 2) puts piece sigma of
