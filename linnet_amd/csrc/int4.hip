@@ -580,7 +580,7 @@ LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* sc
 bool int4_tiled_supports(int M, int N, int K, int G, int dtype);
 
 // Defined in int4_gemv.hip: the one-token dequant-GEMV.
-bool int4_gemv_supports(int N, int K, int G, const void* x, const void* packed, const void* scale,
+bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
                         const void* zero);
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                            const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream);
@@ -621,7 +621,7 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
   hipStream_t s = static_cast<hipStream_t>(stream);
   // The one-workgroup-per-CU GEMV takes 1..16 rows (1: one x row broadcast; 2..16:
   // x row m in MFMA A row m).
-  const bool gemv_ok = M >= 1 && M <= 16 && int4_gemv_supports(N, K, G, x, packed, scale, zero);
+  const bool gemv_ok = int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
   if (kernel == LNQ_KERNEL_GEMV) {
     LNQ_REQUIRE(gemv_ok, "lnq_int4_linear: the one-token kernel does not take rows=%d N=%d K=%d group=%d", M, N, K, G);
   }

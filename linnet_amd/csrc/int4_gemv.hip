@@ -269,6 +269,225 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   }
 }
 
+// One token, K > 4096 (the down projection's 14336): the one-token kernel with
+// each wave owning S consecutive 256-input slices (K / (256 S) waves). Every
+// slice keeps the one-token kernel's loads, LDS layout and MFMA chains; a
+// tile's chains run per slice (A operands read back from LDS, a slice's fold
+// coefficients fetched when it is used) and its folds are added in registers
+// before the cross-wave sum. The LDS arrays are sized for SW(S) waves: tile
+// arrays SW * S * U8 KB, x SW * S * 512 bytes.
+namespace gemv {
+constexpr int slice_waves(int s) { return s == 4 ? 14 : MAX_WAVES; }
+constexpr int slice_max_u8(int s) { return s == 2 ? 4 : 2; }
+constexpr int slice_tile_bytes(int u8, int t, int s) {
+  return 2 * t < u8 ? tile_wave_bytes(u8, t) * s * slice_waves(s) : 16;
+}
+}  // namespace gemv
+
+template <int DT, int U8, bool G128, int S>
+__global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G) {
+  using E = Elem<DT>;
+  constexpr int R = 8 * U8;
+  constexpr int NF = U8 / 2;
+  constexpr bool HALF = (U8 & 1) != 0;
+  constexpr int SW = gemv::slice_waves(S);
+  static_assert(S >= 2 && S <= 4 && U8 <= gemv::slice_max_u8(S), "fits the LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t L0[gemv::slice_tile_bytes(U8, 0, S)];
+  __shared__ __attribute__((aligned(16))) uint8_t L1[gemv::slice_tile_bytes(U8, 1, S)];
+  __shared__ __attribute__((aligned(16))) uint16_t Xsm[SW][256 * S];
+  __shared__ float Rsm[SW][R];
+  // Tile T's bytes of slice s of wave w (tiles 0 and 1 only: U8 <= 4).
+  auto tile_lds = [&](int T, int w, int sl) -> uint8_t* {
+    return (T == 0 ? L0 : L1) + (w * S + sl) * gemv::tile_wave_bytes(U8, T);
+  };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int col = lane & 15, j = lane >> 4;
+  const int n0 = blockIdx.x * R;
+  const int kw = wave * 256 * S;  // the wave's first input
+  const int rowb = K >> 1;
+  const int groups = K / G;
+  uint16_t* Xw = Xsm[wave];
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * rowb));
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint32_t>(K * 2));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
+
+  // ---- loads, small ones first (as in the one-token kernel): per slice the
+  // scales and zero points of lane r's row, then x, then the weights.
+  const int srow = n0 + (lane < R ? lane : R - 1);
+  uint32_t sv[S], zv[S];
+#pragma unroll
+  for (int sl = 0; sl < S; ++sl) {
+    const int g0 = (kw + 256 * sl) / G;
+    if constexpr (G128) {
+      sv[sl] = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);
+      zv[sl] = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);
+    } else {
+      sv[sl] = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
+      zv[sl] = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 xv[S];
+#pragma unroll
+  for (int sl = 0; sl < S; ++sl)
+    xv[sl] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (kw + 256 * sl + 8 * (lane & 31)) * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    // Order: tile, then slice, then the tile's one or two loads, so that each
+    // slice of a tile is multiplied as soon as its own loads land.
+    const int a = lane >> 4, b = lane & 15;
+#pragma unroll
+    for (int T = 0; T < (U8 + 1) / 2; ++T) {
+#pragma unroll
+      for (int sl = 0; sl < S; ++sl) {
+#pragma unroll
+        for (int u = 2 * T; u < 2 * T + 2 && u < U8; ++u) {
+          const int sigma = 2 * a + ((b >> 3) ^ (u & 1));
+          const int row = n0 + 8 * u + (b & 7);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(tile_lds(T, wave, sl) + 1024 * (u & 1)), 16,
+                                                   row * rowb + ((kw + 256 * sl) >> 1) + 16 * sigma, 0, 0,
+                                                   2 /* non-temporal */);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- x of every slice to LDS in pair order; its sums over each half.
+  wait_vm<S * U8>();
+  __builtin_amdgcn_sched_barrier(0);
+  float xs0[S], xs1[S];
+#pragma unroll
+  for (int sl = 0; sl < S; ++sl) {
+    if (lane < 32) *reinterpret_cast<u32x4*>(Xw + 256 * sl + 8 * lane) = permute_x8(xv[sl]);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t d = xv[sl][e];
+      sum += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    sum += __shfl_xor(sum, 8, 64);
+    xs0[sl] = __shfl(sum, 0, 64);
+    xs1[sl] = __shfl(sum, 16, 64);
+    if constexpr (!G128) {
+      sv[sl] = (sv[sl] & 0xffffu) | (sv[sl] << 16);
+      zv[sl] = (zv[sl] & 0xffu) | (zv[sl] << 8);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t nib_mask = 0x000f000fu, nib_magic = E::MAGIC2;
+  hide_in_vgpr(nib_mask);
+  hide_in_vgpr(nib_magic);
+  const int r7 = col & 7;
+  auto chain = [&](const u32x4 (&a)[4], const u32x4 w, int reg) -> float {
+    u32x4 b0, b1, b2, b3;
+    widen_pair<DT>(w.x, w.y, nib_mask, nib_magic, b0, b1);
+    widen_pair<DT>(w.z, w.w, nib_mask, nib_magic, b2, b3);
+    f32x4 C = f32x4{0.f, 0.f, 0.f, 0.f};
+    C = mfma16x16x32<DT>(a[0], b0, C);
+    C = mfma16x16x32<DT>(a[1], b1, C);
+    C = mfma16x16x32<DT>(a[2], b2, C);
+    C = mfma16x16x32<DT>(a[3], b3, C);
+    float c = reg == 0 ? C[0] : C[1];
+    __asm__ volatile("" : "+v"(c) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
+    return c;
+  };
+  // Scale / zero point of output row n (workgroup-local) in slice sl: (s0, s1, -(M + z0), -(M + z1)).
+  auto coeff = [&](int n, int sl, float& s0, float& s1, float& nz0, float& nz1) {
+    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(sv[sl])));
+    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * n, static_cast<int>(zv[sl])));
+    s0 = E::to_f32(static_cast<uint16_t>(sp & 0xffffu));
+    s1 = E::to_f32(static_cast<uint16_t>(sp >> 16));
+    nz0 = -(E::MAGIC_VALUE + static_cast<float>(zp & 0xffu));
+    nz1 = -(E::MAGIC_VALUE + static_cast<float>((zp >> 8) & 0xffu));
+  };
+
+  // ---- tiles as their loads land; each slice's chains, folded and added.
+#pragma unroll
+  for (int T = 0; T < NF; ++T) {
+    const int h = col >> 3;
+    const int p0 = 16 * (j >> 1) + 8 * ((j & 1) ^ h) + r7;
+    const int p1 = 16 * (2 + (j >> 1)) + 8 * ((j & 1) ^ h) + r7;
+    float acc = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) {
+      float s0, s1, nz0, nz1;
+      coeff(8 * (2 * T + h) + r7, sl, s0, s1, nz0, nz1);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm_rt(S * U8 - (2 * S * T + 2 * (sl + 1)));  // this slice's two loads have landed
+      __builtin_amdgcn_sched_barrier(0);
+      u32x4 xa[2][4];
+#pragma unroll
+      for (int H = 0; H < 2; ++H)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          xa[H][t] = *reinterpret_cast<const u32x4*>(Xw + 256 * sl + 128 * H + 32 * j + 8 * t);
+      const uint8_t* Wt = tile_lds(T, wave, sl) + 1024 * h;
+      const u32x4 w0 = *reinterpret_cast<const u32x4*>(Wt + 16 * p0);
+      const u32x4 w1 = *reinterpret_cast<const u32x4*>(Wt + 16 * p1);
+      const float c0 = chain(xa[0], w0, 0);
+      const float c1 = chain(xa[1], w1, 0);
+      acc += fmaf(s0, fmaf(nz0, xs0[sl], c0), s1 * fmaf(nz1, xs1[sl], c1));
+    }
+    if (lane < 16) Rsm[wave][16 * T + lane] = acc;
+  }
+  if constexpr (HALF) {
+    const int H = col >> 3;
+    const int sigma = 4 * H + j;
+    const int pp = 16 * (sigma >> 1) + 8 * (sigma & 1) + r7;
+    float part = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) {
+      float s0, s1, nz0, nz1;
+      coeff(8 * (U8 - 1) + r7, sl, s0, s1, nz0, nz1);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm_rt(S - 1 - sl);  // the half tile's loads come last, one a slice
+      __builtin_amdgcn_sched_barrier(0);
+      u32x4 ac[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        ac[t] = *reinterpret_cast<const u32x4*>(Xw + 256 * sl + (col == 1 ? 128 : 0) + 32 * j + 8 * t);
+      const u32x4 w = *reinterpret_cast<const u32x4*>(tile_lds(NF, wave, sl) + 16 * pp);
+      const float c = chain(ac, w, H);
+      part += H == 0 ? s0 * fmaf(nz0, xs0[sl], c) : s1 * fmaf(nz1, xs1[sl], c);
+    }
+    const float acc = part + __shfl_xor(part, 8, 64);
+    if (lane < 8) Rsm[wave][16 * NF + lane] = acc;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < 4 * R; t += blockDim.x) {
+    const int r = t >> 2, part = t & 3;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
+      const int wv = part * (gemv::MAX_WAVES / 4) + w;
+      if (wv < nw) v += Rsm[wv][r];
+    }
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    const int n = n0 + r;
+    if (part == 0 && n < N) {
+      uint16_t out = E::from_f32(v);
+      if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
+      y[n] = out;
+    }
+  }
+}
+
 // A few tokens (2..MX rows, MX = 4 or 16): the one-token kernel's workgroup
 // shape and weight streams, with A-operand row m of every MFMA holding x row m
 // (lane col = m). Each lane loads its own 128 bytes of x (its row, its 32-input
@@ -466,8 +685,29 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
 
 // Whether the one-token kernel takes this shape (else the caller uses the
 // general skinny kernel).
-bool int4_gemv_supports(int N, int K, int G, const void* x, const void* packed, const void* scale,
+// Slices a wave takes in the K > 4096 one-token kernel (0: it does not take K):
+// the fewest S in 2..4 with K / 256 = S * waves, waves <= slice_waves(S).
+static int gemv_slices(int K) {
+  if (K % 256 != 0 || K <= 256 * gemv::MAX_WAVES) return 0;
+  const int k256 = K / 256;
+  for (int sl = 2; sl <= 4; ++sl)
+    if (k256 % sl == 0 && k256 / sl <= gemv::slice_waves(sl)) return sl;
+  return 0;
+}
+
+static bool gemv_slices_supports(int N, int K, int G, const void* x, const void* packed, const void* scale,
+                                 const void* zero) {
+  const int sl = gemv_slices(K);
+  if (sl == 0 || N <= 0 || (N + 2047) / 2048 > gemv::slice_max_u8(sl)) return false;
+  if (!(G == 128 || G % 256 == 0) || K % G != 0) return false;
+  if (static_cast<size_t>(N) * (K / 2) >= (1ull << 31)) return false;
+  return aligned(x, 16) && aligned(packed, 16) && (G != 128 || aligned(scale, 4)) && (G != 128 || aligned(zero, 2));
+}
+
+bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
                         const void* zero) {
+  if (M < 1 || M > 16) return false;
+  if (M == 1 && gemv_slices_supports(N, K, G, x, packed, scale, zero)) return true;
   if (K % 256 != 0 || K < 256 || K > 256 * gemv::MAX_WAVES) return false;
   if (!(G == 128 || G % 256 == 0) || K % G != 0) return false;
   const int u8 = (N + 2047) / 2048;
@@ -537,9 +777,39 @@ static void launch_rows_dt(const void* x, const uint8_t* packed, const void* sca
   }
 }
 
+template <int DT, int U8, int S>
+static void launch_slices_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                             const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+  const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / (256 * S)));
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* ys = static_cast<uint16_t*>(y);
+  if (G == 128)
+    hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, true, S>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
+                       N, K, G);
+  else
+    hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, false, S>), grid, block, 0, stream, xs, packed, ss, zero, bs,
+                       ys, N, K, G);
+}
+
+template <int DT>
+static void launch_slices_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                             const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+  const int sl = gemv_slices(K), u8 = (N + 2047) / 2048;
+#define LNQ_SLICES(S_, U_) \
+  if (sl == S_ && u8 == U_) return launch_slices_u8<DT, U_, S_>(x, packed, scale, zero, bias, y, N, K, G, stream);
+  LNQ_SLICES(2, 1) LNQ_SLICES(2, 2) LNQ_SLICES(2, 3) LNQ_SLICES(2, 4)
+  LNQ_SLICES(3, 1) LNQ_SLICES(3, 2) LNQ_SLICES(4, 1) LNQ_SLICES(4, 2)
+#undef LNQ_SLICES
+}
+
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                            const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream) {
-  if (M == 1) {
+  if (M == 1 && gemv_slices_supports(N, K, G, x, packed, scale, zero)) {
+    if (dtype == LNQ_BF16) launch_slices_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+    else launch_slices_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+  } else if (M == 1) {
     if (dtype == LNQ_BF16) launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, stream);
     else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, stream);
   } else if (M <= 4) {

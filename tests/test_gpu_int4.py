@@ -203,6 +203,13 @@ def test_unsupported_groups_fall_back_to_the_dequantized_weight() -> None:
         (14336, 4096, 128, torch.bfloat16),  # the decode shape: 256 workgroups of 56 rows
         (1000, 2048, 128, torch.bfloat16),  # 8 waves, ragged last workgroup
         (4096, 4096, 256, torch.float16),  # group 256, 16 rows a workgroup
+        # K > 4096: S slices of 256 inputs a wave
+        (4096, 14336, 128, torch.bfloat16),  # the down projection: S = 4, 14 waves, 16 rows
+        (24, 14336, 128, torch.float16),  # S = 4, one ragged 8-row workgroup
+        (8192, 8192, 128, torch.bfloat16),  # S = 2, 16 waves, 32 rows
+        (1000, 8192, 256, torch.float16),  # S = 2, group 256, 8 rows
+        (5000, 6144, 128, torch.bfloat16),  # S = 2, 12 waves, 24 rows (odd U8)
+        (3000, 12288, 1024, torch.bfloat16),  # S = 3, group 1024, 16 rows
     ],
 )
 def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, group: int, dtype: torch.dtype) -> None:
