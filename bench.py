@@ -47,7 +47,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "all"), default="all")
+    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "llama", "all"), default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
@@ -171,6 +171,10 @@ def main() -> int:
         extra.update(eight_bit(torch, dev, timed_graph, args.steps))
     torch.cuda.synchronize()
 
+    if args.only in ("llama", "all"):
+        extra["llama_int4_decode"] = llama_decode(torch, kernels, dev)
+    torch.cuda.synchronize()
+
     # --- CPU baseline: the reference's CPU path (generated source: the weight
     # dequantized once at prepare, then bf16 F.linear per call), on host cores.
     cpu = None
@@ -192,12 +196,17 @@ def main() -> int:
         config = {"workload": f"int4 g128 prefill dequant-GEMM M=2048 {key}", "baseline_config": 3}
         roofline = {"bound": "mfma", "achieved": entry["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": entry["frac_bf16_peak"], "traffic": None}
-    else:
+    elif "fp8_C4_K8192_N28672" in extra:
         entry = extra["fp8_C4_K8192_N28672"]["M4096"]
         metric_value, unit, ms = entry["tflops"], "TFLOP/s", entry["us"] / 1e3
         config = {"workload": "FP8 weight x per-token FP8 rows, M=4096 K=8192 N=28672", "baseline_config": 4}
         roofline = {"bound": "mfma", "achieved": entry["tflops"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": entry["frac_fp8_peak"], "traffic": None}
+    else:  # --only llama: the batch-1 decode step (its roofline is the GEMV's)
+        entry = extra["llama_int4_decode"]["B1"]
+        metric_value, unit, ms = entry["tokens_per_s"], "tokens/s", entry["ms_per_step"]
+        config = {"workload": "int4 g128 Llama-3.1-8B-shaped decode step, batch 1, context 1024", "baseline_config": 5}
+        roofline = None
     result = {
         "metric": "W4A16 decode GEMV GB/s (% HBM peak); prefill qGEMM TFLOP/s (% MFMA peak)",
         "value": round(float(metric_value), 2),
@@ -268,6 +277,137 @@ def eight_bit(torch, dev, timed_graph, steps: int) -> dict[str, object]:
         del x
     out["fp8_C4_K8192_N28672"] = fp8
     del ops, wq
+    return out
+
+
+class Int4Llama:
+    """A Llama-3.1-8B-shaped decoder whose linear layers are
+    all int4 g128 through this package's `int4_linear` (the `Int4GroupLinear`
+    swap of the reference's `examples/01-llama` card): random-init weights
+    (N(0, 0.02)) quantized on the GPU, RMSNorm, rotary embedding (theta 500000,
+    no frequency scaling), grouped-query attention over a KV cache of `ctx`
+    random entries, SiLU MLP and an int4 lm_head. Attention runs in f32 on
+    contiguous operands (K cache stored transposed). `step(x)` is one decode
+    step of `batch` tokens at position `ctx`; `linear` may be swapped for a
+    reference (dequantized weight and `F.linear`)."""
+
+    def __init__(self, torch, kernels, dev, layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336,
+                 vocab=128256, ctx=1024, batch=1, seed=0):
+        self.torch, self.kernels = torch, kernels
+        self.hidden, self.heads, self.kv_heads, self.hd = hidden, heads, kv_heads, hidden // heads
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def lin(n, k):
+            w = torch.randn(n, k, generator=g, device=dev) * 0.02
+            packed, scale, zero = kernels.quantize_int4(w, 128)
+            return packed, scale.to(torch.bfloat16), zero
+
+        kvd = kv_heads * self.hd
+        self.layers = [dict(q=lin(hidden, hidden), k=lin(kvd, hidden), v=lin(kvd, hidden), o=lin(hidden, hidden),
+                            gate=lin(ffn, hidden), up=lin(ffn, hidden), down=lin(hidden, ffn),
+                            n1=1 + 0.1 * torch.randn(hidden, generator=g, device=dev),
+                            n2=1 + 0.1 * torch.randn(hidden, generator=g, device=dev)) for _ in range(layers)]
+        self.norm = 1 + 0.1 * torch.randn(hidden, generator=g, device=dev)
+        self.head = lin(vocab, hidden)
+        # KV caches, f32: Kt [batch, kv_heads, hd, ctx + 1] (transposed), V [batch, kv_heads, ctx + 1, hd].
+        self.kt = [torch.randn(batch, kv_heads, self.hd, ctx + 1, generator=g, device=dev) for _ in range(layers)]
+        self.vc = [torch.randn(batch, kv_heads, ctx + 1, self.hd, generator=g, device=dev) for _ in range(layers)]
+        self.pos = ctx
+        inv = 1.0 / (500000.0 ** (torch.arange(0, self.hd, 2, device=dev, dtype=torch.float32) / self.hd))
+        ang = ctx * inv
+        self.cos, self.sin = torch.cos(ang), torch.sin(ang)
+        self.linear = lambda x, w: kernels.int4_linear(x, *w)
+
+    def _rms(self, x, w):
+        torch = self.torch
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w).to(torch.bfloat16)
+
+    def _rope(self, t):  # [B, H, hd] f32
+        half = self.hd // 2
+        a, b = t[..., :half], t[..., half:]
+        return self.torch.cat([a * self.cos - b * self.sin, b * self.cos + a * self.sin], dim=-1)
+
+    def step(self, x):
+        torch = self.torch
+        bsz = x.shape[0]
+        grp = self.heads // self.kv_heads
+        for i, p in enumerate(self.layers):
+            h = self._rms(x, p["n1"])
+            q = self._rope(self.linear(h, p["q"]).float().view(bsz, self.heads, self.hd))
+            k = self._rope(self.linear(h, p["k"]).float().view(bsz, self.kv_heads, self.hd))
+            v = self.linear(h, p["v"]).float().view(bsz, self.kv_heads, self.hd)
+            self.kt[i][:, :, :, self.pos] = k
+            self.vc[i][:, :, self.pos, :] = v
+            qg = q.view(bsz, self.kv_heads, grp, self.hd)
+            scores = torch.matmul(qg, self.kt[i]) * (self.hd ** -0.5)  # [B, kvh, grp, ctx + 1]
+            att = torch.matmul(torch.softmax(scores, dim=-1), self.vc[i])  # [B, kvh, grp, hd]
+            x = x + self.linear(att.reshape(bsz, self.hidden).to(torch.bfloat16), p["o"])
+            h = self._rms(x, p["n2"])
+            a = torch.nn.functional.silu(self.linear(h, p["gate"]).float()) * self.linear(h, p["up"]).float()
+            x = x + self.linear(a.to(torch.bfloat16), p["down"])
+        return self.linear(self._rms(x, self.norm), self.head)
+
+
+def llama_decode(torch, kernels, dev) -> dict[str, object]:
+    """Config 5: one decode step of the int4 Llama-3.1-8B-shaped stack at a
+    1024-token context, captured as one HIP graph and replayed; tokens/s =
+    batch / step time. Batch 1 runs every linear on the one-token GEMV
+    kernels, batch 32 on the skinny kernel. `linears_ms` replays the step's
+    225 int4 linear calls alone (the rest of the step is unfused torch glue:
+    norms, rotary embedding, cache writes, f32 attention, SiLU, residuals)."""
+    out: dict[str, object] = {"layers": 32, "hidden": 4096, "heads": "32/8", "ffn": 14336, "vocab": 128256,
+                              "context": 1024, "weights": "int4 g128, bf16 scales, u8 zeros; random-init"}
+    model = Int4Llama(torch, kernels, dev)
+    for batch in (1, 32):
+        if batch != 1:
+            model.kt = [t[:1].expand(batch, -1, -1, -1).contiguous() for t in model.kt]
+            model.vc = [t[:1].expand(batch, -1, -1, -1).contiguous() for t in model.vc]
+        x = (torch.randn(batch, 4096, device=dev) * 0.5).to(torch.bfloat16)
+        for _ in range(3):
+            model.step(x)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits = model.step(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = 20
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / reps
+        # The same step's 225 int4 linear calls alone (inputs and outputs preallocated).
+        calls = []
+        for p in model.layers:
+            for name, k in (("q", 4096), ("k", 4096), ("v", 4096), ("o", 4096), ("gate", 4096), ("up", 4096),
+                            ("down", 14336)):
+                xin = (torch.randn(batch, k, device=dev) * 0.5).to(torch.bfloat16)
+                yout = torch.empty(batch, p[name][0].shape[0], dtype=torch.bfloat16, device=dev)
+                calls.append((xin, p[name], yout))
+        calls.append(((torch.randn(batch, 4096, device=dev) * 0.5).to(torch.bfloat16), model.head,
+                      torch.empty(batch, 128256, dtype=torch.bfloat16, device=dev)))
+        lin_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(lin_graph):
+            for xin, w, yout in calls:
+                kernels.int4_linear(xin, *w, out=yout)
+        lin_graph.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            lin_graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        lin_ms = start.elapsed_time(end) / reps
+        nbytes = sum(w[0].numel() + w[1].numel() * 2 + w[2].numel() for _, w, _ in calls)
+        out[f"B{batch}"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(batch * 1e3 / ms, 1),
+                            "linears_ms": round(lin_ms, 3), "linear_weight_gbps": round(nbytes / lin_ms / 1e6, 1),
+                            "finite": bool(torch.isfinite(logits).all().item())}
+        del graph, lin_graph, calls
+    del model
     return out
 
 
