@@ -289,11 +289,14 @@ class Int4Llama:
     random entries, SiLU MLP and an int4 lm_head. Attention runs in f32 on
     contiguous operands (K cache stored transposed). `step(x)` is one decode
     step of `batch` tokens at position `ctx`; `linear` may be swapped for a
-    reference (dequantized weight and `F.linear`)."""
+    reference (dequantized weight and `F.linear`). `fused` runs the glue between
+    the linear layers as this package's decode kernels (`torch/decode.py`: norm
+    with the residual add, attention with the rotary embedding and cache write,
+    SiLU x up); otherwise as torch ops (the reference for the tests)."""
 
     def __init__(self, torch, kernels, dev, layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336,
-                 vocab=128256, ctx=1024, batch=1, seed=0):
-        self.torch, self.kernels = torch, kernels
+                 vocab=128256, ctx=1024, batch=1, seed=0, fused=True):
+        self.torch, self.kernels, self.fused = torch, kernels, fused
         self.hidden, self.heads, self.kv_heads, self.hd = hidden, heads, kv_heads, hidden // heads
         g = torch.Generator(device=dev).manual_seed(seed)
 
@@ -309,9 +312,11 @@ class Int4Llama:
                             n2=1 + 0.1 * torch.randn(hidden, generator=g, device=dev)) for _ in range(layers)]
         self.norm = 1 + 0.1 * torch.randn(hidden, generator=g, device=dev)
         self.head = lin(vocab, hidden)
-        # KV caches, f32: Kt [batch, kv_heads, hd, ctx + 1] (transposed), V [batch, kv_heads, ctx + 1, hd].
-        self.kt = [torch.randn(batch, kv_heads, self.hd, ctx + 1, generator=g, device=dev) for _ in range(layers)]
-        self.vc = [torch.randn(batch, kv_heads, ctx + 1, self.hd, generator=g, device=dev) for _ in range(layers)]
+        # KV caches, f32, capacity ctx + 1 rounded up to 4: Kt [batch, kv_heads, hd, cap]
+        # (transposed), V [batch, kv_heads, cap, hd]. Position ctx is written by the step.
+        cap = (ctx + 4) // 4 * 4
+        self.kt = [torch.randn(batch, kv_heads, self.hd, cap, generator=g, device=dev) for _ in range(layers)]
+        self.vc = [torch.randn(batch, kv_heads, cap, self.hd, generator=g, device=dev) for _ in range(layers)]
         self.pos = ctx
         inv = 1.0 / (500000.0 ** (torch.arange(0, self.hd, 2, device=dev, dtype=torch.float32) / self.hd))
         ang = ctx * inv
@@ -329,6 +334,8 @@ class Int4Llama:
         return self.torch.cat([a * self.cos - b * self.sin, b * self.cos + a * self.sin], dim=-1)
 
     def step(self, x):
+        if self.fused:
+            return self._step_fused(x)
         torch = self.torch
         bsz = x.shape[0]
         grp = self.heads // self.kv_heads
@@ -340,22 +347,38 @@ class Int4Llama:
             self.kt[i][:, :, :, self.pos] = k
             self.vc[i][:, :, self.pos, :] = v
             qg = q.view(bsz, self.kv_heads, grp, self.hd)
-            scores = torch.matmul(qg, self.kt[i]) * (self.hd ** -0.5)  # [B, kvh, grp, ctx + 1]
-            att = torch.matmul(torch.softmax(scores, dim=-1), self.vc[i])  # [B, kvh, grp, hd]
+            live = self.pos + 1
+            kt = self.kt[i][..., :live].contiguous()
+            scores = torch.matmul(qg, kt) * (self.hd ** -0.5)  # [B, kvh, grp, ctx + 1]
+            att = torch.matmul(torch.softmax(scores, dim=-1), self.vc[i][:, :, :live].contiguous())  # [B, kvh, grp, hd]
             x = x + self.linear(att.reshape(bsz, self.hidden).to(torch.bfloat16), p["o"])
             h = self._rms(x, p["n2"])
             a = torch.nn.functional.silu(self.linear(h, p["gate"]).float()) * self.linear(h, p["up"]).float()
             x = x + self.linear(a.to(torch.bfloat16), p["down"])
         return self.linear(self._rms(x, self.norm), self.head)
 
+    def _step_fused(self, x):
+        from linnet_amd.torch import decode
+
+        x = x.clone()  # the residual stream is updated in place
+        delta = None
+        for i, p in enumerate(self.layers):
+            h = decode.rmsnorm(x, p["n1"], 1e-5, delta)
+            att = decode.decode_attention(self.linear(h, p["q"]), self.linear(h, p["k"]), self.linear(h, p["v"]),
+                                          self.cos, self.sin, self.kt[i], self.vc[i], self.pos)
+            h = decode.rmsnorm(x, p["n2"], 1e-5, self.linear(att, p["o"]))
+            delta = self.linear(decode.silu_mul(self.linear(h, p["gate"]), self.linear(h, p["up"])), p["down"])
+        return self.linear(decode.rmsnorm(x, self.norm, 1e-5, delta), self.head)
+
 
 def llama_decode(torch, kernels, dev) -> dict[str, object]:
     """Config 5: one decode step of the int4 Llama-3.1-8B-shaped stack at a
     1024-token context, captured as one HIP graph and replayed; tokens/s =
     batch / step time. Batch 1 runs every linear on the one-token GEMV
-    kernels, batch 32 on the skinny kernel. `linears_ms` replays the step's
-    225 int4 linear calls alone (the rest of the step is unfused torch glue:
-    norms, rotary embedding, cache writes, f32 attention, SiLU, residuals)."""
+    kernels, batch 32 on the skinny kernel; between them, the decode kernels of
+    `torch/decode.py` (4 a layer). `linears_ms` replays the step's 225 int4
+    linear calls alone; `torch_glue_ms` is the same step with the glue as torch
+    ops (~40 small kernels a layer)."""
     out: dict[str, object] = {"layers": 32, "hidden": 4096, "heads": "32/8", "ffn": 14336, "vocab": 128256,
                               "context": 1024, "weights": "int4 g128, bf16 scales, u8 zeros; random-init"}
     model = Int4Llama(torch, kernels, dev)
@@ -403,10 +426,26 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         torch.cuda.synchronize()
         lin_ms = start.elapsed_time(end) / reps
         nbytes = sum(w[0].numel() + w[1].numel() * 2 + w[2].numel() for _, w, _ in calls)
+        model.fused = False
+        model.step(x)  # eager first: library handles are created outside the capture
+        torch.cuda.synchronize()
+        glue_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(glue_graph):
+            model.step(x)
+        glue_graph.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            glue_graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        glue_ms = start.elapsed_time(end) / reps
+        model.fused = True
         out[f"B{batch}"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(batch * 1e3 / ms, 1),
                             "linears_ms": round(lin_ms, 3), "linear_weight_gbps": round(nbytes / lin_ms / 1e6, 1),
+                            "torch_glue_ms": round(glue_ms, 3),
                             "finite": bool(torch.isfinite(logits).all().item())}
-        del graph, lin_graph, calls
+        del graph, lin_graph, glue_graph, calls
     del model
     return out
 

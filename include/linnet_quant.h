@@ -152,6 +152,42 @@ LNQ_API LnqStatus lnq_mm8(const uint8_t* q, const uint8_t* weight, const float* 
                           const float* scale, void* y, int64_t rows, int64_t out_features,
                           int64_t in_features, int32_t fp8, int32_t dtype, void* stream);
 
+/* ------------------------------------------------------- decode-step glue (bf16)
+ * What a decoder layer runs between its quantized linear layers, for the int4
+ * Llama-shaped decode step of BASELINE config 5. No counterpart in the reference's
+ * quantized-linear path: its generated module runs these as framework ops
+ * (the model card's norms, rotary embedding, attention and MLP,
+ * examples/01-llama/src/lib.linnet, stdlib/nn/mlp.linnet:16-24).
+ */
+
+/* Per row of x [rows, hidden]: with delta (else NULL), x += delta rounded to bf16 in
+ * place; then h = x * rsqrt(mean(x^2) + eps) * weight (weight f32 [hidden]). */
+LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, void* h, int64_t rows,
+                              int64_t hidden, float eps, void* stream);
+
+/* One decode step of grouped-query attention: q [rows, heads*head_dim], k and v
+ * [rows, kv_heads*head_dim] (bf16); rotary embedding of q and k with cos/sin f32
+ * [head_dim/2] (pairs i, i + head_dim/2); k and v stored at `pos` of the f32 caches
+ * kt_cache [rows, kv_heads, head_dim, cap] (transposed) and v_cache [rows, kv_heads,
+ * cap, head_dim]; out [rows, heads*head_dim] = softmax(q K^T / sqrt(head_dim)) V over
+ * positions 0..pos, in chunks of 64 positions merged in order (split-K). head_dim 64
+ * or 128; heads / kv_heads <= 8; cap a multiple of 4 and the caches 16-byte aligned.
+ * `workspace` (f32, caller-owned) holds lnq_decode_attention_workspace(rows, kv_heads,
+ * head_dim, pos) floats. */
+LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
+                                       const float* sin, float* kt_cache, float* v_cache, void* out,
+                                       float* workspace, int64_t workspace_floats, int64_t rows,
+                                       int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t cap,
+                                       int64_t pos, void* stream);
+
+/* Floats of lnq_decode_attention's workspace: rows * kv_heads * ceil((pos + 1) / 64)
+ * * 8 * (head_dim + 2). */
+LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim,
+                                               int64_t pos);
+
+/* a = silu(g) * u = g / (1 + exp(-g)) * u for n bf16 elements, f32 math. */
+LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

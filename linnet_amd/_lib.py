@@ -40,6 +40,9 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_dequantize8": [_p, _p, _p, _i64, _i64, _i32, _i64, _i64, _i32, _p],
     "lnq_rows8": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "lnq_mm8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
+    "lnq_rmsnorm": [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p],
+    "lnq_decode_attention": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "lnq_silu_mul": [_p, _p, _p, _i64, _p],
 }
 
 _lock = threading.Lock()
@@ -67,6 +70,8 @@ def load() -> ctypes.CDLL:
         lib.lnq_abi_version.argtypes = []
         lib.lnq_last_error.restype = ctypes.c_char_p
         lib.lnq_last_error.argtypes = []
+        lib.lnq_decode_attention_workspace.restype = _i64
+        lib.lnq_decode_attention_workspace.argtypes = [_i64, _i64, _i64, _i64]
         version = lib.lnq_abi_version()
         if version != ABI_VERSION:
             raise LinnetError(f"{LIBRARY.name} implements ABI {version}, this package needs {ABI_VERSION}")

@@ -1,0 +1,358 @@
+// Decode-step glue for the int4 Llama-shaped workload (the "Full int4
+// Llama-3.1-8B decode step" that BASELINE config 5 measures): everything a
+// decoder layer does between its quantized linear layers, as three kernels
+// instead of ~40 small framework ops a layer (each a ~3 us graph node here).
+//
+//   rmsnorm:           x += delta (rounded to bf16), h = x * rsqrt(mean(x^2) + eps) * w
+//   decode_attention:  rotary embedding of q and k, k and v written into the KV
+//                      cache at `pos`, softmax(q K^T / sqrt(hd)) V over 0..pos
+//   silu_mul:          a = silu(g) * u
+//
+// All arithmetic is f32 (activations stored bf16, caches f32) in a fixed order,
+// so results do not depend on timing. The reference gets these ops from its
+// generated module (framework ops on the GPU); they are not part of its
+// quantized-linear path.
+#include "common.hpp"
+
+namespace lnq {
+
+namespace decode {
+constexpr int THREADS = 256;
+constexpr int MAX_GROUP = 8;  // query heads per KV head
+constexpr int CHUNK = 64;  // cache positions a workgroup takes
+}  // namespace decode
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over the block (256 threads), the same value returned to every thread.
+__device__ inline float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ inline float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// One workgroup per row.
+__global__ __launch_bounds__(decode::THREADS) void rmsnorm_kernel(uint16_t* __restrict__ x,
+                                                                  const uint16_t* __restrict__ delta,
+                                                                  const float* __restrict__ w,
+                                                                  uint16_t* __restrict__ h, int hidden, float eps) {
+  __shared__ float red[4];
+  uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * hidden;
+  uint16_t* hr = h + static_cast<size_t>(blockIdx.x) * hidden;
+  const uint16_t* dr = delta ? delta + static_cast<size_t>(blockIdx.x) * hidden : nullptr;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < hidden; i += decode::THREADS) {
+    float v = bf16_bits_to_f32(xr[i]);
+    if (dr) {
+      const uint16_t r = f32_to_bf16_bits(v + bf16_bits_to_f32(dr[i]));
+      xr[i] = r;
+      v = bf16_bits_to_f32(r);
+    }
+    ss = fmaf(v, v, ss);
+  }
+  const float scale = rsqrtf(block_sum(ss, red) / static_cast<float>(hidden) + eps);
+  for (int i = threadIdx.x; i < hidden; i += decode::THREADS)
+    hr[i] = f32_to_bf16_bits(bf16_bits_to_f32(xr[i]) * scale * w[i]);
+}
+
+// Split-K decode attention. Workgroup (row, KV head, chunk c) takes positions
+// [64 c, 64 c + 64) of that head's cache for its G query heads: scores, their
+// max m and sum s of exp(score - m), and acc = sum exp(score - m) V, written to
+// the workspace; decode_combine_kernel merges the chunks. Keys and values move
+// as float4: a thread's key loads cover 4 positions x HD/16 dimensions (the
+// partial scores of the 16 dimension groups are added through LDS), its value
+// loads 4 dimensions x 64/(256/(HD/4)) positions. Every workgroup applies the
+// rotary embedding itself (q, and k for position pos, which it reads from LDS
+// rather than the cache); the one whose chunk holds pos writes k and v into the
+// caches. K cache transposed, [rows, kv_heads, HD, cap]; V cache [rows, kv_heads,
+// cap, HD]; cap a multiple of 4.
+template <int HD>
+__global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const float* __restrict__ cosv, const float* __restrict__ sinv, float* __restrict__ kt, float* __restrict__ vc,
+    float* __restrict__ work, int heads, int kv_heads, int cap, int pos, int chunks) {
+  constexpr int C = decode::CHUNK;       // 64 positions
+  constexpr int DG = 16;                 // dimension groups of the scores
+  constexpr int DPG = HD / DG;           // dimensions a score thread takes
+  constexpr int DV = HD / 4;             // value threads across the dimensions
+  constexpr int PG = decode::THREADS / DV;  // value threads across the positions
+  constexpr int G8 = decode::MAX_GROUP;
+  __shared__ float qs[G8][HD];
+  __shared__ float kn[HD], vn[HD];
+  __shared__ float sp[DG][G8][C];   // partial scores
+  __shared__ float p[G8][C];        // exp(score - m)
+  __shared__ float stat[G8][2];     // m, s
+  __shared__ __attribute__((aligned(16))) float pacc[PG][G8][HD];
+  const int G = heads / kv_heads;
+  const int c = blockIdx.x % chunks;
+  const int rk = blockIdx.x / chunks;  // row * kv_heads + kvh
+  const int row = rk / kv_heads, kvh = rk % kv_heads;
+  const int l0 = c * C;
+  const int n = min(C, pos + 1 - l0);  // live positions of this chunk
+  const int tid = threadIdx.x;
+  constexpr int HALF = HD / 2;
+  const float scale = rsqrtf(static_cast<float>(HD));
+  const uint16_t* qr = q + (static_cast<size_t>(row) * heads + kvh * G) * HD;
+  const uint16_t* kr = k + static_cast<size_t>(rk) * HD;
+  const uint16_t* vr = v + static_cast<size_t>(rk) * HD;
+  float* ktb = kt + static_cast<size_t>(rk) * HD * cap;
+  float* vcb = vc + static_cast<size_t>(rk) * cap * HD;
+  const bool owner = pos >= l0 && pos < l0 + C;
+
+  // Rotary embedding (pairs i, i + HD/2); the new key and value into LDS, and into
+  // the caches by the chunk that holds pos.
+  for (int t = tid; t < (G + 1) * HALF; t += decode::THREADS) {
+    const int g = t / HALF, i = t % HALF;
+    const uint16_t* src = g < G ? qr + g * HD : kr;
+    const float a = bf16_bits_to_f32(src[i]), b = bf16_bits_to_f32(src[i + HALF]);
+    const float ra = a * cosv[i] - b * sinv[i], rb = b * cosv[i] + a * sinv[i];
+    if (g < G) {
+      qs[g][i] = ra * scale;
+      qs[g][i + HALF] = rb * scale;
+    } else {
+      kn[i] = ra;
+      kn[i + HALF] = rb;
+      if (owner) {
+        ktb[static_cast<size_t>(i) * cap + pos] = ra;
+        ktb[static_cast<size_t>(i + HALF) * cap + pos] = rb;
+      }
+    }
+  }
+  for (int d = tid; d < HD; d += decode::THREADS) {
+    const float vv = bf16_bits_to_f32(vr[d]);
+    vn[d] = vv;
+    if (owner) vcb[static_cast<size_t>(pos) * HD + d] = vv;
+  }
+  __syncthreads();
+
+  // Partial scores: thread (dimension group dg, positions 4 p4 .. 4 p4 + 3).
+  {
+    const int p4 = tid & 15, dg = tid >> 4;
+    const int lp = l0 + 4 * p4;
+    float acc[G8][4];
+#pragma unroll
+    for (int g = 0; g < G8; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[g][e] = 0.f;
+#pragma unroll
+    for (int dd = 0; dd < DPG; ++dd) {
+      const int d = dg * DPG + dd;
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (lp < cap) kv = *reinterpret_cast<const float4*>(ktb + static_cast<size_t>(d) * cap + lp);
+      float kk[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (lp + e == pos) kk[e] = kn[d];
+#pragma unroll
+      for (int g = 0; g < G8; ++g)
+        if (g < G)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(qs[g][d], kk[e], acc[g][e]);
+    }
+#pragma unroll
+    for (int g = 0; g < G8; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sp[dg][g][4 * p4 + e] = acc[g][e];
+  }
+  __syncthreads();
+  // Scores (16 groups added in order), then per head the max and exp.
+  for (int t = tid; t < G * C; t += decode::THREADS) {
+    const int g = t / C, j = t % C;
+    float sc = 0.f;
+#pragma unroll
+    for (int dg = 0; dg < DG; ++dg) sc += sp[dg][g][j];
+    p[g][j] = j < n ? sc : -INFINITY;
+  }
+  __syncthreads();
+  if (tid < G) {
+    float m = -INFINITY;
+    for (int j = 0; j < n; ++j) m = fmaxf(m, p[tid][j]);
+    stat[tid][0] = m;
+  }
+  __syncthreads();
+  for (int t = tid; t < G * C; t += decode::THREADS) {
+    const int g = t / C, j = t % C;
+    p[g][j] = j < n ? expf(p[g][j] - stat[g][0]) : 0.f;
+  }
+  __syncthreads();
+  if (tid < G) {
+    float sum = 0.f;
+    for (int j = 0; j < n; ++j) sum += p[tid][j];
+    stat[tid][1] = sum;
+  }
+  // acc[g][d] = sum_j p[g][j] V[j][d]: thread (dimensions 4 d4 .. 4 d4 + 3, positions pg, pg + PG, ...).
+  {
+    const int d4 = tid % DV, pg = tid / DV;
+    float acc[G8][4];
+#pragma unroll
+    for (int g = 0; g < G8; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[g][e] = 0.f;
+#pragma unroll
+    for (int j = pg; j < C; j += PG) {
+      if (j >= n) break;
+      const int lj = l0 + j;
+      float4 vv;
+      if (lj == pos) vv = make_float4(vn[4 * d4], vn[4 * d4 + 1], vn[4 * d4 + 2], vn[4 * d4 + 3]);
+      else vv = *reinterpret_cast<const float4*>(vcb + static_cast<size_t>(lj) * HD + 4 * d4);
+#pragma unroll
+      for (int g = 0; g < G8; ++g)
+        if (g < G) {
+          const float pj = p[g][j];
+          acc[g][0] = fmaf(pj, vv.x, acc[g][0]);
+          acc[g][1] = fmaf(pj, vv.y, acc[g][1]);
+          acc[g][2] = fmaf(pj, vv.z, acc[g][2]);
+          acc[g][3] = fmaf(pj, vv.w, acc[g][3]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G8; ++g)
+      *reinterpret_cast<float4*>(&pacc[pg][g][4 * d4]) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+  }
+  __syncthreads();
+  float* wrow = work + static_cast<size_t>(blockIdx.x) * G8 * (HD + 2);
+  for (int t = tid; t < G * HD; t += decode::THREADS) {
+    const int g = t / HD, d = t % HD;
+    float o = 0.f;
+#pragma unroll
+    for (int pp = 0; pp < PG; ++pp) o += pacc[pp][g][d];
+    wrow[g * (HD + 2) + 2 + d] = o;
+  }
+  if (tid < G) {
+    wrow[tid * (HD + 2)] = stat[tid][0];
+    wrow[tid * (HD + 2) + 1] = stat[tid][1];
+  }
+}
+
+// out[row, head] = sum_c acc_c exp(m_c - M) / sum_c s_c exp(m_c - M), chunks in order.
+template <int HD>
+__global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restrict__ work, uint16_t* __restrict__ out,
+                                                            int heads, int kv_heads, int chunks) {
+  const int G = heads / kv_heads;
+  const int row = blockIdx.x / heads, head = blockIdx.x % heads;
+  const int kvh = head / G, g = head % G;
+  const int d = threadIdx.x;
+  const float* base = work + (static_cast<size_t>(row) * kv_heads + kvh) * chunks * decode::MAX_GROUP * (HD + 2) +
+                      g * (HD + 2);
+  const size_t stride = static_cast<size_t>(decode::MAX_GROUP) * (HD + 2);
+  float M = -INFINITY;
+  for (int c = 0; c < chunks; ++c) M = fmaxf(M, base[c * stride]);
+  float S = 0.f, o = 0.f;
+  for (int c = 0; c < chunks; ++c) {
+    const float w = expf(base[c * stride] - M);
+    S = fmaf(base[c * stride + 1], w, S);
+    o = fmaf(base[c * stride + 2 + d], w, o);
+  }
+  out[(static_cast<size_t>(row) * heads + head) * HD + d] = f32_to_bf16_bits(o / S);
+}
+
+__global__ __launch_bounds__(decode::THREADS) void silu_mul_kernel(const uint16_t* __restrict__ g,
+                                                                   const uint16_t* __restrict__ u,
+                                                                   uint16_t* __restrict__ a, int64_t n) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(decode::THREADS) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * decode::THREADS) {
+    const float gv = bf16_bits_to_f32(g[i]);
+    a[i] = f32_to_bf16_bits(gv / (1.f + expf(-gv)) * bf16_bits_to_f32(u[i]));
+  }
+}
+
+}  // namespace lnq
+
+using namespace lnq;
+
+extern "C" {
+
+LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim, int64_t pos);
+
+LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, void* h, int64_t rows,
+                              int64_t hidden, float eps, void* stream) {
+  LNQ_REQUIRE(rows >= 0 && hidden > 0 && hidden <= INT32_MAX && rows <= INT32_MAX, "lnq_rmsnorm: bad shape");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(x && weight && h, "lnq_rmsnorm: null pointer");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(decode::THREADS), 0,
+                     static_cast<hipStream_t>(stream), static_cast<uint16_t*>(x), static_cast<const uint16_t*>(delta),
+                     weight, static_cast<uint16_t*>(h), static_cast<int>(hidden), eps);
+  return launched("rmsnorm");
+}
+
+LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
+                                       const float* sin, float* kt_cache, float* v_cache, void* out, float* workspace,
+                                       int64_t workspace_floats, int64_t rows, int64_t heads, int64_t kv_heads,
+                                       int64_t head_dim, int64_t cap, int64_t pos, void* stream) {
+  LNQ_REQUIRE(head_dim == 64 || head_dim == 128, "lnq_decode_attention: head_dim is 64 or 128, not %lld",
+              static_cast<long long>(head_dim));
+  LNQ_REQUIRE(rows >= 0 && kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= decode::MAX_GROUP,
+              "lnq_decode_attention: heads must be a multiple (at most %d) of kv_heads", decode::MAX_GROUP);
+  LNQ_REQUIRE(pos >= 0 && pos < cap && cap <= INT32_MAX, "lnq_decode_attention: position %lld outside the cache",
+              static_cast<long long>(pos));
+  LNQ_REQUIRE(cap % 4 == 0, "lnq_decode_attention: the cache capacity %lld is not a multiple of 4",
+              static_cast<long long>(cap));
+  const int64_t chunks = (pos + decode::CHUNK) / decode::CHUNK;
+  const int64_t need = lnq_decode_attention_workspace(rows, kv_heads, head_dim, pos);
+  LNQ_REQUIRE(workspace_floats >= need, "lnq_decode_attention: the workspace holds %lld floats, %lld needed",
+              static_cast<long long>(workspace_floats), static_cast<long long>(need));
+  LNQ_REQUIRE(rows * kv_heads * chunks <= INT32_MAX && rows * heads <= INT32_MAX, "lnq_decode_attention: too many rows");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(q && k && v && cos && sin && kt_cache && v_cache && out && workspace, "lnq_decode_attention: null pointer");
+  LNQ_REQUIRE(aligned(kt_cache, 16) && aligned(v_cache, 16), "lnq_decode_attention: caches must be 16-byte aligned");
+  const dim3 grid(static_cast<unsigned>(rows * kv_heads * chunks)), grid2(static_cast<unsigned>(rows * heads));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define LNQ_ATT(HD_)                                                                                              \
+  hipLaunchKernelGGL(decode_attention_kernel<HD_>, grid, dim3(decode::THREADS), 0, s,                             \
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),                              \
+                     static_cast<const uint16_t*>(v), cos, sin, kt_cache, v_cache, workspace,                       \
+                     static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(cap), static_cast<int>(pos), \
+                     static_cast<int>(chunks));                                                                     \
+  hipLaunchKernelGGL(decode_combine_kernel<HD_>, grid2, dim3(HD_), 0, s, workspace, static_cast<uint16_t*>(out),   \
+                     static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(chunks))
+  if (head_dim == 64) {
+    LNQ_ATT(64);
+  } else {
+    LNQ_ATT(128);
+  }
+#undef LNQ_ATT
+  return launched("decode_attention");
+}
+
+LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim, int64_t pos) {
+  const int64_t chunks = (pos + decode::CHUNK) / decode::CHUNK;
+  return rows * kv_heads * chunks * decode::MAX_GROUP * (head_dim + 2);
+}
+
+LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n, void* stream) {
+  LNQ_REQUIRE(n >= 0, "lnq_silu_mul: bad size");
+  if (n == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(g && u && a, "lnq_silu_mul: null pointer");
+  const int64_t blocks = (n + decode::THREADS - 1) / decode::THREADS;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
+                     dim3(decode::THREADS), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(g),
+                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n);
+  return launched("silu_mul");
+}
+
+}  // extern "C"

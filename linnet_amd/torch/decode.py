@@ -1,0 +1,77 @@
+"""Decode-step glue of the int4 Llama-shaped workload, bf16:
+the ops a decoder layer runs between its quantized linear layers, as three HIP
+kernels (`csrc/decode.hip`) instead of ~40 small framework ops a layer. The
+reference gets these from its generated module; they are not part of its
+quantized-linear path. Every call enqueues on the current stream and returns.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..errors import LinnetError
+from .kernels import _on_gpu, _ptr, _stream
+
+
+def _bf16(what: str, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise LinnetError(f"{what}: takes contiguous bf16 tensors, got {t.dtype}")
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: torch.Tensor | None = None) -> torch.Tensor:
+    """`h = x * rsqrt(mean(x^2) + eps) * weight` per row of x [rows, hidden]; with
+    `delta`, first `x += delta` in place (rounded to bf16), as the residual add
+    before a norm. weight: f32 [hidden]."""
+    device = _on_gpu("rmsnorm", x, weight, delta)
+    _bf16("rmsnorm", x, *(() if delta is None else (delta,)))
+    if weight.dtype != torch.float32 or weight.numel() != x.shape[-1]:
+        raise LinnetError("rmsnorm: weight is f32 [hidden]")
+    if delta is not None and delta.shape != x.shape:
+        raise LinnetError("rmsnorm: delta has x's shape")
+    h = torch.empty_like(x)
+    with torch.cuda.device(device):
+        _lib.call("lnq_rmsnorm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(h), x.numel() // x.shape[-1], x.shape[-1],
+                  float(eps), _stream(device))
+    return h
+
+
+def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                     kt_cache: torch.Tensor, v_cache: torch.Tensor, pos: int) -> torch.Tensor:
+    """One decode step of grouped-query attention for q [rows, heads*hd], k, v
+    [rows, kv_heads*hd] (bf16): rotary embedding (cos, sin f32 [hd/2] at `pos`) of
+    q and k, k and v written into the f32 caches at `pos` (K transposed:
+    kt_cache [rows, kv_heads, hd, cap]; v_cache [rows, kv_heads, cap, hd]), then
+    softmax(q K^T / sqrt(hd)) V over positions 0..pos. Returns [rows, heads*hd] bf16."""
+    device = _on_gpu("decode_attention", q, k, v, cos, sin, kt_cache, v_cache)
+    _bf16("decode_attention", q, k, v)
+    rows, kvh, hd, cap = kt_cache.shape
+    if tuple(v_cache.shape) != (rows, kvh, cap, hd) or kt_cache.dtype != torch.float32 or v_cache.dtype != torch.float32:
+        raise LinnetError("decode_attention: caches are f32 [rows, kv_heads, hd, cap] and [rows, kv_heads, cap, hd]")
+    if not (kt_cache.is_contiguous() and v_cache.is_contiguous() and cos.is_contiguous() and sin.is_contiguous()):
+        raise LinnetError("decode_attention: contiguous caches and tables")
+    heads = q.shape[-1] // hd
+    if q.shape != (rows, heads * hd) or k.shape != (rows, kvh * hd) or v.shape != k.shape:
+        raise LinnetError("decode_attention: q [rows, heads*hd], k and v [rows, kv_heads*hd]")
+    if cos.numel() != hd // 2 or sin.numel() != hd // 2 or cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise LinnetError("decode_attention: cos and sin are f32 [hd/2]")
+    out = torch.empty_like(q)
+    floats = _lib.load().lnq_decode_attention_workspace(rows, kvh, hd, pos)
+    work = torch.empty(max(floats, 1), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_decode_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(kt_cache),
+                  _ptr(v_cache), _ptr(out), _ptr(work), work.numel(), rows, heads, kvh, hd, cap, pos, _stream(device))
+    return out
+
+
+def silu_mul(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """`silu(g) * u` elementwise in f32, rounded once to bf16."""
+    device = _on_gpu("silu_mul", g, u)
+    _bf16("silu_mul", g, u)
+    if g.shape != u.shape:
+        raise LinnetError("silu_mul: g and u have one shape")
+    a = torch.empty_like(g)
+    with torch.cuda.device(device):
+        _lib.call("lnq_silu_mul", _ptr(g), _ptr(u), _ptr(a), g.numel(), _stream(device))
+    return a

@@ -29,7 +29,7 @@ def declared() -> list[str]:
 def test_header_declares_the_abi() -> None:
     names = declared()
     assert "lnq_int4_linear" in names and "lnq_mm8" in names
-    assert len(names) == len(set(names)) == 13
+    assert len(names) == len(set(names)) == 17
 
 
 def test_library_exports_every_declared_symbol() -> None:
@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol() -> None:
     exported = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIBRARY)], capture_output=True, text=True, check=True).stdout
     for name in declared():
         assert re.search(rf"\bT {name}\b", exported), name
-    assert set(_lib.SIGNATURES) | {"lnq_abi_version", "lnq_last_error"} == set(declared())
+    assert set(_lib.SIGNATURES) | {"lnq_abi_version", "lnq_last_error", "lnq_decode_attention_workspace"} == set(declared())
 
 
 def test_abi_version() -> None:
@@ -87,12 +87,23 @@ def test_other_entry_points_validate() -> None:
     assert "in % 16" in _status("lnq_dequantize8", FAKE, FAKE, FAKE, 4, 100, 0, 0, 1, _lib.BF16, NULL)[1]
     assert "output is bf16 or f16" in _status("lnq_mm8", FAKE, FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 1, _lib.F32, NULL)[1]
     assert "negative" in _status("lnq_int4_pack", FAKE, FAKE, -1, NULL)[1]
+    big = 1 << 40
+    assert "head_dim is 64 or 128" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 32, 8, 96, 1025, 1024, NULL)[1]
+    assert "outside the cache" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 32, 8, 128, 1024, 1024, NULL)[1]
+    assert "multiple" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 30, 8, 128, 1025, 1024, NULL)[1]
+    need = _lib.load().lnq_decode_attention_workspace(2, 8, 128, 1024)
+    assert need == 2 * 8 * 17 * 8 * 130
+    assert "workspace" in _status("lnq_decode_attention", *[FAKE] * 9, need - 1, 2, 32, 8, 128, 1028, 1024, NULL)[1]
+    assert "multiple of 4" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1025, 1024, NULL)[1]
+    assert "bad shape" in _status("lnq_rmsnorm", FAKE, NULL, FAKE, FAKE, 1, 0, ctypes.c_float(1e-5), NULL)[1]
 
 
 def test_empty_calls_succeed_without_a_device() -> None:
     assert _status("lnq_int4_linear", FAKE, FAKE, FAKE, FAKE, NULL, FAKE, 0, 128, 16, 128, _lib.BF16, 0, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_int4_dequantize", NULL, NULL, NULL, NULL, 0, 128, 128, _lib.BF16, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_rows8", NULL, NULL, NULL, 0, 128, 1, _lib.BF16, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_silu_mul", NULL, NULL, NULL, 0, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_rmsnorm", NULL, NULL, NULL, NULL, 0, 4096, ctypes.c_float(1e-5), NULL)[0] == _lib.LNQ_OK
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU answer")

@@ -30,12 +30,24 @@ def _reference_linear(x, w):
     return torch.nn.functional.linear(x, kernels.int4_weight(*w))
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("batch", [1, 4])
-def test_int4_decode_step_matches_the_dequantized_reference(batch: int) -> None:
-    model = bench.Int4Llama(torch, kernels, DEV, batch=batch, seed=batch, **SMALL)
+def test_int4_decode_step_matches_the_dequantized_reference(batch: int, fused: bool) -> None:
+    """The step (decode kernels or torch glue between the int4 linears) against
+    the torch-glue step with dequantized-bf16 linears."""
+    from linnet_amd.torch import decode
+
+    model = bench.Int4Llama(torch, kernels, DEV, batch=batch, seed=batch, fused=fused, **SMALL)
     x = (torch.randn(batch, SMALL["hidden"], generator=torch.Generator().manual_seed(7)) * 0.5).to(torch.bfloat16).to(DEV)
-    got = model.step(x).float()
-    model.linear = _reference_linear
+    calls = []
+    attention = decode.decode_attention
+    decode.decode_attention = lambda *a: calls.append(1) or attention(*a)
+    try:
+        got = model.step(x).float()
+    finally:
+        decode.decode_attention = attention
+    assert len(calls) == (SMALL["layers"] if fused else 0)
+    model.linear, model.fused = _reference_linear, False
     want = model.step(x).float()
     assert got.shape == (batch, SMALL["vocab"]) and torch.isfinite(got).all()
     err = (got - want).abs().max().item()
@@ -44,8 +56,9 @@ def test_int4_decode_step_matches_the_dequantized_reference(batch: int) -> None:
     assert err <= 3e-2 * scale
 
 
-def test_int4_decode_step_replays_as_a_graph() -> None:
-    model = bench.Int4Llama(torch, kernels, DEV, batch=1, seed=3, **SMALL)
+@pytest.mark.parametrize("fused", [True, False])
+def test_int4_decode_step_replays_as_a_graph(fused: bool) -> None:
+    model = bench.Int4Llama(torch, kernels, DEV, batch=1, seed=3, fused=fused, **SMALL)
     x = (torch.randn(1, SMALL["hidden"], generator=torch.Generator().manual_seed(1)) * 0.5).to(torch.bfloat16).to(DEV)
     eager = model.step(x).clone()
     torch.cuda.synchronize()
@@ -59,3 +72,47 @@ def test_int4_decode_step_replays_as_a_graph() -> None:
         again = model.step(x)  # eager work between the replays
         torch.cuda.synchronize()
         assert torch.equal(again, eager)
+
+
+def test_decode_kernels_match_torch_ops() -> None:
+    """Each decode kernel against the torch ops it replaces (f32 math, bf16 in and out)."""
+    from linnet_amd.torch import decode
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 4096, generator=g).to(torch.bfloat16).to(DEV)
+    d = torch.randn(3, 4096, generator=g).to(torch.bfloat16).to(DEV)
+    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(DEV)
+    want_x = x + d
+    xf = want_x.float()
+    want_h = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w).to(torch.bfloat16)
+    h = decode.rmsnorm(x, w, 1e-5, d)
+    assert torch.equal(x, want_x)
+    assert (h.float() - want_h.float()).abs().max().item() <= 1e-2 * want_h.float().abs().max().item()
+    gg = torch.randn(5, 1000, generator=g).to(torch.bfloat16).to(DEV)
+    uu = torch.randn(5, 1000, generator=g).to(torch.bfloat16).to(DEV)
+    want_a = (torch.nn.functional.silu(gg.float()) * uu.float()).to(torch.bfloat16)
+    assert (decode.silu_mul(gg, uu).float() - want_a.float()).abs().max().item() <= 1e-2
+    # attention: 2 rows, 8 heads over 2 KV heads, hd 128, 37 cached positions
+    rows, heads, kvh, hd, cap, pos = 2, 8, 2, 128, 40, 37
+    q = torch.randn(rows, heads * hd, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(rows, kvh * hd, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(rows, kvh * hd, generator=g).to(torch.bfloat16).to(DEV)
+    kt = torch.randn(rows, kvh, hd, cap, generator=g).to(DEV)
+    vc = torch.randn(rows, kvh, cap, hd, generator=g).to(DEV)
+    ang = pos / (500000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    cos, sin = torch.cos(ang).to(DEV), torch.sin(ang).to(DEV)
+    kt_ref, vc_ref = kt.clone(), vc.clone()
+
+    def rope(t):
+        a, b = t[..., : hd // 2], t[..., hd // 2 :]
+        return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1)
+
+    qr = rope(q.float().view(rows, heads, hd))
+    kt_ref[:, :, :, pos] = rope(k.float().view(rows, kvh, hd))
+    vc_ref[:, :, pos, :] = v.float().view(rows, kvh, hd)
+    s = torch.matmul(qr.view(rows, kvh, heads // kvh, hd), kt_ref[..., : pos + 1].contiguous()) * hd**-0.5
+    want = torch.matmul(torch.softmax(s, dim=-1), vc_ref[:, :, : pos + 1].contiguous()).reshape(rows, heads * hd)
+    got = decode.decode_attention(q, k, v, cos, sin, kt, vc, pos)
+    assert (got.float() - want).abs().max().item() <= 1e-2 * want.abs().max().item()
+    assert torch.equal(kt[:, :, :, pos], kt_ref[:, :, :, pos]) or (kt[:, :, :, pos] - kt_ref[:, :, :, pos]).abs().max() < 1e-5
+    assert torch.equal(vc, vc_ref)
