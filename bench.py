@@ -14,10 +14,11 @@ Also reported (extra keys): M=4 and M=16 GEMV, the prefill dequant-GEMM
 the reference's own prefill strategy (HIP dequantize + hipBLASLt), the 8-bit
 paths (config 1: int8 per-row weight-only GEMV 4096x4096; config 4: FP8 weight
 with per-token FP8 activations, K=8192 N=28672 at M=1/256/4096, against HBM
-and fp8 MFMA peaks), a measured copy-bandwidth ceiling, and the reference's
-CPU path timed on the host cores.
+and fp8 MFMA peaks), the int4 Llama-shaped decode step (config 5), the GPTQ /
+AWQ checkpoint repack kernel, a measured copy-bandwidth ceiling, and the
+reference's CPU path timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|8bit|llama|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|8bit|llama|checkpoint|all]
 
 The default K = 2000 GEMV calls (~16 ms) times the steady state of a decode
 loop; 200 calls (~1.8 ms) read 10-15% slower, the clock still ramping.
@@ -50,7 +51,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=2000)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "llama", "all"), default="all")
+    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "llama", "checkpoint", "all"), default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
@@ -178,6 +179,10 @@ def main() -> int:
         extra["llama_int4_decode"] = llama_decode(torch, kernels, dev)
     torch.cuda.synchronize()
 
+    if args.only in ("checkpoint", "all"):
+        extra["int4_repack_K4096_N14336"] = checkpoint_repack(torch, kernels, dev, timed_graph, not args.no_cpu)
+    torch.cuda.synchronize()
+
     # --- CPU baseline: the reference's CPU path (generated source: the weight
     # dequantized once at prepare, then bf16 F.linear per call), on host cores.
     cpu = None
@@ -205,11 +210,17 @@ def main() -> int:
         config = {"workload": "FP8 weight x per-token FP8 rows, M=4096 K=8192 N=28672", "baseline_config": 4}
         roofline = {"bound": "mfma", "achieved": entry["tflops"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": entry["frac_fp8_peak"], "traffic": None}
-    else:  # --only llama: the batch-1 decode step (its roofline is the GEMV's)
+    elif "llama_int4_decode" in extra:  # --only llama: the batch-1 decode step (its roofline is the GEMV's)
         entry = extra["llama_int4_decode"]["B1"]
         metric_value, unit, ms = entry["tokens_per_s"], "tokens/s", entry["ms_per_step"]
         config = {"workload": "int4 g128 Llama-3.1-8B-shaped decode step, batch 1, context 1024", "baseline_config": 5}
         roofline = None
+    else:  # --only checkpoint: the GPTQ repack of one layer
+        entry = extra["int4_repack_K4096_N14336"]["gptq"]
+        metric_value, unit, ms = entry["gbps"], "GB/s", entry["us"] / 1e3
+        config = {"workload": "GPTQ int4 checkpoint repack, In=4096 Out=14336 group 128"}
+        roofline = {"bound": "hbm", "achieved": entry["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": entry["frac_hbm_peak"], "traffic": None}
     result = {
         "metric": "W4A16 decode GEMV GB/s (% HBM peak); prefill qGEMM TFLOP/s (% MFMA peak)",
         "value": round(float(metric_value), 2),
@@ -451,6 +462,50 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         del graph, lin_graph, glue_graph, calls
     del model
     return out
+
+
+def checkpoint_repack(torch, kernels, dev, timed_graph, with_cpu: bool) -> dict[str, object]:
+    """The GPTQ / AWQ repack kernel (`lnq_int4_repack`) on one Llama-3.1-8B up
+    projection (In 4096, Out 14336, group 128): GPTQ words, GPTQ in activation
+    order, AWQ words. Bytes: the int32 words read and the packed bytes written
+    (In*Out/2 each) plus the zero words read and zero bytes written. Ten copies of
+    the words (290 MB > the Infinity Cache) rotate. Beside it, the reference's numpy
+    repack (`quant.py:307-341`, restated in the oracle) on the same layer, once."""
+    import numpy as np
+
+    in_f, out_f, group = 4096, 14336, 128
+    groups = in_f // group
+    nbytes = 2 * (in_f * out_f // 2) + groups * out_f // 8 * 4 + groups * out_f
+    rng = np.random.default_rng(0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    found: dict[str, object] = {}
+    for kind, method, act in (("gptq", "gptq", False), ("gptq_act_order", "gptq", True), ("awq", "awq", False)):
+        shape = (in_f // 8, out_f) if method == "gptq" else (in_f, out_f // 8)
+        words = [torch.randint(-2**31, 2**31 - 1, shape, generator=g, device=dev, dtype=torch.int32) for _ in range(10)]
+        zeros = torch.randint(-2**31, 2**31 - 1, (groups, out_f // 8), generator=g, device=dev, dtype=torch.int32)
+        order = torch.from_numpy(rng.permutation(in_f).astype(np.int32)).to(dev) if act else None
+        offset = 1 if method == "gptq" else 0
+        launches = [lambda w=w: kernels.int4_repack(w, zeros, method, group, offset, order) for w in words]
+        sec = timed_graph(launches, 200, 10)
+        entry = {"us": round(sec * 1e6, 2), "gbps": round(nbytes / sec / 1e9, 1),
+                 "frac_hbm_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4)}
+        if with_cpu:
+            from oracle import quant
+
+            host_w, host_z = words[0].cpu().numpy(), zeros.cpu().numpy()
+            g_idx = None
+            if act:
+                g_idx = np.empty(in_f, np.int32)
+                g_idx[order.cpu().numpy()] = np.arange(in_f) // group
+            t0 = time.perf_counter()
+            quant.repack_int4(host_w, host_z, method, group, offset, g_idx if method == "gptq" else None)
+            cpu_s = time.perf_counter() - t0
+            entry["cpu_numpy_ms"] = round(cpu_s * 1e3, 1)
+            entry["cpu_numpy_gbps"] = round(nbytes / cpu_s / 1e9, 3)
+        found[kind] = entry
+        del words
+    found["bytes_per_call"] = nbytes
+    return found
 
 
 def traffic_from_profiles(name: str) -> float | None:

@@ -107,6 +107,29 @@ LNQ_API LnqStatus lnq_int4_pack(const uint8_t* codes, uint8_t* packed, int64_t p
 LNQ_API LnqStatus lnq_int4_unpack(const uint8_t* packed, void* codes, int64_t pairs,
                                   int32_t is_signed, void* stream);
 
+/* Packings of calibrated 4-bit checkpoints lnq_int4_repack reads. */
+#define LNQ_PACKING_GPTQ 0
+#define LNQ_PACKING_AWQ 1
+
+/* A 4-bit GPTQ or AWQ layer's int32 words as Int4GroupLinear's weight and zero
+ * points, eight codes a word, lowest bits first:
+ *   GPTQ: qweight [in/8, out], word [c, o] holds input 8c+k of output o at bits 4k;
+ *   AWQ:  qweight [in, out/8], word [i, c] holds output 8c+ORDER[k] at bits 4k,
+ *         ORDER = (0, 2, 4, 6, 1, 3, 5, 7);
+ *   qzeros [groups, out/8] packs the zero points along the outputs the same way
+ *   (GPTQ in order, AWQ interleaved); zero_offset (0 or 1) is added to each (1 for
+ *   GPTQ's first checkpoint format, which stores each less one).
+ * order: GPTQ in activation order, [in] int32 (a permutation; else NULL): input i
+ * of the result is checkpoint input order[i]; an entry outside 0..in-1 reads as 0.
+ * Writes packed [out, in/2] (= [out, groups, in/groups/2], low nibble first) and
+ * zero [out, groups] u8. in and out are multiples of 8, groups divides in.
+ * Replaces: quant.py:222-240, 300-340 (`import_quantized`'s numpy repack: `_nibbles`,
+ * the AWQ column reversal, the `order` gather and `pack_int4_groups`). */
+LNQ_API LnqStatus lnq_int4_repack(const int32_t* qweight, const int32_t* qzeros,
+                                  const int32_t* order, int32_t packing, int32_t zero_offset,
+                                  int64_t in_features, int64_t out_features, int64_t groups,
+                                  uint8_t* packed, uint8_t* zero, void* stream);
+
 /* ----------------------------------------------------------------- 8-bit
  * Weights [out, in] of int8 (fp8 0) or FP8 E4M3 bytes (fp8 1). Scales (f32): one per
  * row ([out], group 0), or [out/row_block, in/group] (int8 groups: row_block 1;

@@ -22,6 +22,7 @@ ABI_VERSION = 1
 LNQ_OK, LNQ_ERROR, LNQ_UNAVAILABLE = 0, 1, 2
 BF16, F16, F32 = 0, 1, 2
 KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV = 0, 1, 2, 3
+PACKING_GPTQ, PACKING_AWQ = 0, 1
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -35,6 +36,7 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_int4_quantize": [_p, _p, _p, _p, _i64, _i64, _i64, _p],
     "lnq_int4_pack": [_p, _p, _i64, _p],
     "lnq_int4_unpack": [_p, _p, _i64, _i32, _p],
+    "lnq_int4_repack": [_p, _p, _p, _i32, _i32, _i64, _i64, _i64, _p, _p, _p],
     "lnq_int8_quantize": [_p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_w8a16": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _i64, _i32, _p],
     "lnq_dequantize8": [_p, _p, _p, _i64, _i64, _i32, _i64, _i64, _i32, _p],

@@ -181,6 +181,49 @@ def unpack4(packed: torch.Tensor, kind: str) -> torch.Tensor:
     return out
 
 
+def int4_repack(
+    qweight: torch.Tensor,
+    qzeros: torch.Tensor,
+    packing: str,
+    group: int,
+    zero_offset: int = 0,
+    order: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """A GPTQ (`qweight [In/8, Out]`) or AWQ (`qweight [In, Out/8]`) layer's int32 codes
+    and `qzeros [In/group, Out/8]` as Int4GroupLinear's `(packed [Out, In/group,
+    group/2] u8, zero [Out, In/group] u8)`; `order` (GPTQ in activation order, [In]
+    int32) picks the checkpoint input each input of the result is. The repack of
+    `import_quantized` (`python/linnet/src/linnet/quant.py:222-240, 300-340`)."""
+    device = _on_gpu("int4_repack", qweight, qzeros, order)
+    kinds = {"gptq": _lib.PACKING_GPTQ, "awq": _lib.PACKING_AWQ}
+    if packing not in kinds:
+        raise LinnetError(f"int4_repack: packing `{packing}` is neither gptq nor awq")
+    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32 or qweight.dim() != 2 or qzeros.dim() != 2:
+        raise LinnetError("int4_repack: qweight and qzeros are 2-D int32")
+    if packing == "gptq":
+        in_features, out_features = qweight.shape[0] * 8, qweight.shape[1]
+    else:
+        in_features, out_features = qweight.shape[0], qweight.shape[1] * 8
+    if group <= 0 or in_features % group or group % 2:
+        raise LinnetError(f"int4_repack: {in_features} inputs do not make even groups of {group}")
+    groups = in_features // group
+    if in_features % 8 or tuple(qzeros.shape) != (groups, out_features // 8):
+        raise LinnetError(f"int4_repack: qzeros is [{groups}, {out_features // 8}], got {tuple(qzeros.shape)}")
+    if order is not None:
+        if packing != "gptq" or order.dtype != torch.int32 or tuple(order.shape) != (in_features,):
+            raise LinnetError(f"int4_repack: an order is GPTQ's, [{in_features}] int32")
+        order = order.contiguous()
+    if zero_offset not in (0, 1):
+        raise LinnetError(f"int4_repack: zero_offset is 0 or 1, not {zero_offset}")
+    qweight, qzeros = qweight.contiguous(), qzeros.contiguous()
+    packed = torch.empty(out_features, groups, group // 2, dtype=torch.uint8, device=device)
+    zero = torch.empty(out_features, groups, dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_int4_repack", _ptr(qweight), _ptr(qzeros), _ptr(order), kinds[packing], zero_offset,
+                  in_features, out_features, groups, _ptr(packed), _ptr(zero), _stream(device))
+    return packed, zero
+
+
 # ------------------------------------------------------------------------ 8-bit
 
 

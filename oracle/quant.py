@@ -122,6 +122,61 @@ def pack_int4_groups(q: np.ndarray, group: int) -> np.ndarray:
     return (grouped[..., 0::2] | (grouped[..., 1::2] << 4)).astype(np.uint8)
 
 
+# ------------------------------------------------ GPTQ / AWQ checkpoint words
+
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)  # quant.py:222-227: bits 4k hold output AWQ_ORDER[k]
+
+
+def nibbles(words: np.ndarray, axis: int) -> np.ndarray:
+    """The eight 4-bit values of each int32, lowest bits first, laid along `axis`
+    (which grows eightfold). Restates `quant.py:230-239` (`_nibbles`).
+
+    Pin: round trip of the GPTQ / AWQ packers the reference's tests write from
+    the formats' definitions (`test_quant_groups.py:198-221`;
+    tests/test_oracle.py::test_repack_inverts_the_format_packers)."""
+    bits = np.asarray(words).astype(np.int64) & 0xFFFFFFFF
+    values = (bits[..., None] >> np.arange(0, 32, 4, dtype=np.int64)) & 15
+    values = np.moveaxis(values, -1, axis + 1)
+    shape = list(np.asarray(words).shape)
+    shape[axis] *= 8
+    return values.reshape(shape).astype(np.uint8)
+
+
+def repack_int4(
+    qweight: np.ndarray, qzeros: np.ndarray, method: str, group: int, zero_offset: int, g_idx: np.ndarray | None
+) -> tuple[np.ndarray, np.ndarray, np.ndarray | None]:
+    """A GPTQ or AWQ layer's words as `(packed [Out, In/group, group/2], zero [Out,
+    In/group] u8, order [In] int32 or None)`. Restates `import_quantized`'s per-layer
+    repack (`quant.py:307-341`): GPTQ codes along the inputs, zero points along the
+    outputs plus `zero_offset`, activation order as the stable argsort of `g_idx`;
+    AWQ codes and zero points along the outputs, columns reversed through
+    `AWQ_ORDER`.
+
+    Pin: as `nibbles` (the format packers' round trip, with and without
+    activation order) and the dequantized weight against the formats' own formula
+    `W[i, o] = (q[i, o] - zero[g(i), o]) * scale[g(i), o]`
+    (tests/test_oracle.py::test_repack_computes_the_format_formula)."""
+    order = None
+    if method == "gptq":
+        q = nibbles(qweight, 0)  # [In, Out]
+        zero = nibbles(qzeros, 1).astype(np.int32) + zero_offset
+        in_features = q.shape[0]
+        size = in_features if group <= 0 else group
+        group_of = np.arange(in_features) // size
+        if g_idx is not None and not np.array_equal(g_idx, group_of):
+            order = np.argsort(g_idx, kind="stable").astype(np.int32)
+            assert np.array_equal(g_idx[order], group_of), "groups of unequal size"
+            q = q[order]
+    else:
+        reverse = [AWQ_ORDER.index(k) for k in range(8)]
+        columns = np.arange(qweight.shape[1] * 8).reshape(-1, 8)[:, reverse].reshape(-1)
+        q = nibbles(qweight, 1)[:, columns]
+        zero = nibbles(qzeros, 1)[:, columns].astype(np.int32)
+        size = q.shape[0] if group <= 0 else group
+    packed = pack_int4_groups(np.ascontiguousarray(q.T), size)
+    return packed, np.ascontiguousarray(zero.T).astype(np.uint8), order
+
+
 def unpack_int4_codes(packed: np.ndarray) -> np.ndarray:
     """Each byte's two codes, low first, along the last axis (the last axis
     doubles). Restates `torch/packed.py:21-24` and `quant.py:133-134`."""

@@ -29,7 +29,7 @@ def declared() -> list[str]:
 def test_header_declares_the_abi() -> None:
     names = declared()
     assert "lnq_int4_linear" in names and "lnq_mm8" in names
-    assert len(names) == len(set(names)) == 17
+    assert len(names) == len(set(names)) == 18
 
 
 def test_library_exports_every_declared_symbol() -> None:
@@ -96,6 +96,11 @@ def test_other_entry_points_validate() -> None:
     assert "workspace" in _status("lnq_decode_attention", *[FAKE] * 9, need - 1, 2, 32, 8, 128, 1028, 1024, NULL)[1]
     assert "multiple of 4" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1025, 1024, NULL)[1]
     assert "bad shape" in _status("lnq_rmsnorm", FAKE, NULL, FAKE, FAKE, 1, 0, ctypes.c_float(1e-5), NULL)[1]
+    assert "neither GPTQ" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 2, 0, 64, 64, 1, FAKE, FAKE, NULL)[1]
+    assert "multiples of 8" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 0, 60, 64, 1, FAKE, FAKE, NULL)[1]
+    assert "equal groups" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 0, 64, 64, 3, FAKE, FAKE, NULL)[1]
+    assert "only GPTQ" in _status("lnq_int4_repack", FAKE, FAKE, FAKE, 1, 0, 64, 64, 1, FAKE, FAKE, NULL)[1]
+    assert "zero_offset" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 2, 64, 64, 1, FAKE, FAKE, NULL)[1]
 
 
 def test_empty_calls_succeed_without_a_device() -> None:
@@ -104,6 +109,7 @@ def test_empty_calls_succeed_without_a_device() -> None:
     assert _status("lnq_rows8", NULL, NULL, NULL, 0, 128, 1, _lib.BF16, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_silu_mul", NULL, NULL, NULL, 0, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_rmsnorm", NULL, NULL, NULL, NULL, 0, 4096, ctypes.c_float(1e-5), NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_int4_repack", NULL, NULL, NULL, 0, 1, 0, 64, 0, NULL, NULL, NULL)[0] == _lib.LNQ_OK
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU answer")

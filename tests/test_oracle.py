@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle import linear, quant
+from tests.formats import calibrated_layer, pack_gptq
 
 
 # ------------------------------------------------------------------ bf16 / fp8
@@ -281,3 +282,55 @@ def test_rows8_product_reference(fp8: bool) -> None:
     deq_x = (quant.decode_fp8(q) if fp8 else q.astype(np.float32)) * xs
     deq_w = (quant.decode_fp8(wq) if fp8 else wq.astype(np.float32)) * ws[:, None]
     np.testing.assert_allclose(got, deq_x.astype(np.float64) @ deq_w.astype(np.float64).T, rtol=1e-6)
+
+
+# ------------------------------------------------------- GPTQ / AWQ repack
+
+CALIBRATED = [("gptq", False), ("gptq", True), ("awq", False)]
+
+
+@pytest.mark.parametrize(("method", "act_order"), CALIBRATED)
+def test_repack_inverts_the_format_packers(method: str, act_order: bool) -> None:
+    """Catches a wrong nibble order, a missed AWQ column reversal, zero points
+    taken along the wrong axis or without GPTQ's offset: the result's input i
+    holds the checkpoint's input order[i] (order the identity unless in
+    activation order), its zero points are the checkpoint's transposed."""
+    layer = calibrated_layer(method, act_order)
+    packed, zero, order = quant.repack_int4(layer["qweight"], layer["qzeros"], method, layer["group"],
+                                            1 if method == "gptq" else 0,
+                                            layer["g_idx"] if method == "gptq" else None)
+    assert (order is not None) == act_order
+    source = order if order is not None else np.arange(layer["q"].shape[0])
+    codes = quant.unpack_int4_codes(packed).reshape(packed.shape[0], -1)
+    assert np.array_equal(codes, layer["q"][source].T)
+    assert np.array_equal(zero, layer["zero"].T)
+    if act_order:
+        assert sorted(order.tolist()) == list(range(len(order)))
+        assert np.array_equal(layer["g_idx"][order], np.arange(len(order)) // layer["group"])
+
+
+@pytest.mark.parametrize(("method", "act_order"), CALIBRATED)
+def test_repack_computes_the_format_formula(method: str, act_order: bool) -> None:
+    """The repacked layer, its inputs gathered by `order` (`take_inputs`,
+    `stdlib/quant.linnet:143-149`), computes `x @ W` for the format's own
+    `W[i, o] = (q[i, o] - zero[g(i), o]) * scale[g(i), o]`
+    (`test_quant_groups.py:228-273`)."""
+    layer = calibrated_layer(method, act_order, seed=4)
+    packed, zero, order = quant.repack_int4(layer["qweight"], layer["qzeros"], method, layer["group"],
+                                            1 if method == "gptq" else 0,
+                                            layer["g_idx"] if method == "gptq" else None)
+    w = quant.dequantize_int4_groups(packed, np.ascontiguousarray(layer["scale"].T).astype(np.float32), zero)
+    x = np.random.default_rng(5).standard_normal((3, layer["q"].shape[0]))
+    taken = x[:, order] if order is not None else x
+    np.testing.assert_allclose(taken @ w.T.astype(np.float64), x @ layer["weight"].astype(np.float64),
+                               rtol=1e-5, atol=1e-5)
+
+
+def test_gptq_second_format_has_no_zero_offset() -> None:
+    """GPTQ's v2 checkpoints store zero points as they are (`quant.py:297-298`)."""
+    rng = np.random.default_rng(8)
+    q = rng.integers(0, 16, (64, 16))
+    zero = rng.integers(0, 16, (1, 16))
+    qweight, qzeros = pack_gptq(q, zero, offset=0)
+    _, got, _ = quant.repack_int4(qweight, qzeros, "gptq", 64, 0, None)
+    assert np.array_equal(got, zero.T)
