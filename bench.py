@@ -290,7 +290,26 @@ def eight_bit(torch, dev, timed_graph, steps: int) -> dict[str, object]:
                         "frac_fp8_peak": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4)}
         del x
     out["fp8_C4_K8192_N28672"] = fp8
-    del ops, wq
+    del ops
+
+    # The same shape as an Fp8BlockLinear (a scale per 128 x 128 weight block),
+    # the rows rounded per 128 inputs (`fp8_groups`) past 32 rows and multiplied
+    # by the block-scaled FP8 product (`quantized.py:154-166`).
+    bscale = (torch.rand(n // 128, k // 128, generator=g, device=dev) + 0.5) * per_tensor.float()
+    bops = [quantized.fp8_block_operands(wq, bscale, 1), quantized.fp8_block_operands(wq.clone(), bscale.clone(), 1)]
+    block: dict[str, object] = {}
+    for m in (256, 4096):
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        calls = max(4, steps // 5) if m < 4096 else 10
+        sec = timed_graph([lambda o=o, x=x: quantized.fp8_block_linear(x, o, None) for o in bops], calls, 2)
+        flops = 2 * m * n * k
+        nbytes = n * k + (n // 128) * (k // 128) * 4 + m * k * 2 + m * n * 2
+        block[f"M{m}"] = {"us": round(sec * 1e6, 2), "gbps": round(nbytes / sec / 1e9, 1),
+                          "tflops": round(flops / sec / 1e12, 1),
+                          "frac_fp8_peak": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4)}
+        del x
+    out["fp8_block_K8192_N28672"] = block
+    del bops, wq
     return out
 
 

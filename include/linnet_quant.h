@@ -175,6 +175,28 @@ LNQ_API LnqStatus lnq_mm8(const uint8_t* q, const uint8_t* weight, const float* 
                           const float* scale, void* y, int64_t rows, int64_t out_features,
                           int64_t in_features, int32_t fp8, int32_t dtype, void* stream);
 
+/* Each 128 inputs (group = 128) of each row of x [rows, in] (`dtype`: bf16, f16 or f32)
+ * rounded to FP8 E4M3 with a scale of their own: scale = max(max|x|, 1e-12) / 448
+ * (f32, IEEE divide), q = E4M3 round-to-nearest-even of clamp(x / scale, +-448); rows
+ * rows .. padded-1 are zeros with scale 1. Writes q [padded, in] and x_scale [in/128,
+ * padded] f32 (x_scale[g * padded + row], the column-major scales of the reference).
+ * Replaces: torch/kernels.py:757-802 `fp8_groups`. */
+LNQ_API LnqStatus lnq_fp8_groups(const void* x, uint8_t* q, float* x_scale, int64_t rows,
+                                 int64_t padded, int64_t in_features, int64_t group,
+                                 int32_t dtype, void* stream);
+
+/* Block-scaled FP8 x FP8: y[rows, out] = sum over 128-input blocks b of
+ * (q[:, b] @ w[:, b]^T) * x_scale[b * xs_stride + row] * scale[out / 128, b], E4M3
+ * operands on the FP8 MFMA, f32 sums, rounded once to `dtype` (bf16 or f16). q [rows,
+ * in], w [out, in] E4M3 bytes (16-byte aligned), x_scale as lnq_fp8_groups writes it
+ * (xs_stride = its padded rows), scale [out/128, in/128] f32. in, out % 128 == 0.
+ * Replaces: `torch._scaled_mm` with block-wise scales as torch/quantized.py:159-166
+ * (`fp8_block_linear`, rounded) calls it. */
+LNQ_API LnqStatus lnq_mm8_block(const uint8_t* qx, const uint8_t* weight, const float* x_scale,
+                                int64_t xs_stride, const float* scale, void* y, int64_t rows,
+                                int64_t out_features, int64_t in_features, int32_t dtype,
+                                void* stream);
+
 /* ------------------------------------------------------- decode-step glue (bf16)
  * What a decoder layer runs between its quantized linear layers, for the int4
  * Llama-shaped decode step of BASELINE config 5. No counterpart in the reference's

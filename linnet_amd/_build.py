@@ -43,7 +43,7 @@ FLAGS = [
 # straight to VALU math, so their accumulators belong in VGPRs (no accvgpr
 # moves). A kernel without AGPRs also gets the whole register budget as VGPRs;
 # one with AGPRs has it split in half, and the GEMV kernels then spill.
-EXTRA = {name: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for name in ("int4.hip", "int4_gemv.hip")}
+EXTRA = {name: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for name in ("int4.hip", "int4_gemv.hip", "fp8_block.hip")}
 
 
 def hipcc() -> str:

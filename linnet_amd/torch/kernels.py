@@ -333,6 +333,61 @@ def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: to
     return y
 
 
+def fp8_groups(x: torch.Tensor, group: int, padded: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Each `group` (128) inputs of each row of `x` [rows, In] rounded to FP8 E4M3 with
+    a scale of their own, the rows padded with zeros (scale 1) to `padded`: `(q
+    [padded, In] float8_e4m3fn, scales [padded, In/group] f32)`, the scales a
+    column-major view (of a [In/group, padded] tensor) as the reference returns
+    them (`torch/kernels.py:757-802`)."""
+    device = _on_gpu("fp8_groups", x)
+    if x.dim() != 2:
+        raise LinnetError(f"fp8_groups: x is [rows, In], got {tuple(x.shape)}")
+    rows, depth = x.shape
+    code = _code(x.dtype, "fp8_groups", (torch.bfloat16, torch.float16, torch.float32))
+    if group != 128 or depth % group:
+        raise LinnetError(f"fp8_groups: groups of 128 dividing In={depth}, not {group}")
+    if padded < rows:
+        raise LinnetError(f"fp8_groups: padded {padded} < rows {rows}")
+    x = x.contiguous()
+    q = torch.empty(padded, depth, dtype=torch.float8_e4m3fn, device=device)
+    scale = torch.empty(depth // group, padded, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_fp8_groups", _ptr(x), _ptr(q), _ptr(scale), rows, padded, depth, group, code, _stream(device))
+    return q, scale.t()
+
+
+def fp8_block_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor,
+                 dtype: torch.dtype) -> torch.Tensor:
+    """The block-scaled FP8 product `torch._scaled_mm(q, weight.t(), scale_a=x_scale,
+    scale_b=scale.t(), out_dtype=dtype)` computes for the reference
+    (`torch/quantized.py:159-166`): `q` [rows, In] and `weight` [Out, In] FP8 E4M3,
+    `x_scale` [rows, In/128] as `fp8_groups` returns it (a column-major view), `scale`
+    [Out/128, In/128] f32; per 128-input block, the block's FP8 MFMA sums times
+    both scales, added in f32, rounded once to `dtype`."""
+    device = _on_gpu("fp8_block_mm", q, weight, x_scale, scale)
+    rows, depth = q.shape
+    width = weight.shape[0]
+    if weight.shape[1] != depth or depth % 128 or width % 128:
+        raise LinnetError(f"fp8_block_mm: weight {tuple(weight.shape)} against In={depth} (both % 128 == 0)")
+    if tuple(scale.shape) != (width // 128, depth // 128):
+        raise LinnetError(f"fp8_block_mm: scale is [{width // 128}, {depth // 128}], got {tuple(scale.shape)}")
+    if tuple(x_scale.shape) != (rows, depth // 128):
+        raise LinnetError(f"fp8_block_mm: x_scale is [{rows}, {depth // 128}], got {tuple(x_scale.shape)}")
+    code = _code(dtype, "fp8_block_mm")
+    # The kernel reads x_scale[b * stride + row]: a column-major [rows, In/128] view.
+    xs = x_scale.to(torch.float32)
+    if xs.stride(0) != 1 or (depth // 128 > 1 and xs.stride(1) < rows):
+        xs = xs.t().contiguous().t()
+    stride = xs.stride(1) if depth // 128 > 1 else max(rows, 1)
+    qb, wb = _bytes(q.contiguous()), _bytes(weight.contiguous())
+    ws = scale.to(torch.float32).contiguous()
+    y = torch.empty(rows, width, dtype=dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_mm8_block", _ptr(qb), _ptr(wb), _ptr(xs), stride, _ptr(ws), _ptr(y), rows, width, depth,
+                  code, _stream(device))
+    return y
+
+
 def int8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     """`(q @ weight.T) * x_scale * scale` in `dtype` for int8 rows and int8 weights
     with one scale a row, summed exactly in int32 on MFMA (`kernels.py:805-915`)."""

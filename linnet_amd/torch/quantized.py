@@ -100,21 +100,31 @@ def fp8_linear(x: torch.Tensor, operands: Fp8Operands, bias: torch.Tensor | None
 
 def fp8_block_operands(weight: torch.Tensor, scale: torch.Tensor, rounded: int) -> Fp8BlockOperands:
     """`weight` [Out, In] FP8 E4M3, `scale` [Out/B, In/B]: bytes, FP8 view, f32
-    scales, and B (`quantized.py:138-151`). The FP8 x FP8 block-scaled product is
-    not built; `rounded` calls take the weight-only kernels."""
+    scales, B, `rounded`, the gate (`quantized.py:138-151`): 2 where the FP8 x FP8
+    block-scaled product takes the blocks (B = 128, as PyTorch's), 1 where only the
+    weight-only kernels do."""
     _gpu(weight)
     weight = weight.contiguous().view(torch.uint8)
     block = weight.shape[0] // scale.shape[0]
     fast = _fp8_kernels(weight) if weight.shape[1] == block * scale.shape[1] else 0
-    return weight, weight.view(torch.float8_e4m3fn), scale.float().contiguous(), block, rounded, min(fast, 1)
+    if block != 128 or weight.shape[0] % 128:
+        fast = min(fast, 1)
+    return weight, weight.view(torch.float8_e4m3fn), scale.float().contiguous(), block, rounded, fast
 
 
 def fp8_block_linear(x: torch.Tensor, operands: Fp8BlockOperands, bias: torch.Tensor | None) -> torch.Tensor:
-    """`quantized.py:154-173`, weight-only on the GPU."""
-    weight, _, scale, block, _rounded, fast = operands
+    """`quantized.py:154-173`: past FEW_ROWS rows with `rounded`, the rows rounded to
+    FP8 per 128 inputs (`fp8_groups`) and the block-scaled FP8 product; else the
+    weight-only kernels."""
+    weight, fp8, scale, block, rounded, fast = operands
     flat = x.reshape(-1, x.shape[-1])
     if fast and flat.dtype in _HALF:
-        y = _weight_only(flat, weight, scale, True, block, block)
+        rows = flat.shape[0]
+        if rounded and fast == 2 and rows > FEW_ROWS:
+            q, scales = kernels.fp8_groups(flat, block, rows)
+            y = kernels.fp8_block_mm(q, fp8, scales, scale, flat.dtype)
+        else:
+            y = _weight_only(flat, weight, scale, True, block, block)
     else:
         decoded = kernels.dequantize8(weight, scale, True, block, block, flat.dtype)
         y = functional.linear(flat, decoded)

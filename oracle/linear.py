@@ -108,3 +108,17 @@ def rows8_product_f64(q: np.ndarray, xs: np.ndarray, wq: np.ndarray, ws: np.ndar
         qx = q.astype(np.float64)
         qw = wq.astype(np.float64)
     return (qx @ qw.T) * xs.reshape(-1, 1).astype(np.float64) * ws.reshape(1, -1).astype(np.float64)
+
+
+def block_product_f64(q: np.ndarray, xs: np.ndarray, wq: np.ndarray, ws: np.ndarray, block: int = 128) -> np.ndarray:
+    """fp64 block-scaled FP8 product: `sum_b (qx[:, b] @ qw[:, b].T) * xs[:, b] *
+    ws[n / block, b]` over the `block`-input blocks b, FP8 codes decoded exactly --
+    the result `torch._scaled_mm` with block-wise scales approximates
+    (`torch/quantized.py:159-166`; dequantized operands, `:167-172`)."""
+    qx = quant.decode_fp8(q).astype(np.float64)
+    qw = quant.decode_fp8(wq).astype(np.float64)
+    rows, depth = qx.shape
+    width = qw.shape[0]
+    x = (qx.reshape(rows, depth // block, block) * xs.astype(np.float64)[:, :, None]).reshape(rows, depth)
+    w = (qw.reshape(width // block, block, depth // block, block) * ws.astype(np.float64)[:, None, :, None])
+    return x @ w.reshape(width, depth).T

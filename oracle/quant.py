@@ -315,3 +315,25 @@ def rows8(x: np.ndarray, fp8: bool) -> tuple[np.ndarray, np.ndarray]:
         return encode_fp8(np.clip(v, np.float32(-448.0), np.float32(448.0))), scale
     half = np.where(v >= 0, v + np.float32(0.5), v - np.float32(0.5)).astype(np.float32)
     return np.clip(np.trunc(half), -127, 127).astype(np.int8), scale
+
+
+def fp8_groups(x: np.ndarray, group: int, padded: int) -> tuple[np.ndarray, np.ndarray]:
+    """Each `group` inputs of each row of `x` (f32 values of the input) rounded to
+    FP8 E4M3 with a scale of their own, `rows8`'s arithmetic per group, the rows
+    padded with zeros (scale 1) to `padded`. Returns (codes [padded, In] uint8, scales
+    [padded, In/group] f32). Restates `torch/kernels.py:757-795` (`_fp8_groups_kernel`,
+    `_fp8_groups`), with IEEE division.
+
+    Pin: each group equals `rows8` (already pinned against torch's cast) applied
+    to that group alone, and padded rows are zero codes with scale 1
+    (tests/test_oracle.py::test_fp8_groups_is_rows8_per_group)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, depth = x.shape
+    groups = depth // group
+    full = np.zeros((padded, depth), np.float32)
+    full[:rows] = x
+    grouped = full.reshape(padded * groups, group)
+    codes, scale = rows8(grouped, True)
+    scale = scale.reshape(padded, groups)
+    scale[rows:] = np.float32(1.0)
+    return codes.reshape(padded, depth), scale

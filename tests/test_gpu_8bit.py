@@ -167,8 +167,55 @@ def test_quantized_dispatch_against_the_reference_cpu_path(kind: str, rounded: i
         decoded = q.view(torch.float8_e4m3fn).float() * scale.to(torch.bfloat16).float().repeat_interleave(128, 0).repeat_interleave(128, 1)
         want = torch.nn.functional.linear(x, decoded.to(torch.bfloat16)) + bias
     err, top = _err(got.float().cpu().numpy(), want.float().numpy())
-    is_rounded = rounded and rows > 32 and kind in ("fp8", "int8")
+    is_rounded = rounded and rows > 32 and kind in ("fp8", "int8", "fp8_block")
     assert err <= (0.06 if is_rounded else 0.01) * top
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("rows", "padded", "width"), [(5, 8, 384), (1, 1, 128), (33, 36, 8192), (300, 300, 1152)])
+def test_fp8_groups_matches_the_oracle(dtype: torch.dtype, rows: int, padded: int, width: int) -> None:
+    """Codes and scales bit for bit, padded rows zero with scale 1, the scales a
+    column-major view as `torch._scaled_mm` reads them."""
+    g = torch.Generator().manual_seed(rows + width)
+    x = (torch.randn(rows, width, generator=g) * torch.logspace(-3, 3, rows)[:, None]).to(dtype)
+    x[0, :128] = 0
+    q, s = kernels.fp8_groups(x.to(DEV), 128, padded)
+    assert q.shape == (padded, width) and s.shape == (padded, width // 128) and s.stride(0) == 1
+    want_q, want_s = quant.fp8_groups(x.float().numpy(), 128, padded)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), want_q)
+    assert np.array_equal(s.cpu().numpy(), want_s)
+
+
+@pytest.mark.parametrize(("rows", "out", "width"), [(1, 128, 128), (37, 256, 384), (300, 384, 1024), (600, 512, 2048), (64, 1024, 8192)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fp8_block_product(rows: int, out: int, width: int, dtype: torch.dtype) -> None:
+    """The block-scaled FP8 product of rows rounded per 128 inputs and FP8 weights
+    with a scale per 128 x 128 block, against the fp64 block product of the same
+    codes and scales (f32 sums and one rounding to 16 bits apart)."""
+    g = torch.Generator().manual_seed(rows * 7 + out)
+    x = torch.randn(rows, width, generator=g).to(dtype)
+    w = torch.randn(out, width, generator=g) * 0.05
+    ws = (torch.rand(out // 128, width // 128, generator=g) + 0.5) * 1e-3
+    wq = (w / ws.repeat_interleave(128, 0).repeat_interleave(128, 1)).clamp(-448, 448).to(torch.float8_e4m3fn)
+    q, xs = kernels.fp8_groups(x.to(DEV), 128, rows)
+    y = kernels.fp8_block_mm(q, wq.to(DEV), xs, ws.to(DEV), dtype).float().cpu().numpy()
+    want = linear.block_product_f64(q.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                    wq.view(torch.uint8).numpy(), ws.numpy())
+    err, top = _err(y, want)
+    assert err <= 8e-3 * top
+    assert np.all(np.abs(y - want) <= 8e-3 * np.abs(want) + 1e-3 * top)
+
+
+def test_fp8_block_product_takes_row_major_scales() -> None:
+    """x scales given row-major [rows, In/128] (not `fp8_groups`' view) give the same product."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(40, 512, generator=g).to(torch.bfloat16)
+    wq = (torch.randn(256, 512, generator=g) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    ws = torch.rand(2, 4, generator=g) + 0.5
+    q, xs = kernels.fp8_groups(x.to(DEV), 128, 40)
+    a = kernels.fp8_block_mm(q, wq.to(DEV), xs, ws.to(DEV), torch.bfloat16)
+    b = kernels.fp8_block_mm(q, wq.to(DEV), xs.contiguous(), ws.to(DEV), torch.bfloat16)
+    assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("rows", [1, 256])

@@ -334,3 +334,42 @@ def test_gptq_second_format_has_no_zero_offset() -> None:
     qweight, qzeros = pack_gptq(q, zero, offset=0)
     _, got, _ = quant.repack_int4(qweight, qzeros, "gptq", 64, 0, None)
     assert np.array_equal(got, zero.T)
+
+
+# ------------------------------------------------- FP8 groups / block product
+
+
+def test_fp8_groups_is_rows8_per_group() -> None:
+    """Catches a scale taken over the row instead of the group, groups laid out
+    wrongly, or padded rows that are not zero codes with scale 1."""
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal((3, 384)) * np.array([1.0, 100.0, 1e-3])[:, None]).astype(np.float32)
+    x[1, 128:256] = 0.0  # an all-zero group: scale 1e-12 / 448, codes 0
+    q, s = quant.fp8_groups(x, 128, 5)
+    assert q.shape == (5, 384) and s.shape == (5, 3)
+    for r in range(3):
+        for g in range(3):
+            cq, cs = quant.rows8(x[r:r + 1, 128 * g:128 * (g + 1)], True)
+            assert np.array_equal(q[r, 128 * g:128 * (g + 1)], cq[0]) and s[r, g] == cs[0, 0]
+    assert not q[3:].any() and np.all(s[3:] == 1.0)
+    assert s[1, 1] == np.float32(1e-12) / np.float32(448.0)
+
+
+def test_block_product_reference_against_a_loop() -> None:
+    """The block product against a brute-force loop over blocks (catches a
+    weight scale indexed by the wrong block axis or an x scale per row instead of
+    per block)."""
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    q, xs = quant.fp8_groups(x, 128, 2)
+    wq = quant.encode_fp8(np.clip(rng.standard_normal((256, 256)) * 30, -448, 448).astype(np.float32))
+    ws = rng.random((2, 2)).astype(np.float32) + 0.5
+    got = linear.block_product_f64(q, xs, wq, ws)
+    dq, dw = quant.decode_fp8(q).astype(np.float64), quant.decode_fp8(wq).astype(np.float64)
+    want = np.zeros((2, 256))
+    for m in range(2):
+        for n in range(256):
+            for b in range(2):
+                k = slice(128 * b, 128 * (b + 1))
+                want[m, n] += (dq[m, k] @ dw[n, k]) * xs[m, b] * ws[n // 128, b]
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
