@@ -15,10 +15,10 @@ the reference's own prefill strategy (HIP dequantize + hipBLASLt), the 8-bit
 paths (config 1: int8 per-row weight-only GEMV 4096x4096; config 4: FP8 weight
 with per-token FP8 activations, K=8192 N=28672 at M=1/256/4096, against HBM
 and fp8 MFMA peaks), the int4 Llama-shaped decode step (config 5), the GPTQ /
-AWQ checkpoint repack kernel, a measured copy-bandwidth ceiling, and the
+AWQ checkpoint repack kernel, gpt-oss-20B's MXFP4 expert projections at decode, a measured copy-bandwidth ceiling, and the
 reference's CPU path timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|8bit|llama|checkpoint|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|8bit|llama|checkpoint|mxfp4|all]
 
 The default K = 2000 GEMV calls (~16 ms) times the steady state of a decode
 loop; 200 calls (~1.8 ms) read 10-15% slower, the clock still ramping.
@@ -51,7 +51,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=2000)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "llama", "checkpoint", "all"), default="all")
+    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "llama", "checkpoint", "mxfp4", "all"), default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
@@ -179,6 +179,10 @@ def main() -> int:
         extra["llama_int4_decode"] = llama_decode(torch, kernels, dev)
     torch.cuda.synchronize()
 
+    if args.only in ("mxfp4", "all"):
+        extra["mxfp4_experts_gpt_oss_20b"] = mxfp4_decode(torch, kernels, dev, timed_graph, not args.no_cpu)
+    torch.cuda.synchronize()
+
     if args.only in ("checkpoint", "all"):
         extra["int4_repack_K4096_N14336"] = checkpoint_repack(torch, kernels, dev, timed_graph, not args.no_cpu)
     torch.cuda.synchronize()
@@ -215,6 +219,12 @@ def main() -> int:
         metric_value, unit, ms = entry["tokens_per_s"], "tokens/s", entry["ms_per_step"]
         config = {"workload": "int4 g128 Llama-3.1-8B-shaped decode step, batch 1, context 1024", "baseline_config": 5}
         roofline = None
+    elif "mxfp4_experts_gpt_oss_20b" in extra:  # --only mxfp4: the gate/up projection at batch 1
+        entry = extra["mxfp4_experts_gpt_oss_20b"]["gate_up_B1"]
+        metric_value, unit, ms = entry["gbps"], "GB/s", entry["us"] / 1e3
+        config = {"workload": "MXFP4 experts (gpt-oss-20B gate/up, 32 experts, top 4), batch 1"}
+        roofline = {"bound": "hbm", "achieved": entry["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": entry["frac_hbm_peak"], "traffic": None}
     else:  # --only checkpoint: the GPTQ repack of one layer
         entry = extra["int4_repack_K4096_N14336"]["gptq"]
         metric_value, unit, ms = entry["gbps"], "GB/s", entry["us"] / 1e3
@@ -481,6 +491,58 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         del graph, lin_graph, glue_graph, calls
     del model
     return out
+
+
+def mxfp4_decode(torch, kernels, dev, timed_graph, with_cpu: bool) -> dict[str, object]:
+    """gpt-oss-20B's MXFP4 expert projections at a decoding step
+    (`std.quant::mxfp4_experts`, `torch/kernels.py:94-209`): 32 experts, top 4,
+    gate/up 2880 -> 5760 and down 2880 -> 2880, batch 1 and 8. Random codes and
+    scales (E8M0 118..135), random-init; each call picks the next 4 (or 32) of the
+    experts over two copies of the expert weights (564 MB for gate/up > the
+    Infinity Cache), so the chosen experts' bytes come from HBM. Bytes: the chosen
+    experts' blocks and scales (distinct experts once each: the kernel reads a pair's
+    expert in full, a repeated expert from L2 / the Infinity Cache), x and y."""
+    count, top, width = 32, 4, 2880
+    groups = width // 32
+    g = torch.Generator(device=dev).manual_seed(0)
+    found: dict[str, object] = {}
+    for name, out in (("gate_up", 5760), ("down", 2880)):
+        copies = [(torch.randint(0, 256, (count, out, groups, 16), generator=g, device=dev, dtype=torch.uint8),
+                   torch.randint(118, 136, (count, out, groups), generator=g, device=dev, dtype=torch.uint8))
+                  for _ in range(2)]
+        for batch in (1, 8):
+            x = torch.randn(batch, top, width, generator=g, device=dev).to(torch.bfloat16)
+            sets = []
+            for i in range(16):
+                ids = (torch.arange(batch * top, device=dev) + i * batch * top) % count
+                sets.append((copies[i % 2], ids.reshape(batch, top)))
+            launches = [lambda c=c, e=e: kernels.mxfp4_experts(x, c[0], c[1], e) for c, e in sets]
+            sec = timed_graph(launches, 400, 10)
+            distinct = min(batch * top, count)
+            nbytes = distinct * out * (groups * 16 + groups) + batch * top * (width * 2 + out * 2)
+            entry = {"us": round(sec * 1e6, 2), "gbps": round(nbytes / sec / 1e9, 1),
+                     "frac_hbm_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4), "bytes_per_call": nbytes}
+            if with_cpu and batch == 1:
+                # The reference's fallback (generated `_mxfp4_experts` off its kernel,
+                # `torch_source.cpp:1595-1601`): gather the chosen experts, widen in f32, einsum.
+                table = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0,
+                                      -4.0, -6.0])
+                blocks, scales = copies[0][0].cpu(), copies[0][1].cpu()
+                xc, ec = x.cpu(), sets[0][1].cpu()
+                t0 = time.perf_counter()
+                taken = blocks[ec]
+                values = torch.stack([table[(taken & 15).long()], table[(taken >> 4).long()]], dim=-1)
+                factor = torch.exp2(scales[ec].float() - 127)[..., None]
+                weight = (values.reshape(*taken.shape[:-1], 32) * factor).reshape(*taken.shape[:-2], -1)
+                torch.einsum("rki,rkoi->rko", xc.float(), weight).to(xc.dtype)
+                cpu_s = time.perf_counter() - t0
+                entry["cpu_reference_fallback_ms"] = round(cpu_s * 1e3, 1)
+                entry["cpu_reference_fallback_gbps"] = round(nbytes / cpu_s / 1e9, 3)
+                del blocks, scales, taken, values, weight
+            found[f"{name}_B{batch}"] = entry
+            del x
+        del copies
+    return found
 
 
 def checkpoint_repack(torch, kernels, dev, timed_graph, with_cpu: bool) -> dict[str, object]:

@@ -197,6 +197,27 @@ LNQ_API LnqStatus lnq_mm8_block(const uint8_t* qx, const uint8_t* weight, const 
                                 int64_t out_features, int64_t in_features, int32_t dtype,
                                 void* stream);
 
+/* ------------------------------------------------------------------- MXFP4
+ * gpt-oss's expert weights: blocks [E, out, in/32, 16] bytes (32 FP4 E2M1 values a
+ * block, element 2j in the low nibble of byte j), scales [E, out, in/32] E8M0 bytes
+ * (a block's weights are its E2M1 values times 2^(scale - 127)).
+ */
+
+/* y[r, k, o] = sum_i x[r, k, i] * W[experts[r, k], o, i] for rows x chosen (r, k)
+ * pairs, x [rows, chosen, in] of `dtype` (bf16 or f16) with element strides
+ * x_row_stride and x_slot_stride (0 for an input the chosen experts of a row
+ * share; both multiples of 8, x 16-byte aligned, its last axis contiguous),
+ * experts [rows, chosen] int64, y [rows, chosen, out] of `dtype`. Each block's
+ * products are summed in f32 and scaled, the blocks added in f32, the sum rounded
+ * once. An expert index outside 0 .. num_experts-1 gives zeros. in % 32 == 0,
+ * in <= 8192. Replaces: torch/kernels.py:94-209 `mxfp4_experts` (the generated
+ * `_mxfp4_experts`, src/backend/torch_source.cpp:1579-1600). */
+LNQ_API LnqStatus lnq_mxfp4_experts(const void* x, int64_t x_row_stride, int64_t x_slot_stride,
+                                    const uint8_t* blocks, const uint8_t* scales,
+                                    const int64_t* experts, void* y, int64_t rows, int64_t chosen,
+                                    int64_t num_experts, int64_t out_features,
+                                    int64_t in_features, int32_t dtype, void* stream);
+
 /* ------------------------------------------------------- decode-step glue (bf16)
  * What a decoder layer runs between its quantized linear layers, for the int4
  * Llama-shaped decode step of BASELINE config 5. No counterpart in the reference's

@@ -251,6 +251,14 @@ __device__ inline void wait_vm_rt(int n) {
 #define LNQ_MFMA_IN_AGPRS() __asm__ volatile("" ::: "a0")
 
 // Wave-wide reductions (64 lanes).
+// Butterfly sum over the wave: every lane gets the same value, added in the
+// same order on every lane.
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 __device__ inline float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -22,12 +22,6 @@ constexpr int MAX_GROUP = 8;  // query heads per KV head
 constexpr int CHUNK = 64;  // cache positions a workgroup takes
 }  // namespace decode
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 // Sum over the block (256 threads), the same value returned to every thread.
 __device__ inline float block_sum(float v, float* red) {
   v = wave_sum(v);

@@ -12,6 +12,10 @@ and no bytes are held beyond the model's own. Otherwise it returns the
 reference's `_int4_pack` falls back (`torch_source.cpp:1501-1504`), and
 `_int4_linear` multiplies it with `F.linear`.
 
+`_mxfp4_experts(x, blocks, scales, experts)` is the helper for
+`std.quant::mxfp4_experts` (`torch_source.cpp:1579-1600`): the chosen experts'
+MXFP4 weights multiplied by one HIP kernel.
+
 CPU tensors raise: this package has no CPU path.
 """
 
@@ -72,3 +76,16 @@ def _int4_linear(
     y = functional.linear(flat, weight.to(flat.dtype))
     y = y.reshape(*x.shape[:-1], y.shape[-1])
     return y if bias is None else y + bias
+
+
+def _mxfp4_experts(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, experts: torch.Tensor) -> torch.Tensor:
+    """`std.quant::mxfp4_experts` as the generated module calls it
+    (`torch_source.cpp:426-438, 1579-1600`): the chosen experts' MXFP4 bytes read as
+    they are by one HIP kernel. The reference takes its kernel for up to 32 (row,
+    slot) pairs and otherwise gathers the chosen experts as f32 weights; the HIP
+    kernel runs at any count here (each pair still reads its own expert's bytes,
+    never a widened copy). `x` is [R, K, In], or [R, 1, In] expanded by the caller
+    for the shared form."""
+    if not x.is_cuda:
+        raise LinnetError("_mxfp4_experts: linnet_amd runs on the GPU; x is on " + str(x.device))
+    return kernels.mxfp4_experts(x, blocks, scales, experts)

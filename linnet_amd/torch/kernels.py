@@ -224,6 +224,38 @@ def int4_repack(
     return packed, zero
 
 
+# ------------------------------------------------------------------------ MXFP4
+
+
+def mxfp4_experts(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, experts: torch.Tensor) -> torch.Tensor:
+    """`y[r, k, o] = sum_i x[r, k, i] * W[experts[r, k], o, i]`, with `W` the MXFP4
+    weights `blocks` ([E, Out, G, 16] u8) and `scales` ([E, Out, G] u8, E8M0)
+    read as they are and widened in registers (`torch/kernels.py:94-209`). `x` is
+    [R, K, In] bf16 or f16 (an expanded view with a zero slot stride, for an input
+    the chosen experts share, is read without a copy)."""
+    device = _on_gpu("mxfp4_experts", x, blocks, scales, experts)
+    if x.dim() != 3 or blocks.dim() != 4 or scales.dim() != 3 or experts.dim() != 2:
+        raise LinnetError("mxfp4_experts: x [R, K, In], blocks [E, Out, G, 16], scales [E, Out, G], experts [R, K]")
+    rows, chosen, width = x.shape
+    count, out_features, groups, sixteen = blocks.shape
+    if sixteen != 16 or blocks.dtype != torch.uint8 or scales.dtype != torch.uint8:
+        raise LinnetError("mxfp4_experts: blocks are [E, Out, G, 16] and scales [E, Out, G], both uint8")
+    if tuple(scales.shape) != (count, out_features, groups) or width != groups * 32:
+        raise LinnetError(f"mxfp4_experts: x's In={width}, blocks {tuple(blocks.shape)}, scales {tuple(scales.shape)}")
+    if tuple(experts.shape) != (rows, chosen) or experts.is_floating_point():
+        raise LinnetError(f"mxfp4_experts: experts are integers [{rows}, {chosen}]")
+    code = _code(x.dtype, "mxfp4_experts")
+    if (x.stride(2) != 1 or x.data_ptr() % 16 or x.stride(0) % 8 or x.stride(1) % 8):
+        x = x.contiguous()
+    blocks, scales = blocks.contiguous(), scales.contiguous()
+    ids = experts.to(torch.int64).contiguous()
+    y = torch.empty(rows, chosen, out_features, dtype=x.dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_mxfp4_experts", _ptr(x), x.stride(0), x.stride(1), _ptr(blocks), _ptr(scales), _ptr(ids),
+                  _ptr(y), rows, chosen, count, out_features, width, code, _stream(device))
+    return y
+
+
 # ------------------------------------------------------------------------ 8-bit
 
 

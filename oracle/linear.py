@@ -122,3 +122,12 @@ def block_product_f64(q: np.ndarray, xs: np.ndarray, wq: np.ndarray, ws: np.ndar
     x = (qx.reshape(rows, depth // block, block) * xs.astype(np.float64)[:, :, None]).reshape(rows, depth)
     w = (qw.reshape(width // block, block, depth // block, block) * ws.astype(np.float64)[:, None, :, None])
     return x @ w.reshape(width, depth).T
+
+
+def mxfp4_experts_f64(x: np.ndarray, blocks: np.ndarray, scales: np.ndarray, experts: np.ndarray) -> np.ndarray:
+    """fp64 `y[r, k, o] = sum_i x[r, k, i] * W[experts[r, k], o, i]` with `W` the
+    dequantized MXFP4 experts (`stdlib/quant.linnet:343-356`, `mxfp4_experts`; the
+    generated fallback, `torch_source.cpp:1595-1601`, computes it in f32)."""
+    weight = quant.dequantize_mxfp4(blocks, scales).astype(np.float64)  # [E, Out, In]
+    chosen = weight[np.asarray(experts)]  # [R, K, Out, In]
+    return np.einsum("rki,rkoi->rko", np.asarray(x, dtype=np.float64), chosen)

@@ -337,3 +337,28 @@ def fp8_groups(x: np.ndarray, group: int, padded: int) -> tuple[np.ndarray, np.n
     scale = scale.reshape(padded, groups)
     scale[rows:] = np.float32(1.0)
     return codes.reshape(padded, depth), scale
+
+
+# ---------------------------------------------------------------------- MXFP4
+
+# E2M1 values by code, as the generated module's fallback tabulates them
+# (`src/backend/torch_source.cpp:1585-1586`, `_FP4`).
+FP4_VALUES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0],
+                      dtype=np.float32)
+
+
+def dequantize_mxfp4(blocks: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """MXFP4 blocks [..., G, 16] bytes and E8M0 scales [..., G] as the f32 weights
+    [..., G * 32]: byte j's low nibble is element 2j, its high one 2j + 1, each
+    E2M1 code's value times 2^(scale - 127). Restates `stdlib/quant.linnet:334-341`
+    (`dequantize_mxfp4`) and the generated fallback (`torch_source.cpp:1597-1600`).
+
+    Pin: `FP4_VALUES` against E2M1's definition (sign, two exponent bits of bias
+    1, one mantissa bit, exponent 0 subnormal), the scale against `np.ldexp`, and
+    the element order against a hand-built block
+    (tests/test_oracle.py::test_mxfp4_decoding_from_the_format_definition)."""
+    b = np.asarray(blocks, dtype=np.uint8)
+    values = np.stack([FP4_VALUES[b & 15], FP4_VALUES[b >> 4]], axis=-1)
+    values = values.reshape(*b.shape[:-1], 32)
+    factor = np.ldexp(np.float32(1.0), np.asarray(scales).astype(np.int32) - 127).astype(np.float32)
+    return (values * factor[..., None]).reshape(*b.shape[:-2], b.shape[-2] * 32)

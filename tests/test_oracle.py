@@ -373,3 +373,39 @@ def test_block_product_reference_against_a_loop() -> None:
                 k = slice(128 * b, 128 * (b + 1))
                 want[m, n] += (dq[m, k] @ dw[n, k]) * xs[m, b] * ws[n // 128, b]
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+
+
+# ---------------------------------------------------------------------- MXFP4
+
+
+def test_mxfp4_decoding_from_the_format_definition() -> None:
+    """E2M1: sign bit 3, exponent bits 1-2 (bias 1), mantissa bit 0, exponent 0
+    subnormal (value = mantissa / 2); E8M0: 2^(s - 127). Catches a swapped nibble
+    order, a wrong table entry or an off-by-one scale bias."""
+    def e2m1(code: int) -> float:
+        sign = -1.0 if code & 8 else 1.0
+        exponent, mantissa = (code >> 1) & 3, code & 1
+        value = mantissa * 0.5 if exponent == 0 else 2.0 ** (exponent - 1) * (1 + mantissa / 2)
+        return sign * value
+
+    assert [float(v) for v in quant.FP4_VALUES] == [e2m1(c) for c in range(16)]
+    block = np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4)  # byte j: low j, high 15-j
+    got = quant.dequantize_mxfp4(block.reshape(1, 16), np.array([130], np.uint8))
+    want = np.array([[e2m1(j) * 8, e2m1(15 - j) * 8] for j in range(16)], np.float32).reshape(32)
+    assert np.array_equal(got, want)
+    assert quant.dequantize_mxfp4(np.full((1, 16), 0x22, np.uint8), np.array([0], np.uint8))[0] == np.float32(2.0**-127)
+
+
+def test_mxfp4_product_reference_against_a_loop() -> None:
+    rng = np.random.default_rng(15)
+    blocks = rng.integers(0, 256, (3, 4, 2, 16)).astype(np.uint8)
+    scales = rng.integers(120, 134, (3, 4, 2)).astype(np.uint8)
+    x = rng.standard_normal((2, 2, 64))
+    experts = np.array([[2, 0], [1, 2]])
+    got = linear.mxfp4_experts_f64(x, blocks, scales, experts)
+    w = quant.dequantize_mxfp4(blocks, scales)
+    for r in range(2):
+        for k in range(2):
+            for o in range(4):
+                assert np.isclose(got[r, k, o], sum(x[r, k, i] * float(w[experts[r, k], o, i]) for i in range(64)),
+                                  rtol=1e-12, atol=1e-12)
