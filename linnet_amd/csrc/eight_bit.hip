@@ -214,6 +214,130 @@ __global__ __launch_bounds__(256) void w8_skinny_kernel(
   }
 }
 
+// =================================================================== one row
+// One row of x (a decoding step), groups a multiple of 128 inputs, K % 512 == 0.
+// The skinny kernel's workgroups (16 output features, 4 waves each a quarter of
+// K, x staged in LDS) with wider reads: a wave instruction reads 8 rows x 128
+// contiguous bytes (lane: row l % 8, 16-byte piece l / 8) instead of 16 rows x 64
+// bytes, which streams faster (a 235 MB pure read in this workgroup shape: 34-35
+// against 39 us). Lane l then holds, for B column c = l % 16, piece 2 (l / 16) +
+// c / 8 of row c % 8: columns 0-7 carry the even pieces and 8-15 the odd ones
+// of the same 8 rows, so A row 0 takes x at the even pieces and A row 1 at the
+// odd ones, and row r's sum is C[0][r] + C[1][8 + r]. Two loads (rows 0-7 and
+// 8-15) per 128 inputs, each two MFMA 16x16x32 (bytes 0-7 and 8-15 of a piece).
+template <int DT, int FP8>
+__global__ __launch_bounds__(256) void w8_row_kernel(const uint16_t* __restrict__ x,
+                                                     const uint8_t* __restrict__ weight,
+                                                     const float* __restrict__ scale,
+                                                     uint16_t* __restrict__ y, int N, int K, int G,
+                                                     int row_block, int scale_cols) {
+  using E = Elem<DT>;
+  constexpr float offset = FP8 ? 0.0f : 128.0f;
+  constexpr int D = 16;  // loads in flight per wave (8 steps of 128 inputs)
+  __shared__ float red[4][16];
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int j = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int steps = K >> 7;  // 128 inputs a step
+  const int per_wave = steps >> 2;
+  const int sb = wave * per_wave, se = sb + per_wave;
+  const int steps_per_group = G >> 7;
+
+  // Load rows: half h reads rows n0 + 8h + l % 8 (clamped: rows past N are not stored).
+  const uint8_t* wrow[2];
+  const float* srow[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    wrow[h] = weight + static_cast<size_t>(min(n0 + 8 * h + (lane & 7), N - 1)) * K + 16 * (lane >> 3);
+    // The scale of this lane's B column (row n0 + 8h + col % 8).
+    const int srow_n = min(n0 + 8 * h + (col & 7), N - 1);
+    srow[h] = scale + static_cast<size_t>(srow_n / row_block) * scale_cols;
+  }
+  u32x4 ones;
+  ones.x = ones.y = ones.z = ones.w = E::ONE2;
+  f32x4 acc[2], C[2], Cx;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+    C[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  Cx = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 rw[D];
+  auto fetch = [&](int slot, int step) {
+    rw[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[slot & 1] + 128 * step));
+  };
+#pragma unroll
+  for (int i = 0; i < D; ++i)
+    if (sb + (i >> 1) < se) fetch(i, sb + (i >> 1));
+  for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
+    *reinterpret_cast<u32x4*>(&xl[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
+  __syncthreads();
+  // A row m (lane m = l % 16): x at piece 2 j + (m & 1); rows 2..15 repeat rows
+  // 0 / 1 and their outputs are not used.
+  const int apiece = 2 * j + (col & 1);
+  for (int s0 = sb; s0 < se; s0 += D / 2) {
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i) {
+      const int step = s0 + i;
+      if (step >= se) break;
+      u32x4 xa[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) xa[t] = *reinterpret_cast<const u32x4*>(&xl[128 * step + 16 * apiece + 8 * t]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 w = rw[2 * i + h];
+        if (step + D / 2 < se) fetch(2 * i + h, step + D / 2);
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          uint32_t b0, b1, b2, b3;
+          widen4<DT, FP8>(words[2 * t], b0, b1);
+          widen4<DT, FP8>(words[2 * t + 1], b2, b3);
+          C[h] = mfma16x16x32<DT>(xa[t], u32x4{b0, b1, b2, b3}, C[h]);
+        }
+      }
+      if constexpr (!FP8) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) Cx = mfma16x16x32<DT>(xa[t], ones, Cx);
+      }
+      // A group closes at its last step or where this wave's quarter of K ends.
+      if ((step + 1) % steps_per_group == 0 || step + 1 == se) {
+        const int g = step / steps_per_group;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float sc = srow[h][g];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float d = FP8 ? C[h][r] : fmaf(-offset, Cx[r], C[h][r]);
+            acc[h][r] = fmaf(sc, d, acc[h][r]);
+          }
+          C[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        Cx = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+  // Lane col (j = 0) holds A row 0 in register 0 and row 1 in register 1: row
+  // col % 8 of half h is C[0][col % 8] + C[1][8 + col % 8].
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float mine = col < 8 ? acc[h][0] : acc[h][1];
+    const float v = mine + __shfl_xor(mine, 8, 64);
+    if (j == 0 && col < 8) red[wave][8 * h + col] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int n = n0 + threadIdx.x;
+    const float v = red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] + red[3][threadIdx.x];
+    if (n < N) y[n] = E::from_f32(v);
+  }
+}
+
 // ================================================================== dequant8
 // 16 weight bytes per thread: out = widen(w) * scale in f32, rounded once.
 template <int DT, int FP8>
@@ -390,7 +514,10 @@ static void launch_w8_skinny(const void* x, const uint8_t* w, const float* s, vo
                              int N, int K, int G, int rb, int cols, hipStream_t stream) {
   const auto* xs = static_cast<const uint16_t*>(x);
   auto* ys = static_cast<uint16_t*>(y);
-  if (M == 1 && K <= 32768)
+  if (M == 1 && K <= 32768 && K % 512 == 0 && G % 128 == 0)
+    hipLaunchKernelGGL((w8_row_kernel<DT, FP8>), dim3((N + 15) / 16), dim3(256), K * 2, stream, xs, w, s, ys, N, K, G,
+                       rb, cols);
+  else if (M == 1 && K <= 32768)
     hipLaunchKernelGGL((w8_skinny_kernel<DT, FP8, 1, true>), dim3((N + 15) / 16, 1), dim3(256), K * 2, stream,
                        xs, w, s, ys, M, N, K, G, rb, cols);
   else if (M <= 16)

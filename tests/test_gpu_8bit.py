@@ -124,6 +124,25 @@ def test_weight_only_kernels(fp8: bool, rows: int, out: int, group: int, row_blo
 
 
 @pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize(("out", "width", "group", "row_block", "dtype"), [
+    (300, 1024, 0, 1, torch.bfloat16), (77, 2048, 128, 1, torch.float16), (256, 4096, 128, 128, torch.bfloat16),
+    (40, 384, 0, 1, torch.bfloat16), (1000, 8192, 256, 1, torch.bfloat16), (128, 16384, 0, 1, torch.float16),
+    (24, 512, 64, 1, torch.bfloat16),
+])
+def test_one_row_kernels(fp8: bool, out: int, width: int, group: int, row_block: int, dtype: torch.dtype) -> None:
+    """One row of x: the wide-read one-row kernel (K % 512 == 0, groups of 128k) and
+    the skinny kernel's one-row form (the rest), against the f64 product."""
+    if group and out % row_block:
+        pytest.skip("blocks tile the weight")
+    q, scale, deq = _eight_bit(out, width, fp8, seed=out + width, group=group, row_block=row_block)
+    x = torch.randn(1, width, generator=torch.Generator().manual_seed(width)).to(dtype)
+    y = kernels.gemv8(x.to(DEV), q.to(DEV), scale.to(DEV), fp8, group, row_block).float().cpu().numpy()
+    want = linear.product_f64(x.float().numpy(), deq)
+    err, top = _err(y, want)
+    assert err <= 0.01 * top
+
+
+@pytest.mark.parametrize("fp8", [True, False])
 @pytest.mark.parametrize(("rows", "out", "width"), [(33, 256, 512), (256, 200, 1024), (130, 128, 128), (1, 64, 256)])
 def test_8bit_products(fp8: bool, rows: int, out: int, width: int) -> None:
     q, scale, deq = _eight_bit(out, width, fp8, seed=out)
