@@ -224,6 +224,21 @@ def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, 
     assert (y.float() - other).abs().max().item() <= 1e-2 * other.abs().max().item()
 
 
+@pytest.mark.parametrize("rows", [17, 32, 45, 64])
+def test_wide_outputs_run_the_gemv_per_16_rows(rows: int) -> None:
+    """17..64 rows over N >= 8192: the automatic choice runs the few-token GEMV
+    once per 16-row chunk (with a ragged last chunk and the bias in each)."""
+    packed, scale, zero = _layer(8192, 1024, 128, seed=rows)
+    x = torch.randn(rows, 1024, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+    bias = torch.randn(8192, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    args = (packed.to(DEV), scale.to(DEV), zero.to(DEV))
+    y = kernels.int4_linear(x.to(DEV), *args)
+    _check_linear(x, packed, scale, zero, y)
+    for c in range(0, rows, 16):
+        assert torch.equal(y[c:c + 16], kernels.int4_linear(x[c:c + 16].to(DEV), *args, kernel="gemv"))
+    assert torch.equal(kernels.int4_linear(x.to(DEV), *args, bias), y + bias)
+
+
 def test_out_receives_the_product() -> None:
     packed, scale, zero = _layer(96, 512, 128, seed=8)
     args = (packed.to(DEV), scale.to(DEV), zero.to(DEV))
