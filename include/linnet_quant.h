@@ -237,7 +237,8 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
  * kt_cache [rows, kv_heads, head_dim, cap] (transposed) and v_cache [rows, kv_heads,
  * cap, head_dim]; out [rows, heads*head_dim] = softmax(q K^T / sqrt(head_dim)) V over
  * positions 0..pos, in chunks of 64 positions merged in order (split-K). head_dim 64
- * or 128; heads / kv_heads <= 8; cap a multiple of 4 and the caches 16-byte aligned.
+ * or 128; heads / kv_heads <= 8; pos < 262144; cap a multiple of 4 and the caches
+ * 16-byte aligned.
  * `workspace` (f32, caller-owned) holds lnq_decode_attention_workspace(rows, kv_heads,
  * head_dim, pos) floats. */
 LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,

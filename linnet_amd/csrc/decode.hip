@@ -20,6 +20,7 @@ namespace decode {
 constexpr int THREADS = 256;
 constexpr int MAX_GROUP = 8;  // query heads per KV head
 constexpr int CHUNK = 64;  // cache positions a workgroup takes
+constexpr int MAX_CHUNKS = 4096;  // chunks the merge holds: positions up to 262144
 }  // namespace decode
 
 // Sum over the block (256 threads), the same value returned to every thread.
@@ -63,6 +64,73 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_kernel(uint16_t* __re
   const float scale = rsqrtf(block_sum(ss, red) / static_cast<float>(hidden) + eps);
   for (int i = threadIdx.x; i < hidden; i += decode::THREADS)
     hr[i] = f32_to_bf16_bits(bf16_bits_to_f32(xr[i]) * scale * w[i]);
+}
+
+// The same with the row held in registers: thread t owns 16-byte chunks t,
+// t + 256, ... (CH of them: hidden <= 2048 CH, hidden % 8 == 0), every load of x,
+// delta and the weight issued before any is used (the scalar loop above waits on
+// each of its 16 loads a thread in turn: 14 us for one 4096-wide row).
+template <int CH>
+__global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* __restrict__ x,
+                                                                      const uint16_t* __restrict__ delta,
+                                                                      const float* __restrict__ w,
+                                                                      uint16_t* __restrict__ h, int hidden, float eps) {
+  __shared__ float red[4];
+  uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * hidden;
+  uint16_t* hr = h + static_cast<size_t>(blockIdx.x) * hidden;
+  const uint16_t* dr = delta ? delta + static_cast<size_t>(blockIdx.x) * hidden : nullptr;
+  const int chunks = hidden >> 3;
+  u32x4 xv[CH], dv[CH];
+  f32x4 wv[CH][2];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int i = threadIdx.x + c * decode::THREADS;
+    if (i < chunks) {
+      xv[c] = *reinterpret_cast<const u32x4*>(xr + 8 * i);
+      dv[c] = dr ? *reinterpret_cast<const u32x4*>(dr + 8 * i) : u32x4{0u, 0u, 0u, 0u};
+      wv[c][0] = *reinterpret_cast<const f32x4*>(w + 8 * i);
+      wv[c][1] = *reinterpret_cast<const f32x4*>(w + 8 * i + 4);
+    }
+  }
+  float v[CH][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int i = threadIdx.x + c * decode::THREADS;
+    if (i >= chunks) continue;
+    u32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float lo = bf16_bits_to_f32(static_cast<uint16_t>(xv[c][e] & 0xffffu));
+      float hi = bf16_bits_to_f32(static_cast<uint16_t>(xv[c][e] >> 16));
+      if (dr) {
+        lo = bf16_bits_to_f32(f32_to_bf16_bits(lo + bf16_bits_to_f32(static_cast<uint16_t>(dv[c][e] & 0xffffu))));
+        hi = bf16_bits_to_f32(f32_to_bf16_bits(hi + bf16_bits_to_f32(static_cast<uint16_t>(dv[c][e] >> 16))));
+      }
+      v[c][2 * e] = lo;
+      v[c][2 * e + 1] = hi;
+      out[e] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+    }
+    if (dr) *reinterpret_cast<u32x4*>(xr + 8 * i) = out;
+    // (The sum of squares runs chunk by chunk: another order of additions than
+    // the scalar kernel's, element by element.)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(v[c][e], v[c][e], ss);
+  }
+  const float scale = rsqrtf(block_sum(ss, red) / static_cast<float>(hidden) + eps);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int i = threadIdx.x + c * decode::THREADS;
+    if (i >= chunks) continue;
+    u32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = f32_to_bf16_bits(v[c][2 * e] * scale * wv[c][e >> 1][(2 * e) & 3]);
+      const uint32_t hi = f32_to_bf16_bits(v[c][2 * e + 1] * scale * wv[c][e >> 1][(2 * e + 1) & 3]);
+      out[e] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(hr + 8 * i) = out;
+  }
 }
 
 // Split-K decode attention. Workgroup (row, KV head, chunk c) takes positions
@@ -109,6 +177,28 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   float* vcb = vc + static_cast<size_t>(rk) * cap * HD;
   const bool owner = pos >= l0 && pos < l0 + C;
 
+  // The chunk's keys and values: every load issued first (registers), the
+  // rotary embedding and the scores after. Key thread (dimension group dg,
+  // positions 4 p4 .. 4 p4 + 3); value thread (dimensions 4 d4 .. 4 d4 + 3,
+  // positions pg, pg + PG, ...). Position pos is the new key / value (from LDS).
+  const int p4 = tid & 15, dg = tid >> 4;
+  const int lp = l0 + 4 * p4;
+  const int d4 = tid % DV, pg = tid / DV;
+  constexpr int VJ = C / PG;  // value positions a thread takes
+  float4 kreg[DPG], vreg[VJ];
+#pragma unroll
+  for (int dd = 0; dd < DPG; ++dd) {
+    const int d = dg * DPG + dd;
+    kreg[dd] = lp < cap ? *reinterpret_cast<const float4*>(ktb + static_cast<size_t>(d) * cap + lp)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int jj = 0; jj < VJ; ++jj) {
+    const int j = pg + jj * PG;
+    vreg[jj] = j < n && l0 + j != pos ? *reinterpret_cast<const float4*>(vcb + static_cast<size_t>(l0 + j) * HD + 4 * d4)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
   // Rotary embedding (pairs i, i + HD/2); the new key and value into LDS, and into
   // the caches by the chunk that holds pos.
   for (int t = tid; t < (G + 1) * HALF; t += decode::THREADS) {
@@ -135,10 +225,8 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   }
   __syncthreads();
 
-  // Partial scores: thread (dimension group dg, positions 4 p4 .. 4 p4 + 3).
+  // Partial scores of this thread's dimension group.
   {
-    const int p4 = tid & 15, dg = tid >> 4;
-    const int lp = l0 + 4 * p4;
     float acc[G8][4];
 #pragma unroll
     for (int g = 0; g < G8; ++g)
@@ -147,9 +235,7 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
 #pragma unroll
     for (int dd = 0; dd < DPG; ++dd) {
       const int d = dg * DPG + dd;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (lp < cap) kv = *reinterpret_cast<const float4*>(ktb + static_cast<size_t>(d) * cap + lp);
-      float kk[4] = {kv.x, kv.y, kv.z, kv.w};
+      float kk[4] = {kreg[dd].x, kreg[dd].y, kreg[dd].z, kreg[dd].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (lp + e == pos) kk[e] = kn[d];
@@ -165,46 +251,38 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
       for (int e = 0; e < 4; ++e) sp[dg][g][4 * p4 + e] = acc[g][e];
   }
   __syncthreads();
-  // Scores (16 groups added in order), then per head the max and exp.
+  // Scores (16 groups added in order); a wave holds one head's 64 positions
+  // (C = 64), so its max and its sum of exp(score - max) are wave reductions.
+  static_assert(C == 64, "one head's chunk a wave");
   for (int t = tid; t < G * C; t += decode::THREADS) {
     const int g = t / C, j = t % C;
     float sc = 0.f;
 #pragma unroll
-    for (int dg = 0; dg < DG; ++dg) sc += sp[dg][g][j];
-    p[g][j] = j < n ? sc : -INFINITY;
+    for (int q = 0; q < DG; ++q) sc += sp[q][g][j];
+    sc = j < n ? sc : -INFINITY;
+    const float m = wave_max(sc);
+    const float e = j < n ? expf(sc - m) : 0.f;
+    const float sum = wave_sum(e);
+    p[g][j] = e;
+    if (j == 0) {
+      stat[g][0] = m;
+      stat[g][1] = sum;
+    }
   }
   __syncthreads();
-  if (tid < G) {
-    float m = -INFINITY;
-    for (int j = 0; j < n; ++j) m = fmaxf(m, p[tid][j]);
-    stat[tid][0] = m;
-  }
-  __syncthreads();
-  for (int t = tid; t < G * C; t += decode::THREADS) {
-    const int g = t / C, j = t % C;
-    p[g][j] = j < n ? expf(p[g][j] - stat[g][0]) : 0.f;
-  }
-  __syncthreads();
-  if (tid < G) {
-    float sum = 0.f;
-    for (int j = 0; j < n; ++j) sum += p[tid][j];
-    stat[tid][1] = sum;
-  }
-  // acc[g][d] = sum_j p[g][j] V[j][d]: thread (dimensions 4 d4 .. 4 d4 + 3, positions pg, pg + PG, ...).
+  // acc[g][d] = sum_j p[g][j] V[j][d] over this thread's positions.
   {
-    const int d4 = tid % DV, pg = tid / DV;
     float acc[G8][4];
 #pragma unroll
     for (int g = 0; g < G8; ++g)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[g][e] = 0.f;
 #pragma unroll
-    for (int j = pg; j < C; j += PG) {
+    for (int jj = 0; jj < VJ; ++jj) {
+      const int j = pg + jj * PG;
       if (j >= n) break;
-      const int lj = l0 + j;
-      float4 vv;
-      if (lj == pos) vv = make_float4(vn[4 * d4], vn[4 * d4 + 1], vn[4 * d4 + 2], vn[4 * d4 + 3]);
-      else vv = *reinterpret_cast<const float4*>(vcb + static_cast<size_t>(lj) * HD + 4 * d4);
+      const float4 vv =
+          l0 + j == pos ? make_float4(vn[4 * d4], vn[4 * d4 + 1], vn[4 * d4 + 2], vn[4 * d4 + 3]) : vreg[jj];
 #pragma unroll
       for (int g = 0; g < G8; ++g)
         if (g < G) {
@@ -238,6 +316,12 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
 template <int HD>
 __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restrict__ work, uint16_t* __restrict__ out,
                                                             int heads, int kv_heads, int chunks) {
+  // The chunks' (m, s) are read by all threads at once (thread t: chunks t, t +
+  // HD, ...), their weights exp(m - M) kept in LDS, and thread d sums its
+  // dimension over the chunks in order, eight loads in flight.
+  constexpr int WAVES = HD / 64;
+  __shared__ float wts[decode::MAX_CHUNKS];
+  __shared__ float red[WAVES];
   const int G = heads / kv_heads;
   const int row = blockIdx.x / heads, head = blockIdx.x % heads;
   const int kvh = head / G, g = head % G;
@@ -245,14 +329,36 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
   const float* base = work + (static_cast<size_t>(row) * kv_heads + kvh) * chunks * decode::MAX_GROUP * (HD + 2) +
                       g * (HD + 2);
   const size_t stride = static_cast<size_t>(decode::MAX_GROUP) * (HD + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < chunks; ++c) M = fmaxf(M, base[c * stride]);
-  float S = 0.f, o = 0.f;
-  for (int c = 0; c < chunks; ++c) {
+  auto block_reduce = [&](float v, bool is_max) {
+    v = is_max ? wave_max(v) : wave_sum(v);
+    __syncthreads();
+    if ((d & 63) == 0) red[d >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < WAVES; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+    return r;
+  };
+  float m = -INFINITY;
+  for (int c = d; c < chunks; c += HD) m = fmaxf(m, base[c * stride]);
+  const float M = block_reduce(m, true);
+  float sp = 0.f;
+  for (int c = d; c < chunks; c += HD) {
     const float w = expf(base[c * stride] - M);
-    S = fmaf(base[c * stride + 1], w, S);
-    o = fmaf(base[c * stride + 2 + d], w, o);
+    wts[c] = w;
+    sp = fmaf(base[c * stride + 1], w, sp);
   }
+  const float S = block_reduce(sp, false);  // its barriers also publish wts
+  float o = 0.f;
+  int c = 0;
+  for (; c + 8 <= chunks; c += 8) {
+    float a[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = base[(c + i) * stride + 2 + d];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o = fmaf(a[i], wts[c + i], o);
+  }
+  for (; c < chunks; ++c) o = fmaf(base[c * stride + 2 + d], wts[c], o);
   out[(static_cast<size_t>(row) * heads + head) * HD + d] = f32_to_bf16_bits(o / S);
 }
 
@@ -282,9 +388,19 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
     return LNQ_OK;
   }
   LNQ_REQUIRE(x && weight && h, "lnq_rmsnorm: null pointer");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(decode::THREADS), 0,
-                     static_cast<hipStream_t>(stream), static_cast<uint16_t*>(x), static_cast<const uint16_t*>(delta),
-                     weight, static_cast<uint16_t*>(h), static_cast<int>(hidden), eps);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto* xs = static_cast<uint16_t*>(x);
+  const auto* ds = static_cast<const uint16_t*>(delta);
+  auto* hs = static_cast<uint16_t*>(h);
+  const int H = static_cast<int>(hidden);
+  const int ch = (H + 8 * decode::THREADS - 1) / (8 * decode::THREADS);
+  const bool vec = H % 8 == 0 && ch <= 4 && aligned(x, 16) && aligned(h, 16) && aligned(weight, 16) &&
+                   (delta == nullptr || aligned(delta, 16));
+  const dim3 grid(static_cast<unsigned>(rows)), block(decode::THREADS);
+  if (vec && ch == 1) hipLaunchKernelGGL(rmsnorm_vec_kernel<1>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else if (vec && ch == 2) hipLaunchKernelGGL(rmsnorm_vec_kernel<2>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else if (vec) hipLaunchKernelGGL(rmsnorm_vec_kernel<4>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else hipLaunchKernelGGL(rmsnorm_kernel, grid, block, 0, s, xs, ds, weight, hs, H, eps);
   return launched("rmsnorm");
 }
 
@@ -301,6 +417,8 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
   LNQ_REQUIRE(cap % 4 == 0, "lnq_decode_attention: the cache capacity %lld is not a multiple of 4",
               static_cast<long long>(cap));
   const int64_t chunks = (pos + decode::CHUNK) / decode::CHUNK;
+  LNQ_REQUIRE(chunks <= decode::MAX_CHUNKS, "lnq_decode_attention: position %lld past the %d the merge takes",
+              static_cast<long long>(pos), decode::MAX_CHUNKS * decode::CHUNK - 1);
   const int64_t need = lnq_decode_attention_workspace(rows, kv_heads, head_dim, pos);
   LNQ_REQUIRE(workspace_floats >= need, "lnq_decode_attention: the workspace holds %lld floats, %lld needed",
               static_cast<long long>(workspace_floats), static_cast<long long>(need));

@@ -79,15 +79,24 @@ def test_decode_kernels_match_torch_ops() -> None:
     from linnet_amd.torch import decode
 
     g = torch.Generator().manual_seed(5)
-    x = torch.randn(3, 4096, generator=g).to(torch.bfloat16).to(DEV)
-    d = torch.randn(3, 4096, generator=g).to(torch.bfloat16).to(DEV)
-    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(DEV)
-    want_x = x + d
-    xf = want_x.float()
-    want_h = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w).to(torch.bfloat16)
-    h = decode.rmsnorm(x, w, 1e-5, d)
-    assert torch.equal(x, want_x)
-    assert (h.float() - want_h.float()).abs().max().item() <= 1e-2 * want_h.float().abs().max().item()
+    # hidden: two and four 16-byte chunks a thread (4096, 8192), a partial third
+    # (5120), and the element-wise kernel (1000, not a multiple of 8)
+    for hidden in (4096, 8192, 5120, 1000):
+        x = torch.randn(3, hidden, generator=g).to(torch.bfloat16).to(DEV)
+        d = torch.randn(3, hidden, generator=g).to(torch.bfloat16).to(DEV)
+        w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(DEV)
+        want_x = x + d
+        xf = want_x.float()
+        want_h = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w).to(torch.bfloat16)
+        h = decode.rmsnorm(x, w, 1e-5, d)
+        assert torch.equal(x, want_x)
+        assert (h.float() - want_h.float()).abs().max().item() <= 1e-2 * want_h.float().abs().max().item()
+        plain = x.clone()
+        h2 = decode.rmsnorm(plain, w, 1e-5)
+        assert torch.equal(plain, x)
+        xf = x.float()
+        want_h2 = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w).to(torch.bfloat16)
+        assert (h2.float() - want_h2.float()).abs().max().item() <= 1e-2 * want_h2.float().abs().max().item()
     gg = torch.randn(5, 1000, generator=g).to(torch.bfloat16).to(DEV)
     uu = torch.randn(5, 1000, generator=g).to(torch.bfloat16).to(DEV)
     want_a = (torch.nn.functional.silu(gg.float()) * uu.float()).to(torch.bfloat16)
@@ -114,5 +123,24 @@ def test_decode_kernels_match_torch_ops() -> None:
     want = torch.matmul(torch.softmax(s, dim=-1), vc_ref[:, :, : pos + 1].contiguous()).reshape(rows, heads * hd)
     got = decode.decode_attention(q, k, v, cos, sin, kt, vc, pos)
     assert (got.float() - want).abs().max().item() <= 1e-2 * want.abs().max().item()
+    # many chunks (the merge's eight-at-a-time loop and its tail): 2000 positions = 32 chunks, 700 = 11
+    for cap2, pos2 in ((2048, 1999), (704, 700)):
+        kt2 = torch.randn(rows, kvh, hd, cap2, generator=g).to(DEV)
+        vc2 = torch.randn(rows, kvh, cap2, hd, generator=g).to(DEV)
+        ang2 = pos2 / (500000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+        c2, s2 = torch.cos(ang2).to(DEV), torch.sin(ang2).to(DEV)
+        kr2, vr2 = kt2.clone(), vc2.clone()
+
+        def rope2(t):
+            a, b = t[..., : hd // 2], t[..., hd // 2 :]
+            return torch.cat([a * c2 - b * s2, b * c2 + a * s2], dim=-1)
+
+        q2 = rope2(q.float().view(rows, heads, hd))
+        kr2[:, :, :, pos2] = rope2(k.float().view(rows, kvh, hd))
+        vr2[:, :, pos2, :] = v.float().view(rows, kvh, hd)
+        s2_ = torch.matmul(q2.view(rows, kvh, heads // kvh, hd), kr2[..., : pos2 + 1].contiguous()) * hd**-0.5
+        want2 = torch.matmul(torch.softmax(s2_, dim=-1), vr2[:, :, : pos2 + 1].contiguous()).reshape(rows, heads * hd)
+        got2 = decode.decode_attention(q, k, v, c2, s2, kt2, vc2, pos2)
+        assert (got2.float() - want2).abs().max().item() <= 1e-2 * want2.abs().max().item()
     assert torch.equal(kt[:, :, :, pos], kt_ref[:, :, :, pos]) or (kt[:, :, :, pos] - kt_ref[:, :, :, pos]).abs().max() < 1e-5
     assert torch.equal(vc, vc_ref)
