@@ -355,11 +355,14 @@ class Int4Llama:
                             n2=1 + 0.1 * torch.randn(hidden, generator=g, device=dev)) for _ in range(layers)]
         self.norm = 1 + 0.1 * torch.randn(hidden, generator=g, device=dev)
         self.head = lin(vocab, hidden)
-        # KV caches, f32, capacity ctx + 1 rounded up to 4: Kt [batch, kv_heads, hd, cap]
-        # (transposed), V [batch, kv_heads, cap, hd]. Position ctx is written by the step.
+        # KV caches, bf16 (the model's dtype), capacity ctx + 1 rounded up to 4: Kt
+        # [batch, kv_heads, hd, cap] (transposed), V [batch, kv_heads, cap, hd].
+        # Position ctx is written by the step.
         cap = (ctx + 4) // 4 * 4
-        self.kt = [torch.randn(batch, kv_heads, self.hd, cap, generator=g, device=dev) for _ in range(layers)]
-        self.vc = [torch.randn(batch, kv_heads, cap, self.hd, generator=g, device=dev) for _ in range(layers)]
+        self.kt = [torch.randn(batch, kv_heads, self.hd, cap, generator=g, device=dev).to(torch.bfloat16)
+                   for _ in range(layers)]
+        self.vc = [torch.randn(batch, kv_heads, cap, self.hd, generator=g, device=dev).to(torch.bfloat16)
+                   for _ in range(layers)]
         self.pos = ctx
         inv = 1.0 / (500000.0 ** (torch.arange(0, self.hd, 2, device=dev, dtype=torch.float32) / self.hd))
         ang = ctx * inv
@@ -391,9 +394,9 @@ class Int4Llama:
             self.vc[i][:, :, self.pos, :] = v
             qg = q.view(bsz, self.kv_heads, grp, self.hd)
             live = self.pos + 1
-            kt = self.kt[i][..., :live].contiguous()
+            kt = self.kt[i][..., :live].float()
             scores = torch.matmul(qg, kt) * (self.hd ** -0.5)  # [B, kvh, grp, ctx + 1]
-            att = torch.matmul(torch.softmax(scores, dim=-1), self.vc[i][:, :, :live].contiguous())  # [B, kvh, grp, hd]
+            att = torch.matmul(torch.softmax(scores, dim=-1), self.vc[i][:, :, :live].float())  # [B, kvh, grp, hd]
             x = x + self.linear(att.reshape(bsz, self.hidden).to(torch.bfloat16), p["o"])
             h = self._rms(x, p["n2"])
             a = torch.nn.functional.silu(self.linear(h, p["gate"]).float()) * self.linear(h, p["up"]).float()

@@ -233,16 +233,16 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
 
 /* One decode step of grouped-query attention: q [rows, heads*head_dim], k and v
  * [rows, kv_heads*head_dim] (bf16); rotary embedding of q and k with cos/sin f32
- * [head_dim/2] (pairs i, i + head_dim/2); k and v stored at `pos` of the f32 caches
- * kt_cache [rows, kv_heads, head_dim, cap] (transposed) and v_cache [rows, kv_heads,
- * cap, head_dim]; out [rows, heads*head_dim] = softmax(q K^T / sqrt(head_dim)) V over
+ * [head_dim/2] (pairs i, i + head_dim/2); k and v stored (rounded to bf16) at `pos`
+ * of the bf16 caches kt_cache [rows, kv_heads, head_dim, cap] (transposed) and
+ * v_cache [rows, kv_heads, cap, head_dim]; out [rows, heads*head_dim] = softmax(q K^T / sqrt(head_dim)) V over
  * positions 0..pos, in chunks of 64 positions merged in order (split-K). head_dim 64
  * or 128; heads / kv_heads <= 8; pos < 262144; cap a multiple of 4 and the caches
  * 16-byte aligned.
  * `workspace` (f32, caller-owned) holds lnq_decode_attention_workspace(rows, kv_heads,
  * head_dim, pos) floats. */
 LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
-                                       const float* sin, float* kt_cache, float* v_cache, void* out,
+                                       const float* sin, void* kt_cache, void* v_cache, void* out,
                                        float* workspace, int64_t workspace_floats, int64_t rows,
                                        int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t cap,
                                        int64_t pos, void* stream);

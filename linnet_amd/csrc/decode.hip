@@ -8,7 +8,7 @@
 //                      cache at `pos`, softmax(q K^T / sqrt(hd)) V over 0..pos
 //   silu_mul:          a = silu(g) * u
 //
-// All arithmetic is f32 (activations stored bf16, caches f32) in a fixed order,
+// All arithmetic is f32 (activations and KV caches stored bf16) in a fixed order,
 // so results do not depend on timing. The reference gets these ops from its
 // generated module (framework ops on the GPU); they are not part of its
 // quantized-linear path.
@@ -137,24 +137,27 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
 // [64 c, 64 c + 64) of that head's cache for its G query heads: scores, their
 // max m and sum s of exp(score - m), and acc = sum exp(score - m) V, written to
 // the workspace; decode_combine_kernel merges the chunks. Keys and values move
-// as float4: a thread's key loads cover 4 positions x HD/16 dimensions (the
-// partial scores of the 16 dimension groups are added through LDS), its value
-// loads 4 dimensions x 64/(256/(HD/4)) positions. Every workgroup applies the
-// rotary embedding itself (q, and k for position pos, which it reads from LDS
-// rather than the cache); the one whose chunk holds pos writes k and v into the
-// caches. K cache transposed, [rows, kv_heads, HD, cap]; V cache [rows, kv_heads,
-// cap, HD]; cap a multiple of 4.
-template <int HD>
+// four values (8 bytes) at a time: a thread's key loads cover 4 positions x
+// HD/16 dimensions (the partial scores of the 16 dimension groups are added
+// through LDS), its value loads 4 dimensions x 64/(256/(HD/4)) positions. Every
+// workgroup applies the rotary embedding itself (q, and k for position pos, which
+// it reads from LDS rather than the cache, rounded to bf16 as the cache holds
+// it); the one whose chunk holds pos writes k and v into the caches. bf16 caches:
+// K transposed, [rows, kv_heads, HD, cap]; V [rows, kv_heads, cap, HD]; cap a
+// multiple of 4.
+template <int HD, int GT>
 __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const float* __restrict__ cosv, const float* __restrict__ sinv, float* __restrict__ kt, float* __restrict__ vc,
-    float* __restrict__ work, int heads, int kv_heads, int cap, int pos, int chunks) {
+    const float* __restrict__ cosv, const float* __restrict__ sinv, uint16_t* __restrict__ kt,
+    uint16_t* __restrict__ vc, float* __restrict__ work, int heads, int kv_heads, int cap, int pos, int chunks) {
   constexpr int C = decode::CHUNK;       // 64 positions
   constexpr int DG = 16;                 // dimension groups of the scores
   constexpr int DPG = HD / DG;           // dimensions a score thread takes
   constexpr int DV = HD / 4;             // value threads across the dimensions
   constexpr int PG = decode::THREADS / DV;  // value threads across the positions
-  constexpr int G8 = decode::MAX_GROUP;
+  // GT: query heads per KV head the LDS arrays hold (G <= GT); smaller arrays
+  // let more workgroups share a CU (G = 4: ~35 KB against ~70 KB at 8).
+  constexpr int G8 = GT;
   __shared__ float qs[G8][HD];
   __shared__ float kn[HD], vn[HD];
   __shared__ float sp[DG][G8][C];   // partial scores
@@ -173,8 +176,8 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   const uint16_t* qr = q + (static_cast<size_t>(row) * heads + kvh * G) * HD;
   const uint16_t* kr = k + static_cast<size_t>(rk) * HD;
   const uint16_t* vr = v + static_cast<size_t>(rk) * HD;
-  float* ktb = kt + static_cast<size_t>(rk) * HD * cap;
-  float* vcb = vc + static_cast<size_t>(rk) * cap * HD;
+  uint16_t* ktb = kt + static_cast<size_t>(rk) * HD * cap;
+  uint16_t* vcb = vc + static_cast<size_t>(rk) * cap * HD;
   const bool owner = pos >= l0 && pos < l0 + C;
 
   // The chunk's keys and values: every load issued first (registers), the
@@ -185,19 +188,23 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   const int lp = l0 + 4 * p4;
   const int d4 = tid % DV, pg = tid / DV;
   constexpr int VJ = C / PG;  // value positions a thread takes
-  float4 kreg[DPG], vreg[VJ];
+  // (bf16 caches: four values are 8 bytes.)
+  u32x2 kreg[DPG], vreg[VJ];
 #pragma unroll
   for (int dd = 0; dd < DPG; ++dd) {
     const int d = dg * DPG + dd;
-    kreg[dd] = lp < cap ? *reinterpret_cast<const float4*>(ktb + static_cast<size_t>(d) * cap + lp)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    kreg[dd] = lp < cap ? *reinterpret_cast<const u32x2*>(ktb + static_cast<size_t>(d) * cap + lp) : u32x2{0u, 0u};
   }
 #pragma unroll
   for (int jj = 0; jj < VJ; ++jj) {
     const int j = pg + jj * PG;
-    vreg[jj] = j < n && l0 + j != pos ? *reinterpret_cast<const float4*>(vcb + static_cast<size_t>(l0 + j) * HD + 4 * d4)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    vreg[jj] = j < n && l0 + j != pos ? *reinterpret_cast<const u32x2*>(vcb + static_cast<size_t>(l0 + j) * HD + 4 * d4)
+                                      : u32x2{0u, 0u};
   }
+  auto widen = [](u32x2 w) {
+    return make_float4(bf16_bits_to_f32(static_cast<uint16_t>(w.x & 0xffffu)), bf16_bits_to_f32(static_cast<uint16_t>(w.x >> 16)),
+                       bf16_bits_to_f32(static_cast<uint16_t>(w.y & 0xffffu)), bf16_bits_to_f32(static_cast<uint16_t>(w.y >> 16)));
+  };
 
   // Rotary embedding (pairs i, i + HD/2); the new key and value into LDS, and into
   // the caches by the chunk that holds pos.
@@ -210,18 +217,19 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
       qs[g][i] = ra * scale;
       qs[g][i + HALF] = rb * scale;
     } else {
-      kn[i] = ra;
-      kn[i + HALF] = rb;
+      // The new key as the cache holds it (rounded to bf16).
+      const uint16_t ba = f32_to_bf16_bits(ra), bb = f32_to_bf16_bits(rb);
+      kn[i] = bf16_bits_to_f32(ba);
+      kn[i + HALF] = bf16_bits_to_f32(bb);
       if (owner) {
-        ktb[static_cast<size_t>(i) * cap + pos] = ra;
-        ktb[static_cast<size_t>(i + HALF) * cap + pos] = rb;
+        ktb[static_cast<size_t>(i) * cap + pos] = ba;
+        ktb[static_cast<size_t>(i + HALF) * cap + pos] = bb;
       }
     }
   }
   for (int d = tid; d < HD; d += decode::THREADS) {
-    const float vv = bf16_bits_to_f32(vr[d]);
-    vn[d] = vv;
-    if (owner) vcb[static_cast<size_t>(pos) * HD + d] = vv;
+    vn[d] = bf16_bits_to_f32(vr[d]);
+    if (owner) vcb[static_cast<size_t>(pos) * HD + d] = vr[d];
   }
   __syncthreads();
 
@@ -235,7 +243,8 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
 #pragma unroll
     for (int dd = 0; dd < DPG; ++dd) {
       const int d = dg * DPG + dd;
-      float kk[4] = {kreg[dd].x, kreg[dd].y, kreg[dd].z, kreg[dd].w};
+      const float4 kw = widen(kreg[dd]);
+      float kk[4] = {kw.x, kw.y, kw.z, kw.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (lp + e == pos) kk[e] = kn[d];
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
       const int j = pg + jj * PG;
       if (j >= n) break;
       const float4 vv =
-          l0 + j == pos ? make_float4(vn[4 * d4], vn[4 * d4 + 1], vn[4 * d4 + 2], vn[4 * d4 + 3]) : vreg[jj];
+          l0 + j == pos ? make_float4(vn[4 * d4], vn[4 * d4 + 1], vn[4 * d4 + 2], vn[4 * d4 + 3]) : widen(vreg[jj]);
 #pragma unroll
       for (int g = 0; g < G8; ++g)
         if (g < G) {
@@ -298,7 +307,7 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
       *reinterpret_cast<float4*>(&pacc[pg][g][4 * d4]) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
   }
   __syncthreads();
-  float* wrow = work + static_cast<size_t>(blockIdx.x) * G8 * (HD + 2);
+  float* wrow = work + static_cast<size_t>(blockIdx.x) * decode::MAX_GROUP * (HD + 2);
   for (int t = tid; t < G * HD; t += decode::THREADS) {
     const int g = t / HD, d = t % HD;
     float o = 0.f;
@@ -405,7 +414,7 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
 }
 
 LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
-                                       const float* sin, float* kt_cache, float* v_cache, void* out, float* workspace,
+                                       const float* sin, void* kt_cache, void* v_cache, void* out, float* workspace,
                                        int64_t workspace_floats, int64_t rows, int64_t heads, int64_t kv_heads,
                                        int64_t head_dim, int64_t cap, int64_t pos, void* stream) {
   LNQ_REQUIRE(head_dim == 64 || head_dim == 128, "lnq_decode_attention: head_dim is 64 or 128, not %lld",
@@ -431,20 +440,30 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
   LNQ_REQUIRE(aligned(kt_cache, 16) && aligned(v_cache, 16), "lnq_decode_attention: caches must be 16-byte aligned");
   const dim3 grid(static_cast<unsigned>(rows * kv_heads * chunks)), grid2(static_cast<unsigned>(rows * heads));
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define LNQ_ATT(HD_)                                                                                              \
-  hipLaunchKernelGGL(decode_attention_kernel<HD_>, grid, dim3(decode::THREADS), 0, s,                             \
+#define LNQ_ATT_G(HD_, GT_)                                                                                       \
+  hipLaunchKernelGGL((decode_attention_kernel<HD_, GT_>), grid, dim3(decode::THREADS), 0, s,                      \
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),                              \
-                     static_cast<const uint16_t*>(v), cos, sin, kt_cache, v_cache, workspace,                       \
+                     static_cast<const uint16_t*>(v), cos, sin, static_cast<uint16_t*>(kt_cache),                    \
+                     static_cast<uint16_t*>(v_cache), workspace,                                                    \
                      static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(cap), static_cast<int>(pos), \
                      static_cast<int>(chunks));                                                                     \
   hipLaunchKernelGGL(decode_combine_kernel<HD_>, grid2, dim3(HD_), 0, s, workspace, static_cast<uint16_t*>(out),   \
                      static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(chunks))
+#define LNQ_ATT(HD_)                                      \
+  switch (group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8) { \
+    case 1: LNQ_ATT_G(HD_, 1); break;                     \
+    case 2: LNQ_ATT_G(HD_, 2); break;                     \
+    case 4: LNQ_ATT_G(HD_, 4); break;                     \
+    default: LNQ_ATT_G(HD_, 8); break;                    \
+  }
+  const int64_t group = heads / kv_heads;
   if (head_dim == 64) {
     LNQ_ATT(64);
   } else {
     LNQ_ATT(128);
   }
 #undef LNQ_ATT
+#undef LNQ_ATT_G
   return launched("decode_attention");
 }
 

@@ -41,14 +41,14 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
                      kt_cache: torch.Tensor, v_cache: torch.Tensor, pos: int) -> torch.Tensor:
     """One decode step of grouped-query attention for q [rows, heads*hd], k, v
     [rows, kv_heads*hd] (bf16): rotary embedding (cos, sin f32 [hd/2] at `pos`) of
-    q and k, k and v written into the f32 caches at `pos` (K transposed:
+    q and k, k and v written (rounded) into the bf16 caches at `pos` (K transposed:
     kt_cache [rows, kv_heads, hd, cap]; v_cache [rows, kv_heads, cap, hd]), then
     softmax(q K^T / sqrt(hd)) V over positions 0..pos. Returns [rows, heads*hd] bf16."""
     device = _on_gpu("decode_attention", q, k, v, cos, sin, kt_cache, v_cache)
     _bf16("decode_attention", q, k, v)
     rows, kvh, hd, cap = kt_cache.shape
-    if tuple(v_cache.shape) != (rows, kvh, cap, hd) or kt_cache.dtype != torch.float32 or v_cache.dtype != torch.float32:
-        raise LinnetError("decode_attention: caches are f32 [rows, kv_heads, hd, cap] and [rows, kv_heads, cap, hd]")
+    if tuple(v_cache.shape) != (rows, kvh, cap, hd) or kt_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise LinnetError("decode_attention: caches are bf16 [rows, kv_heads, hd, cap] and [rows, kv_heads, cap, hd]")
     if not (kt_cache.is_contiguous() and v_cache.is_contiguous() and cos.is_contiguous() and sin.is_contiguous()):
         raise LinnetError("decode_attention: contiguous caches and tables")
     heads = q.shape[-1] // hd

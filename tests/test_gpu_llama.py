@@ -101,13 +101,21 @@ def test_decode_kernels_match_torch_ops() -> None:
     uu = torch.randn(5, 1000, generator=g).to(torch.bfloat16).to(DEV)
     want_a = (torch.nn.functional.silu(gg.float()) * uu.float()).to(torch.bfloat16)
     assert (decode.silu_mul(gg, uu).float() - want_a.float()).abs().max().item() <= 1e-2
-    # attention: 2 rows, 8 heads over 2 KV heads, hd 128, 37 cached positions
-    rows, heads, kvh, hd, cap, pos = 2, 8, 2, 128, 40, 37
+    for rows, heads, kvh, hd, cap, pos in ((2, 8, 2, 128, 40, 37), (2, 8, 2, 128, 2048, 1999), (1, 8, 2, 128, 704, 700),
+                                           (2, 8, 1, 128, 132, 130), (3, 6, 2, 64, 100, 64), (1, 4, 4, 64, 68, 3)):
+        _attention_case(decode, g, rows, heads, kvh, hd, cap, pos)
+
+
+def _attention_case(decode, g, rows: int, heads: int, kvh: int, hd: int, cap: int, pos: int) -> None:
+    """One attention step against torch (bf16 caches, f32 math): group sizes 4, 8,
+    3 and 1 (the LDS arrays sized 4, 8, 4, 1), head sizes 128 and 64, chunks from
+    1 to 32 (the merge's eight-at-a-time loop and its tail)."""
+    print(f"attention rows={rows} heads={heads} kv_heads={kvh} hd={hd} cap={cap} pos={pos}", flush=True)
     q = torch.randn(rows, heads * hd, generator=g).to(torch.bfloat16).to(DEV)
     k = torch.randn(rows, kvh * hd, generator=g).to(torch.bfloat16).to(DEV)
     v = torch.randn(rows, kvh * hd, generator=g).to(torch.bfloat16).to(DEV)
-    kt = torch.randn(rows, kvh, hd, cap, generator=g).to(DEV)
-    vc = torch.randn(rows, kvh, cap, hd, generator=g).to(DEV)
+    kt = torch.randn(rows, kvh, hd, cap, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(rows, kvh, cap, hd, generator=g).to(torch.bfloat16).to(DEV)
     ang = pos / (500000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
     cos, sin = torch.cos(ang).to(DEV), torch.sin(ang).to(DEV)
     kt_ref, vc_ref = kt.clone(), vc.clone()
@@ -119,28 +127,10 @@ def test_decode_kernels_match_torch_ops() -> None:
     qr = rope(q.float().view(rows, heads, hd))
     kt_ref[:, :, :, pos] = rope(k.float().view(rows, kvh, hd))
     vc_ref[:, :, pos, :] = v.float().view(rows, kvh, hd)
-    s = torch.matmul(qr.view(rows, kvh, heads // kvh, hd), kt_ref[..., : pos + 1].contiguous()) * hd**-0.5
-    want = torch.matmul(torch.softmax(s, dim=-1), vc_ref[:, :, : pos + 1].contiguous()).reshape(rows, heads * hd)
+    s = torch.matmul(qr.view(rows, kvh, heads // kvh, hd), kt_ref[..., : pos + 1].float()) * hd**-0.5
+    want = torch.matmul(torch.softmax(s, dim=-1), vc_ref[:, :, : pos + 1].float()).reshape(rows, heads * hd)
     got = decode.decode_attention(q, k, v, cos, sin, kt, vc, pos)
     assert (got.float() - want).abs().max().item() <= 1e-2 * want.abs().max().item()
-    # many chunks (the merge's eight-at-a-time loop and its tail): 2000 positions = 32 chunks, 700 = 11
-    for cap2, pos2 in ((2048, 1999), (704, 700)):
-        kt2 = torch.randn(rows, kvh, hd, cap2, generator=g).to(DEV)
-        vc2 = torch.randn(rows, kvh, cap2, hd, generator=g).to(DEV)
-        ang2 = pos2 / (500000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
-        c2, s2 = torch.cos(ang2).to(DEV), torch.sin(ang2).to(DEV)
-        kr2, vr2 = kt2.clone(), vc2.clone()
-
-        def rope2(t):
-            a, b = t[..., : hd // 2], t[..., hd // 2 :]
-            return torch.cat([a * c2 - b * s2, b * c2 + a * s2], dim=-1)
-
-        q2 = rope2(q.float().view(rows, heads, hd))
-        kr2[:, :, :, pos2] = rope2(k.float().view(rows, kvh, hd))
-        vr2[:, :, pos2, :] = v.float().view(rows, kvh, hd)
-        s2_ = torch.matmul(q2.view(rows, kvh, heads // kvh, hd), kr2[..., : pos2 + 1].contiguous()) * hd**-0.5
-        want2 = torch.matmul(torch.softmax(s2_, dim=-1), vr2[:, :, : pos2 + 1].contiguous()).reshape(rows, heads * hd)
-        got2 = decode.decode_attention(q, k, v, c2, s2, kt2, vc2, pos2)
-        assert (got2.float() - want2).abs().max().item() <= 1e-2 * want2.abs().max().item()
-    assert torch.equal(kt[:, :, :, pos], kt_ref[:, :, :, pos]) or (kt[:, :, :, pos] - kt_ref[:, :, :, pos]).abs().max() < 1e-5
+    # the new key and value in the caches as bf16 (the key rounded once from f32)
+    assert (kt[:, :, :, pos].float() - kt_ref[:, :, :, pos].float()).abs().max().item() <= 1e-2
     assert torch.equal(vc, vc_ref)
