@@ -240,12 +240,15 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
  * or 128; heads / kv_heads <= 8; pos < 262144; cap a multiple of 4 and the caches
  * 16-byte aligned.
  * `workspace` (f32, caller-owned) holds lnq_decode_attention_workspace(rows, kv_heads,
- * head_dim, pos) floats. */
+ * head_dim, pos) floats. q_stride and kv_stride are the row strides (elements) of q
+ * and of k / v, 0 for rows back to back: q, k and v may be column slices of one
+ * joined q|k|v projection's output. */
 LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
                                        const float* sin, void* kt_cache, void* v_cache, void* out,
                                        float* workspace, int64_t workspace_floats, int64_t rows,
                                        int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t cap,
-                                       int64_t pos, void* stream);
+                                       int64_t pos, int64_t q_stride,
+                                       int64_t kv_stride, void* stream);
 
 /* Floats of lnq_decode_attention's workspace: rows * kv_heads * ceil((pos + 1) / 64)
  * * 8 * (head_dim + 2). */

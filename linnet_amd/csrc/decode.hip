@@ -149,7 +149,8 @@ template <int HD, int GT>
 __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const float* __restrict__ cosv, const float* __restrict__ sinv, uint16_t* __restrict__ kt,
-    uint16_t* __restrict__ vc, float* __restrict__ work, int heads, int kv_heads, int cap, int pos, int chunks) {
+    uint16_t* __restrict__ vc, float* __restrict__ work, int heads, int kv_heads, int cap, int pos, int chunks,
+    int64_t q_stride, int64_t kv_stride) {
   constexpr int C = decode::CHUNK;       // 64 positions
   constexpr int DG = 16;                 // dimension groups of the scores
   constexpr int DPG = HD / DG;           // dimensions a score thread takes
@@ -173,9 +174,9 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   const int tid = threadIdx.x;
   constexpr int HALF = HD / 2;
   const float scale = rsqrtf(static_cast<float>(HD));
-  const uint16_t* qr = q + (static_cast<size_t>(row) * heads + kvh * G) * HD;
-  const uint16_t* kr = k + static_cast<size_t>(rk) * HD;
-  const uint16_t* vr = v + static_cast<size_t>(rk) * HD;
+  const uint16_t* qr = q + row * q_stride + kvh * G * HD;
+  const uint16_t* kr = k + row * kv_stride + kvh * HD;
+  const uint16_t* vr = v + row * kv_stride + kvh * HD;
   uint16_t* ktb = kt + static_cast<size_t>(rk) * HD * cap;
   uint16_t* vcb = vc + static_cast<size_t>(rk) * cap * HD;
   const bool owner = pos >= l0 && pos < l0 + C;
@@ -416,7 +417,8 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
 LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
                                        const float* sin, void* kt_cache, void* v_cache, void* out, float* workspace,
                                        int64_t workspace_floats, int64_t rows, int64_t heads, int64_t kv_heads,
-                                       int64_t head_dim, int64_t cap, int64_t pos, void* stream) {
+                                       int64_t head_dim, int64_t cap, int64_t pos, int64_t q_stride,
+                                       int64_t kv_stride, void* stream) {
   LNQ_REQUIRE(head_dim == 64 || head_dim == 128, "lnq_decode_attention: head_dim is 64 or 128, not %lld",
               static_cast<long long>(head_dim));
   LNQ_REQUIRE(rows >= 0 && kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= decode::MAX_GROUP,
@@ -446,7 +448,7 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
                      static_cast<const uint16_t*>(v), cos, sin, static_cast<uint16_t*>(kt_cache),                    \
                      static_cast<uint16_t*>(v_cache), workspace,                                                    \
                      static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(cap), static_cast<int>(pos), \
-                     static_cast<int>(chunks));                                                                     \
+                     static_cast<int>(chunks), qs_, kvs_);                                                          \
   hipLaunchKernelGGL(decode_combine_kernel<HD_>, grid2, dim3(HD_), 0, s, workspace, static_cast<uint16_t*>(out),   \
                      static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(chunks))
 #define LNQ_ATT(HD_)                                      \
@@ -457,6 +459,13 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
     default: LNQ_ATT_G(HD_, 8); break;                    \
   }
   const int64_t group = heads / kv_heads;
+  // Row strides of q and of k / v in elements (0: rows packed back to back), so
+  // q, k and v may be column slices of one joined projection's output.
+  const int64_t qs_ = q_stride == 0 ? heads * head_dim : q_stride;
+  const int64_t kvs_ = kv_stride == 0 ? kv_heads * head_dim : kv_stride;
+  LNQ_REQUIRE(qs_ >= heads * head_dim && kvs_ >= kv_heads * head_dim,
+              "lnq_decode_attention: row strides %lld / %lld shorter than a row", static_cast<long long>(qs_),
+              static_cast<long long>(kvs_));
   if (head_dim == 64) {
     LNQ_ATT(64);
   } else {

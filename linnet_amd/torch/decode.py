@@ -45,7 +45,8 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
     kt_cache [rows, kv_heads, hd, cap]; v_cache [rows, kv_heads, cap, hd]), then
     softmax(q K^T / sqrt(hd)) V over positions 0..pos. Returns [rows, heads*hd] bf16."""
     device = _on_gpu("decode_attention", q, k, v, cos, sin, kt_cache, v_cache)
-    _bf16("decode_attention", q, k, v)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise LinnetError("decode_attention: q, k and v are bf16")
     rows, kvh, hd, cap = kt_cache.shape
     if tuple(v_cache.shape) != (rows, kvh, cap, hd) or kt_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
         raise LinnetError("decode_attention: caches are bf16 [rows, kv_heads, hd, cap] and [rows, kv_heads, cap, hd]")
@@ -54,6 +55,10 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
     heads = q.shape[-1] // hd
     if q.shape != (rows, heads * hd) or k.shape != (rows, kvh * hd) or v.shape != k.shape:
         raise LinnetError("decode_attention: q [rows, heads*hd], k and v [rows, kv_heads*hd]")
+    # q, k and v may be column slices of one joined projection (rows strided, each
+    # row contiguous; k and v with the same row stride).
+    if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(0) != v.stride(0):
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if cos.numel() != hd // 2 or sin.numel() != hd // 2 or cos.dtype != torch.float32 or sin.dtype != torch.float32:
         raise LinnetError("decode_attention: cos and sin are f32 [hd/2]")
     out = torch.empty_like(q)
@@ -61,7 +66,8 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
     work = torch.empty(max(floats, 1), dtype=torch.float32, device=device)
     with torch.cuda.device(device):
         _lib.call("lnq_decode_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(kt_cache),
-                  _ptr(v_cache), _ptr(out), _ptr(work), work.numel(), rows, heads, kvh, hd, cap, pos, _stream(device))
+                  _ptr(v_cache), _ptr(out), _ptr(work), work.numel(), rows, heads, kvh, hd, cap, pos, q.stride(0),
+                  k.stride(0), _stream(device))
     return out
 
 

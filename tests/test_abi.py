@@ -88,13 +88,14 @@ def test_other_entry_points_validate() -> None:
     assert "output is bf16 or f16" in _status("lnq_mm8", FAKE, FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 1, _lib.F32, NULL)[1]
     assert "negative" in _status("lnq_int4_pack", FAKE, FAKE, -1, NULL)[1]
     big = 1 << 40
-    assert "head_dim is 64 or 128" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 32, 8, 96, 1025, 1024, NULL)[1]
-    assert "outside the cache" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 32, 8, 128, 1024, 1024, NULL)[1]
-    assert "multiple" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 30, 8, 128, 1025, 1024, NULL)[1]
+    assert "head_dim is 64 or 128" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 32, 8, 96, 1025, 1024, 0, 0, NULL)[1]
+    assert "outside the cache" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 32, 8, 128, 1024, 1024, 0, 0, NULL)[1]
+    assert "multiple" in _status("lnq_decode_attention", *[FAKE] * 9, big, 1, 30, 8, 128, 1025, 1024, 0, 0, NULL)[1]
     need = _lib.load().lnq_decode_attention_workspace(2, 8, 128, 1024)
     assert need == 2 * 8 * 17 * 8 * 130
-    assert "workspace" in _status("lnq_decode_attention", *[FAKE] * 9, need - 1, 2, 32, 8, 128, 1028, 1024, NULL)[1]
-    assert "multiple of 4" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1025, 1024, NULL)[1]
+    assert "workspace" in _status("lnq_decode_attention", *[FAKE] * 9, need - 1, 2, 32, 8, 128, 1028, 1024, 0, 0, NULL)[1]
+    assert "multiple of 4" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1025, 1024, 0, 0, NULL)[1]
+    assert "strides" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1028, 1024, 4000, 0, NULL)[1]
     assert "bad shape" in _status("lnq_rmsnorm", FAKE, NULL, FAKE, FAKE, 1, 0, ctypes.c_float(1e-5), NULL)[1]
     assert "neither GPTQ" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 2, 0, 64, 64, 1, FAKE, FAKE, NULL)[1]
     assert "multiples of 8" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 0, 60, 64, 1, FAKE, FAKE, NULL)[1]
