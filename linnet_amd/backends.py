@@ -1,0 +1,159 @@
+"""This package's int4 product as a Linnet backend plugin: the contract of
+`linnet.backends` (`python/linnet/src/linnet/backends/contract.py:228-323`,
+`docs/backends.md`), shaped as the reference's own plugin example
+(`examples/09-backends/marlin/linnet_marlin/__init__.py`).
+
+A `std.quant::linear_int4_groups` call (an `Int4GroupLinear`) runs on
+`lnq_int4_linear`: the HIP kernels read the model's int4 bytes, scales and zero
+points as they are stored, so `prepare` converts nothing and the executable
+holds no bytes of its own (Marlin keeps a repacked copy). `execute` enqueues on
+the caller's stream and never waits, allocates its output with PyTorch, and may
+be recorded into a HIP graph.
+
+The contract's types (`Capabilities`, `ExecutableMeta`, `TensorSpec`, `Region`,
+`PlanError`) are Linnet's: they are imported from `linnet.backends` and
+`linnet.compiler` when the backend is made, unless `types` supplies objects
+with the same fields (as the tests do where Linnet is not installed). A
+package registers the backend in the `linnet.backends` entry-point group
+(`backends/__init__.py:67-75`) as `linnet-amd = linnet_amd.backends:MI355XInt4`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Iterable, Sequence
+from types import SimpleNamespace
+from typing import Any
+
+import torch
+
+from . import __version__, _lib
+from .errors import LinnetError
+from .torch import kernels
+
+CALLEE = "std.quant::linear_int4_groups"
+DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _linnet_types() -> SimpleNamespace:
+    try:
+        from linnet.backends import Capabilities, ExecutableMeta, Region, TensorSpec  # type: ignore[import-not-found]
+        from linnet.compiler import PlanError  # type: ignore[import-not-found]
+    except ImportError as error:
+        raise LinnetError("linnet is not installed: pass `types` with the contract's classes") from error
+    return SimpleNamespace(Capabilities=Capabilities, ExecutableMeta=ExecutableMeta, Region=Region,
+                           TensorSpec=TensorSpec, PlanError=PlanError)
+
+
+def _fused_group(group: int) -> bool:
+    """The groups the HIP kernels take (`lnq_int4_linear`)."""
+    return group in (32, 64) or (group > 0 and group % 128 == 0)
+
+
+class MI355XInt4:
+    """Takes the group-wise int4 `linear` calls the gfx950 kernels run."""
+
+    contract = 1  # the version of `linnet.backends` it is written for
+
+    def __init__(self, types: Any = None) -> None:
+        self._t = types if types is not None else _linnet_types()
+
+    @property
+    def name(self) -> str:
+        return "linnet-amd"
+
+    @property
+    def version(self) -> str:
+        return __version__
+
+    def probe(self, target: Any) -> Any:
+        """Capabilities on a gfx950 GPU (PyTorch on ROCm names it `cuda`), else None."""
+        if target.kind != "cuda":
+            return None
+        try:
+            lib = _lib.load()
+        except LinnetError:
+            return None
+        is_gfx950, units = ctypes.c_int32(), ctypes.c_int32()
+        if lib.lnq_device_probe(int(target.index), ctypes.byref(is_gfx950), ctypes.byref(units)) != _lib.LNQ_OK:
+            return None
+        if not is_gfx950.value:
+            return None
+        return self._t.Capabilities({"linnet_amd": self.version}, frozenset(DTYPES))
+
+    def match(self, graph: Any, target: Any) -> Iterable[Any]:
+        """Each `linear_int4_groups(x, q, scale, zero, bias)` call whose weight the
+        kernels take: bf16 / f16 x with scales of its dtype, In % 128 == 0, a group
+        of 32, 64 or a multiple of 128, the weight (and bias) persistent, x the
+        region's one input."""
+        persistent = set(graph.parameters.values())
+        for call in graph.semantic_calls(CALLEE):
+            if len(call.arguments) != 5:
+                continue
+            x, q, scale, zero, bias = call.arguments
+            if len(q.shape) != 3:
+                continue
+            _, groups, group = q.shape
+            region = self._t.Region.of(graph, call.start, call.stop, call.index)
+            if (
+                x.dtype in DTYPES
+                and scale.dtype == x.dtype
+                and (groups * group) % 128 == 0
+                and _fused_group(group)
+                and all(v.value in persistent for v in (q, scale, zero))
+                and (bias.value is None or bias.value in persistent)
+                and tuple(region.inputs) == (x.value,)
+            ):
+                yield region
+
+    def compile(self, region: Any, target: Any, options: Any) -> _Int4Linear:
+        graph = region.graph
+        if region.call is None:
+            raise self._t.PlanError("linnet-amd takes a `linear_int4_groups` call")
+        x, q, scale, zero, bias = graph.calls[region.call].arguments
+        path = {value: p for p, value in graph.parameters.items()}
+        values = graph.values
+        meta = self._t.ExecutableMeta(
+            tuple(self._t.TensorSpec(values[v].shape, values[v].dtype) for v in region.inputs),
+            tuple(self._t.TensorSpec(values[v].shape, values[v].dtype) for v in region.outputs),
+            holds=0,
+        )
+        return _Int4Linear(meta, (path[q.value], path[scale.value], path[zero.value]),
+                           path[bias.value] if bias.value is not None else None, DTYPES[x.dtype])
+
+    def estimate_cost(self, region: Any, target: Any) -> Any:
+        return None  # the planner measures
+
+
+class _Int4Linear:
+    """One `linear_int4_groups` call on `lnq_int4_linear`."""
+
+    def __init__(self, meta: Any, paths: tuple[str, str, str], bias: str | None, dtype: torch.dtype) -> None:
+        self._meta = meta
+        self._paths = paths
+        self._bias = bias
+        self._dtype = dtype
+
+    @property
+    def meta(self) -> Any:
+        return self._meta
+
+    def prepare(self, context: Any) -> None:
+        """Nothing to convert: the kernels read the parameters as stored. Checks
+        that they are where and what the kernels need."""
+        q, scale, zero = (context.parameters[p] for p in self._paths)
+        if not (q.is_cuda and scale.is_cuda and zero.is_cuda):
+            raise LinnetError("linnet-amd: the int4 parameters are not on the GPU")
+        if q.dtype != torch.uint8 or zero.dtype != torch.uint8 or scale.dtype != self._dtype:
+            raise LinnetError("linnet-amd: int4 bytes and zero points are uint8, scales the input's dtype")
+
+    def execute(self, inputs: Sequence[torch.Tensor], outputs: Sequence[torch.Tensor], context: Any) -> Sequence[torch.Tensor]:
+        q, scale, zero = (context.parameters[p] for p in self._paths)
+        bias = context.parameters[self._bias] if self._bias is not None else None
+        (x,) = inputs
+        rows = x.reshape(-1, x.shape[-1])
+        y = kernels.int4_linear(rows, q, scale, zero, bias)
+        return [y.reshape(*x.shape[:-1], y.shape[-1])]
+
+
+__all__ = ["CALLEE", "MI355XInt4"]

@@ -1,0 +1,103 @@
+"""The plugin adapter (`linnet_amd.backends.MI355XInt4`) against the
+`linnet.backends` contract (`backends/contract.py:228-323`), with stand-in
+types and graphs (`tests/backend_fakes.py`): which `linear_int4_groups` calls
+it takes, what it compiles them to, and (GPU) that the executable computes the
+product the reference's fallback computes, as `backends/conformance.py` checks
+a backend: same inputs, outputs within a tolerance."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from linnet_amd.backends import CALLEE, MI355XInt4
+from tests.backend_fakes import TYPES, Graph
+
+
+def _graph() -> tuple[Graph, list[bool]]:
+    g = Graph()
+    cases = [
+        (dict(name="a", rows=4, out=256, inp=512, group=128), True),
+        (dict(name="b", rows=1, out=64, inp=1024, group=64, dtype="f16", bias=True), True),
+        (dict(name="c", rows=2, out=32, inp=512, group=16), False),  # group 16
+        (dict(name="d", rows=2, out=32, inp=192, group=64), False),  # In % 128
+        (dict(name="e", rows=2, out=32, inp=512, group=128, dtype="f32"), False),  # f32 x
+        (dict(name="f", rows=2, out=32, inp=512, group=128, persistent=False), False),  # weight not a parameter
+        (dict(name="h", rows=2, out=32, inp=512, group=128, extra_input=True), False),  # six arguments
+    ]
+    for kwargs, _ in cases:
+        g.linear(**kwargs)
+    return g, [ok for _, ok in cases]
+
+
+def test_match_takes_the_calls_the_kernels_run() -> None:
+    g, ok = _graph()
+    backend = MI355XInt4(types=TYPES)
+    assert backend.name == "linnet-amd" and backend.contract == 1
+    taken = {r.call for r in backend.match(g, SimpleNamespace(kind="cuda", index=0))}
+    assert taken == {i for i, good in enumerate(ok) if good}
+    assert all(c.callee == CALLEE for c in g.calls)
+
+
+def test_compile_describes_the_executable() -> None:
+    g, _ = _graph()
+    backend = MI355XInt4(types=TYPES)
+    region = next(iter(backend.match(g, SimpleNamespace(kind="cuda", index=0))))
+    made = backend.compile(region, SimpleNamespace(kind="cuda"), None)
+    assert made.meta.holds == 0 and made.meta.capturable and made.meta.stream == "caller"
+    assert [s.shape for s in made.meta.inputs] == [(4, 512)] and [s.shape for s in made.meta.outputs] == [(4, 256)]
+    assert backend.estimate_cost(region, None) is None
+    with pytest.raises(TYPES.PlanError):
+        backend.compile(TYPES.Region(g, 0, 1, (), (), None), None, None)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the answer without a GPU")
+def test_probe_without_a_gpu() -> None:
+    backend = MI355XInt4(types=TYPES)
+    assert backend.probe(SimpleNamespace(kind="cpu", index=0)) is None
+    assert backend.probe(SimpleNamespace(kind="cuda", index=0)) is None
+
+
+@pytest.mark.gpu
+def test_executable_conforms_to_the_fallback() -> None:
+    """Region by region as `conform` runs them: the executable and the
+    reference's fallback (dequantize, then `F.linear`) on the same inputs."""
+    from linnet_amd.torch import kernels
+
+    backend = MI355XInt4(types=TYPES)
+    assert backend.probe(SimpleNamespace(kind="cuda", index=0)).dtypes == frozenset({"bf16", "f16"})
+    g, _ = _graph()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    params = {}
+    for call in g.calls:
+        x, q, s, z, b = call.arguments[:5]
+        out, groups, group = q.shape
+        if group % 2 or s.dtype not in ("bf16", "f16"):
+            continue
+        dtype = torch.bfloat16 if s.dtype == "bf16" else torch.float16
+        w = torch.randn(out, groups * group, generator=gen, device="cuda") * 0.02
+        packed, scale, zero = kernels.quantize_int4(w, group)
+        name = call.arguments[2]
+        prefix = [p for p, v in g.parameters.items() if v == name.value][0].removesuffix("scale")
+        params[prefix + "weight"], params[prefix + "scale"], params[prefix + "zero"] = packed, scale.to(dtype), zero
+        if b.value is not None:
+            params[prefix + "bias"] = torch.randn(out, generator=gen, device="cuda").to(dtype)
+    context = SimpleNamespace(parameters=params, target=SimpleNamespace(kind="cuda", index=0))
+    for region in backend.match(g, context.target):
+        made = backend.compile(region, context.target, None)
+        made.prepare(context)
+        x, q, s, z, b = g.calls[region.call].arguments
+        dtype = torch.bfloat16 if x.dtype == "bf16" else torch.float16
+        xin = torch.randn(*x.shape, generator=gen, device="cuda").to(dtype)
+        (got,) = made.execute([xin], [], context)
+        prefix = [p for p, v in g.parameters.items() if v == s.value][0].removesuffix("scale")
+        weight = kernels.int4_weight(params[prefix + "weight"], params[prefix + "scale"], params[prefix + "zero"])
+        want = torch.nn.functional.linear(xin, weight)
+        if b.value is not None:
+            want = want + params[prefix + "bias"]
+        err = (got.float() - want.float()).abs().max().item()
+        assert got.shape == want.shape and err <= 1e-2 * want.float().abs().max().item(), err
+    np.testing.assert_equal(len(list(backend.match(g, context.target))), 2)
