@@ -14,7 +14,8 @@ reference's `_int4_pack` falls back (`torch_source.cpp:1501-1504`), and
 
 `_mxfp4_experts(x, blocks, scales, experts)` is the helper for
 `std.quant::mxfp4_experts` (`torch_source.cpp:1579-1600`): the chosen experts'
-MXFP4 weights multiplied by one HIP kernel.
+MXFP4 weights multiplied by one HIP kernel; `_mxfp4_grouped` the one for the
+shared and combine forms (`torch_source.cpp:1705-1735`) on the same kernel.
 
 CPU tensors raise: this package has no CPU path.
 """
@@ -89,3 +90,26 @@ def _mxfp4_experts(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, 
     if not x.is_cuda:
         raise LinnetError("_mxfp4_experts: linnet_amd runs on the GPU; x is on " + str(x.device))
     return kernels.mxfp4_experts(x, blocks, scales, experts)
+
+
+def _mxfp4_grouped(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, experts: torch.Tensor,
+                   weights: torch.Tensor | None = None) -> torch.Tensor:
+    """`std.quant::mxfp4_linear_experts_shared` (no `weights`, `x` [R, In]: every
+    chosen expert of a row reads the row) and `mxfp4_combine_experts` (`x` [R, K, In],
+    the products weighed by `weights` [R, K] and summed per row in f32, as the
+    reference's helper sums its grouped product, `torch_source.cpp:1705-1735`).
+    The MXFP4 products run on the decode kernel, each (row, slot) pair reading its
+    expert's bytes as stored: the semantics of the grouped path for any number of
+    rows, without its expert-sorted MFMA schedule (each pair reads its expert again,
+    from the caches past the first)."""
+    if not x.is_cuda:
+        raise LinnetError("_mxfp4_grouped: linnet_amd runs on the GPU; x is on " + str(x.device))
+    rows, chosen = experts.shape
+    if weights is None:
+        if x.dim() != 2 or x.shape[0] != rows:
+            raise LinnetError(f"_mxfp4_grouped: the shared form takes x [R, In] with R = {rows}")
+        return kernels.mxfp4_experts(x[:, None, :].expand(rows, chosen, x.shape[1]), blocks, scales, experts)
+    if x.dim() != 3 or tuple(x.shape[:2]) != (rows, chosen) or tuple(weights.shape) != (rows, chosen):
+        raise LinnetError("_mxfp4_grouped: the combine form takes x [R, K, In] and weights [R, K]")
+    y = kernels.mxfp4_experts(x, blocks, scales, experts)
+    return (y.float() * weights.float()[..., None]).sum(1).to(x.dtype)

@@ -74,3 +74,32 @@ def test_out_of_range_experts_give_zero_rows() -> None:
     want = linear.mxfp4_experts_f64(x.float().numpy(), blocks, scales, ok)
     _check(got[0, :1], want[0, :1])
     _check(got[1, 1:], want[1, 1:])
+
+
+@pytest.mark.parametrize("rows", [1, 37, 256])
+def test_grouped_forms(rows: int) -> None:
+    """`mxfp4_linear_experts_shared` and `mxfp4_combine_experts` through the generated
+    `_mxfp4_grouped` helper, against the fp64 dense forms of `stdlib/quant.linnet:358-406`."""
+    print(f"mxfp4_grouped rows={rows}", flush=True)
+    rng = np.random.default_rng(rows)
+    count, out, width, chosen = 8, 96, 256, 4
+    blocks = rng.integers(0, 256, (count, out, width // 32, 16)).astype(np.uint8)
+    scales = rng.integers(118, 136, (count, out, width // 32)).astype(np.uint8)
+    experts = rng.integers(0, count, (rows, chosen)).astype(np.int64)
+    b, s, e = torch.from_numpy(blocks).to(DEV), torch.from_numpy(scales).to(DEV), torch.from_numpy(experts).to(DEV)
+    x = torch.randn(rows, width, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+    shared = generated._mxfp4_grouped(x.to(DEV), b, s, e)
+    want = linear.mxfp4_experts_f64(x.float().numpy()[:, None, :].repeat(chosen, 1), blocks, scales, experts)
+    _check(shared, want)
+    xk = torch.randn(rows, chosen, width, generator=torch.Generator().manual_seed(rows + 1)).to(torch.bfloat16)
+    wk = torch.softmax(torch.randn(rows, chosen, generator=torch.Generator().manual_seed(2)), -1).to(torch.bfloat16)
+    combined = generated._mxfp4_grouped(xk.to(DEV), b, s, e, wk.to(DEV))
+    per_pair = linear.mxfp4_experts_f64(xk.float().numpy(), blocks, scales, experts)
+    terms = per_pair * wk.float().numpy()[..., None]
+    want_c = terms.sum(1)
+    # Each pair's product is rounded to bf16 before the weighted sum (as the
+    # reference's helper does), so the bound follows the terms, not their sum.
+    got_c = combined.float().cpu().numpy()
+    scale_c = np.abs(terms).sum(1)
+    assert np.all(np.abs(got_c - want_c) <= 8e-3 * scale_c + 1e-3 * np.abs(want_c).max())
+
