@@ -12,13 +12,13 @@
 // f32, as the reference applies the scale after the block's products.
 //
 // Layout of the work: one workgroup per (row, chosen slot) pair and 16 output
-// rows of its expert, 4 waves of 4 rows. Lane l owns
-// blocks l, l + 64, ... of every row it visits, so its 32 inputs of x per block
-// stay in registers across the rows and a wave's weight loads read 64
-// consecutive blocks (1 KB) of a row. All of a wave's weight and scale loads are
-// issued before any is used (buffer loads: rows past Out, blocks past G and the
-// rows of an out-of-range expert read zeros through the range check). A row's
-// sum is the lanes' partial sums added across the wave (fixed order).
+// rows of its expert, 4 waves of 4 rows. Lane l owns blocks l, l + 64, ... of
+// every row it visits, so its 32 inputs of x per block stay in registers across
+// the rows and a wave's weight loads read 64 consecutive blocks (1 KB) of a row.
+// All of a wave's loads are issued before any is used, x and the scales first
+// (buffer loads: rows past Out, blocks past G and the rows of an out-of-range
+// expert read zeros through the range check). A row's sum is the lanes' partial
+// sums added across the wave (fixed order).
 #include "common.hpp"
 
 namespace lnq {
@@ -82,21 +82,10 @@ __global__ __launch_bounds__(64 * mx::WAVES) void mxfp4_experts_kernel(
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scales + e0, valid ? static_cast<uint32_t>(expert_blocks) : 0);
   const uint16_t* xp = x + r * x_row_stride + k * x_slot_stride;
 
-  // Every weight and scale load of the wave first (one round trip), then x.
-  u32x4 w[ROWS][SLOTS];
-  int sc[ROWS][SLOTS];
-#pragma unroll
-  for (int i = 0; i < ROWS; ++i)
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const int g = lane + 64 * s;
-      const int o = o0 + i;
-      // Blocks of rows past Out, or past G within a row, land outside the range.
-      const uint32_t blk = o < out_features && g < groups ? static_cast<uint32_t>(o * groups + g) : 0xffffffffu >> 4;
-      w[i][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, blk * 16, 0, 2 /* non-temporal */));
-      sc[i][s] = __builtin_amdgcn_raw_buffer_load_b8(rs, blk, 0, 0);
-    }
-  // x of this lane's blocks: 32 values (16 dwords, element order) a block.
+  // x of this lane's blocks first (32 values, 16 dwords in element order, a
+  // block), then the scales, then the weights: the memory pipeline serves a CU's
+  // loads in the order they arrive, so the small loads issued first land first
+  // and the multiply starts as soon as the weights do (one round trip in all).
   u32x4 xv[SLOTS][4];
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s) {
@@ -105,6 +94,24 @@ __global__ __launch_bounds__(64 * mx::WAVES) void mxfp4_experts_kernel(
     for (int q = 0; q < 4; ++q)
       xv[s][q] = g < groups ? *reinterpret_cast<const u32x4*>(xp + g * 32 + 8 * q) : u32x4{0u, 0u, 0u, 0u};
   }
+  // Blocks of rows past Out, or past G within a row, land outside the range.
+  uint32_t blk[ROWS][SLOTS];
+  int sc[ROWS][SLOTS];
+#pragma unroll
+  for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      const int g = lane + 64 * s;
+      const int o = o0 + i;
+      blk[i][s] = o < out_features && g < groups ? static_cast<uint32_t>(o * groups + g) : 0xffffffffu >> 4;
+      sc[i][s] = __builtin_amdgcn_raw_buffer_load_b8(rs, blk[i][s], 0, 0);
+    }
+  u32x4 w[ROWS][SLOTS];
+#pragma unroll
+  for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s)
+      w[i][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, blk[i][s] * 16, 0, 2 /* non-temporal */));
 
   float acc[ROWS];
 #pragma unroll
