@@ -271,11 +271,12 @@ __global__ __launch_bounds__(256) void w8_row_kernel(const uint16_t* __restrict_
   auto fetch = [&](int slot, int step) {
     rw[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[slot & 1] + 128 * step));
   };
+  // x first (it lands ahead of the weight loads issued after it), then the ring.
+  for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
+    *reinterpret_cast<u32x4*>(&xl[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
 #pragma unroll
   for (int i = 0; i < D; ++i)
     if (sb + (i >> 1) < se) fetch(i, sb + (i >> 1));
-  for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
-    *reinterpret_cast<u32x4*>(&xl[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
   __syncthreads();
   // A row m (lane m = l % 16): x at piece 2 j + (m & 1); rows 2..15 repeat rows
   // 0 / 1 and their outputs are not used.
