@@ -45,8 +45,9 @@ typedef int32_t LnqStatus;
 #define LNQ_KERNEL_SKINNY 1 /* dequant-GEMV/skinny GEMM on MFMA, rows <= 64 */
 #define LNQ_KERNEL_TILED 2  /* prefill dequant-GEMM, LDS-staged bf16 tiles on MFMA */
 #define LNQ_KERNEL_GEMV 3   /* few-token dequant-GEMV, one workgroup per CU (rows 1..16;
-                               in % 256 == 0 and <= 4096, group 128 or a multiple of 256,
-                               out <= 16384; one row also in = 256 * S * waves for S = 2..4
+                               in % 256 == 0 and <= 4096, group 128 or a multiple of 256;
+                               past 16384 outputs, more workgroups of 64 rows than CUs;
+                               one row also in = 256 * S * waves for S = 2..4
                                slices a wave (e.g. 6144, 8192, 12288, 14336) with out <=
                                8192 (S = 2) or 4096 (S = 3, 4)) */
 

@@ -710,8 +710,9 @@ bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* p
   if (M == 1 && gemv_slices_supports(N, K, G, x, packed, scale, zero)) return true;
   if (K % 256 != 0 || K < 256 || K > 256 * gemv::MAX_WAVES) return false;
   if (!(G == 128 || G % 256 == 0) || K % G != 0) return false;
-  const int u8 = (N + 2047) / 2048;
-  if (N <= 0 || u8 > gemv::MAX_U8) return false;
+  // Past 16384 outputs the workgroups keep 64 rows each (U8 = 8) and the grid
+  // grows past one workgroup a CU.
+  if (N <= 0) return false;
   if (static_cast<size_t>(N) * (K / 2) >= (1ull << 31)) return false;
   // 16-byte x and weight loads; scale pairs as dwords (group 128).
   return aligned(x, 16) && aligned(packed, 16) && (G != 128 || aligned(scale, 4)) && (G != 128 || aligned(zero, 2));

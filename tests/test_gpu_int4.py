@@ -210,6 +210,8 @@ def test_unsupported_groups_fall_back_to_the_dequantized_weight() -> None:
         (1000, 8192, 256, torch.float16),  # S = 2, group 256, 8 rows
         (5000, 6144, 128, torch.bfloat16),  # S = 2, 12 waves, 24 rows (odd U8)
         (3000, 12288, 1024, torch.bfloat16),  # S = 3, group 1024, 16 rows
+        (20000, 1024, 128, torch.bfloat16),  # past 16384 outputs: 313 workgroups of 64 rows
+        (40008, 512, 128, torch.float16),  # 626 workgroups, ragged last
     ],
 )
 def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, group: int, dtype: torch.dtype) -> None:
@@ -224,13 +226,14 @@ def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, 
     assert (y.float() - other).abs().max().item() <= 1e-2 * other.abs().max().item()
 
 
-@pytest.mark.parametrize("rows", [17, 32, 45, 64])
-def test_wide_outputs_run_the_gemv_per_16_rows(rows: int) -> None:
-    """17..64 rows over N >= 8192: the automatic choice runs the few-token GEMV
-    once per 16-row chunk (with a ragged last chunk and the bias in each)."""
-    packed, scale, zero = _layer(8192, 1024, 128, seed=rows)
+@pytest.mark.parametrize(("rows", "out"), [(17, 8192), (32, 8192), (45, 8192), (64, 8192), (5, 20000), (32, 20000)])
+def test_wide_outputs_run_the_gemv_per_16_rows(rows: int, out: int) -> None:
+    """5..64 rows over N >= 8192: the automatic choice runs the few-token GEMV
+    once per 16-row chunk (with a ragged last chunk and the bias in each); past
+    16384 outputs with more workgroups than CUs."""
+    packed, scale, zero = _layer(out, 1024, 128, seed=rows)
     x = torch.randn(rows, 1024, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
-    bias = torch.randn(8192, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    bias = torch.randn(out, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
     args = (packed.to(DEV), scale.to(DEV), zero.to(DEV))
     y = kernels.int4_linear(x.to(DEV), *args)
     _check_linear(x, packed, scale, zero, y)
