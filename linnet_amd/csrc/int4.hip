@@ -628,8 +628,10 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
   }
   if (kernel == LNQ_KERNEL_AUTO) {
     // Measured (bf16, group 128, K = 4096): one row always takes the GEMV (N =
-    // 128256: 56 against 69 us; 16384: 7.8 against 9.4). At 2..4 rows the skinny
-    // kernel is ahead (N = 16384: 10.9 against 11.9 us; 28672: 17.5 against 22.2).
+    // 128256: 56 against 69 us; 16384: 7.8 against 9.4). At 2..4 rows the GEMV
+    // holds up to 56-row workgroups (N = 14336: 11.4 against 11.7 us) and the
+    // skinny kernel is ahead past them (N = 16384: 10.9 against 11.9 us; 28672:
+    // 17.5 against 22.2).
     // From 5 rows over a wide output the few-token GEMV wins (N = 14336: 13.7
     // against 21.7 us at 16 rows), and at 17..64 rows it still does once per 16-row
     // chunk, each chunk streaming the weight again (26.7 against 35.6 us at 32 rows,
@@ -637,7 +639,9 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
     // 16-feature workgroups each read all of x. Over N < 8192 the skinny kernel is
     // ahead from 16 rows on (N = 4096: 7.2 against 7.9 us; N = 1024: 6.3 against 7.3).
     const bool wide = N >= 8192;
-    if (gemv_ok && (M == 1 || (M > 4 && wide))) return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
+    const bool few = M <= 4 && N <= 14336;
+    if (gemv_ok && (M == 1 || few || (M > 4 && wide)))
+      return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
     if (wide && M > 16 && M <= 64 && int4_gemv_supports(16, N, K, G, x, packed, scale, zero)) {
       const size_t xrow = static_cast<size_t>(K) * 2, yrow = static_cast<size_t>(N) * 2;
       for (int c = 0; c < M; c += 16) {
