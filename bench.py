@@ -355,9 +355,10 @@ class Int4Llama:
                             n2=1 + 0.1 * torch.randn(hidden, generator=g, device=dev)) for _ in range(layers)]
         # The decode kernels' step runs q, k and v as one joined projection (their
         # int4 rows stacked: one launch, one weight stream) and reads q, k and v as
-        # column slices of its output.
+        # column slices of its output; gate and up likewise.
         for p in self.layers:
             p["qkv"] = tuple(torch.cat([p["q"][i], p["k"][i], p["v"][i]], dim=0) for i in range(3))
+            p["gate_up"] = tuple(torch.cat([p["gate"][i], p["up"][i]], dim=0) for i in range(3))
         self.norm = 1 + 0.1 * torch.randn(hidden, generator=g, device=dev)
         self.head = lin(vocab, hidden)
         # KV caches, bf16 (the model's dtype), capacity ctx + 1 rounded up to 4: Kt
@@ -420,7 +421,9 @@ class Int4Llama:
             q, k, v = qkv[:, : self.hidden], qkv[:, self.hidden : self.hidden + kvd], qkv[:, self.hidden + kvd :]
             att = decode.decode_attention(q, k, v, self.cos, self.sin, self.kt[i], self.vc[i], self.pos)
             h = decode.rmsnorm(x, p["n2"], 1e-5, self.linear(att, p["o"]))
-            delta = self.linear(decode.silu_mul(self.linear(h, p["gate"]), self.linear(h, p["up"])), p["down"])
+            gu = self.linear(h, p["gate_up"])
+            ffn = gu.shape[1] // 2
+            delta = self.linear(decode.silu_mul(gu[:, :ffn], gu[:, ffn:]), p["down"])
         return self.linear(decode.rmsnorm(x, self.norm, 1e-5, delta), self.head)
 
 
@@ -429,10 +432,10 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
     1024-token context, captured as one HIP graph and replayed; tokens/s =
     batch / step time. Batch 1 runs every linear on the one-token GEMV
     kernels, batch 32 on the few-token GEMV (gate, up) and the skinny kernel;
-    q, k and v run as one joined projection; between the linears, the decode
-    kernels of `torch/decode.py` (4 a layer). `linears_ms` replays the step's
-    193 int4 linear calls alone; `torch_glue_ms` is the same step with the glue
-    as torch ops (~40 small kernels a layer) and q, k, v apart."""
+    q|k|v and gate|up run as joined projections; between the linears, the
+    decode kernels of `torch/decode.py` (4 a layer). `linears_ms` replays the
+    step's 161 int4 linear calls alone; `torch_glue_ms` is the same step with the
+    glue as torch ops (~40 small kernels a layer) and the projections apart."""
     out: dict[str, object] = {"layers": 32, "hidden": 4096, "heads": "32/8", "ffn": 14336, "vocab": 128256,
                               "context": 1024, "weights": "int4 g128, bf16 scales, u8 zeros; random-init"}
     model = Int4Llama(torch, kernels, dev)
@@ -457,10 +460,10 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         end.record()
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / reps
-        # The same step's 193 int4 linear calls alone (inputs and outputs preallocated).
+        # The same step's 161 int4 linear calls alone (inputs and outputs preallocated).
         calls = []
         for p in model.layers:
-            for name, k in (("qkv", 4096), ("o", 4096), ("gate", 4096), ("up", 4096), ("down", 14336)):
+            for name, k in (("qkv", 4096), ("o", 4096), ("gate_up", 4096), ("down", 14336)):
                 xin = (torch.randn(batch, k, device=dev) * 0.5).to(torch.bfloat16)
                 yout = torch.empty(batch, p[name][0].shape[0], dtype=torch.bfloat16, device=dev)
                 calls.append((xin, p[name], yout))

@@ -259,6 +259,12 @@ LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, i
 /* a = silu(g) * u = g / (1 + exp(-g)) * u for n bf16 elements, f32 math. */
 LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n, void* stream);
 
+/* The same over rows: a [rows, width] (contiguous) = silu(g) * u with the rows of
+ * g and u g_stride and u_stride elements apart (e.g. the halves of a joined
+ * gate|up projection's output [rows, 2*width]: u = g + width, both strides 2*width). */
+LNQ_API LnqStatus lnq_silu_mul_rows(const void* g, const void* u, void* a, int64_t rows, int64_t width,
+                                    int64_t g_stride, int64_t u_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -374,11 +374,16 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
 
 __global__ __launch_bounds__(decode::THREADS) void silu_mul_kernel(const uint16_t* __restrict__ g,
                                                                    const uint16_t* __restrict__ u,
-                                                                   uint16_t* __restrict__ a, int64_t n) {
+                                                                   uint16_t* __restrict__ a, int64_t n, int64_t width,
+                                                                   int64_t g_stride, int64_t u_stride) {
+  // Element i of a [rows, width]: row i / width of g and u, whose rows are
+  // g_stride and u_stride elements apart (the two halves of a joined gate|up
+  // projection's output, say).
   for (int64_t i = blockIdx.x * static_cast<int64_t>(decode::THREADS) + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * decode::THREADS) {
-    const float gv = bf16_bits_to_f32(g[i]);
-    a[i] = f32_to_bf16_bits(gv / (1.f + expf(-gv)) * bf16_bits_to_f32(u[i]));
+    const int64_t r = i / width, c = i - r * width;
+    const float gv = bf16_bits_to_f32(g[r * g_stride + c]);
+    a[i] = f32_to_bf16_bits(gv / (1.f + expf(-gv)) * bf16_bits_to_f32(u[r * u_stride + c]));
   }
 }
 
@@ -491,8 +496,24 @@ LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n,
   const int64_t blocks = (n + decode::THREADS - 1) / decode::THREADS;
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
                      dim3(decode::THREADS), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(g),
-                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n);
+                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n, n, int64_t{0}, int64_t{0});
   return launched("silu_mul");
+}
+
+LNQ_API LnqStatus lnq_silu_mul_rows(const void* g, const void* u, void* a, int64_t rows, int64_t width,
+                                    int64_t g_stride, int64_t u_stride, void* stream) {
+  LNQ_REQUIRE(rows >= 0 && width >= 0 && g_stride >= width && u_stride >= width, "lnq_silu_mul_rows: bad shape");
+  if (rows == 0 || width == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(g && u && a, "lnq_silu_mul_rows: null pointer");
+  const int64_t n = rows * width;
+  const int64_t blocks = (n + decode::THREADS - 1) / decode::THREADS;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
+                     dim3(decode::THREADS), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(g),
+                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n, width, g_stride, u_stride);
+  return launched("silu_mul_rows");
 }
 
 }  // extern "C"

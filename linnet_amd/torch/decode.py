@@ -72,12 +72,24 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
 
 
 def silu_mul(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
-    """`silu(g) * u` elementwise in f32, rounded once to bf16."""
+    """`silu(g) * u` elementwise in f32, rounded once to bf16. g and u may be 2-D
+    column slices (rows strided, each row contiguous), e.g. the two halves of a
+    joined gate|up projection's output; the result is contiguous."""
     device = _on_gpu("silu_mul", g, u)
-    _bf16("silu_mul", g, u)
+    if g.dtype != torch.bfloat16 or u.dtype != torch.bfloat16:
+        raise LinnetError("silu_mul: g and u are bf16")
     if g.shape != u.shape:
         raise LinnetError("silu_mul: g and u have one shape")
-    a = torch.empty_like(g)
+    if g.is_contiguous() and u.is_contiguous():
+        a = torch.empty_like(g)
+        with torch.cuda.device(device):
+            _lib.call("lnq_silu_mul", _ptr(g), _ptr(u), _ptr(a), g.numel(), _stream(device))
+        return a
+    if g.dim() != 2 or g.stride(1) != 1 or u.stride(1) != 1:
+        g, u = g.contiguous(), u.contiguous()
+    rows, width = g.shape
+    a = torch.empty(rows, width, dtype=g.dtype, device=device)
     with torch.cuda.device(device):
-        _lib.call("lnq_silu_mul", _ptr(g), _ptr(u), _ptr(a), g.numel(), _stream(device))
+        _lib.call("lnq_silu_mul_rows", _ptr(g), _ptr(u), _ptr(a), rows, width, g.stride(0), u.stride(0),
+                  _stream(device))
     return a

@@ -29,7 +29,7 @@ def declared() -> list[str]:
 def test_header_declares_the_abi() -> None:
     names = declared()
     assert "lnq_int4_linear" in names and "lnq_mm8" in names
-    assert len(names) == len(set(names)) == 21
+    assert len(names) == len(set(names)) == 22
 
 
 def test_library_exports_every_declared_symbol() -> None:
@@ -109,6 +109,8 @@ def test_empty_calls_succeed_without_a_device() -> None:
     assert _status("lnq_int4_dequantize", NULL, NULL, NULL, NULL, 0, 128, 128, _lib.BF16, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_rows8", NULL, NULL, NULL, 0, 128, 1, _lib.BF16, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_silu_mul", NULL, NULL, NULL, 0, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_silu_mul_rows", NULL, NULL, NULL, 0, 8, 16, 16, NULL)[0] == _lib.LNQ_OK
+    assert "bad shape" in _status("lnq_silu_mul_rows", FAKE, FAKE, FAKE, 2, 8, 4, 16, NULL)[1]
     assert _status("lnq_rmsnorm", NULL, NULL, NULL, NULL, 0, 4096, ctypes.c_float(1e-5), NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_int4_repack", NULL, NULL, NULL, 0, 1, 0, 64, 0, NULL, NULL, NULL)[0] == _lib.LNQ_OK
 

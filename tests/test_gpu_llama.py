@@ -101,6 +101,9 @@ def test_decode_kernels_match_torch_ops() -> None:
     uu = torch.randn(5, 1000, generator=g).to(torch.bfloat16).to(DEV)
     want_a = (torch.nn.functional.silu(gg.float()) * uu.float()).to(torch.bfloat16)
     assert (decode.silu_mul(gg, uu).float() - want_a.float()).abs().max().item() <= 1e-2
+    # the two halves of a joined gate|up output (strided rows) give the same bits
+    joined = torch.cat([gg, uu], dim=1)
+    assert torch.equal(decode.silu_mul(joined[:, :1000], joined[:, 1000:]), decode.silu_mul(gg, uu))
     for rows, heads, kvh, hd, cap, pos in ((2, 8, 2, 128, 40, 37), (2, 8, 2, 128, 2048, 1999), (1, 8, 2, 128, 704, 700),
                                            (2, 8, 1, 128, 132, 130), (3, 6, 2, 64, 100, 64), (1, 4, 4, 64, 68, 3)):
         _attention_case(decode, g, rows, heads, kvh, hd, cap, pos)
