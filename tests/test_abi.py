@@ -102,6 +102,14 @@ def test_other_entry_points_validate() -> None:
     assert "equal groups" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 0, 64, 64, 3, FAKE, FAKE, NULL)[1]
     assert "only GPTQ" in _status("lnq_int4_repack", FAKE, FAKE, FAKE, 1, 0, 64, 64, 1, FAKE, FAKE, NULL)[1]
     assert "zero_offset" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 2, 64, 64, 1, FAKE, FAKE, NULL)[1]
+    assert "groups of 128" in _status("lnq_fp8_groups", FAKE, FAKE, FAKE, 2, 2, 256, 64, _lib.BF16, NULL)[1]
+    assert "padded >= rows" in _status("lnq_fp8_groups", FAKE, FAKE, FAKE, 3, 2, 256, 128, _lib.BF16, NULL)[1]
+    assert "in, out % 128" in _status("lnq_mm8_block", FAKE, FAKE, FAKE, 4, FAKE, FAKE, 4, 100, 256, _lib.BF16, NULL)[1]
+    assert "stride" in _status("lnq_mm8_block", FAKE, FAKE, FAKE, 2, FAKE, FAKE, 4, 128, 256, _lib.BF16, NULL)[1]
+    assert "multiple of 32" in _status("lnq_mxfp4_experts", FAKE, 0, 0, FAKE, FAKE, FAKE, FAKE, 1, 4, 32, 64, 100,
+                                       _lib.BF16, NULL)[1]
+    assert "bf16 or f16" in _status("lnq_mxfp4_experts", FAKE, 0, 0, FAKE, FAKE, FAKE, FAKE, 1, 4, 32, 64, 128,
+                                    _lib.F32, NULL)[1]
 
 
 def test_empty_calls_succeed_without_a_device() -> None:
@@ -110,6 +118,9 @@ def test_empty_calls_succeed_without_a_device() -> None:
     assert _status("lnq_rows8", NULL, NULL, NULL, 0, 128, 1, _lib.BF16, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_silu_mul", NULL, NULL, NULL, 0, NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_silu_mul_rows", NULL, NULL, NULL, 0, 8, 16, 16, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_fp8_groups", NULL, NULL, NULL, 0, 0, 256, 128, _lib.BF16, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_mm8_block", NULL, NULL, NULL, 0, NULL, NULL, 0, 128, 256, _lib.BF16, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_mxfp4_experts", NULL, 0, 0, NULL, NULL, NULL, NULL, 0, 4, 32, 64, 128, _lib.BF16, NULL)[0] == _lib.LNQ_OK
     assert "bad shape" in _status("lnq_silu_mul_rows", FAKE, FAKE, FAKE, 2, 8, 4, 16, NULL)[1]
     assert _status("lnq_rmsnorm", NULL, NULL, NULL, NULL, 0, 4096, ctypes.c_float(1e-5), NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_int4_repack", NULL, NULL, NULL, 0, 1, 0, 64, 0, NULL, NULL, NULL)[0] == _lib.LNQ_OK
