@@ -11,10 +11,12 @@ instead of falling back to anything here.
 Modules:
 
 - `oracle.quant`   -- group-wise int4 / int8 quantize, pack, unpack,
-  dequantize; bf16 and fp8 bit encodings; per-token activation rounding
-  (numpy, bit-exact restatements).
+  dequantize; bf16 and fp8 bit encodings; per-token and per-group activation
+  rounding; GPTQ / AWQ checkpoint repack; MXFP4 decoding (numpy, bit-exact
+  restatements).
 - `oracle.linear`  -- the reference's CPU linear paths (torch on the CPU, as
-  the reference itself runs them) and an fp64 product for tolerances.
+  the reference itself runs them) and fp64 products for tolerances (plain,
+  8-bit rows, block-scaled FP8, MXFP4 experts).
 
 Parity pins (what fixes each function independently of its own formula) are
 listed in each function's docstring and exercised in `tests/test_oracle.py`.
