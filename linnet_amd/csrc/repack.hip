@@ -59,11 +59,21 @@ __global__ __launch_bounds__(repack::THREADS) void int4_repack_kernel(
           word |= ((w >> shift) & 15u) << (4 * k);
         }
       } else if (order != nullptr) {
+        // The eight source inputs first, then their eight words (independent
+        // loads, all in flight), then the codes.
+        int src[8];
+        uint32_t w[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) src[k] = order[8 * c + k];
+#pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const int src = order[8 * c + k];
-          if (src < 0 || src >= in_features) continue;  // not a permutation entry: code 0
-          const uint32_t w = static_cast<uint32_t>(qweight[static_cast<int64_t>(src >> 3) * out_features + o]);
-          word |= ((w >> (4 * (src & 7))) & 15u) << (4 * k);
+          const int sk = min(max(src[k], 0), static_cast<int>(in_features) - 1);
+          w[k] = static_cast<uint32_t>(qweight[static_cast<int64_t>(sk >> 3) * out_features + o]);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const bool ok = src[k] >= 0 && src[k] < in_features;  // not a permutation entry: code 0
+          word |= (ok ? (w[k] >> (4 * (src[k] & 7))) & 15u : 0u) << (4 * k);
         }
       } else {
         word = static_cast<uint32_t>(qweight[c * out_features + o]);
