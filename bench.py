@@ -323,110 +323,6 @@ def eight_bit(torch, dev, timed_graph, steps: int) -> dict[str, object]:
     return out
 
 
-class Int4Llama:
-    """A Llama-3.1-8B-shaped decoder whose linear layers are
-    all int4 g128 through this package's `int4_linear` (the `Int4GroupLinear`
-    swap of the reference's `examples/01-llama` card): random-init weights
-    (N(0, 0.02)) quantized on the GPU, RMSNorm, rotary embedding (theta 500000,
-    no frequency scaling), grouped-query attention over a KV cache of `ctx`
-    random entries, SiLU MLP and an int4 lm_head. Attention runs in f32 on
-    contiguous operands (K cache stored transposed). `step(x)` is one decode
-    step of `batch` tokens at position `ctx`; `linear` may be swapped for a
-    reference (dequantized weight and `F.linear`). `fused` runs the glue between
-    the linear layers as this package's decode kernels (`torch/decode.py`: norm
-    with the residual add, attention with the rotary embedding and cache write,
-    SiLU x up); otherwise as torch ops (the reference for the tests)."""
-
-    def __init__(self, torch, kernels, dev, layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336,
-                 vocab=128256, ctx=1024, batch=1, seed=0, fused=True):
-        self.torch, self.kernels, self.fused = torch, kernels, fused
-        self.hidden, self.heads, self.kv_heads, self.hd = hidden, heads, kv_heads, hidden // heads
-        g = torch.Generator(device=dev).manual_seed(seed)
-
-        def lin(n, k):
-            w = torch.randn(n, k, generator=g, device=dev) * 0.02
-            packed, scale, zero = kernels.quantize_int4(w, 128)
-            return packed, scale.to(torch.bfloat16), zero
-
-        kvd = kv_heads * self.hd
-        self.layers = [dict(q=lin(hidden, hidden), k=lin(kvd, hidden), v=lin(kvd, hidden), o=lin(hidden, hidden),
-                            gate=lin(ffn, hidden), up=lin(ffn, hidden), down=lin(hidden, ffn),
-                            n1=1 + 0.1 * torch.randn(hidden, generator=g, device=dev),
-                            n2=1 + 0.1 * torch.randn(hidden, generator=g, device=dev)) for _ in range(layers)]
-        # The decode kernels' step runs q, k and v as one joined projection (their
-        # int4 rows stacked: one launch, one weight stream) and reads q, k and v as
-        # column slices of its output; gate and up likewise.
-        for p in self.layers:
-            p["qkv"] = tuple(torch.cat([p["q"][i], p["k"][i], p["v"][i]], dim=0) for i in range(3))
-            p["gate_up"] = tuple(torch.cat([p["gate"][i], p["up"][i]], dim=0) for i in range(3))
-        self.norm = 1 + 0.1 * torch.randn(hidden, generator=g, device=dev)
-        self.head = lin(vocab, hidden)
-        # KV caches, bf16 (the model's dtype), capacity ctx + 1 rounded up to 4: Kt
-        # [batch, kv_heads, hd, cap] (transposed), V [batch, kv_heads, cap, hd].
-        # Position ctx is written by the step.
-        cap = (ctx + 4) // 4 * 4
-        self.kt = [torch.randn(batch, kv_heads, self.hd, cap, generator=g, device=dev).to(torch.bfloat16)
-                   for _ in range(layers)]
-        self.vc = [torch.randn(batch, kv_heads, cap, self.hd, generator=g, device=dev).to(torch.bfloat16)
-                   for _ in range(layers)]
-        self.pos = ctx
-        inv = 1.0 / (500000.0 ** (torch.arange(0, self.hd, 2, device=dev, dtype=torch.float32) / self.hd))
-        ang = ctx * inv
-        self.cos, self.sin = torch.cos(ang), torch.sin(ang)
-        self.linear = lambda x, w: kernels.int4_linear(x, *w)
-
-    def _rms(self, x, w):
-        torch = self.torch
-        xf = x.float()
-        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w).to(torch.bfloat16)
-
-    def _rope(self, t):  # [B, H, hd] f32
-        half = self.hd // 2
-        a, b = t[..., :half], t[..., half:]
-        return self.torch.cat([a * self.cos - b * self.sin, b * self.cos + a * self.sin], dim=-1)
-
-    def step(self, x):
-        if self.fused:
-            return self._step_fused(x)
-        torch = self.torch
-        bsz = x.shape[0]
-        grp = self.heads // self.kv_heads
-        for i, p in enumerate(self.layers):
-            h = self._rms(x, p["n1"])
-            q = self._rope(self.linear(h, p["q"]).float().view(bsz, self.heads, self.hd))
-            k = self._rope(self.linear(h, p["k"]).float().view(bsz, self.kv_heads, self.hd))
-            v = self.linear(h, p["v"]).float().view(bsz, self.kv_heads, self.hd)
-            self.kt[i][:, :, :, self.pos] = k
-            self.vc[i][:, :, self.pos, :] = v
-            qg = q.view(bsz, self.kv_heads, grp, self.hd)
-            live = self.pos + 1
-            kt = self.kt[i][..., :live].float()
-            scores = torch.matmul(qg, kt) * (self.hd ** -0.5)  # [B, kvh, grp, ctx + 1]
-            att = torch.matmul(torch.softmax(scores, dim=-1), self.vc[i][:, :, :live].float())  # [B, kvh, grp, hd]
-            x = x + self.linear(att.reshape(bsz, self.hidden).to(torch.bfloat16), p["o"])
-            h = self._rms(x, p["n2"])
-            a = torch.nn.functional.silu(self.linear(h, p["gate"]).float()) * self.linear(h, p["up"]).float()
-            x = x + self.linear(a.to(torch.bfloat16), p["down"])
-        return self.linear(self._rms(x, self.norm), self.head)
-
-    def _step_fused(self, x):
-        from linnet_amd.torch import decode
-
-        x = x.clone()  # the residual stream is updated in place
-        delta = None
-        for i, p in enumerate(self.layers):
-            h = decode.rmsnorm(x, p["n1"], 1e-5, delta)
-            qkv = self.linear(h, p["qkv"])
-            kvd = self.kv_heads * self.hd
-            q, k, v = qkv[:, : self.hidden], qkv[:, self.hidden : self.hidden + kvd], qkv[:, self.hidden + kvd :]
-            att = decode.decode_attention(q, k, v, self.cos, self.sin, self.kt[i], self.vc[i], self.pos)
-            h = decode.rmsnorm(x, p["n2"], 1e-5, self.linear(att, p["o"]))
-            gu = self.linear(h, p["gate_up"])
-            ffn = gu.shape[1] // 2
-            delta = self.linear(decode.silu_mul(gu[:, :ffn], gu[:, ffn:]), p["down"])
-        return self.linear(decode.rmsnorm(x, self.norm, 1e-5, delta), self.head)
-
-
 def llama_decode(torch, kernels, dev) -> dict[str, object]:
     """Config 5: one decode step of the int4 Llama-3.1-8B-shaped stack at a
     1024-token context, captured as one HIP graph and replayed; tokens/s =
@@ -438,6 +334,8 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
     glue as torch ops (~40 small kernels a layer) and the projections apart."""
     out: dict[str, object] = {"layers": 32, "hidden": 4096, "heads": "32/8", "ffn": 14336, "vocab": 128256,
                               "context": 1024, "weights": "int4 g128, bf16 scales, u8 zeros; random-init"}
+    from linnet_amd.llama import Int4Llama
+
     model = Int4Llama(torch, kernels, dev)
     for batch in (1, 32):
         if batch != 1:

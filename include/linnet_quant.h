@@ -50,6 +50,8 @@ typedef int32_t LnqStatus;
                                one row also in = 256 * S * waves for S = 2..4
                                slices a wave (e.g. 6144, 8192, 12288, 14336) with out <=
                                8192 (S = 2) or 4096 (S = 3, 4)) */
+#define LNQ_KERNEL_TILED_128 4 /* the tiled kernel with tiles of 128 output columns */
+#define LNQ_KERNEL_TILED_256 5 /* the tiled kernel with tiles of 256 output columns */
 
 /* The ABI version this library implements (LNQ_ABI_VERSION). */
 LNQ_API uint32_t lnq_abi_version(void);
@@ -78,6 +80,16 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
                                   const uint8_t* zero, const void* bias, void* y, int64_t rows,
                                   int64_t in_features, int64_t out_features, int64_t group,
                                   int32_t dtype, int32_t kernel, void* stream);
+
+/* The kernel lnq_int4_linear runs for these arguments on the current device, its
+ * operands 16-byte aligned: *chosen = LNQ_KERNEL_GEMV, LNQ_KERNEL_SKINNY,
+ * LNQ_KERNEL_TILED_128 or LNQ_KERNEL_TILED_256 (GEMV also for 17..64 rows run as
+ * 16-row chunks). Fails as lnq_int4_linear would on arguments it refuses.
+ * No counterpart in the reference (its dispatch is Python, torch_source.cpp:1553-1570):
+ * lets a caller or a test see which kernel a shape takes. */
+LNQ_API LnqStatus lnq_int4_linear_plan(int64_t rows, int64_t in_features, int64_t out_features,
+                                       int64_t group, int32_t dtype, int32_t kernel,
+                                       int32_t* chosen);
 
 /* out[out, in] = (q - zero) * scale computed in f32 and rounded once to `dtype`
  * (the scale's dtype: bf16, f16 or f32). Any even group dividing `in`.
@@ -121,7 +133,9 @@ LNQ_API LnqStatus lnq_int4_unpack(const uint8_t* packed, void* codes, int64_t pa
  *   (GPTQ in order, AWQ interleaved); zero_offset (0 or 1) is added to each (1 for
  *   GPTQ's first checkpoint format, which stores each less one).
  * order: GPTQ in activation order, [in] int32 (a permutation; else NULL): input i
- * of the result is checkpoint input order[i]; an entry outside 0..in-1 reads as 0.
+ * of the result is checkpoint input order[i]. The entries are device memory and are
+ * not checked here (an entry outside 0..in-1 reads as code 0, not a zero weight):
+ * the caller passes a permutation (the Python wrapper checks it).
  * Writes packed [out, in/2] (= [out, groups, in/groups/2], low nibble first) and
  * zero [out, groups] u8. in and out are multiples of 8, groups divides in.
  * Replaces: quant.py:222-240, 300-340 (`import_quantized`'s numpy repack: `_nibbles`,
@@ -175,6 +189,20 @@ LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t r
 LNQ_API LnqStatus lnq_mm8(const uint8_t* q, const uint8_t* weight, const float* x_scale,
                           const float* scale, void* y, int64_t rows, int64_t out_features,
                           int64_t in_features, int32_t fp8, int32_t dtype, void* stream);
+
+/* lnq_mm8 with the tile width named: tile_n 128 or 256 output columns a workgroup,
+ * 0 for lnq_mm8's own choice (256 while that still gives every compute unit a
+ * tile). No counterpart in the reference (`torch._scaled_mm` / `int8_mm` choose
+ * internally): lets a test run each instance. */
+LNQ_API LnqStatus lnq_mm8_tiles(const uint8_t* q, const uint8_t* weight, const float* x_scale,
+                                const float* scale, void* y, int64_t rows, int64_t out_features,
+                                int64_t in_features, int32_t fp8, int32_t dtype, int32_t tile_n,
+                                void* stream);
+
+/* The tile width (128 or 256) lnq_mm8 takes for rows x out_features on the current
+ * device. */
+LNQ_API LnqStatus lnq_mm8_plan(int64_t rows, int64_t out_features, int64_t in_features,
+                               int32_t* tile_n);
 
 /* Each 128 inputs (group = 128) of each row of x [rows, in] (`dtype`: bf16, f16 or f32)
  * rounded to FP8 E4M3 with a scale of their own: scale = max(max|x|, 1e-12) / 448
@@ -242,8 +270,8 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
  * 16-byte aligned.
  * `workspace` (f32, caller-owned) holds lnq_decode_attention_workspace(rows, kv_heads,
  * head_dim, pos) floats. q_stride and kv_stride are the row strides (elements) of q
- * and of k / v, 0 for rows back to back: q, k and v may be column slices of one
- * joined q|k|v projection's output. */
+ * and of k / v, at least a row each when rows > 1 (unread at one row): q, k and v may
+ * be column slices of one joined q|k|v projection's output. */
 LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
                                        const float* sin, void* kt_cache, void* v_cache, void* out,
                                        float* workspace, int64_t workspace_floats, int64_t rows,

@@ -21,7 +21,7 @@ ABI_VERSION = 1
 
 LNQ_OK, LNQ_ERROR, LNQ_UNAVAILABLE = 0, 1, 2
 BF16, F16, F32 = 0, 1, 2
-KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV = 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV, KERNEL_TILED_128, KERNEL_TILED_256 = 0, 1, 2, 3, 4, 5
 PACKING_GPTQ, PACKING_AWQ = 0, 1
 
 _p = ctypes.c_void_p
@@ -32,6 +32,7 @@ _i32 = ctypes.c_int32
 SIGNATURES: dict[str, list[object]] = {
     "lnq_device_probe": [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "lnq_int4_linear": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
+    "lnq_int4_linear_plan": [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i32)],
     "lnq_int4_dequantize": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_int4_quantize": [_p, _p, _p, _p, _i64, _i64, _i64, _p],
     "lnq_int4_pack": [_p, _p, _i64, _p],
@@ -42,6 +43,8 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_dequantize8": [_p, _p, _p, _i64, _i64, _i32, _i64, _i64, _i32, _p],
     "lnq_rows8": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "lnq_mm8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
+    "lnq_mm8_tiles": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p],
+    "lnq_mm8_plan": [_i64, _i64, _i64, ctypes.POINTER(_i32)],
     "lnq_fp8_groups": [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "lnq_mm8_block": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_mxfp4_experts": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],

@@ -464,13 +464,15 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
     default: LNQ_ATT_G(HD_, 8); break;                    \
   }
   const int64_t group = heads / kv_heads;
-  // Row strides of q and of k / v in elements (0: rows packed back to back), so
-  // q, k and v may be column slices of one joined projection's output.
-  const int64_t qs_ = q_stride == 0 ? heads * head_dim : q_stride;
-  const int64_t kvs_ = kv_stride == 0 ? kv_heads * head_dim : kv_stride;
-  LNQ_REQUIRE(qs_ >= heads * head_dim && kvs_ >= kv_heads * head_dim,
-              "lnq_decode_attention: row strides %lld / %lld shorter than a row", static_cast<long long>(qs_),
-              static_cast<long long>(kvs_));
+  // Row strides of q and of k / v in elements, so q, k and v may be column
+  // slices of one joined projection's output. Past one row each stride spans at
+  // least a row: a stride of 0 (a row broadcast over rows) is refused rather
+  // than read as rows that are not there. One row reads no stride.
+  LNQ_REQUIRE(rows == 1 || (q_stride >= heads * head_dim && kv_stride >= kv_heads * head_dim),
+              "lnq_decode_attention: row strides %lld / %lld shorter than a row", static_cast<long long>(q_stride),
+              static_cast<long long>(kv_stride));
+  const int64_t qs_ = rows == 1 ? heads * head_dim : q_stride;
+  const int64_t kvs_ = rows == 1 ? kv_heads * head_dim : kv_stride;
   if (head_dim == 64) {
     LNQ_ATT(64);
   } else {

@@ -661,15 +661,29 @@ LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t r
   return launched("rows8");
 }
 
-LNQ_API LnqStatus lnq_mm8(const uint8_t* qx, const uint8_t* weight, const float* x_scale,
-                          const float* scale, void* y, int64_t rows, int64_t out_features,
-                          int64_t in_features, int32_t fp8, int32_t dtype, void* stream) {
+// The tile width of mm8_kernel: 256-column tiles read half the bytes per FLOP
+// of 128-column ones, but only pay while they still give every compute unit a tile.
+static int mm8_width(int M, int N) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+  }
+  const long tiles256 = static_cast<long>((M + mm8::BM - 1) / mm8::BM) * ((N + 255) / 256);
+  return tiles256 >= cus ? 256 : 128;
+}
+
+LNQ_API LnqStatus lnq_mm8_tiles(const uint8_t* qx, const uint8_t* weight, const float* x_scale,
+                                const float* scale, void* y, int64_t rows, int64_t out_features,
+                                int64_t in_features, int32_t fp8, int32_t dtype, int32_t tile_n,
+                                void* stream) {
   LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16, "lnq_mm8: output is bf16 or f16, not dtype %d", dtype);
   LNQ_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0 && in_features % 128 == 0,
               "lnq_mm8: bad shape rows=%lld out=%lld in=%lld (in %% 128 == 0)", (long long)rows,
               (long long)out_features, (long long)in_features);
   LNQ_REQUIRE(rows <= INT32_MAX && out_features <= INT32_MAX && in_features <= INT32_MAX,
               "lnq_mm8: sizes exceed 2^31");
+  LNQ_REQUIRE(tile_n == 0 || tile_n == 128 || tile_n == 256, "lnq_mm8: tile_n is 0, 128 or 256, not %d", tile_n);
   LNQ_REQUIRE(qx && weight && x_scale && scale && y, "lnq_mm8: null pointer");
   LNQ_REQUIRE(aligned(qx, 16) && aligned(weight, 16), "lnq_mm8: operands must be 16-byte aligned");
   if (rows == 0) {
@@ -681,16 +695,8 @@ LNQ_API LnqStatus lnq_mm8(const uint8_t* qx, const uint8_t* weight, const float*
               "lnq_mm8: operands exceed the 2 GiB buffer range");
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto* ys = static_cast<uint16_t*>(y);
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-  }
-  // 256-column tiles read half the bytes per FLOP of 128-column ones, but only
-  // pay while they still give every compute unit a tile.
-  const long tiles256 = static_cast<long>((M + mm8::BM - 1) / mm8::BM) * ((N + 255) / 256);
-  const bool wide = tiles256 >= cus;
-  const int bn = wide ? 256 : 128;
+  const int bn = tile_n == 0 ? mm8_width(M, N) : tile_n;
+  const bool wide = bn == 256;
   const int tiles = ((M + mm8::BM - 1) / mm8::BM) * ((N + bn - 1) / bn);
 #define LNQ_MM8(DT, F, BN)                                                                          \
   hipLaunchKernelGGL((mm8_kernel<DT, F, BN>), dim3(tiles), dim3(mm8::THREADS), 0, s, qx, weight,   \
@@ -702,6 +708,23 @@ LNQ_API LnqStatus lnq_mm8(const uint8_t* qx, const uint8_t* weight, const float*
 #undef LNQ_MM8_BN
 #undef LNQ_MM8
   return launched("mm8");
+}
+
+LNQ_API LnqStatus lnq_mm8(const uint8_t* qx, const uint8_t* weight, const float* x_scale,
+                          const float* scale, void* y, int64_t rows, int64_t out_features,
+                          int64_t in_features, int32_t fp8, int32_t dtype, void* stream) {
+  return lnq_mm8_tiles(qx, weight, x_scale, scale, y, rows, out_features, in_features, fp8, dtype, 0, stream);
+}
+
+LNQ_API LnqStatus lnq_mm8_plan(int64_t rows, int64_t out_features, int64_t in_features, int32_t* tile_n) {
+  LNQ_REQUIRE(tile_n != nullptr, "lnq_mm8_plan: null pointer");
+  LNQ_REQUIRE(rows >= 0 && rows <= INT32_MAX && out_features > 0 && out_features <= INT32_MAX &&
+                  in_features > 0 && in_features % 128 == 0,
+              "lnq_mm8_plan: bad shape rows=%lld out=%lld in=%lld", (long long)rows, (long long)out_features,
+              (long long)in_features);
+  *tile_n = mm8_width(static_cast<int>(rows), static_cast<int>(out_features));
+  clear_error();
+  return LNQ_OK;
 }
 
 }  // extern "C"

@@ -573,11 +573,13 @@ static LnqStatus launch_skinny(const void* x, const uint8_t* packed, const void*
   return launch_skinny_lw<DT, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
 }
 
-// Defined in int4_gemm.hip: the prefill dequant-GEMM.
+// Defined in int4_gemm.hip: the prefill dequant-GEMM. `bn` is the tile width
+// (128 or 256 output columns); int4_tiled_width gives the automatic one.
 LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale,
                             const uint8_t* zero, const void* bias, void* y, int M, int N, int K,
-                            int G, int dtype, hipStream_t stream);
+                            int G, int dtype, int bn, hipStream_t stream);
 bool int4_tiled_supports(int M, int N, int K, int G, int dtype);
+int int4_tiled_width(int M, int N);
 
 // Defined in int4_gemv.hip: the one-token dequant-GEMV.
 bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
@@ -585,46 +587,53 @@ bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* p
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                            const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream);
 
-}  // namespace lnq
-
-using namespace lnq;
-
-extern "C" {
-
-LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const void* scale,
-                                  const uint8_t* zero, const void* bias, void* y, int64_t rows,
-                                  int64_t in_features, int64_t out_features, int64_t group,
-                                  int32_t dtype, int32_t kernel, void* stream) {
-  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16,
-              "lnq_int4_linear: activations are bf16 or f16, not dtype %d", dtype);
-  LNQ_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0,
-              "lnq_int4_linear: bad shape rows=%lld in=%lld out=%lld", (long long)rows,
-              (long long)in_features, (long long)out_features);
-  LNQ_REQUIRE(in_features % 128 == 0, "lnq_int4_linear: in_features %lld is not a multiple of 128",
-              (long long)in_features);
-  LNQ_REQUIRE(group > 0 && in_features % group == 0 && (group == 32 || group == 64 || group % 128 == 0),
-              "lnq_int4_linear: a group of %lld is not 32, 64 or a multiple of 128 dividing %lld",
-              (long long)group, (long long)in_features);
-  LNQ_REQUIRE(rows <= INT32_MAX && in_features <= INT32_MAX && out_features <= INT32_MAX,
-              "lnq_int4_linear: sizes exceed 2^31");
-  LNQ_REQUIRE(x && packed && scale && zero && y, "lnq_int4_linear: null pointer");
-  LNQ_REQUIRE(aligned(x, 16) && aligned(packed, 16),
-              "lnq_int4_linear: x and packed must be 16-byte aligned");
-  LNQ_REQUIRE(kernel >= LNQ_KERNEL_AUTO && kernel <= LNQ_KERNEL_GEMV,
-              "lnq_int4_linear: unknown kernel %d", kernel);
-  if (rows == 0) {
-    clear_error();
-    return LNQ_OK;
+// The argument checks of lnq_int4_linear that do not look at the operands;
+// false (with the message set) when one fails.
+static bool check_int4_linear(int64_t rows, int64_t in_features, int64_t out_features, int64_t group,
+                              int32_t dtype, int32_t kernel, const char* who) {
+  if (!(dtype == LNQ_BF16 || dtype == LNQ_F16)) {
+    set_error("%s: activations are bf16 or f16, not dtype %d", who, dtype);
+    return false;
   }
-  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
-  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!(rows >= 0 && out_features > 0 && in_features > 0)) {
+    set_error("%s: bad shape rows=%lld in=%lld out=%lld", who, (long long)rows, (long long)in_features,
+              (long long)out_features);
+    return false;
+  }
+  if (in_features % 128 != 0) {
+    set_error("%s: in_features %lld is not a multiple of 128", who, (long long)in_features);
+    return false;
+  }
+  if (!(group > 0 && in_features % group == 0 && (group == 32 || group == 64 || group % 128 == 0))) {
+    set_error("%s: a group of %lld is not 32, 64 or a multiple of 128 dividing %lld", who, (long long)group,
+              (long long)in_features);
+    return false;
+  }
+  if (!(rows <= INT32_MAX && in_features <= INT32_MAX && out_features <= INT32_MAX)) {
+    set_error("%s: sizes exceed 2^31", who);
+    return false;
+  }
+  if (!(kernel >= LNQ_KERNEL_AUTO && kernel <= LNQ_KERNEL_TILED_256)) {
+    set_error("%s: unknown kernel %d", who, kernel);
+    return false;
+  }
+  return true;
+}
+
+// The kernel lnq_int4_linear runs (LNQ_KERNEL_GEMV, _SKINNY, _TILED_128 or
+// _TILED_256), or -1 with the message set when the one asked for does not take
+// the shape. GEMV at 17..64 rows means the few-token GEMV per 16-row chunk.
+static int choose_int4_kernel(int M, int N, int K, int G, int dtype, int kernel, const void* x,
+                              const void* packed, const void* scale, const void* zero) {
   // The one-workgroup-per-CU GEMV takes 1..16 rows (1: one x row broadcast; 2..16:
   // x row m in MFMA A row m).
   const bool gemv_ok = int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
   if (kernel == LNQ_KERNEL_GEMV) {
-    LNQ_REQUIRE(gemv_ok, "lnq_int4_linear: the one-token kernel does not take rows=%d N=%d K=%d group=%d", M, N, K, G);
-    return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
+    if (!gemv_ok) {
+      set_error("lnq_int4_linear: the one-token kernel does not take rows=%d N=%d K=%d group=%d", M, N, K, G);
+      return -1;
+    }
+    return LNQ_KERNEL_GEMV;
   }
   if (kernel == LNQ_KERNEL_AUTO) {
     // Measured (bf16, group 128, K = 4096): one row always takes the GEMV (N =
@@ -640,30 +649,86 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
     // ahead from 16 rows on (N = 4096: 7.2 against 7.9 us; N = 1024: 6.3 against 7.3).
     const bool wide = N >= 8192;
     const bool few = M <= 4 && N <= 14336;
-    if (gemv_ok && (M == 1 || few || (M > 4 && wide)))
-      return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
-    if (wide && M > 16 && M <= 64 && int4_gemv_supports(16, N, K, G, x, packed, scale, zero)) {
-      const size_t xrow = static_cast<size_t>(K) * 2, yrow = static_cast<size_t>(N) * 2;
-      for (int c = 0; c < M; c += 16) {
-        const int rc = M - c < 16 ? M - c : 16;
-        const LnqStatus st = launch_int4_gemv(static_cast<const uint8_t*>(x) + c * xrow, packed, scale, zero, bias,
-                                              static_cast<uint8_t*>(y) + c * yrow, rc, N, K, G, dtype, s);
-        if (st != LNQ_OK) return st;
-      }
-      return LNQ_OK;
+    if (gemv_ok && (M == 1 || few || (M > 4 && wide))) return LNQ_KERNEL_GEMV;
+    if (wide && M > 16 && M <= 64 && int4_gemv_supports(16, N, K, G, x, packed, scale, zero)) return LNQ_KERNEL_GEMV;
+    if (M > 64 && int4_tiled_supports(M, N, K, G, dtype))
+      return int4_tiled_width(M, N) == 256 ? LNQ_KERNEL_TILED_256 : LNQ_KERNEL_TILED_128;
+    return LNQ_KERNEL_SKINNY;
+  }
+  if (kernel == LNQ_KERNEL_SKINNY) return LNQ_KERNEL_SKINNY;
+  if (!int4_tiled_supports(M, N, K, G, dtype)) {
+    set_error("lnq_int4_linear: the tiled kernel does not take M=%d N=%d K=%d group=%d", M, N, K, G);
+    return -1;
+  }
+  if (kernel == LNQ_KERNEL_TILED)
+    return int4_tiled_width(M, N) == 256 ? LNQ_KERNEL_TILED_256 : LNQ_KERNEL_TILED_128;
+  return kernel;
+}
+
+}  // namespace lnq
+
+using namespace lnq;
+
+extern "C" {
+
+LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const void* scale,
+                                  const uint8_t* zero, const void* bias, void* y, int64_t rows,
+                                  int64_t in_features, int64_t out_features, int64_t group,
+                                  int32_t dtype, int32_t kernel, void* stream) {
+  if (!check_int4_linear(rows, in_features, out_features, group, dtype, kernel, "lnq_int4_linear"))
+    return LNQ_ERROR;
+  LNQ_REQUIRE(x && packed && scale && zero && y, "lnq_int4_linear: null pointer");
+  LNQ_REQUIRE(aligned(x, 16) && aligned(packed, 16),
+              "lnq_int4_linear: x and packed must be 16-byte aligned");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int code = choose_int4_kernel(M, N, K, G, dtype, kernel, x, packed, scale, zero);
+  if (code < 0) return LNQ_ERROR;
+  if (code == LNQ_KERNEL_GEMV) {
+    if (M <= 16) return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
+    // 17..64 rows over a wide output: the few-token GEMV once per 16-row chunk.
+    const size_t xrow = static_cast<size_t>(K) * 2, yrow = static_cast<size_t>(N) * 2;
+    for (int c = 0; c < M; c += 16) {
+      const int rc = M - c < 16 ? M - c : 16;
+      const LnqStatus st = launch_int4_gemv(static_cast<const uint8_t*>(x) + c * xrow, packed, scale, zero, bias,
+                                            static_cast<uint8_t*>(y) + c * yrow, rc, N, K, G, dtype, s);
+      if (st != LNQ_OK) return st;
     }
+    return LNQ_OK;
   }
-  bool tiled = kernel == LNQ_KERNEL_TILED;
-  if (kernel == LNQ_KERNEL_AUTO) tiled = M > 64 && int4_tiled_supports(M, N, K, G, dtype);
-  if (tiled) {
-    LNQ_REQUIRE(int4_tiled_supports(M, N, K, G, dtype),
-                "lnq_int4_linear: the tiled kernel does not take M=%d N=%d K=%d group=%d", M, N,
-                K, G);
-    return launch_int4_tiled(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
-  }
+  if (code == LNQ_KERNEL_TILED_128 || code == LNQ_KERNEL_TILED_256)
+    return launch_int4_tiled(x, packed, scale, zero, bias, y, M, N, K, G, dtype,
+                             code == LNQ_KERNEL_TILED_256 ? 256 : 128, s);
   if (dtype == LNQ_BF16)
     return launch_skinny<LNQ_BF16>(x, packed, scale, zero, bias, y, M, N, K, G, s);
   return launch_skinny<LNQ_F16>(x, packed, scale, zero, bias, y, M, N, K, G, s);
+}
+
+LNQ_API LnqStatus lnq_int4_linear_plan(int64_t rows, int64_t in_features, int64_t out_features,
+                                       int64_t group, int32_t dtype, int32_t kernel,
+                                       int32_t* chosen) {
+  LNQ_REQUIRE(chosen != nullptr, "lnq_int4_linear_plan: null pointer");
+  if (!check_int4_linear(rows, in_features, out_features, group, dtype, kernel, "lnq_int4_linear_plan"))
+    return LNQ_ERROR;
+  if (rows == 0) {
+    *chosen = LNQ_KERNEL_SKINNY;
+    clear_error();
+    return LNQ_OK;
+  }
+  // Any 16-byte aligned address stands for the operands.
+  static const uint8_t* const kAligned = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(256));
+  const int code = choose_int4_kernel(static_cast<int>(rows), static_cast<int>(out_features),
+                                      static_cast<int>(in_features), static_cast<int>(group), dtype, kernel,
+                                      kAligned, kAligned, kAligned, kAligned);
+  if (code < 0) return LNQ_ERROR;
+  *chosen = code;
+  clear_error();
+  return LNQ_OK;
 }
 
 LNQ_API LnqStatus lnq_int4_dequantize(const uint8_t* packed, const void* scale,

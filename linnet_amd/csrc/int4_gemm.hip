@@ -424,13 +424,18 @@ static void launch_tiled(const void* x, const uint8_t* packed, const void* scale
                      static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, K, gshift);
 }
 
-LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                            const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream) {
-  const int gshift = __builtin_ctz(static_cast<unsigned>(G));
-  // 256-column tiles read half the x bytes per FLOP of 128-column ones, but
-  // only pay while they still give every compute unit a tile.
+// 256-column tiles read half the x bytes per FLOP of 128-column ones, but only
+// pay while they still give every compute unit a tile.
+int int4_tiled_width(int M, int N) {
   const long tiles256 = static_cast<long>((M + gemm::BM - 1) / gemm::BM) * ((N + 255) / 256);
-  const bool wide = tiles256 >= compute_units();
+  return tiles256 >= compute_units() ? 256 : 128;
+}
+
+LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                            const void* bias, void* y, int M, int N, int K, int G, int dtype, int bn,
+                            hipStream_t stream) {
+  const int gshift = __builtin_ctz(static_cast<unsigned>(G));
+  const bool wide = bn == 256;
   if (dtype == LNQ_BF16) {
     if (wide) launch_tiled<LNQ_BF16, 256>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
     else launch_tiled<LNQ_BF16, 128>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);

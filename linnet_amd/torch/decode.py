@@ -28,6 +28,7 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: tor
     _bf16("rmsnorm", x, *(() if delta is None else (delta,)))
     if weight.dtype != torch.float32 or weight.numel() != x.shape[-1]:
         raise LinnetError("rmsnorm: weight is f32 [hidden]")
+    weight = weight.contiguous()  # a strided view (a column of stacked weights) is read packed
     if delta is not None and delta.shape != x.shape:
         raise LinnetError("rmsnorm: delta has x's shape")
     h = torch.empty_like(x)
@@ -56,8 +57,10 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
     if q.shape != (rows, heads * hd) or k.shape != (rows, kvh * hd) or v.shape != k.shape:
         raise LinnetError("decode_attention: q [rows, heads*hd], k and v [rows, kv_heads*hd]")
     # q, k and v may be column slices of one joined projection (rows strided, each
-    # row contiguous; k and v with the same row stride).
-    if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(0) != v.stride(0):
+    # row contiguous; k and v with the same row stride). A row broadcast over rows
+    # (stride 0, or any stride shorter than a row) is copied out first.
+    short = rows > 1 and (q.stride(0) < q.shape[1] or k.stride(0) < k.shape[1] or v.stride(0) < v.shape[1])
+    if short or q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(0) != v.stride(0):
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if cos.numel() != hd // 2 or sin.numel() != hd // 2 or cos.dtype != torch.float32 or sin.dtype != torch.float32:
         raise LinnetError("decode_attention: cos and sin are f32 [hd/2]")

@@ -19,7 +19,15 @@ from ..errors import LinnetError
 
 _CODES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
 _HALF = (torch.bfloat16, torch.float16)
-KERNELS = {"auto": _lib.KERNEL_AUTO, "skinny": _lib.KERNEL_SKINNY, "tiled": _lib.KERNEL_TILED, "gemv": _lib.KERNEL_GEMV}
+KERNELS = {
+    "auto": _lib.KERNEL_AUTO,
+    "skinny": _lib.KERNEL_SKINNY,
+    "tiled": _lib.KERNEL_TILED,
+    "gemv": _lib.KERNEL_GEMV,
+    "tiled128": _lib.KERNEL_TILED_128,
+    "tiled256": _lib.KERNEL_TILED_256,
+}
+_KERNEL_NAMES = {code: name for name, code in KERNELS.items()}
 
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
@@ -109,6 +117,19 @@ def int4_linear(
             rows, depth, width, group, code, KERNELS[kernel], _stream(device),
         )
     return y
+
+
+def int4_linear_plan(rows: int, in_features: int, out_features: int, group: int,
+                     dtype: torch.dtype = torch.bfloat16, kernel: str = "auto") -> str:
+    """The kernel `int4_linear` runs for this shape on the current device: "gemv"
+    (17..64 rows: the few-token GEMV per 16-row chunk), "skinny", "tiled128" or
+    "tiled256". Raises as `int4_linear` would for a shape it refuses."""
+    if kernel not in KERNELS:
+        raise LinnetError(f"int4_linear_plan: kernel is one of {', '.join(KERNELS)}")
+    chosen = ctypes.c_int32(-1)
+    _lib.call("lnq_int4_linear_plan", rows, in_features, out_features, group, _code(dtype, "int4_linear_plan"),
+              KERNELS[kernel], ctypes.byref(chosen))
+    return _KERNEL_NAMES[chosen.value]
 
 
 def int4_weight(raw: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor) -> torch.Tensor:
@@ -213,6 +234,11 @@ def int4_repack(
         if packing != "gptq" or order.dtype != torch.int32 or tuple(order.shape) != (in_features,):
             raise LinnetError(f"int4_repack: an order is GPTQ's, [{in_features}] int32")
         order = order.contiguous()
+        # The kernel reads whatever input an entry names (an entry out of range as
+        # code 0): only a permutation gives the layer's weights, so anything else
+        # is refused here, at load time (one host sync).
+        if not torch.equal(torch.sort(order).values, torch.arange(in_features, dtype=torch.int32, device=device)):
+            raise LinnetError(f"int4_repack: order is not a permutation of 0..{in_features - 1}")
     if zero_offset not in (0, 1):
         raise LinnetError(f"int4_repack: zero_offset is 0 or 1, not {zero_offset}")
     qweight, qzeros = qweight.contiguous(), qzeros.contiguous()
@@ -346,8 +372,11 @@ def int8_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return _rows8(x, False)
 
 
-def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype, fp8: bool) -> torch.Tensor:
+def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype, fp8: bool,
+         tile_n: int = 0) -> torch.Tensor:
     device = _on_gpu("mm8", q, weight, x_scale, scale)
+    if tile_n not in (0, 128, 256):
+        raise LinnetError(f"mm8: tile_n is 0 (automatic), 128 or 256, not {tile_n}")
     rows, depth = q.shape
     width = weight.shape[0]
     if weight.shape[1] != depth:
@@ -360,9 +389,17 @@ def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: to
     ws = scale.to(torch.float32).contiguous()
     y = torch.empty(rows, width, dtype=dtype, device=device)
     with torch.cuda.device(device):
-        _lib.call("lnq_mm8", _ptr(qb), _ptr(wb), _ptr(xs), _ptr(ws), _ptr(y), rows, width, depth,
-                  int(fp8), code, _stream(device))
+        _lib.call("lnq_mm8_tiles", _ptr(qb), _ptr(wb), _ptr(xs), _ptr(ws), _ptr(y), rows, width, depth,
+                  int(fp8), code, tile_n, _stream(device))
     return y
+
+
+def mm8_plan(rows: int, out_features: int, in_features: int) -> int:
+    """The tile width (128 or 256 output columns) `int8_mm` / `fp8_mm` take for this
+    shape on the current device."""
+    tile = ctypes.c_int32(0)
+    _lib.call("lnq_mm8_plan", rows, out_features, in_features, ctypes.byref(tile))
+    return tile.value
 
 
 def fp8_groups(x: torch.Tensor, group: int, padded: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -420,17 +457,21 @@ def fp8_block_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, s
     return y
 
 
-def int8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+def int8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype,
+            tile_n: int = 0) -> torch.Tensor:
     """`(q @ weight.T) * x_scale * scale` in `dtype` for int8 rows and int8 weights
-    with one scale a row, summed exactly in int32 on MFMA (`kernels.py:805-915`)."""
-    return _mm8(q, weight, x_scale, scale, dtype, False)
+    with one scale a row, summed exactly in int32 on MFMA (`kernels.py:805-915`).
+    `tile_n` (128 or 256) forces the tile width, 0 lets the library choose."""
+    return _mm8(q, weight, x_scale, scale, dtype, False, tile_n)
 
 
-def fp8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+def fp8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype,
+           tile_n: int = 0) -> torch.Tensor:
     """`(q @ weight.T) * x_scale * scale` in `dtype` for FP8 E4M3 rows and weights on
     gfx950's FP8 MFMA, summed in f32: what `torch._scaled_mm(q, W.t(), scale_a,
-    scale_b, out_dtype)` computes for the reference (`torch/quantized.py:129`)."""
-    return _mm8(q, weight, x_scale, scale, dtype, True)
+    scale_b, out_dtype)` computes for the reference (`torch/quantized.py:129`).
+    `tile_n` (128 or 256) forces the tile width, 0 lets the library choose."""
+    return _mm8(q, weight, x_scale, scale, dtype, True, tile_n)
 
 
 def quantize_int8(weight: torch.Tensor, group: int, dtype: str) -> tuple[torch.Tensor, torch.Tensor]:

@@ -28,8 +28,10 @@ def declared() -> list[str]:
 
 def test_header_declares_the_abi() -> None:
     names = declared()
-    assert "lnq_int4_linear" in names and "lnq_mm8" in names
-    assert len(names) == len(set(names)) == 22
+    expected = {"lnq_int4_linear", "lnq_int4_linear_plan", "lnq_int4_dequantize", "lnq_int4_quantize", "lnq_mm8",
+                "lnq_mm8_tiles", "lnq_mm8_plan", "lnq_w8a16", "lnq_rows8", "lnq_mxfp4_experts"}
+    assert expected <= set(names)
+    assert len(names) == len(set(names))
 
 
 def test_library_exports_every_declared_symbol() -> None:
@@ -96,6 +98,9 @@ def test_other_entry_points_validate() -> None:
     assert "workspace" in _status("lnq_decode_attention", *[FAKE] * 9, need - 1, 2, 32, 8, 128, 1028, 1024, 0, 0, NULL)[1]
     assert "multiple of 4" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1025, 1024, 0, 0, NULL)[1]
     assert "strides" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1028, 1024, 4000, 0, NULL)[1]
+    # a row broadcast over rows (stride 0) is refused, not read as packed rows
+    assert "strides" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1028, 1024, 0, 1024, NULL)[1]
+    assert "strides" in _status("lnq_decode_attention", *[FAKE] * 9, big, 2, 32, 8, 128, 1028, 1024, 4096, 0, NULL)[1]
     assert "bad shape" in _status("lnq_rmsnorm", FAKE, NULL, FAKE, FAKE, 1, 0, ctypes.c_float(1e-5), NULL)[1]
     assert "neither GPTQ" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 2, 0, 64, 64, 1, FAKE, FAKE, NULL)[1]
     assert "multiples of 8" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 0, 60, 64, 1, FAKE, FAKE, NULL)[1]
@@ -169,3 +174,25 @@ def test_bench_refuses_more_than_one_gpu() -> None:
     done = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True, timeout=300)
     assert done.returncode == 2
     assert "one GPU" in done.stderr
+
+
+def test_plan_queries_name_the_kernel_without_a_device() -> None:
+    """The kernel choice a shape takes (256 compute units assumed with no device):
+    config 2's decode rows on the GEMV, config 3's M = 2048 shapes on the tiled
+    kernel with 256- or 128-column tiles, config 4 at 4096 rows on 256-column
+    8-bit tiles; a forced kernel that does not take the shape is refused."""
+    assert kernels.int4_linear_plan(1, 4096, 14336, 128) == "gemv"
+    assert kernels.int4_linear_plan(16, 4096, 14336, 128) == "gemv"
+    assert kernels.int4_linear_plan(2048, 4096, 14336, 128) == "tiled256"
+    assert kernels.int4_linear_plan(2048, 4096, 4096, 128) == "tiled128"
+    assert kernels.int4_linear_plan(2048, 14336, 4096, 128) == "tiled128"
+    assert kernels.int4_linear_plan(8, 512, 64, 128) == "skinny"
+    assert kernels.int4_linear_plan(8, 512, 64, 128, kernel="tiled256") == "tiled256"
+    with pytest.raises(LinnetError, match="one-token kernel"):
+        kernels.int4_linear_plan(1, 512, 64, 32, kernel="gemv")
+    with pytest.raises(LinnetError, match="unknown kernel"):
+        _lib.call("lnq_int4_linear_plan", 1, 512, 64, 128, _lib.BF16, 9, ctypes.byref(ctypes.c_int32()))
+    assert kernels.mm8_plan(4096, 28672, 8192) == 256
+    assert kernels.mm8_plan(256, 28672, 8192) == 128
+    with pytest.raises(LinnetError, match="tile_n"):
+        _lib.call("lnq_mm8_tiles", *[ctypes.c_void_p(256)] * 5, 4, 256, 128, 1, _lib.BF16, 64, None)

@@ -188,3 +188,20 @@ def test_repack_any_tile_edges() -> None:
                                                method, group, 0)
             assert np.array_equal(got_p.cpu().numpy(), packed), (method, in_features, out_features)
             assert np.array_equal(got_z.cpu().numpy(), zero), (method, in_features, out_features)
+
+
+def test_repack_refuses_an_order_that_is_not_a_permutation() -> None:
+    from linnet_amd.errors import LinnetError
+
+    g = torch.Generator().manual_seed(4)
+    words = torch.randint(-2**31, 2**31 - 1, (32, 64), generator=g, dtype=torch.int32).to(DEV)
+    qzeros = torch.randint(-2**31, 2**31 - 1, (2, 8), generator=g, dtype=torch.int32).to(DEV)
+    good = torch.randperm(256, generator=g).to(torch.int32)
+    kernels.int4_repack(words, qzeros, "gptq", 128, 1, good.to(DEV))
+    repeated = good.clone()
+    repeated[5] = repeated[6]
+    out_of_range = good.clone()
+    out_of_range[0] = 256
+    for bad in (repeated, out_of_range):
+        with pytest.raises(LinnetError, match="permutation"):
+            kernels.int4_repack(words, qzeros, "gptq", 128, 1, bad.to(DEV))

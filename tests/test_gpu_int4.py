@@ -226,7 +226,8 @@ def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, 
     assert (y.float() - other).abs().max().item() <= 1e-2 * other.abs().max().item()
 
 
-@pytest.mark.parametrize(("rows", "out"), [(17, 8192), (32, 8192), (45, 8192), (64, 8192), (5, 20000), (32, 20000)])
+@pytest.mark.parametrize(("rows", "out"), [(17, 8192), (32, 8192), (45, 8192), (64, 8192), (5, 20000), (32, 20000),
+                                           (34, 20000), (19, 28672)])
 def test_wide_outputs_run_the_gemv_per_16_rows(rows: int, out: int) -> None:
     """5..64 rows over N >= 8192: the automatic choice runs the few-token GEMV
     once per 16-row chunk (with a ragged last chunk and the bias in each); past
@@ -235,6 +236,7 @@ def test_wide_outputs_run_the_gemv_per_16_rows(rows: int, out: int) -> None:
     x = torch.randn(rows, 1024, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
     bias = torch.randn(out, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
     args = (packed.to(DEV), scale.to(DEV), zero.to(DEV))
+    assert kernels.int4_linear_plan(rows, 1024, out, 128) == "gemv"
     y = kernels.int4_linear(x.to(DEV), *args)
     _check_linear(x, packed, scale, zero, y)
     for c in range(0, rows, 16):

@@ -1,4 +1,4 @@
-"""The int4 decode step of bench.py's Llama-shaped stack, small:
+"""The int4 decode step of the Llama-shaped stack (`linnet_amd.llama`):
 every linear through the C ABI kernels against the same step with the reference's
 fallback product (the weight dequantized to bf16, then `F.linear`,
 `torch_source.cpp:1567-1568`), and its HIP-graph replays against eager steps.
@@ -10,16 +10,11 @@ below, max errors printed)."""
 
 from __future__ import annotations
 
-import sys
-from pathlib import Path
-
 import pytest
 import torch
 
-sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
-
-import bench  # noqa: E402
-from linnet_amd.torch import kernels  # noqa: E402
+from linnet_amd.llama import Int4Llama
+from linnet_amd.torch import kernels
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -37,7 +32,7 @@ def test_int4_decode_step_matches_the_dequantized_reference(batch: int, fused: b
     the torch-glue step with dequantized-bf16 linears."""
     from linnet_amd.torch import decode
 
-    model = bench.Int4Llama(torch, kernels, DEV, batch=batch, seed=batch, fused=fused, **SMALL)
+    model = Int4Llama(torch, kernels, DEV, batch=batch, seed=batch, fused=fused, **SMALL)
     x = (torch.randn(batch, SMALL["hidden"], generator=torch.Generator().manual_seed(7)) * 0.5).to(torch.bfloat16).to(DEV)
     calls = []
     attention = decode.decode_attention
@@ -56,9 +51,71 @@ def test_int4_decode_step_matches_the_dequantized_reference(batch: int, fused: b
     assert err <= 3e-2 * scale
 
 
+def _exact_linear(x, w):
+    """The product the kernels compute: the weight dequantized exactly in f32, f32
+    sums, one rounding of the output to x's dtype."""
+    packed, scale, zero = w
+    return (x.float() @ kernels.int4_weight(packed, scale.float(), zero).T).to(x.dtype)
+
+
+def _compare(what: str, got: torch.Tensor, want: torch.Tensor) -> tuple[float, float]:
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    rel = (got - want).norm().item() / want.norm().item()
+    agree = (got.argmax(-1) == want.argmax(-1)).float().mean().item()
+    print(f"{what}: logits max abs err {err:.3e}, rel to max|logit| {err / scale:.3e}, relative L2 {rel:.3e}, "
+          f"top-1 agreement {agree:.3f}", flush=True)
+    return err / scale, agree
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_full_size_decode_step_matches_the_dequantized_reference(batch: int) -> None:
+    """Config 5 at full size (32 layers, hidden 4096, 32/8 heads, FFN 14336, vocab
+    128256, context 1024), layer by layer: each layer of the step (decode kernels,
+    joined int4 projections) and the head take the same input as the torch-glue
+    layer whose linears multiply (a) the exactly dequantized f32 weight -- the
+    product the kernels compute -- and (b) the weight rounded to bf16, the
+    reference's fallback (`torch_source.cpp:1567-1568`); the layer's attention and
+    MLP branch outputs (each a chain of products with bf16 intermediates, every
+    product held to 1e-2 on its own) must agree within 1e-2 of their largest
+    element, the logits within 1e-2 (a) / 2e-2 (b) of max|logit|. The reference's
+    output feeds the next layer, so an error is not compounded over 32 random
+    layers: run end to end, the two steps' logits part by about 4% of their max
+    (printed below) from summation-order differences alone."""
+    print(f"full config-5 step batch={batch}", flush=True)
+    model = Int4Llama(torch, kernels, DEV, batch=batch, seed=11, fused=True)
+    x = (torch.randn(batch, 4096, generator=torch.Generator().manual_seed(2)) * 0.5).to(torch.bfloat16).to(DEV)
+    errors = {(name, part): [] for name in ("exact", "bf16") for part in ("attn", "mlp")}
+    cur = x
+    for i in range(32):
+        got = {}
+        got["mlp"] = model.layer_fused(i, cur.clone(), None, got).float()
+        for name, lin in (("exact", _exact_linear), ("bf16", _reference_linear)):
+            want = {}
+            model.layer_torch(i, cur, lin, want)
+            for part in ("attn", "mlp"):
+                w = want[part].float()
+                errors[name, part].append((got[part].float() - w).abs().max().item() / w.abs().max().item())
+        cur = model.layer_torch(i, cur, _exact_linear)
+    for (name, part), errs in errors.items():
+        print(f"batch {batch}: {part} branch error rel to its max vs {name}-weight layers: max {max(errs):.3e}, "
+              f"mean {sum(errs) / len(errs):.3e}; " + " ".join(f"{e:.1e}" for e in errs), flush=True)
+        assert max(errs) <= 1e-2
+    logits = model.head_fused(cur.clone(), None).float()
+    for name, lin, bound in (("exact", _exact_linear, 1e-2), ("bf16", _reference_linear, 2e-2)):
+        rel, agree = _compare(f"batch {batch} head vs {name}-weight", logits, model.head_torch(cur, lin).float())
+        assert rel <= bound and agree >= 0.95
+    # End to end (reported only: chaotic over 32 random layers, see above).
+    model.pos = 1024
+    end = model.step(x).float()
+    model.fused, model.linear = False, _reference_linear
+    _compare(f"batch {batch} end to end vs bf16-weight step", end, model.step(x).float())
+    del model
+
+
 @pytest.mark.parametrize("fused", [True, False])
 def test_int4_decode_step_replays_as_a_graph(fused: bool) -> None:
-    model = bench.Int4Llama(torch, kernels, DEV, batch=1, seed=3, fused=fused, **SMALL)
+    model = Int4Llama(torch, kernels, DEV, batch=1, seed=3, fused=fused, **SMALL)
     x = (torch.randn(1, SMALL["hidden"], generator=torch.Generator().manual_seed(1)) * 0.5).to(torch.bfloat16).to(DEV)
     eager = model.step(x).clone()
     torch.cuda.synchronize()
@@ -137,3 +194,23 @@ def _attention_case(decode, g, rows: int, heads: int, kvh: int, hd: int, cap: in
     # the new key and value in the caches as bf16 (the key rounded once from f32)
     assert (kt[:, :, :, pos].float() - kt_ref[:, :, :, pos].float()).abs().max().item() <= 1e-2
     assert torch.equal(vc, vc_ref)
+
+
+def test_decode_attention_copies_a_row_broadcast_over_rows() -> None:
+    """q, k, v expanded from one row over two (row stride 0) are read as two equal
+    rows, not as packed rows past the one that exists."""
+    from linnet_amd.torch import decode
+
+    g = torch.Generator().manual_seed(8)
+    heads, kvh, hd, cap, pos = 8, 2, 128, 68, 40
+    q1 = torch.randn(1, heads * hd, generator=g).to(torch.bfloat16).to(DEV)
+    k1 = torch.randn(1, kvh * hd, generator=g).to(torch.bfloat16).to(DEV)
+    v1 = torch.randn(1, kvh * hd, generator=g).to(torch.bfloat16).to(DEV)
+    kt1 = torch.randn(1, kvh, hd, cap, generator=g).to(torch.bfloat16).to(DEV)
+    vc1 = torch.randn(1, kvh, cap, hd, generator=g).to(torch.bfloat16).to(DEV)
+    ang = pos / (500000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    cos, sin = torch.cos(ang).to(DEV), torch.sin(ang).to(DEV)
+    kt2, vc2 = kt1.expand(2, -1, -1, -1).contiguous(), vc1.expand(2, -1, -1, -1).contiguous()
+    got = decode.decode_attention(q1.expand(2, -1), k1.expand(2, -1), v1.expand(2, -1), cos, sin, kt2, vc2, pos)
+    one = decode.decode_attention(q1, k1, v1, cos, sin, kt1, vc1, pos)
+    assert torch.equal(got[0], one[0]) and torch.equal(got[1], one[0])
