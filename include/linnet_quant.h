@@ -284,6 +284,26 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
 LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim,
                                                int64_t pos);
 
+/* Floats of the workspace lnq_decode_attention_noalloc holds on each GPU (32 MiB). */
+#define LNQ_DECODE_ATTENTION_SCRATCH_FLOATS 8388608
+
+/* lnq_decode_attention without a workspace argument and without allocating: the
+ * split-K partial results go to a static device array of the library,
+ * LNQ_DECODE_ATTENTION_SCRATCH_FLOATS floats on each GPU it runs on, held until the
+ * process ends (its address looked up once per device on the first call there).
+ * Refuses a step whose workspace (lnq_decode_attention_workspace) exceeds it, e.g.
+ * past 32 rows x 8 KV heads x 1984 positions at head_dim 128. Every call on a GPU
+ * shares that GPU's array, which keeps the last call's contents (no entry needs to
+ * start at zero): calls that overlap on one GPU (two streams, two threads) race.
+ * No counterpart in the reference: for callers that cannot allocate device memory --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. */
+LNQ_API LnqStatus lnq_decode_attention_noalloc(const void* q, const void* k, const void* v,
+                                               const float* cos, const float* sin, void* kt_cache,
+                                               void* v_cache, void* out, int64_t rows, int64_t heads,
+                                               int64_t kv_heads, int64_t head_dim, int64_t cap,
+                                               int64_t pos, int64_t q_stride, int64_t kv_stride,
+                                               void* stream);
+
 /* a = silu(g) * u = g / (1 + exp(-g)) * u for n bf16 elements, f32 math. */
 LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n, void* stream);
 

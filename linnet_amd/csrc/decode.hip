@@ -12,6 +12,8 @@
 // so results do not depend on timing. The reference gets these ops from its
 // generated module (framework ops on the GPU); they are not part of its
 // quantized-linear path.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace lnq {
@@ -21,7 +23,45 @@ constexpr int THREADS = 256;
 constexpr int MAX_GROUP = 8;  // query heads per KV head
 constexpr int CHUNK = 64;  // cache positions a workgroup takes
 constexpr int MAX_CHUNKS = 4096;  // chunks the merge holds: positions up to 262144
+constexpr int MAX_DEVICES = 64;
 }  // namespace decode
+
+static_assert(LNQ_DECODE_ATTENTION_SCRATCH_FLOATS % 64 == 0, "scratch size");
+
+// The split-K partial results of lnq_decode_attention_noalloc: one array on each
+// GPU the library runs on, held until the process ends. Host code never passes
+// this name to a kernel (on the host it stands for no device address); it
+// passes the address hipGetSymbolAddress gives for the current device.
+static __device__ __align__(256) float scratch[LNQ_DECODE_ATTENTION_SCRATCH_FLOATS];
+
+namespace {
+std::mutex scratch_mutex;
+float* scratch_address[decode::MAX_DEVICES] = {};
+}  // namespace
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept; nullptr with the error set if
+// the lookup fails.
+static float* scratch_on_current_device() {
+  int device = -1;
+  const hipError_t got = hipGetDevice(&device);
+  if (got != hipSuccess || device < 0 || device >= decode::MAX_DEVICES) {
+    set_error("lnq_decode_attention_noalloc: no current device (%s)", hipGetErrorString(got));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address[device] == nullptr) {
+    void* address = nullptr;
+    const hipError_t found = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (found != hipSuccess || address == nullptr) {
+      set_error("lnq_decode_attention_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                hipGetErrorString(found));
+      return nullptr;
+    }
+    scratch_address[device] = static_cast<float*>(address);
+  }
+  return scratch_address[device];
+}
 
 // Sum over the block (256 threads), the same value returned to every thread.
 __device__ inline float block_sum(float v, float* red) {
@@ -486,6 +526,34 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
 LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim, int64_t pos) {
   const int64_t chunks = (pos + decode::CHUNK) / decode::CHUNK;
   return rows * kv_heads * chunks * decode::MAX_GROUP * (head_dim + 2);
+}
+
+LNQ_API LnqStatus lnq_decode_attention_noalloc(const void* q, const void* k, const void* v, const float* cos,
+                                               const float* sin, void* kt_cache, void* v_cache, void* out,
+                                               int64_t rows, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                               int64_t cap, int64_t pos, int64_t q_stride, int64_t kv_stride,
+                                               void* stream) {
+  // The sizes the workspace depends on, checked before any device call.
+  LNQ_REQUIRE(head_dim == 64 || head_dim == 128, "lnq_decode_attention_noalloc: head_dim is 64 or 128, not %lld",
+              static_cast<long long>(head_dim));
+  LNQ_REQUIRE(rows >= 0 && rows <= INT32_MAX && kv_heads > 0 && kv_heads <= INT32_MAX && pos >= 0 &&
+                  pos < decode::MAX_CHUNKS * decode::CHUNK,
+              "lnq_decode_attention_noalloc: bad shape rows=%lld kv_heads=%lld pos=%lld",
+              static_cast<long long>(rows), static_cast<long long>(kv_heads), static_cast<long long>(pos));
+  const int64_t need = lnq_decode_attention_workspace(rows, kv_heads, head_dim, pos);
+  LNQ_REQUIRE(need <= LNQ_DECODE_ATTENTION_SCRATCH_FLOATS,
+              "lnq_decode_attention_noalloc: the step needs %lld workspace floats, more than the %lld the library "
+              "holds (use lnq_decode_attention with a workspace of that size)",
+              static_cast<long long>(need), static_cast<long long>(LNQ_DECODE_ATTENTION_SCRATCH_FLOATS));
+  float* work = nullptr;
+  if (rows > 0) {
+    work = scratch_on_current_device();
+    if (work == nullptr) return LNQ_ERROR;
+  }
+  // The kernels write every workspace entry the merge reads in the same call, so
+  // nothing in `scratch` has to start at zero.
+  return lnq_decode_attention(q, k, v, cos, sin, kt_cache, v_cache, out, work, LNQ_DECODE_ATTENTION_SCRATCH_FLOATS,
+                              rows, heads, kv_heads, head_dim, cap, pos, q_stride, kv_stride, stream);
 }
 
 LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n, void* stream) {
