@@ -5,8 +5,10 @@
 // rounding), so that every MFMA product is x * bf16(W) as in the reference's
 // dequant + BLAS path (src/backend/torch_source.cpp:1561-1566).
 //
-// Tiles: 256 rows of x by BN = 256 or 128 columns of W per workgroup of 8
-// waves, two per SIMD. A wave owns a 128 x 64 (BN = 256) or 64 x 64 (BN = 128)
+// Two kernels, by tile width:
+//
+// int4_tiled_kernel (256-column tiles, wide outputs). 256 rows of x by 256
+// columns of W per workgroup of 8 waves, two per SIMD. A wave owns a 128 x 64
 // block of MFMA 32x32x16 tiles; 64 inputs per step. Two waves per SIMD is what
 // lets the matrix core run while a wave's loads and dequantization issue: on
 // gfx950 an MFMA 32x32x16 holds its wave's issue for about 20 of its 32
@@ -40,6 +42,19 @@
 // Workgroups are numbered so that each XCD (workgroup b runs on XCD b % 8)
 // owns a contiguous run of tiles, ordered in groups of 4 row tiles: the
 // tiles resident on one XCD share x and W tiles in its L2.
+//
+// int4_narrow_kernel (128-column tiles: one tile per CU at N = 4096, M =
+// 2048). 4 waves, one per SIMD, each owning 32 columns of W for all 256 rows
+// of x, so no column is dequantized twice and the dequantized weights never go
+// through LDS: lane l of a wave loads the packed dwords of its column (l % 32)
+// and dequantizes them straight into its MFMA operand registers. A 32x32x16
+// operand lane holds 8 consecutive inputs of one column -- one packed dword --
+// and lane half h = l / 32 takes input blocks 4 h .. 4 h + 3 of a 64-input
+// step (16 bytes, one load), so MFMA kk (0..3) sums blocks kk and kk + 4; the
+// x operand reads the same blocks from LDS. With W out of LDS, x gets a ring
+// of four 32 KB stages, DMA'd three steps ahead. Measured against the
+// 8-wave kernel with 128-column tiles on config 3's N = 4096 shapes (M =
+// 2048): K = 4096 72 against 84-92 us, K = 14336 231 against 240-245 us.
 #include "common.hpp"
 
 namespace lnq {
@@ -58,12 +73,6 @@ struct Cfg<256> {
   static constexpr int WAVES_N = 4;  // waves of 128 x 64, 2 x 4
   static constexpr int FA = 4;       // 32-row fragments of a wave
   static constexpr int FB = 2;       // 32-column fragments of a wave
-};
-template <>
-struct Cfg<128> {
-  static constexpr int WAVES_N = 2;  // waves of 64 x 64, 4 x 2
-  static constexpr int FA = 2;
-  static constexpr int FB = 2;
 };
 }  // namespace gemm
 
@@ -393,6 +402,245 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   }
 }
 
+// ------------------------------------------------- 128-column tiles: int4_narrow_kernel
+namespace narrow {
+constexpr int WAVES = 4;
+constexpr int THREADS = 64 * WAVES;
+constexpr int WB = 32;            // columns of W a wave owns
+constexpr int BN = WAVES * WB;    // 128
+constexpr int FA = gemm::BM / 32;  // 8 row fragments of 32
+constexpr int NS = 4;             // x stages
+constexpr int LPS = 3 + 8;        // loads a wave issues a step: weights, scale, zero, 8 x DMAs
+}  // namespace narrow
+
+template <int DT>
+__global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint8_t* __restrict__ zero, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
+    int gshift) {
+  using namespace narrow;
+  using gemm::BK;
+  using gemm::BM;
+  using E = Elem<DT>;
+  __shared__ __attribute__((aligned(16))) uint16_t XS[NS * BM * BK];
+  LNQ_MFMA_IN_AGPRS();
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  if (tm >= tiles_m || tn >= tiles_n) return;
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  const int groups = K >> gshift;
+  const int steps = K / BK;
+
+  // Rows past M (and columns past N) read zeros through the buffer range check;
+  // a step past the end reads through a 0-byte descriptor.
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint32_t>(static_cast<size_t>(M) * K * 2));
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * (K >> 1)));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
+  const __amdgpu_buffer_rsrc_t rnull = buffer_rsrc(packed, 0);
+
+  // x: DMA i (0..7) of wave w writes rows 32 i + 8 w .. + 7 of a stage, in the
+  // swizzled layout of int4_tiled_kernel (the key (row >> 1) & 7 = (4 w + l /
+  // 16) & 7 does not depend on i).
+  const int xrow = 8 * wave + (lane >> 3);
+  const int xcol = (lane & 7) ^ ((xrow >> 1) & 7);
+  const int xoff = (m0 + xrow) * K * 2 + xcol * 16;
+  auto load_x = [&](int stage, __amdgpu_buffer_rsrc_t r, int k0, int i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(XS + stage * BM * BK + wave * 512 + i * 32 * BK), 16, xoff,
+                                              2 * k0 + i * 64 * K, 0, 0);
+  };
+
+  // W: lane -> column n0 + 32 wave + lane % 32; half h = lane / 32 reads input
+  // blocks 4 h .. 4 h + 3 of a step (16 bytes), all in one group (G >= 32).
+  const int h = lane >> 5;
+  const int ncol = n0 + wave * WB + (lane & 31);
+  const int woff = ncol * (K >> 1) + 16 * h;
+  const int soff = ncol * groups * 2;
+  const int zoff = ncol * groups;
+  struct WRegs {
+    u32x4 w;
+    uint32_t s, z;
+  };
+  auto load_w = [&](WRegs& r, int ks) {
+    const bool in = ks < steps;
+    const int k0 = in ? ks * BK : 0;
+    const int g = (k0 + 32 * h) >> gshift;
+    const __amdgpu_buffer_rsrc_t qs = in ? rs : rnull, qz = in ? rz : rnull, qw = in ? rw : rnull;
+    r.w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qw, woff, k0 >> 1, 0));
+    r.s = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(qs, soff + 2 * g, 0, 0));
+    r.z = __builtin_amdgcn_raw_buffer_load_b8(qz, zoff + g, 0, 0);
+  };
+
+  // A dword's 8 codes dequantized into one operand fragment, as 8 positions of
+  // about three VALU instructions: (q - z) * s = fma(q, s, -z * s) in f32
+  // (exact), one rounding to the 16-bit type, as int4_tiled_kernel does.
+  struct Deq {
+    uint32_t lo, hi;
+    float f0, f1, v0, v1;
+  };
+  Deq q;
+  float sv = 0.f, nzs = 0.f;
+  auto cvtb = [](uint32_t v, int byte) -> float { return static_cast<float>((v >> (8 * byte)) & 0xffu); };
+  auto set_scale = [&](const WRegs& r) {
+    sv = E::to_f32(static_cast<uint16_t>(r.s));
+    nzs = -static_cast<float>(r.z & 0xffu) * sv;
+  };
+  auto deq_slot = [&](uint32_t w, int pos, u32x4& o) {
+    switch (pos) {
+      case 0:
+        q.lo = opaque(w & 0x0f0f0f0fu);
+        q.hi = opaque((w >> 4) & 0x0f0f0f0fu);
+        break;
+      case 1: q.f0 = cvtb(q.lo, 0); q.f1 = cvtb(q.hi, 0); q.v0 = fmaf(q.f0, sv, nzs); break;
+      case 2: q.v1 = fmaf(q.f1, sv, nzs); o.x = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 1); break;
+      case 3: q.f1 = cvtb(q.hi, 1); q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); break;
+      case 4: o.y = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 2); q.f1 = cvtb(q.hi, 2); break;
+      case 5: q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); o.z = pack2<DT>(q.v0, q.v1); break;
+      case 6: q.f0 = cvtb(q.lo, 3); q.f1 = cvtb(q.hi, 3); q.v0 = fmaf(q.f0, sv, nzs); break;
+      default: q.v1 = fmaf(q.f1, sv, nzs); o.w = pack2<DT>(q.v0, q.v1); break;
+    }
+  };
+
+  f32x16 acc[FA];
+#pragma unroll
+  for (int a = 0; a < FA; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[a][r] = 0.f;
+
+  // x operand of MFMA kk, fragment a: rows 32 a + lane % 32, input block kk + 4 h.
+  // The fragments of one kk share the swizzle key: one offset register per kk.
+  const int lrow = lane & 31;
+  uint32_t aoff[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    aoff[kk] = static_cast<uint32_t>(lrow * 128 + (((kk + 4 * h) ^ ((lrow >> 1) & 7)) << 4));
+  auto rd = [&](int stage, int kk, int a) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(XS) + stage * BM * BK * 2 + aoff[kk] +
+                                           a * 4096);
+  };
+
+  u32x4 a0[FA], a1[FA];
+  u32x4 b0[4], b1[4];
+
+  // Region kk: FA MFMA slots on (ca, bc[kk]); slot s reads the next x fragment
+  // s, runs dequantization position s of dword kk of the next step's weights
+  // (registers dn, into bn[kk]) and the loads vm(s). Each slot is its own
+  // scheduling region, which pins the interleave.
+  auto region = [&](int kk, const u32x4* ca, u32x4* na, int nstage, int nkk, const u32x4* bc, u32x4* bn,
+                    const WRegs& dn, auto&& vm) {
+#pragma unroll
+    for (int s = 0; s < FA; ++s) {
+      acc[s] = mfma32x32x16<DT>(bc[kk], ca[s], acc[s]);
+      na[s] = rd(nstage, nkk, s);
+      deq_slot(dn.w[kk], s, bn[kk]);
+      vm(s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Step ks: MFMAs on x stage ks % NS and B fragments bc (dequantized during
+  // step ks - 1); dequantizes step ks + 1's weights (dn) into bn, requests step
+  // ks + 4's weights into req (step ks's registers, no longer read) and DMAs x
+  // of step ks + 3 into stage (ks + 3) % NS (step ks - 1's, which every wave
+  // finished reading before the previous barrier).
+  auto step = [&](int ks, int st, const u32x4* bc, u32x4* bn, const WRegs& dn, WRegs& req) {
+    const bool xin = ks + 3 < steps;
+    const __amdgpu_buffer_rsrc_t xr = xin ? rx : rnull;
+    const int xk0 = xin ? (ks + 3) * BK : 0;
+    const int xst = (st + 3) % NS;
+    auto vm = [&](int r, int s) {
+      if (r == 0 && s == 0) load_w(req, ks + 4);
+      if (r < 2 && (s & 1)) load_x(xst, xr, xk0, 4 * r + s / 2);
+    };
+    set_scale(dn);
+    region(0, a0, a1, st, 1, bc, bn, dn, [&](int s) { vm(0, s); });
+    region(1, a1, a0, st, 2, bc, bn, dn, [&](int s) { vm(1, s); });
+    region(2, a0, a1, st, 3, bc, bn, dn, [&](int s) { vm(2, s); });
+    // This wave's x DMA of step ks + 1 (issued in step ks - 2) has landed once
+    // at most the loads of steps ks - 1 and ks remain; past the barrier every
+    // wave's has, and region 3 reads step ks + 1's first x fragments.
+    wait_vm<2 * LPS>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    region(3, a1, a0, (st + 1) % NS, 0, bc, bn, dn, [&](int s) { vm(3, s); });
+  };
+
+  // Prologue: weights of steps 0..3 requested, x of steps 0..2 DMA'd, step 0's
+  // weights dequantized into b0, its first x fragments read.
+  WRegs w0, w1, w2, w3;
+  load_w(w0, 0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) load_x(0, rx, 0, i);
+  load_w(w1, 1);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) load_x(1, steps > 1 ? rx : rnull, steps > 1 ? BK : 0, i);
+  load_w(w2, 2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) load_x(2, steps > 2 ? rx : rnull, steps > 2 ? 2 * BK : 0, i);
+  load_w(w3, 3);
+  wait_vm<0>();
+  set_scale(w0);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int p = 0; p < 8; ++p) deq_slot(w0.w[kk], p, b0[kk]);
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int a = 0; a < FA; ++a) a0[a] = rd(0, 0, a);
+
+  // Step j: x stage j % 4, weight registers (w0..w3)[j % 4], B fragments b0 / b1 by parity.
+  int ks = 0;
+  for (; ks + 4 <= steps; ks += 4) {
+    step(ks + 0, 0, b0, b1, w1, w0);
+    step(ks + 1, 1, b1, b0, w2, w1);
+    step(ks + 2, 2, b0, b1, w3, w2);
+    step(ks + 3, 3, b1, b0, w0, w3);
+  }
+  const int rest = steps - ks;
+  if (rest > 0) step(ks + 0, 0, b0, b1, w1, w0);
+  if (rest > 1) step(ks + 1, 1, b1, b0, w2, w1);
+  if (rest > 2) step(ks + 2, 2, b0, b1, w3, w2);
+  // Loads of the steps past the end (zeros through rnull) may be in flight.
+  wait_vm<0>();
+
+  // Epilogue: lane l, register r of fragment a holds token 32 a + l % 32 and
+  // feature 8 (r / 4) + 4 h + r % 4 of the wave's 32 columns: registers 4q..4q+3
+  // are four consecutive features of one row of y.
+  const bool vec_out = (N & 3) == 0;
+#pragma unroll
+  for (int a = 0; a < FA; ++a) {
+    const int m = m0 + a * 32 + (lane & 31);
+    if (m >= M) continue;
+    uint16_t* yrow = y + static_cast<size_t>(m) * N;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int n = n0 + wave * WB + 8 * q4 + 4 * h;
+      uint16_t out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[i] = E::from_f32(acc[a][4 * q4 + i]);
+        if (bias != nullptr && n + i < N) out[i] = E::from_f32(E::to_f32(out[i]) + E::to_f32(bias[n + i]));
+      }
+      if (vec_out && n + 3 < N) {
+        *reinterpret_cast<u32x2*>(yrow + n) =
+            u32x2{static_cast<uint32_t>(out[0]) | (static_cast<uint32_t>(out[1]) << 16),
+                  static_cast<uint32_t>(out[2]) | (static_cast<uint32_t>(out[3]) << 16)};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n + i < N) yrow[n + i] = out[i];
+      }
+    }
+  }
+}
+
 bool int4_tiled_supports(int M, int N, int K, int G, int dtype) {
   // Buffer offsets are 32-bit: x and the packed weight stay under 2 GiB. A
   // thread's 16 or 32 weights of a step lie in one group: G is a power of two
@@ -415,13 +663,19 @@ static int compute_units() {
   return cached[dev];
 }
 
-template <int DT, int BN>
+template <int DT>
 static void launch_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                         const void* bias, void* y, int M, int N, int K, int gshift, hipStream_t stream) {
-  const int tiles = ((M + gemm::BM - 1) / gemm::BM) * ((N + BN - 1) / BN);
-  hipLaunchKernelGGL((int4_tiled_kernel<DT, BN>), dim3(tiles), dim3(gemm::THREADS), 0, stream,
-                     static_cast<const uint16_t*>(x), packed, static_cast<const uint16_t*>(scale), zero,
-                     static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, K, gshift);
+                         const void* bias, void* y, int M, int N, int K, int gshift, bool wide, hipStream_t stream) {
+  const int bn = wide ? 256 : narrow::BN;
+  const int tiles = ((M + gemm::BM - 1) / gemm::BM) * ((N + bn - 1) / bn);
+  if (wide)
+    hipLaunchKernelGGL((int4_tiled_kernel<DT, 256>), dim3(tiles), dim3(gemm::THREADS), 0, stream,
+                       static_cast<const uint16_t*>(x), packed, static_cast<const uint16_t*>(scale), zero,
+                       static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, K, gshift);
+  else
+    hipLaunchKernelGGL((int4_narrow_kernel<DT>), dim3(tiles), dim3(narrow::THREADS), 0, stream,
+                       static_cast<const uint16_t*>(x), packed, static_cast<const uint16_t*>(scale), zero,
+                       static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, K, gshift);
 }
 
 // 256-column tiles read half the x bytes per FLOP of 128-column ones, but only
@@ -436,13 +690,8 @@ LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* sc
                             hipStream_t stream) {
   const int gshift = __builtin_ctz(static_cast<unsigned>(G));
   const bool wide = bn == 256;
-  if (dtype == LNQ_BF16) {
-    if (wide) launch_tiled<LNQ_BF16, 256>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
-    else launch_tiled<LNQ_BF16, 128>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
-  } else {
-    if (wide) launch_tiled<LNQ_F16, 256>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
-    else launch_tiled<LNQ_F16, 128>(x, packed, scale, zero, bias, y, M, N, K, gshift, stream);
-  }
+  if (dtype == LNQ_BF16) launch_tiled<LNQ_BF16>(x, packed, scale, zero, bias, y, M, N, K, gshift, wide, stream);
+  else launch_tiled<LNQ_F16>(x, packed, scale, zero, bias, y, M, N, K, gshift, wide, stream);
   return launched("int4_tiled");
 }
 
