@@ -145,6 +145,70 @@ LNQ_API LnqStatus lnq_int4_repack(const int32_t* qweight, const int32_t* qzeros,
                                   int64_t in_features, int64_t out_features, int64_t groups,
                                   uint8_t* packed, uint8_t* zero, void* stream);
 
+/* ------------------------------------------------------- executables
+ * The reference runtime's executable shape (include/linnet/runtime/runtime.h:44-94):
+ * DLPack-laid-out tensors, a per-call context, and an executable of four callbacks that
+ * a plan calls (ln_plan_add / ln_plan_run, runtime.h:112-131). The layouts are the
+ * reference's, so its runtime can hold an executable made here; when its header is
+ * included first, its declarations are used. The stream is a hipStream_t. */
+#ifndef LINNET_RUNTIME_H
+#define LN_CPU 1
+#define LN_CUDA 2
+typedef struct LnDevice {
+  int32_t type; /* DLPack device type: LN_CPU, LN_CUDA; 10 is DLPack's ROCm */
+  int32_t id;
+} LnDevice;
+typedef struct LnDataType {
+  uint8_t code; /* DLPack: 0 int, 1 uint, 2 float, 4 bfloat */
+  uint8_t bits;
+  uint16_t lanes;
+} LnDataType;
+typedef struct LnTensor {
+  void* data;
+  LnDevice device;
+  int32_t ndim;
+  LnDataType dtype;
+  int64_t* shape;
+  int64_t* strides; /* in elements; NULL for a contiguous tensor */
+  uint64_t byte_offset;
+} LnTensor;
+typedef struct LnContext {
+  uint32_t abi_version;
+  LnDevice device;
+  void* stream; /* here a hipStream_t (NULL: the null stream) */
+  void* workspace;
+  size_t workspace_bytes;
+  int32_t capturing; /* nonzero while a graph records the stream */
+} LnContext;
+typedef struct LnExecutable {
+  uint32_t abi_version;
+  void* state;
+  int (*prepare)(void* state, LnContext* context);
+  int (*execute)(void* state, const LnTensor* inputs, size_t input_count, LnTensor* outputs,
+                 size_t output_count, LnContext* context);
+  const char* (*error)(void* state);
+  void (*destroy)(void* state);
+} LnExecutable;
+#endif
+
+#define LNQ_DL_ROCM 10 /* DLPack's device type of a ROCm GPU */
+
+/* An executable for std.quant::linear_int4_groups of one layer shape (in_features,
+ * out_features, group; checked as lnq_int4_linear checks them; kernel an LNQ_KERNEL_*):
+ * inputs x [*S, in] (bf16 or f16, contiguous), packed [out, in/group, group/2] u8,
+ * scale [out, in/group] of x's dtype, zero [out, in/group] u8, and an optional fifth,
+ * bias [out]; output y [*S, out] of x's dtype. Tensors are borrowed (contiguous, on a
+ * ROCm or CUDA-typed device); the context's abi_version is LNQ_ABI_VERSION.
+ * prepare checks the device is a gfx950 (LNQ_UNAVAILABLE otherwise) and holds nothing;
+ * execute enqueues on context->stream and never waits or allocates, so it may run under
+ * graph capture; error gives the state's last message; destroy frees the state.
+ * *out is filled in; the caller owns it and calls destroy once.
+ * Replaces: the linnet.backends executable a plugin returns for linear_int4_groups
+ * (backends/contract.py:228-323, runtime.h:82-94), with the generated `_int4_linear`'s
+ * semantics (torch_source.cpp:1553-1570). */
+LNQ_API LnqStatus lnq_int4_linear_executable(int64_t in_features, int64_t out_features,
+                                             int64_t group, int32_t kernel, LnExecutable* out);
+
 /* ----------------------------------------------------------------- 8-bit
  * Weights [out, in] of int8 (fp8 0) or FP8 E4M3 bytes (fp8 1). Scales (f32): one per
  * row ([out], group 0), or [out/row_block, in/group] (int8 groups: row_block 1;

@@ -33,6 +33,7 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_device_probe": [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "lnq_int4_linear": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
     "lnq_int4_linear_plan": [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i32)],
+    "lnq_int4_linear_executable": [_i64, _i64, _i64, _i32, _p],
     "lnq_int4_dequantize": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_int4_quantize": [_p, _p, _p, _p, _i64, _i64, _i64, _p],
     "lnq_int4_pack": [_p, _p, _i64, _p],
