@@ -133,6 +133,16 @@ def main() -> int:
             gemv[f"M{m}"] = {"us": round(sec * 1e6, 3), "gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
             if m == 1:
                 headline = (sec, gbps)
+        # GPTQ's activation order at one token: the take_inputs gather fused
+        # into the GEMV's x staging (lnq_int4_linear_ordered).
+        order = torch.randperm(k, generator=g, device=dev).to(torch.int32)
+        x = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+        launches = [lambda l=l: kernels.int4_linear(x, *l, out=y, order=order) for l in layers]
+        sec = timed_graph(launches, args.steps, args.warmup)
+        gbps = gemv_bytes(1, k, n) / sec / 1e9
+        gemv["M1_act_order"] = {"us": round(sec * 1e6, 3), "gbps": round(gbps, 1),
+                                "frac_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
         extra["gemv"] = gemv
         extra["gemv_weight_copies"] = copies
         del layers

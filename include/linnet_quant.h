@@ -81,6 +81,29 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
                                   int64_t in_features, int64_t out_features, int64_t group,
                                   int32_t dtype, int32_t kernel, void* stream);
 
+/* std.quant::take_inputs (stdlib/quant.linnet:142-149): taken[r, k] = x[r, order[k]]
+ * for `rows` rows of n elements of `dtype` (bf16, f16 or f32); order [n] int32. An
+ * index outside [0, n) reads 0 (the reference's index_select raises; checkpoint
+ * import checks that an order is a permutation). taken must not be x.
+ * Replaces: the `torch.index_select` candidate (src/opt/candidates.cpp:18) as the
+ * generated module emits it (src/backend/torch_source.cpp:397-398) and the
+ * interpreter's entry (python/linnet/src/linnet/torch/native.py:269-271). */
+LNQ_API LnqStatus lnq_take_inputs(const void* x, const int32_t* order, void* taken, int64_t rows, int64_t n,
+                                  int32_t dtype, void* stream);
+
+/* Int4GroupLinear.forward with an input order (GPTQ's activation order,
+ * stdlib/quant.linnet:163-174): lnq_int4_linear of take_inputs(x, order). One row at
+ * group 128 (the decode step) runs one kernel, the gather fused into the one-token
+ * GEMV's staging of x (order 16-byte aligned, kernel AUTO or GEMV); any other call
+ * gathers into `taken` (rows * in elements of `dtype`, 16-byte aligned; may be NULL
+ * when the gather is fused) and multiplies that. order NULL: lnq_int4_linear.
+ * Replaces: the two steps the generated module runs for the layer
+ * (torch_source.cpp:397-398, then `_int4_linear`, :1553-1570). */
+LNQ_API LnqStatus lnq_int4_linear_ordered(const void* x, const int32_t* order, const uint8_t* packed,
+                                          const void* scale, const uint8_t* zero, const void* bias, void* y,
+                                          void* taken, int64_t rows, int64_t in_features, int64_t out_features,
+                                          int64_t group, int32_t dtype, int32_t kernel, void* stream);
+
 /* The kernel lnq_int4_linear runs for these arguments on the current device, its
  * operands 16-byte aligned: *chosen = LNQ_KERNEL_GEMV, LNQ_KERNEL_SKINNY,
  * LNQ_KERNEL_TILED_128 or LNQ_KERNEL_TILED_256 (GEMV also for 17..64 rows run as
@@ -119,6 +142,20 @@ LNQ_API LnqStatus lnq_int4_pack(const uint8_t* codes, uint8_t* packed, int64_t p
  * (is_signed 1). Replaces: torch/packed.py:27-35 `unpack4` (i4/u4). */
 LNQ_API LnqStatus lnq_int4_unpack(const uint8_t* packed, void* codes, int64_t pairs,
                                   int32_t is_signed, void* stream);
+
+/* std.quant::Int4Linear (stdlib/quant.linnet:24-29, 101-111): a signed 4-bit weight
+ * [out, in] (i4 bytes [out, in/2], element 2k low, two's complement) with one scale a
+ * row, weight[o, i] = q[o, i] * scale[o], in the group layout lnq_int4_linear takes:
+ * packed [out, in/group, group/2] = weight ^ 0x88 (the code q + 8 of each value),
+ * group_scale [out, in/group] = scale[o] (in `dtype`: bf16, f16 or f32), zero [out,
+ * in/group] = 8, so that (code - zero) * scale is q * scale exactly, the product the
+ * reference forms before its one rounding. in % 32 == 0, even groups dividing in.
+ * No fused candidate exists in the reference (the layer runs its body, dequantize and
+ * `linear`): the layout change is prepare-time, holding in * out / 2 bytes more, as the
+ * reference's tinygemm repack of Int4GroupLinear does (torch_source.cpp:1482-1500). */
+LNQ_API LnqStatus lnq_int4_row_prepare(const uint8_t* weight, const void* scale, uint8_t* packed,
+                                       void* group_scale, uint8_t* zero, int64_t out_features,
+                                       int64_t in_features, int64_t group, int32_t dtype, void* stream);
 
 /* Packings of calibrated 4-bit checkpoints lnq_int4_repack reads. */
 #define LNQ_PACKING_GPTQ 0

@@ -38,6 +38,9 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_int4_quantize": [_p, _p, _p, _p, _i64, _i64, _i64, _p],
     "lnq_int4_pack": [_p, _p, _i64, _p],
     "lnq_int4_unpack": [_p, _p, _i64, _i32, _p],
+    "lnq_int4_row_prepare": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "lnq_take_inputs": [_p, _p, _p, _i64, _i64, _i32, _p],
+    "lnq_int4_linear_ordered": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
     "lnq_int4_repack": [_p, _p, _p, _i32, _i32, _i64, _i64, _i64, _p, _p, _p],
     "lnq_int8_quantize": [_p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_w8a16": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _i64, _i32, _p],

@@ -6,7 +6,10 @@
 A `std.quant::linear_int4_groups` call (an `Int4GroupLinear`) runs on
 `lnq_int4_linear`: the HIP kernels read the model's int4 bytes, scales and zero
 points as they are stored, so `prepare` converts nothing and the executable
-holds no bytes of its own (Marlin keeps a repacked copy). `execute` enqueues on
+holds no bytes of its own (Marlin keeps a repacked copy). A layer in GPTQ's
+activation order (`take_inputs(x, order)` right before the product,
+`stdlib/quant.linnet:163-174`) is taken as one region of both calls and runs on
+`lnq_int4_linear_ordered`, the gather fused into the one-token GEMV. `execute` enqueues on
 the caller's stream and never waits, allocates its output with PyTorch, and may
 be recorded into a HIP graph.
 
@@ -32,6 +35,7 @@ from .errors import LinnetError
 from .torch import kernels
 
 CALLEE = "std.quant::linear_int4_groups"
+TAKE = "std.quant::take_inputs"
 DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16}
 
 
@@ -87,6 +91,7 @@ class MI355XInt4:
         of 32, 64 or a multiple of 128, the weight (and bias) persistent, x the
         region's one input."""
         persistent = set(graph.parameters.values())
+        takes = _takes(graph, persistent)
         for call in graph.semantic_calls(CALLEE):
             if len(call.arguments) != 5:
                 continue
@@ -94,24 +99,40 @@ class MI355XInt4:
             if len(q.shape) != 3:
                 continue
             _, groups, group = q.shape
-            region = self._t.Region.of(graph, call.start, call.stop, call.index)
-            if (
+            if not (
                 x.dtype in DTYPES
                 and scale.dtype == x.dtype
                 and (groups * group) % 128 == 0
                 and _fused_group(group)
                 and all(v.value in persistent for v in (q, scale, zero))
                 and (bias.value is None or bias.value in persistent)
-                and tuple(region.inputs) == (x.value,)
             ):
+                continue
+            take = takes.get(x.value)
+            if take is not None and take.stop == call.start:
+                # take_inputs, then the product: one region whose one input is the
+                # untaken x, if nothing after it reads the taken x.
+                region = self._t.Region.of(graph, take.start, call.stop, call.index)
+                if tuple(region.inputs) == (take.arguments[0].value,) and len(region.outputs) == 1:
+                    yield region
+                    continue
+            region = self._t.Region.of(graph, call.start, call.stop, call.index)
+            if tuple(region.inputs) == (x.value,):
                 yield region
 
     def compile(self, region: Any, target: Any, options: Any) -> _Int4Linear:
         graph = region.graph
         if region.call is None:
             raise self._t.PlanError("linnet-amd takes a `linear_int4_groups` call")
-        x, q, scale, zero, bias = graph.calls[region.call].arguments
+        call = graph.calls[region.call]
+        x, q, scale, zero, bias = call.arguments
         path = {value: p for p, value in graph.parameters.items()}
+        order = None
+        if region.start != call.start:
+            take = _takes(graph, set(path)).get(x.value)
+            if take is None or region.start != take.start:
+                raise self._t.PlanError("linnet-amd takes `take_inputs` only right before `linear_int4_groups`")
+            order = path[take.arguments[1].value]
         values = graph.values
         meta = self._t.ExecutableMeta(
             tuple(self._t.TensorSpec(values[v].shape, values[v].dtype) for v in region.inputs),
@@ -119,20 +140,33 @@ class MI355XInt4:
             holds=0,
         )
         return _Int4Linear(meta, (path[q.value], path[scale.value], path[zero.value]),
-                           path[bias.value] if bias.value is not None else None, DTYPES[x.dtype])
+                           path[bias.value] if bias.value is not None else None, DTYPES[x.dtype], order)
 
     def estimate_cost(self, region: Any, target: Any) -> Any:
         return None  # the planner measures
 
 
-class _Int4Linear:
-    """One `linear_int4_groups` call on `lnq_int4_linear`."""
+def _takes(graph: Any, persistent: set[int]) -> dict[int, Any]:
+    """The `take_inputs(x, order)` calls whose order is a parameter, by the value
+    each makes."""
+    found = {}
+    for call in graph.semantic_calls(TAKE):
+        if len(call.arguments) == 2 and len(call.results) == 1 and call.arguments[1].value in persistent:
+            found[call.results[0].value] = call
+    return found
 
-    def __init__(self, meta: Any, paths: tuple[str, str, str], bias: str | None, dtype: torch.dtype) -> None:
+
+class _Int4Linear:
+    """One `linear_int4_groups` call (after its `take_inputs`, with `order`) on
+    `lnq_int4_linear` / `lnq_int4_linear_ordered`."""
+
+    def __init__(self, meta: Any, paths: tuple[str, str, str], bias: str | None, dtype: torch.dtype,
+                 order: str | None = None) -> None:
         self._meta = meta
         self._paths = paths
         self._bias = bias
         self._dtype = dtype
+        self._order = order
 
     @property
     def meta(self) -> Any:
@@ -146,14 +180,19 @@ class _Int4Linear:
             raise LinnetError("linnet-amd: the int4 parameters are not on the GPU")
         if q.dtype != torch.uint8 or zero.dtype != torch.uint8 or scale.dtype != self._dtype:
             raise LinnetError("linnet-amd: int4 bytes and zero points are uint8, scales the input's dtype")
+        if self._order is not None:
+            order = context.parameters[self._order]
+            if not order.is_cuda or order.dtype != torch.int32:
+                raise LinnetError("linnet-amd: the input order is an int32 parameter on the GPU")
 
     def execute(self, inputs: Sequence[torch.Tensor], outputs: Sequence[torch.Tensor], context: Any) -> Sequence[torch.Tensor]:
         q, scale, zero = (context.parameters[p] for p in self._paths)
         bias = context.parameters[self._bias] if self._bias is not None else None
+        order = context.parameters[self._order] if self._order is not None else None
         (x,) = inputs
         rows = x.reshape(-1, x.shape[-1])
-        y = kernels.int4_linear(rows, q, scale, zero, bias)
+        y = kernels.int4_linear(rows, q, scale, zero, bias, order=order)
         return [y.reshape(*x.shape[:-1], y.shape[-1])]
 
 
-__all__ = ["CALLEE", "MI355XInt4"]
+__all__ = ["CALLEE", "TAKE", "MI355XInt4"]

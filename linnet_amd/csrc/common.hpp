@@ -225,6 +225,23 @@ __device__ inline void wait_vm() {
   __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Workgroup barrier for LDS written with ds_write: waits for this wave's LDS
+// operations only, not for its vector-memory loads still in flight (a fence
+// would wait for every buffer_load ... lds too). The memory clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ inline void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// x[o] for the 8 indices of o0, o1 (int32, as loaded), read from the n values at
+// xall in LDS, packed two a dword in index order; an index outside [0, n) reads 0.
+__device__ inline u32x4 gather_x8(const uint16_t* xall, u32x4 o0, u32x4 o1, uint32_t n) {
+  auto at = [&](uint32_t i) -> uint32_t {
+    const uint32_t v = xall[i < n ? i : 0u];
+    return i < n ? v : 0u;
+  };
+  return u32x4{at(o0.x) | (at(o0.y) << 16), at(o0.z) | (at(o0.w) << 16), at(o1.x) | (at(o1.y) << 16),
+               at(o1.z) | (at(o1.w) << 16)};
+}
+
 // wait_vm with a count known only after unrolling (folds to one s_waitcnt).
 __device__ inline void wait_vm_rt(int n) {
   switch (n) {

@@ -376,11 +376,11 @@ __global__ __launch_bounds__(256) void int4_dequant_fast(
   const int g = gshift >= 0 ? k0 >> gshift : k0 / G;
   const float s = E::load(scale + n * groups + g);
   const float zf = static_cast<float>(zero[n * groups + g]);
-  // z * s is exact for a 16-bit scale (4 bits times at most 11), not for an f32 one.
-  const float zs = zf * s;
   const uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(packed + n * (K >> 1)) + unit);
-  // 16-bit scale: (q - z) * s = fma(q, s, -z*s), exact in f32, then one
-  // rounding to the output type. f32 scale: (q - z) * s, one f32 rounding.
+  // (q - z) * s as the reference writes it: q - z is exact, and so is the product
+  // for a 16-bit scale (5 bits times at most 11), then one rounding to the output
+  // type; an f32 scale rounds once in f32. (fma(q, s, -z s) would equal it but
+  // give +0 where q == z and s < 0; the product gives -0, as the reference does.)
   const uint32_t lo = opaque(w & 0x0f0f0f0fu);
   const uint32_t hi = opaque((w >> 4) & 0x0f0f0f0fu);
   float v[8];
@@ -388,13 +388,8 @@ __global__ __launch_bounds__(256) void int4_dequant_fast(
   for (int b = 0; b < 4; ++b) {
     const float q0 = static_cast<float>((lo >> (8 * b)) & 0xffu);
     const float q1 = static_cast<float>((hi >> (8 * b)) & 0xffu);
-    if constexpr (DT == LNQ_F32) {
-      v[2 * b] = (q0 - zf) * s;
-      v[2 * b + 1] = (q1 - zf) * s;
-    } else {
-      v[2 * b] = fmaf(q0, s, -zs);
-      v[2 * b + 1] = fmaf(q1, s, -zs);
-    }
+    v[2 * b] = (q0 - zf) * s;
+    v[2 * b + 1] = (q1 - zf) * s;
   }
   S* dst = out + n * K + k0;
   if constexpr (DT == LNQ_BF16) {
@@ -494,6 +489,46 @@ __global__ __launch_bounds__(256) void int4_unpack_kernel(const uint8_t* __restr
   codes[2 * i + 1] = static_cast<uint8_t>(hi);
 }
 
+// std.quant::Int4Linear's weight (signed 4-bit i4, one scale a row) in the
+// group layout the fused kernels read: the code c = nibble ^ 8 is v + 8 for the
+// signed value v, so with zero point 8 every group gives (c - 8) * s = v * s,
+// the product the reference forms before its one rounding (stdlib/quant.linnet:
+// 24-29, 101-111). Thread t: bytes 16 t .. 16 t + 15 of the weight (a whole
+// number of 16-byte pieces: rows of in/2 bytes, in % 32 == 0), and entry t of the
+// per-group scales and zero points.
+template <int DT>
+__global__ __launch_bounds__(256) void int4_row_prepare_kernel(const uint8_t* __restrict__ weight,
+                                                               const typename Elem<DT>::storage* __restrict__ scale,
+                                                               uint8_t* __restrict__ packed,
+                                                               typename Elem<DT>::storage* __restrict__ group_scale,
+                                                               uint8_t* __restrict__ zero, int64_t pieces,
+                                                               int64_t entries, int groups) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < pieces) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(weight + 16 * t);
+    *reinterpret_cast<u32x4*>(packed + 16 * t) = w ^ 0x88888888u;
+  }
+  if (t < entries) {
+    group_scale[t] = scale[t / groups];
+    zero[t] = 8;
+  }
+}
+
+// std.quant::take_inputs (stdlib/quant.linnet:142-149): taken[r, k] = x[r, order[k]]
+// over `rows` rows of n elements of type T; an index outside [0, n) reads 0.
+// One thread an output element; a row's gathered reads stay within its n
+// elements, which the caches hold after the first touch.
+template <typename T>
+__global__ __launch_bounds__(256) void take_inputs_kernel(const T* __restrict__ x, const int32_t* __restrict__ order,
+                                                          T* __restrict__ taken, int64_t total, int64_t n) {
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = t / n, k = t - r * n;
+    const int64_t i = order[k];
+    taken[t] = (i >= 0 && i < n) ? x[r * n + i] : T(0);
+  }
+}
+
 // ============================================================ launch helpers
 
 template <int DT, int LOADW, int MT, bool XL, bool SV>
@@ -585,7 +620,10 @@ int int4_tiled_width(int M, int N);
 bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
                         const void* zero);
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream);
+                           const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream,
+                           const int32_t* order = nullptr);
+bool int4_gemv_takes_order(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
+                           const void* zero, const void* order);
 
 // The argument checks of lnq_int4_linear that do not look at the operands;
 // false (with the message set) when one fails.
@@ -818,6 +856,94 @@ LNQ_API LnqStatus lnq_int4_pack(const uint8_t* codes, uint8_t* packed, int64_t p
   hipLaunchKernelGGL(int4_pack_kernel, dim3(static_cast<unsigned>((pairs + 255) / 256)), dim3(256),
                      0, static_cast<hipStream_t>(stream), codes, packed, pairs);
   return launched("int4_pack");
+}
+
+LNQ_API LnqStatus lnq_int4_row_prepare(const uint8_t* weight, const void* scale, uint8_t* packed,
+                                       void* group_scale, uint8_t* zero, int64_t out_features,
+                                       int64_t in_features, int64_t group, int32_t dtype, void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16 || dtype == LNQ_F32,
+              "lnq_int4_row_prepare: scales are bf16, f16 or f32, not dtype %d", dtype);
+  LNQ_REQUIRE(out_features >= 0 && in_features >= 0 && in_features % 32 == 0,
+              "lnq_int4_row_prepare: bad shape out=%lld in=%lld (in %% 32 == 0)", (long long)out_features,
+              (long long)in_features);
+  LNQ_REQUIRE(group > 0 && group % 2 == 0 && (in_features == 0 || in_features % group == 0),
+              "lnq_int4_row_prepare: groups of %lld must be even and divide %lld", (long long)group,
+              (long long)in_features);
+  const int64_t pieces = out_features * (in_features / 32);
+  const int64_t entries = out_features * (in_features / group);
+  if (pieces == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(weight && scale && packed && group_scale && zero, "lnq_int4_row_prepare: null pointer");
+  LNQ_REQUIRE(aligned(weight, 16) && aligned(packed, 16), "lnq_int4_row_prepare: weights must be 16-byte aligned");
+  LNQ_REQUIRE(in_features / group <= INT32_MAX, "lnq_int4_row_prepare: too many groups");
+  const int64_t n = pieces > entries ? pieces : entries;
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  const int groups = static_cast<int>(in_features / group);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define LNQ_ROWS(DT)                                                                                           \
+  hipLaunchKernelGGL((int4_row_prepare_kernel<DT>), grid, dim3(256), 0, s, weight,                             \
+                     static_cast<const typename Elem<DT>::storage*>(scale), packed,                             \
+                     static_cast<typename Elem<DT>::storage*>(group_scale), zero, pieces, entries, groups)
+  if (dtype == LNQ_BF16) LNQ_ROWS(LNQ_BF16);
+  else if (dtype == LNQ_F16) LNQ_ROWS(LNQ_F16);
+  else LNQ_ROWS(LNQ_F32);
+#undef LNQ_ROWS
+  return launched("int4_row_prepare");
+}
+
+LNQ_API LnqStatus lnq_take_inputs(const void* x, const int32_t* order, void* taken, int64_t rows, int64_t n,
+                                  int32_t dtype, void* stream) {
+  LNQ_REQUIRE(dtype == LNQ_BF16 || dtype == LNQ_F16 || dtype == LNQ_F32,
+              "lnq_take_inputs: x is bf16, f16 or f32, not dtype %d", dtype);
+  LNQ_REQUIRE(rows >= 0 && n >= 0, "lnq_take_inputs: bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
+  if (rows == 0 || n == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(x && order && taken, "lnq_take_inputs: null pointer");
+  LNQ_REQUIRE(x != taken, "lnq_take_inputs: taken must not be x");
+  const int64_t total = rows * n;
+  const int64_t blocks = (total + 255) / 256;
+  const dim3 grid(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == LNQ_F32)
+    hipLaunchKernelGGL((take_inputs_kernel<uint32_t>), grid, dim3(256), 0, s, static_cast<const uint32_t*>(x), order,
+                       static_cast<uint32_t*>(taken), total, n);
+  else
+    hipLaunchKernelGGL((take_inputs_kernel<uint16_t>), grid, dim3(256), 0, s, static_cast<const uint16_t*>(x), order,
+                       static_cast<uint16_t*>(taken), total, n);
+  return launched("take_inputs");
+}
+
+LNQ_API LnqStatus lnq_int4_linear_ordered(const void* x, const int32_t* order, const uint8_t* packed,
+                                          const void* scale, const uint8_t* zero, const void* bias, void* y,
+                                          void* taken, int64_t rows, int64_t in_features, int64_t out_features,
+                                          int64_t group, int32_t dtype, int32_t kernel, void* stream) {
+  if (order == nullptr)
+    return lnq_int4_linear(x, packed, scale, zero, bias, y, rows, in_features, out_features, group, dtype, kernel,
+                           stream);
+  if (!check_int4_linear(rows, in_features, out_features, group, dtype, kernel, "lnq_int4_linear_ordered"))
+    return LNQ_ERROR;
+  LNQ_REQUIRE(x && packed && scale && zero && y, "lnq_int4_linear_ordered: null pointer");
+  LNQ_REQUIRE(aligned(x, 16) && aligned(packed, 16), "lnq_int4_linear_ordered: x and packed must be 16-byte aligned");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  if ((kernel == LNQ_KERNEL_AUTO || kernel == LNQ_KERNEL_GEMV) &&
+      int4_gemv_takes_order(M, N, K, G, x, packed, scale, zero, order))
+    return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, static_cast<hipStream_t>(stream),
+                            order);
+  LNQ_REQUIRE(taken != nullptr && aligned(taken, 16),
+              "lnq_int4_linear_ordered: %d rows x %d inputs need a 16-byte aligned `taken` buffer of as many elements "
+              "(the gather is fused only for one row, group 128)", M, K);
+  if (lnq_take_inputs(x, order, taken, rows, in_features, dtype, stream) != LNQ_OK) return LNQ_ERROR;
+  return lnq_int4_linear(taken, packed, scale, zero, bias, y, rows, in_features, out_features, group, dtype, kernel,
+                         stream);
 }
 
 LNQ_API LnqStatus lnq_int4_unpack(const uint8_t* packed, void* codes, int64_t pairs,

@@ -30,6 +30,13 @@
 // * An odd U8 leaves a last tile of 8 rows: its two 128-input halves run as
 //   one MFMA chain, half 0 in A row 0 / B columns 0-7 and half 1 in A row 1 /
 //   B columns 8-15 (only row 0 of A carries x otherwise).
+// * Inputs in another order (ORD: GPTQ's activation order, take_inputs of
+//   stdlib/quant.linnet:142-149 ahead of the product, group 128): the packed
+//   row's k-th weight is input order[k]'s. Each lane loads its 8 entries of
+//   order with its x slice (before the weights, so nothing waits twice); once
+//   they land, the workgroup's x slices sit in LDS in input order, each lane
+//   reads x[order[k]] for its 8 k, and the taken slice continues as x does
+//   above. The gather costs two LDS barriers and no extra HBM round trip.
 #include "common.hpp"
 
 namespace lnq {
@@ -77,12 +84,14 @@ __device__ inline void widen_pair(uint32_t lo, uint32_t hi, uint32_t mask, uint3
 // Workgroup: NW = K / 256 waves, R = 8 * U8 rows. G128: group 128 (a wave's two
 // halves have consecutive groups, scales loaded as one dword); otherwise G is
 // a multiple of 256 (both halves share one group).
-template <int DT, int U8, bool G128>
+template <int DT, int U8, bool G128, bool ORD = false>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G) {
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G,
+    const int32_t* __restrict__ order) {
   using E = Elem<DT>;
+  static_assert(!ORD || G128, "inputs in another order: group 128");
   constexpr int R = 8 * U8;
   constexpr int NF = U8 / 2;            // full 16-row tiles
   constexpr bool HALF = (U8 & 1) != 0;  // a last tile of 8 rows
@@ -121,7 +130,14 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  const u32x4 xv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (k0 + 8 * (lane & 31)) * 2, 0, 0));
+  u32x4 xv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (k0 + 8 * (lane & 31)) * 2, 0, 0));
+  u32x4 ov0{}, ov1{};  // ORD: order[k0 + 8 (lane & 31) ...], 8 entries
+  if constexpr (ORD) {
+    const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(order, static_cast<uint32_t>(K * 4));
+    const int ob = (k0 + 8 * (lane & 31)) * 4;
+    ov0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob, 0, 0));
+    ov1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16, 0, 0));
+  }
   __builtin_amdgcn_sched_barrier(0);
   // Every wave's small loads enter the CU's memory pipeline before any weight
   // load: without this barrier the waves that reach their first load last find
@@ -129,24 +145,42 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   // late and their tiles are all multiplied after the stream has ended.
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  {
-    // Load u: rows n0 + 8u + (lane & 7) at 16-byte piece sigma of the wave's 128
-    // bytes; sigma = 2 (lane / 16) + ((lane / 8) % 2 ^ u % 2) puts piece sigma of
-    // row r at LDS slot 16 (sigma / 2) + 8 (sigma % 2 ^ u % 2) + r.
+  // Load u: rows n0 + 8u + (lane & 7) at 16-byte piece sigma of the wave's 128
+  // bytes; sigma = 2 (lane / 16) + ((lane / 8) % 2 ^ u % 2) puts piece sigma of
+  // row r at LDS slot 16 (sigma / 2) + 8 (sigma % 2 ^ u % 2) + r.
+  auto load_weights = [&](int u) {
     const int a = lane >> 4, b = lane & 15;
+    const int sigma = 2 * a + ((b >> 3) ^ (u & 1));
+    const int row = n0 + 8 * u + (b & 7);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(tile_lds(u >> 1, wave) + 1024 * (u & 1)), 16,
+                                             row * rowb + (k0 >> 1) + 16 * sigma, 0, 0, 2 /* non-temporal */);
+  };
+  // With an input order the gather needs every wave's x: only PRE loads go out
+  // before it, so that no wave reaches its barrier late behind a queue of its
+  // own weight loads; the rest follow the gather (loads still retire in issue
+  // order, so the counts of the waits below are unchanged).
+  constexpr int PRE = ORD && U8 > 4 ? 4 : U8;
 #pragma unroll
-    for (int u = 0; u < U8; ++u) {
-      const int sigma = 2 * a + ((b >> 3) ^ (u & 1));
-      const int row = n0 + 8 * u + (b & 7);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(tile_lds(u >> 1, wave) + 1024 * (u & 1)), 16,
-                                               row * rowb + (k0 >> 1) + 16 * sigma, 0, 0, 2 /* non-temporal */);
-    }
-  }
+  for (int u = 0; u < PRE; ++u) load_weights(u);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- x: wait for it (and the scales), stage it in pair order, sums of both halves.
-  wait_vm<U8>();
+  wait_vm<PRE>();
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ORD) {
+    // The workgroup's x in input order (Xsm holds exactly K values), then each
+    // lane's 8 taken inputs; the second barrier keeps Xsm until all have read it.
+    // Lanes 32..63 store the same values as lanes 0..31: a store under a lane
+    // condition would let the compiler sink the x load into it, behind the weights.
+    *reinterpret_cast<u32x4*>(Xw + 8 * (lane & 31)) = xv;
+    lds_barrier();
+    xv = gather_x8(&Xsm[0][0], ov0, ov1, static_cast<uint32_t>(K));
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = PRE; u < U8; ++u) load_weights(u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   if (lane < 32) *reinterpret_cast<u32x4*>(Xw + 8 * lane) = permute_x8(xv);
   float sum = 0.f;
 #pragma unroll
@@ -284,12 +318,14 @@ constexpr int slice_tile_bytes(int u8, int t, int s) {
 }
 }  // namespace gemv
 
-template <int DT, int U8, bool G128, int S>
+template <int DT, int U8, bool G128, int S, bool ORD = false>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G) {
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G,
+    const int32_t* __restrict__ order) {
   using E = Elem<DT>;
+  static_assert(!ORD || G128, "inputs in another order: group 128");
   constexpr int R = 8 * U8;
   constexpr int NF = U8 / 2;
   constexpr bool HALF = (U8 & 1) != 0;
@@ -339,19 +375,32 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
   for (int sl = 0; sl < S; ++sl)
     xv[sl] = __builtin_bit_cast(
         u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (kw + 256 * sl + 8 * (lane & 31)) * 2, 0, 0));
+  u32x4 ov[S][2];  // ORD: each slice's 8 entries of order
+  if constexpr (ORD) {
+    const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(order, static_cast<uint32_t>(K * 4));
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) {
+      const int ob = (kw + 256 * sl + 8 * (lane & 31)) * 4;
+      ov[sl][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob, 0, 0));
+      ov[sl][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16, 0, 0));
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  {
-    // Order: tile, then slice, then the tile's one or two loads, so that each
-    // slice of a tile is multiplied as soon as its own loads land.
+  // Order: tile, then slice, then the tile's one or two loads, so that each
+  // slice of a tile is multiplied as soon as its own loads land. Loads lo..hi-1
+  // of that sequence:
+  auto load_weights = [&](int lo, int hi) {
     const int a = lane >> 4, b = lane & 15;
+    int i = 0;
 #pragma unroll
     for (int T = 0; T < (U8 + 1) / 2; ++T) {
 #pragma unroll
       for (int sl = 0; sl < S; ++sl) {
 #pragma unroll
-        for (int u = 2 * T; u < 2 * T + 2 && u < U8; ++u) {
+        for (int u = 2 * T; u < 2 * T + 2 && u < U8; ++u, ++i) {
+          if (i < lo || i >= hi) continue;
           const int sigma = 2 * a + ((b >> 3) ^ (u & 1));
           const int row = n0 + 8 * u + (b & 7);
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(tile_lds(T, wave, sl) + 1024 * (u & 1)), 16,
@@ -360,12 +409,28 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
         }
       }
     }
-  }
+  };
+  // As in the one-token kernel: with an input order, PRE loads before the gather.
+  constexpr int PRE = ORD && S * U8 > 4 ? 4 : S * U8;
+  load_weights(0, PRE);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- x of every slice to LDS in pair order; its sums over each half.
-  wait_vm<S * U8>();
+  wait_vm<PRE>();
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ORD) {
+    // As in the one-token kernel: x in input order (Xsm holds K values for the
+    // nw * S slices), then each slice's taken inputs.
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) *reinterpret_cast<u32x4*>(Xw + 256 * sl + 8 * (lane & 31)) = xv[sl];
+    lds_barrier();
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) xv[sl] = gather_x8(&Xsm[0][0], ov[sl][0], ov[sl][1], static_cast<uint32_t>(K));
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    load_weights(PRE, S * U8);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float xs0[S], xs1[S];
 #pragma unroll
   for (int sl = 0; sl < S; ++sl) {
@@ -718,32 +783,46 @@ bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* p
   return aligned(x, 16) && aligned(packed, 16) && (G != 128 || aligned(scale, 4)) && (G != 128 || aligned(zero, 2));
 }
 
+// Whether the one-token kernels fuse an input order (take_inputs) for this shape:
+// one row, group 128, order 16-byte aligned.
+bool int4_gemv_takes_order(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
+                           const void* zero, const void* order) {
+  return M == 1 && G == 128 && aligned(order, 16) && int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
+}
+
 template <int DT, int U8>
 static void launch_gemv_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+                           const void* bias, void* y, int N, int K, int G, const int32_t* order,
+                           hipStream_t stream) {
   const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / 256));
   const auto* xs = static_cast<const uint16_t*>(x);
   const auto* ss = static_cast<const uint16_t*>(scale);
   const auto* bs = static_cast<const uint16_t*>(bias);
   auto* ys = static_cast<uint16_t*>(y);
-  if (G == 128)
-    hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K, G);
+  if (order != nullptr)
+    hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N,
+                       K, G, order);
+  else if (G == 128)
+    hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K, G,
+                       nullptr);
   else
-    hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, false>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K, G);
+    hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, false>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K,
+                       G, nullptr);
 }
 
 template <int DT>
 static void launch_gemv_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+                           const void* bias, void* y, int N, int K, int G, const int32_t* order,
+                           hipStream_t stream) {
   switch ((N + 2047) / 2048) {
-    case 1: launch_gemv_u8<DT, 1>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
-    case 2: launch_gemv_u8<DT, 2>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
-    case 3: launch_gemv_u8<DT, 3>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
-    case 4: launch_gemv_u8<DT, 4>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
-    case 5: launch_gemv_u8<DT, 5>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
-    case 6: launch_gemv_u8<DT, 6>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
-    case 7: launch_gemv_u8<DT, 7>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
-    default: launch_gemv_u8<DT, 8>(x, packed, scale, zero, bias, y, N, K, G, stream); break;
+    case 1: launch_gemv_u8<DT, 1>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    case 2: launch_gemv_u8<DT, 2>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    case 3: launch_gemv_u8<DT, 3>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    case 4: launch_gemv_u8<DT, 4>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    case 5: launch_gemv_u8<DT, 5>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    case 6: launch_gemv_u8<DT, 6>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    case 7: launch_gemv_u8<DT, 7>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    default: launch_gemv_u8<DT, 8>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
   }
 }
 
@@ -780,39 +859,50 @@ static void launch_rows_dt(const void* x, const uint8_t* packed, const void* sca
 
 template <int DT, int U8, int S>
 static void launch_slices_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                             const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+                             const void* bias, void* y, int N, int K, int G, const int32_t* order,
+                             hipStream_t stream) {
   const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / (256 * S)));
   const auto* xs = static_cast<const uint16_t*>(x);
   const auto* ss = static_cast<const uint16_t*>(scale);
   const auto* bs = static_cast<const uint16_t*>(bias);
   auto* ys = static_cast<uint16_t*>(y);
-  if (G == 128)
+  if (order != nullptr)
+    hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, true, S, true>), grid, block, 0, stream, xs, packed, ss, zero,
+                       bs, ys, N, K, G, order);
+  else if (G == 128)
     hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, true, S>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
-                       N, K, G);
+                       N, K, G, nullptr);
   else
     hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, false, S>), grid, block, 0, stream, xs, packed, ss, zero, bs,
-                       ys, N, K, G);
+                       ys, N, K, G, nullptr);
 }
 
 template <int DT>
 static void launch_slices_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                             const void* bias, void* y, int N, int K, int G, hipStream_t stream) {
+                             const void* bias, void* y, int N, int K, int G, const int32_t* order,
+                             hipStream_t stream) {
   const int sl = gemv_slices(K), u8 = (N + 2047) / 2048;
 #define LNQ_SLICES(S_, U_) \
-  if (sl == S_ && u8 == U_) return launch_slices_u8<DT, U_, S_>(x, packed, scale, zero, bias, y, N, K, G, stream);
+  if (sl == S_ && u8 == U_)  \
+    return launch_slices_u8<DT, U_, S_>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
   LNQ_SLICES(2, 1) LNQ_SLICES(2, 2) LNQ_SLICES(2, 3) LNQ_SLICES(2, 4)
   LNQ_SLICES(3, 1) LNQ_SLICES(3, 2) LNQ_SLICES(4, 1) LNQ_SLICES(4, 2)
 #undef LNQ_SLICES
 }
 
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream) {
+                           const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream,
+                           const int32_t* order) {
+  if (order != nullptr && !int4_gemv_takes_order(M, N, K, G, x, packed, scale, zero, order)) {
+    set_error("launch_int4_gemv: the one-token kernels take no input order for this shape");
+    return LNQ_ERROR;
+  }
   if (M == 1 && gemv_slices_supports(N, K, G, x, packed, scale, zero)) {
-    if (dtype == LNQ_BF16) launch_slices_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, stream);
-    else launch_slices_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+    if (dtype == LNQ_BF16) launch_slices_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
+    else launch_slices_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
   } else if (M == 1) {
-    if (dtype == LNQ_BF16) launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, stream);
-    else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, stream);
+    if (dtype == LNQ_BF16) launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
+    else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
   } else if (M <= 4) {
     if (dtype == LNQ_BF16) launch_rows_dt<LNQ_BF16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
     else launch_rows_dt<LNQ_F16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);

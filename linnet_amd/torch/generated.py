@@ -12,6 +12,9 @@ and no bytes are held beyond the model's own. Otherwise it returns the
 reference's `_int4_pack` falls back (`torch_source.cpp:1501-1504`), and
 `_int4_linear` multiplies it with `F.linear`.
 
+`_int4_row_pack` / `_int4_row_linear` run `std.quant::Int4Linear` (per-row
+signed int4) on the same kernels.
+
 `_mxfp4_experts(x, blocks, scales, experts)` is the helper for
 `std.quant::mxfp4_experts` (`torch_source.cpp:1579-1600`): the chosen experts'
 MXFP4 weights multiplied by one HIP kernel; `_mxfp4_grouped` the one for the
@@ -76,6 +79,43 @@ def _int4_linear(
     weight = packed[0] if len(packed) == 1 else kernels.int4_weight(raw, scale, zero)
     y = functional.linear(flat, weight.to(flat.dtype))
     y = y.reshape(*x.shape[:-1], y.shape[-1])
+    return y if bias is None else y + bias
+
+
+def _int4_row_pack(weight: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, ...]:
+    """Prepare-time for `std.quant::Int4Linear` (`stdlib/quant.linnet:101-111`;
+    `weight` [Out, In/2] u8 of i4 values, `scale` [Out, 1] in the model dtype).
+    The reference's generated module has no helper for this layer: it runs the
+    body, `linear(x, cast<T>(f32(i4) * scale))`. Here the weight is rewritten once
+    into the group layout `_int4_pack` returns -- each code the value plus 8, zero
+    point 8, the row's scale for each group of 128 -- so the fused kernels read 4
+    bits a weight; that copy holds In * Out / 2 bytes beside the parameter, as the
+    reference's tinygemm repack does. Layers the kernels do not take (In % 128 != 0,
+    f32 scales) get the 1-tuple of the weight dequantized once by the body's
+    formula, on the GPU."""
+    if not weight.is_cuda:
+        raise LinnetError("_int4_row_pack: linnet_amd runs on the GPU; the weight is on " + str(weight.device))
+    in_features = 2 * weight.shape[1]
+    rows = scale.reshape(-1)
+    if scale.dtype in _FUSED_DTYPES and in_features % 128 == 0:
+        return kernels.int4_row_prepare(weight, rows, 128)
+    if in_features % 32 == 0:
+        return (kernels.int4_weight(*kernels.int4_row_prepare(weight, rows, in_features)),)
+    values = kernels.unpack4(weight, "i4")
+    return ((values.float() * rows.float()[:, None]).to(scale.dtype),)
+
+
+def _int4_row_linear(x: torch.Tensor, packed: tuple[torch.Tensor, ...], bias: torch.Tensor | None) -> torch.Tensor:
+    """`Int4Linear.forward`: `linear(x, dequantize_int4(weight, scale), bias)`
+    (`stdlib/quant.linnet:108-110`) with the weight prepared by `_int4_row_pack`."""
+    flat = x.reshape(-1, x.shape[-1])
+    if len(packed) == 3 and x.dtype == packed[1].dtype:
+        y = kernels.int4_linear(flat, *packed, bias)
+        return y.reshape(*x.shape[:-1], y.shape[-1])
+    if not x.is_cuda:
+        raise LinnetError("_int4_row_linear: linnet_amd runs on the GPU; x is on " + str(x.device))
+    weight = packed[0] if len(packed) == 1 else kernels.int4_weight(*packed)
+    y = functional.linear(flat, weight.to(flat.dtype)).reshape(*x.shape[:-1], weight.shape[0])
     return y if bias is None else y + bias
 
 

@@ -70,6 +70,7 @@ def int4_linear(
     bias: torch.Tensor | None = None,
     kernel: str = "auto",
     out: torch.Tensor | None = None,
+    order: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """`F.linear(x, W) (+ bias)` for `x` [rows, In] (bf16 or f16) and the group-wise
     4-bit weight of `std.quant::linear_int4_groups` -- `packed` ([Out, Groups,
@@ -81,9 +82,14 @@ def int4_linear(
     given, is a contiguous [rows, Out] tensor of x's dtype on x's device that
     receives the result (and is returned) instead of a new one.
 
+    `order` ([In] int32, GPTQ's activation order) multiplies `take_inputs(x, order)`
+    instead of x, as `Int4GroupLinear.forward` does (`stdlib/quant.linnet:163-174`):
+    one row at group 128 gathers inside the one-token GEMV, other calls gather
+    first with `take_inputs`'s kernel.
+
     Replaces `kernels.py:277-323` (`int4_linear`) and tinygemm's
     `aten._weight_int4pack_mm` (`src/backend/torch_source.cpp:1556-1558`)."""
-    device = _on_gpu("int4_linear", x, packed, scale, zero, bias)
+    device = _on_gpu("int4_linear", x, packed, scale, zero, bias, order)
     if x.dim() != 2 or packed.dim() != 3:
         raise LinnetError(f"int4_linear: x is [rows, In] and packed [Out, Groups, Group/2], got {tuple(x.shape)} and {tuple(packed.shape)}")
     rows, depth = x.shape
@@ -111,12 +117,41 @@ def int4_linear(
         if tuple(out.shape) != (rows, width) or out.dtype != x.dtype or out.device != device or not out.is_contiguous():
             raise LinnetError(f"int4_linear: out is a contiguous [{rows}, {width}] {x.dtype} tensor on {device}")
         y = out
+    if order is not None:
+        if order.dtype != torch.int32 or tuple(order.shape) != (depth,):
+            raise LinnetError(f"int4_linear: order is [{depth}] int32")
+        order = order.contiguous()
+        taken = torch.empty_like(x)
+        with torch.cuda.device(device):
+            _lib.call(
+                "lnq_int4_linear_ordered", _ptr(x), _ptr(order), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias),
+                _ptr(y), _ptr(taken), rows, depth, width, group, code, KERNELS[kernel], _stream(device),
+            )
+        return y
     with torch.cuda.device(device):
         _lib.call(
             "lnq_int4_linear", _ptr(x), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),
             rows, depth, width, group, code, KERNELS[kernel], _stream(device),
         )
     return y
+
+
+def take_inputs(x: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
+    """`std.quant::take_inputs` (`stdlib/quant.linnet:142-149`): `x[..., order[k]]`
+    over x's last axis, in one HIP gather kernel; `order` is [N] int32 (the
+    reference runs `x.index_select(-1, order.long())`,
+    `src/backend/torch_source.cpp:397-398`). An index outside [0, N) reads 0."""
+    device = _on_gpu("take_inputs", x, order)
+    code = _code(x.dtype, "take_inputs", (torch.bfloat16, torch.float16, torch.float32))
+    n = x.shape[-1] if x.dim() else 0
+    if x.dim() == 0 or order.dtype != torch.int32 or tuple(order.shape) != (n,):
+        raise LinnetError(f"take_inputs: order is [{n}] int32 over x's last axis")
+    x, order = x.contiguous(), order.contiguous()
+    taken = torch.empty_like(x)
+    with torch.cuda.device(device):
+        _lib.call("lnq_take_inputs", _ptr(x), _ptr(order), _ptr(taken), x.numel() // max(n, 1), n, code,
+                  _stream(device))
+    return taken
 
 
 def int4_linear_plan(rows: int, in_features: int, out_features: int, group: int,
@@ -202,6 +237,32 @@ def unpack4(packed: torch.Tensor, kind: str) -> torch.Tensor:
     return out
 
 
+def int4_row_prepare(weight: torch.Tensor, scale: torch.Tensor, group: int = 128
+                     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """`std.quant::Int4Linear`'s weight (`weight` [Out, In/2] u8 of signed 4-bit
+    values, element 2k low; `scale` [Out] or [Out, 1], bf16 / f16 / f32) in the group
+    layout `int4_linear` reads: `(packed [Out, In/group, group/2], scale [Out,
+    In/group], zero [Out, In/group] = 8)`, each code the value plus 8, so the layer's
+    weight `q * scale` is unchanged (`stdlib/quant.linnet:24-29, 101-111`)."""
+    device = _on_gpu("int4_row_prepare", weight, scale)
+    if weight.dtype != torch.uint8 or weight.dim() != 2:
+        raise LinnetError("int4_row_prepare: the weight is [Out, In/2] uint8 bytes of i4 values")
+    width, depth = weight.shape[0], 2 * weight.shape[1]
+    code = _code(scale.dtype, "int4_row_prepare", (torch.bfloat16, torch.float16, torch.float32))
+    if scale.numel() != width:
+        raise LinnetError(f"int4_row_prepare: one scale a row ({width}), got {tuple(scale.shape)}")
+    if depth % 32 or group <= 0 or group % 2 or depth % group:
+        raise LinnetError(f"int4_row_prepare: In={depth} is a multiple of 32 split into even groups of {group}")
+    weight, scale = weight.contiguous(), scale.contiguous()
+    packed = torch.empty(width, depth // group, group // 2, dtype=torch.uint8, device=device)
+    group_scale = torch.empty(width, depth // group, dtype=scale.dtype, device=device)
+    zero = torch.empty(width, depth // group, dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_int4_row_prepare", _ptr(weight), _ptr(scale), _ptr(packed), _ptr(group_scale), _ptr(zero),
+                  width, depth, group, code, _stream(device))
+    return packed, group_scale, zero
+
+
 def int4_repack(
     qweight: torch.Tensor,
     qzeros: torch.Tensor,
@@ -236,8 +297,12 @@ def int4_repack(
         order = order.contiguous()
         # The kernel reads whatever input an entry names (an entry out of range as
         # code 0): only a permutation gives the layer's weights, so anything else
-        # is refused here, at load time (one host sync).
-        if not torch.equal(torch.sort(order).values, torch.arange(in_features, dtype=torch.int32, device=device)):
+        # is refused here, at load time (one host sync). A call being captured
+        # into a graph cannot wait for the device: it is checked when the order is
+        # first used eagerly, not while captured.
+        if not torch.cuda.is_current_stream_capturing() and not torch.equal(
+            torch.sort(order).values, torch.arange(in_features, dtype=torch.int32, device=device)
+        ):
             raise LinnetError(f"int4_repack: order is not a permutation of 0..{in_features - 1}")
     if zero_offset not in (0, 1):
         raise LinnetError(f"int4_repack: zero_offset is 0 or 1, not {zero_offset}")

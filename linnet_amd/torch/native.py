@@ -1,5 +1,6 @@
 """The quantized entries of the reference interpreter's `NATIVE` table
-(`python/linnet/src/linnet/torch/native.py:417-480, 556-566`), keyed by the same
+and its `take_inputs` gather (`python/linnet/src/linnet/torch/native.py:269-271,
+417-480, 556-572`), keyed by the same
 candidate names, running the HIP kernels. Each entry takes the call's arguments
 as a tuple, as the interpreter passes them."""
 
@@ -9,7 +10,7 @@ from collections.abc import Callable, Sequence
 
 import torch
 
-from . import generated, quantized
+from . import generated, kernels, quantized
 
 Native = Callable[[Sequence[object]], torch.Tensor]
 
@@ -59,6 +60,14 @@ def _int8_group_linear(args: Sequence[object]) -> torch.Tensor:
     return quantized.int8_group_linear(x, quantized.int8_group_operands(weight, scale), bias)  # type: ignore[arg-type]
 
 
+def _index_select(args: Sequence[object]) -> torch.Tensor:
+    """`std.quant::take_inputs` (`native.py:269-271`): `x[..., order[k]]`, on the HIP
+    gather kernel."""
+    x, order = args
+    assert isinstance(x, torch.Tensor) and isinstance(order, torch.Tensor)
+    return kernels.take_inputs(x, order if order.dtype == torch.int32 else order.to(torch.int32))
+
+
 NATIVE: dict[str, Native] = {
     "torch.ops.aten._weight_int4pack_mm": _int4_groups_linear,
     "linnet.decode_fp8": _decode_fp8,
@@ -69,4 +78,5 @@ NATIVE: dict[str, Native] = {
     "linnet.int8_linear": _int8_linear(0),
     "linnet.int8_linear(w8a8)": _int8_linear(1),
     "linnet.int8_group_linear": _int8_group_linear,
+    "torch.index_select": _index_select,
 }

@@ -261,6 +261,24 @@ def dequantize_int4_weight(packed: np.ndarray, scale_raw: np.ndarray, zero: np.n
     return encode_storage(weight, dtype)
 
 
+def dequantize_int4_rows(packed: np.ndarray, scale_raw: np.ndarray, dtype: str) -> np.ndarray:
+    """`std.quant::dequantize_int4` as `Int4Linear.forward` calls it
+    (`stdlib/quant.linnet:22-29, 101-111`, through `dequantize_int8`, lines 13-20):
+    `packed` [Out, In/2] holds signed 4-bit values two a byte, element 2k low
+    (`tests/torch/test_quant.py:62-66`); `scale_raw` [Out] or [Out, 1] is the
+    per-row scale in storage dtype `dtype`, widened to f32. Returns the raw storage
+    array of `cast<T>(f32(q) * f32(scale))`, one rounding.
+
+    Pins: the closed form on every code -8..7 at exact scales, and on random
+    layers the f64 product of independently drawn int8 values and scales rounded
+    once (tests/test_oracle.py::test_int4_rows_*)."""
+    q = unpack4(packed, "i4").astype(np.float32)
+    scale = decode_storage(np.asarray(scale_raw).reshape(-1), dtype).astype(np.float32)
+    if scale.shape[0] != q.shape[0]:
+        raise ValueError(f"one scale a row: {q.shape[0]} rows, {scale.shape[0]} scales")
+    return encode_storage(q * scale[:, None], dtype)
+
+
 # ------------------------------------------------------------ int8 quantize
 
 

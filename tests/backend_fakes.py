@@ -76,10 +76,23 @@ class Region:
 
     @classmethod
     def of(cls, graph, start, stop, call=None):
-        c = graph.calls[call]
+        """As `contract.py:151-220` computes them, over the calls inside the range:
+        inputs are the values they read that none of them made (parameters
+        aside), outputs the values they made that a call after the range reads or
+        that the last call returns."""
+        inside = [c for c in graph.calls if start <= c.start and c.stop <= stop]
         persistent = set(graph.parameters.values())
-        inputs = tuple(a.value for a in c.arguments if a.value is not None and a.value not in persistent)
-        return cls(graph, start, stop, inputs, tuple(r.value for r in c.results), call)
+        made: set[int] = set()
+        inputs: dict[int, None] = {}
+        for c in inside:
+            for a in c.arguments:
+                if a.value is not None and a.value not in persistent and a.value not in made:
+                    inputs[a.value] = None
+            made.update(r.value for r in c.results)
+        read_after = {a.value for c in graph.calls if c.start >= stop for a in c.arguments}
+        last = {r.value for r in inside[-1].results}
+        outputs = tuple(v for c in inside for v in (r.value for r in c.results) if v in read_after or v in last)
+        return cls(graph, start, stop, tuple(inputs), outputs, call)
 
 
 class Graph:
@@ -97,8 +110,19 @@ class Graph:
             self.parameters[path] = vid
         return Operand(vid, tuple(shape), dtype)
 
-    def linear(self, name, rows, out, inp, group, dtype="bf16", persistent=True, bias=False, extra_input=False):
+    def take(self, name, rows, inp, dtype="bf16"):
+        """`std.quant::take_inputs(x, order)` with `order` the parameter `name.order`."""
         x = self.value((rows, inp), dtype)
+        order = self.value((inp,), "i32", f"{name}.order")
+        taken = self.value((rows, inp), dtype)
+        n = len(self.calls)
+        start = self.calls[-1].stop if self.calls else 0
+        self.calls.append(Call(n, "std.quant::take_inputs", True, (x, order), (taken,), start, start + 1))
+        return self.calls[-1]
+
+    def linear(self, name, rows, out, inp, group, dtype="bf16", persistent=True, bias=False, extra_input=False,
+               x=None):
+        x = self.value((rows, inp), dtype) if x is None else x
         q = self.value((out, inp // group, group), "u4", f"{name}.weight" if persistent else None)
         s = self.value((out, inp // group), dtype, f"{name}.scale")
         z = self.value((out, inp // group), "u8", f"{name}.zero")
@@ -106,7 +130,16 @@ class Graph:
         args = (x, q, s, z, b) if not extra_input else (x, q, s, z, b, self.value((rows, inp), dtype))
         y = self.value((rows, out), dtype)
         n = len(self.calls)
-        self.calls.append(Call(n, "std.quant::linear_int4_groups", True, args, (y,), 2 * n, 2 * n + 1))
+        # Each call's range starts where the previous one stopped.
+        start = self.calls[-1].stop if self.calls else 0
+        self.calls.append(Call(n, "std.quant::linear_int4_groups", True, args, (y,), start, start + 1))
+        return self.calls[-1]
+
+    def read(self, operand):
+        """A later call (another op) that reads `operand`."""
+        n = len(self.calls)
+        start = self.calls[-1].stop if self.calls else 0
+        self.calls.append(Call(n, "std.core::other", True, (operand,), (), start, start + 1))
         return self.calls[-1]
 
     def semantic_calls(self, callee=None):

@@ -107,6 +107,14 @@ def test_other_entry_points_validate() -> None:
     assert "equal groups" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 0, 64, 64, 3, FAKE, FAKE, NULL)[1]
     assert "only GPTQ" in _status("lnq_int4_repack", FAKE, FAKE, FAKE, 1, 0, 64, 64, 1, FAKE, FAKE, NULL)[1]
     assert "zero_offset" in _status("lnq_int4_repack", FAKE, FAKE, NULL, 0, 2, 64, 64, 1, FAKE, FAKE, NULL)[1]
+    assert "bf16, f16 or f32" in _status("lnq_int4_row_prepare", FAKE, FAKE, FAKE, FAKE, FAKE, 4, 128, 128, 7, NULL)[1]
+    assert "in % 32" in _status("lnq_int4_row_prepare", FAKE, FAKE, FAKE, FAKE, FAKE, 4, 48, 16, _lib.BF16, NULL)[1]
+    assert "must be even" in _status("lnq_int4_row_prepare", FAKE, FAKE, FAKE, FAKE, FAKE, 4, 128, 96, _lib.BF16,
+                                     NULL)[1]
+    assert "taken" in _status("lnq_int4_linear_ordered", FAKE, FAKE, FAKE, FAKE, FAKE, NULL, FAKE, NULL, 4, 4096, 4096,
+                              128, _lib.BF16, 0, NULL)[1]
+    assert "bf16, f16 or f32" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, 9, NULL)[1]
+    assert "must not be x" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, _lib.BF16, NULL)[1]
     assert "groups of 128" in _status("lnq_fp8_groups", FAKE, FAKE, FAKE, 2, 2, 256, 64, _lib.BF16, NULL)[1]
     assert "padded >= rows" in _status("lnq_fp8_groups", FAKE, FAKE, FAKE, 3, 2, 256, 128, _lib.BF16, NULL)[1]
     assert "in, out % 128" in _status("lnq_mm8_block", FAKE, FAKE, FAKE, 4, FAKE, FAKE, 4, 100, 256, _lib.BF16, NULL)[1]
@@ -129,6 +137,10 @@ def test_empty_calls_succeed_without_a_device() -> None:
     assert "bad shape" in _status("lnq_silu_mul_rows", FAKE, FAKE, FAKE, 2, 8, 4, 16, NULL)[1]
     assert _status("lnq_rmsnorm", NULL, NULL, NULL, NULL, 0, 4096, ctypes.c_float(1e-5), NULL)[0] == _lib.LNQ_OK
     assert _status("lnq_int4_repack", NULL, NULL, NULL, 0, 1, 0, 64, 0, NULL, NULL, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_int4_row_prepare", NULL, NULL, NULL, NULL, NULL, 0, 128, 128, _lib.BF16, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_take_inputs", NULL, NULL, NULL, 0, 8, _lib.BF16, NULL)[0] == _lib.LNQ_OK
+    assert _status("lnq_int4_linear_ordered", FAKE, FAKE, FAKE, FAKE, FAKE, NULL, FAKE, NULL, 0, 4096, 4096, 128,
+                   _lib.BF16, 0, NULL)[0] == _lib.LNQ_OK
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU answer")

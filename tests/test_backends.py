@@ -101,3 +101,64 @@ def test_executable_conforms_to_the_fallback() -> None:
         err = (got.float() - want.float()).abs().max().item()
         assert got.shape == want.shape and err <= 1e-2 * want.float().abs().max().item(), err
     np.testing.assert_equal(len(list(backend.match(g, context.target))), 2)
+
+
+def _ordered_graph() -> Graph:
+    """Two layers in activation order (`take_inputs`, then the product); the second
+    one's taken input is also read after it, so only its product is taken."""
+    g = Graph()
+    take = g.take("p", rows=1, inp=512)
+    g.linear("p", rows=1, out=256, inp=512, group=128, x=take.results[0])
+    take2 = g.take("r", rows=3, inp=256, dtype="f16")
+    g.linear("r", rows=3, out=64, inp=256, group=128, dtype="f16", x=take2.results[0])
+    g.read(take2.results[0])
+    return g
+
+
+def test_match_takes_an_ordered_layer_as_one_region() -> None:
+    g = _ordered_graph()
+    backend = MI355XInt4(types=TYPES)
+    regions = list(backend.match(g, SimpleNamespace(kind="cuda", index=0)))
+    assert [r.call for r in regions] == [1, 3]
+    fused, plain = regions
+    assert (fused.start, fused.stop) == (g.calls[0].start, g.calls[1].stop)
+    assert fused.inputs == (g.calls[0].arguments[0].value,)
+    assert (plain.start, plain.stop) == (g.calls[3].start, g.calls[3].stop)
+    assert plain.inputs == (g.calls[2].results[0].value,)
+    made = backend.compile(fused, SimpleNamespace(kind="cuda"), None)
+    assert made._order == "p.order" and [s.shape for s in made.meta.inputs] == [(1, 512)]
+    assert backend.compile(plain, SimpleNamespace(kind="cuda"), None)._order is None
+
+
+@pytest.mark.gpu
+def test_ordered_executable_conforms_to_the_fallback() -> None:
+    """The fused region against the reference's body: `x.index_select(-1, order)`,
+    then dequantize and `F.linear`."""
+    from linnet_amd.torch import kernels
+
+    backend = MI355XInt4(types=TYPES)
+    g = _ordered_graph()
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    params = {}
+    for name, call in (("p.", g.calls[1]), ("r.", g.calls[3])):
+        out, groups, group = call.arguments[1].shape
+        dtype = torch.bfloat16 if call.arguments[2].dtype == "bf16" else torch.float16
+        w = torch.randn(out, groups * group, generator=gen, device="cuda") * 0.02
+        packed, scale, zero = kernels.quantize_int4(w, group)
+        params[name + "weight"], params[name + "scale"], params[name + "zero"] = packed, scale.to(dtype), zero
+        params[name + "order"] = torch.randperm(groups * group, generator=gen, device="cuda").to(torch.int32)
+    context = SimpleNamespace(parameters=params, target=SimpleNamespace(kind="cuda", index=0))
+    for region in backend.match(g, context.target):
+        made = backend.compile(region, context.target, None)
+        made.prepare(context)
+        x = g.values[region.inputs[0]]
+        dtype = torch.bfloat16 if x.dtype == "bf16" else torch.float16
+        xin = torch.randn(*x.shape, generator=gen, device="cuda").to(dtype)
+        (got,) = made.execute([xin], [], context)
+        name = "p." if region.call == 1 else "r."
+        weight = kernels.int4_weight(params[name + "weight"], params[name + "scale"], params[name + "zero"])
+        taken = xin.index_select(-1, params[name + "order"].long()) if region.call == 1 else xin
+        want = torch.nn.functional.linear(taken, weight)
+        err = (got.float() - want.float()).abs().max().item()
+        print(f"region {region.call}: max abs err {err:.3e}")
+        assert got.shape == want.shape and err <= 1e-2 * want.float().abs().max().item(), err

@@ -80,6 +80,39 @@ def test_pack_layout_closed_form() -> None:
     np.testing.assert_array_equal(quant.pack4(np.array([2.7, -9.5]), "i4"), np.array([(2 & 15) | ((-9 & 15) << 4)], np.uint8))
 
 
+def test_int4_rows_closed_form() -> None:
+    """`dequantize_int4` on every code -8..7 with exact scales: `q * s` exactly,
+    element 2k from the low nibble (a swapped nibble order, a missing sign
+    extension or a column-indexed scale fails)."""
+    values = np.array([np.arange(-8, 8), np.arange(7, -9, -1)], dtype=np.int8)
+    low = values[:, 0::2].astype(np.int32) & 15
+    high = values[:, 1::2].astype(np.int32) & 15
+    packed = ((high << 4) | low).astype(np.uint8)
+    for dtype in ("bf16", "f16", "f32"):
+        scale = quant.encode_storage(np.array([[0.5], [-2.0]], np.float32), dtype)
+        weight = quant.decode_storage(quant.dequantize_int4_rows(packed, scale, dtype), dtype)
+        np.testing.assert_array_equal(weight, values.astype(np.float32) * np.array([[0.5], [-2.0]], np.float32))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_int4_rows_match_torch(dtype: str) -> None:
+    """Random [Out, In] i4 layers (Out != In, so a transposed scale fails): the
+    oracle equals torch's `(q.float() * s.float()).to(T)` on int8 values drawn
+    apart from the packing (`tests/torch/test_quant.py:68-95`'s construction)."""
+    rng = np.random.default_rng(5)
+    q4 = rng.integers(-8, 8, size=(12, 40)).astype(np.int8)
+    low = q4[:, 0::2].astype(np.int32) & 15
+    high = q4[:, 1::2].astype(np.int32) & 15
+    packed = ((high << 4) | low).astype(np.uint8)
+    torch_dtype = torch.bfloat16 if dtype == "bf16" else torch.float16
+    scale = torch.tensor(rng.uniform(-0.3, 0.3, size=(12, 1)).astype(np.float32)).to(torch_dtype)
+    expected = (torch.tensor(q4).float() * scale.float()).to(torch_dtype)
+    raw = scale.view(torch.int16).numpy().view(np.uint16) if dtype == "bf16" else scale.numpy()
+    got = quant.dequantize_int4_rows(packed, raw, dtype)
+    want = expected.view(torch.int16).numpy().view(np.uint16) if dtype == "bf16" else expected.numpy()
+    np.testing.assert_array_equal(got, want)
+
+
 def test_int4_storage_bytes() -> None:
     """Int4GroupLinear<256, 64, 128, bf16> holds 64*2*64 + 64*2*2 + 64*2 bytes
     (`tests/test_resources.py:184-202`)."""
