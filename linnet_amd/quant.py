@@ -24,6 +24,7 @@ from __future__ import annotations
 import fnmatch
 import json
 from collections.abc import Iterable, Mapping
+from dataclasses import dataclass
 from pathlib import Path
 
 import numpy as np
@@ -99,55 +100,55 @@ def dequantize_int8_groups(q, scale):
 
 
 # ---------------------------------------------------------------- checkpoints
+#
+# Both tools write a checkpoint with every tensor of the input under its Linnet
+# path, the chosen linear layers replaced by the tensors of their quantized
+# block: `P.weight`, `P.scale` (in the model's scale dtype) and, for 4 bits,
+# `P.zero` -- plus `P.order` for a GPTQ layer in activation order -- where `P.`
+# names the layer's parameters (`siblings`).
 
-Entry = tuple[str, str, tuple[int, ...], "bytes | weights.TensorLocation"]
+
+def siblings(path: str) -> str:
+    """The prefix shared by the parameters of the block owning `path`'s weight:
+    `"attn.q."` for `"attn.q.weight"`, `""` for a root block's `"weight"`, and
+    `path + "."` for a path that is not a weight (the reference names them the
+    same way, `quant.py:198-204`)."""
+    head, dot, last = path.rpartition(".")
+    return head + dot if last == "weight" else path + "."
 
 
-def _paths_of(bindings: str | Path | Mapping[str, str] | None) -> dict[str, list[str]]:
-    """Checkpoint name -> the Linnet paths bound to it (`quant.py:184-195`)."""
+def _scale_name(dtype: str) -> str:
+    try:
+        return weights.STORAGE[dtype]
+    except KeyError:
+        raise LinnetError(f"scale dtype {dtype!r}: choose bf16, f16 or f32") from None
+
+
+def _bound(bindings: str | Path | Mapping[str, str] | None) -> dict[str, list[str]]:
+    """Each checkpoint tensor's Linnet paths (its own name when unbound)."""
     if bindings is None:
-        mapping: dict[str, str] = {}
-    elif isinstance(bindings, Mapping):
-        mapping = {str(k): str(v) for k, v in bindings.items()}
-    else:
-        mapping = weights.read_bindings(bindings)
-    return weights.paths_by_tensor(mapping)
+        return {}
+    table = dict(bindings) if isinstance(bindings, Mapping) else weights.read_bindings(bindings)
+    return weights.paths_by_tensor({str(k): str(v) for k, v in table.items()})
 
 
-def _prefix(path: str) -> str:
-    """What names a weight's siblings: `proj.` for `proj.weight`, nothing for a
-    root block's own `weight` (`quant.py:198-204`)."""
-    if path == "weight":
-        return ""
-    return path.removesuffix("weight") if path.endswith(".weight") else path + "."
+def _block_tensors(prefix: str, dtype: str, weight: torch.Tensor, weight_dtype: str, scale: torch.Tensor,
+                   zero: torch.Tensor | None = None, order: np.ndarray | None = None):
+    """The checkpoint entries of one quantized block, in the order its parameters
+    are declared (weight, scale, zero, order)."""
+    yield prefix + "weight", weight_dtype, tuple(weight.shape), weights.tensor_bytes(weight)
+    stored = _scale_name(dtype)
+    yield prefix + "scale", stored, tuple(scale.shape), weights.encode_floats(scale, stored)
+    if zero is not None:
+        yield prefix + "zero", "U8", tuple(zero.shape), weights.tensor_bytes(zero)
+    if order is not None:
+        yield prefix + "order", "I32", (order.size,), order.astype("<i4").tobytes()
 
 
-def _storage(dtype: str) -> str:
-    if dtype not in weights.STORAGE:
-        raise LinnetError(f"scales are stored as bf16, f16, or f32, not {dtype}")
-    return weights.STORAGE[dtype]
-
-
-def _scale_tensor(prefix: str, scale: torch.Tensor, dtype: str) -> Entry:
-    stored = _storage(dtype)
-    return (prefix + "scale", stored, tuple(scale.shape), weights.encode_floats(scale, stored))
-
-
-def _int4_tensors(prefix: str, packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, dtype: str) -> list[Entry]:
-    """`.weight` (U8 `[Out, In/group, group/2]`), `.scale` in `dtype`, `.zero` (U8)
-    (`quant.py:207-219`)."""
-    _storage(dtype)
-    return [
-        (prefix + "weight", "U8", tuple(packed.shape), weights.tensor_bytes(packed)),
-        _scale_tensor(prefix, scale, dtype),
-        (prefix + "zero", "U8", tuple(zero.shape), weights.tensor_bytes(zero)),
-    ]
-
-
-def _gpu(device: torch.device | str | None) -> torch.device:
+def _on_gpu(device: torch.device | str | None) -> torch.device:
     if not torch.cuda.is_available():
-        raise LinnetError("linnet_amd's checkpoint tools quantize and repack on the GPU; no GPU is available")
-    return torch.device(device if device is not None else "cuda")
+        raise LinnetError("the checkpoint tools of linnet_amd run their kernels on a GPU, and none is visible")
+    return torch.device("cuda" if device is None else device)
 
 
 def quantize_checkpoint(
@@ -161,51 +162,136 @@ def quantize_checkpoint(
     bits: int = 4,
     device: torch.device | str | None = None,
 ) -> list[str]:
-    """Writes `output` with every tensor of the checkpoint `weights_path` under its
-    Linnet path, the `.weight` tensors whose path matches one of `patterns`
-    quantized on the GPU: into `.weight`, `.scale` (in `dtype`) and `.zero` for
-    `Int4GroupLinear` (`bits` 4), or `.weight` and `.scale` for `Int8GroupLinear`
-    (`bits` 8); every other tensor copied as it is. Returns the quantized paths.
-    The reference's `quantize_checkpoint` (`quant.py:139-181`), with its rounding
-    bit for bit (the kernels of `quantize_int4_groups` / `quantize_int8_groups`)."""
+    """Quantizes a SafeTensors checkpoint on the GPU: every `.weight` whose Linnet
+    path matches one of the glob `patterns` becomes an `Int4GroupLinear` (`bits`
+    4: `.weight`, `.scale`, `.zero`) or `Int8GroupLinear` (`bits` 8: `.weight`,
+    `.scale`) block with scales stored in `dtype`; every other tensor is copied.
+    The codes and scales are those of `quantize_int4_groups` /
+    `quantize_int8_groups`, bit for bit. Returns the quantized paths in file
+    order. Replaces the reference's `quantize_checkpoint` (`quant.py:139-181`)."""
     if bits not in (4, 8):
-        raise LinnetError(f"weights are quantized to 4 or 8 bits, not {bits}")
-    _storage(dtype)
-    target = _gpu(device)
-    paths_of = _paths_of(bindings)
-    chosen = list(patterns)
-    out: list[Entry] = []
-    quantized: list[str] = []
-    for tensor in weights.iter_safetensors(weights_path):
-        for path in paths_of.get(tensor.name, [tensor.name]):
-            if path.endswith(".weight") and any(fnmatch.fnmatchcase(path, p) for p in chosen):
-                values = weights.float_tensor(tensor, target)
-                prefix = _prefix(path)
-                if bits == 8:
-                    q, scale = kernels.quantize_int8(values, group, dtype)
-                    out.append((prefix + "weight", "I8", tuple(q.shape), weights.tensor_bytes(q)))
-                    out.append(_scale_tensor(prefix, scale, dtype))
-                else:
-                    packed, scale, zero = kernels.quantize_int4(values, group)
-                    out += _int4_tensors(prefix, packed, scale, zero, dtype)
-                quantized.append(path)
+        raise LinnetError(f"bits={bits}: the quantized blocks hold 4-bit or 8-bit weights")
+    _scale_name(dtype)
+    target = _on_gpu(device)
+    globs = tuple(patterns)
+
+    def chosen(path: str) -> bool:
+        return path.endswith(".weight") and any(fnmatch.fnmatchcase(path, g) for g in globs)
+
+    paths = _bound(bindings)
+    writer = weights.CheckpointWriter()
+    done: list[str] = []
+    for stored in weights.open_checkpoint(weights_path).values():
+        for path in paths.get(stored.name) or [stored.name]:
+            if not chosen(path):
+                writer.add(path, stored.dtype, stored.shape, stored)
+                continue
+            values = weights.float_tensor(stored, target)
+            if bits == 4:
+                packed, scale, zero = kernels.quantize_int4(values, group)
+                block = _block_tensors(siblings(path), dtype, packed, "U8", scale, zero)
             else:
-                out.append((path, tensor.dtype, tensor.shape, tensor.data))
-    if not quantized:
-        raise LinnetError("no weight matched " + ", ".join(chosen))
-    weights.write_safetensors(output, out, metadata={"format": "pt"})
-    return quantized
+                q, scale = kernels.quantize_int8(values, group, dtype)
+                block = _block_tensors(siblings(path), dtype, q, "I8", scale)
+            for entry in block:
+                writer.add(*entry)
+            done.append(path)
+    if not done:
+        raise LinnetError(f"no `.weight` path matched {', '.join(globs) or 'the (empty) patterns'}")
+    writer.write(output, {"format": "pt"})
+    return done
 
 
-def _setting(config: Mapping[str, object], key: str, alias: str, default: int) -> int:
-    """`config[key]` (or its AWQ name `alias`, or `default`) as an integer (`quant.py:251-256`)."""
-    value = config.get(key, config.get(alias, default))
-    if isinstance(value, bool) or not isinstance(value, (int, float, str)):
-        raise LinnetError(f"the quantization_config's `{key}` is {value!r}, not a number")
+# ------------------------------------------------------- GPTQ / AWQ import
+#
+# What a calibrated checkpoint's `quantization_config` may say, with the names
+# GPTQ and AWQ give each setting, first name first.
+_SETTINGS = {"bits": ("bits", "w_bit"), "group": ("group_size", "q_group_size")}
+
+
+def _config_number(config: Mapping[str, object], setting: str, default: int) -> int:
+    names = _SETTINGS[setting]
+    raw = next((config[n] for n in names if n in config), default)
+    if isinstance(raw, bool) or not isinstance(raw, (int, float, str)):
+        raise LinnetError(f"quantization_config: {names[0]} = {raw!r} is not an integer")
     try:
-        return int(value)
+        return int(raw)
     except ValueError:
-        raise LinnetError(f"the quantization_config's `{key}` is {value!r}, not a number") from None
+        raise LinnetError(f"quantization_config: {names[0]} = {raw!r} is not an integer") from None
+
+
+@dataclass(frozen=True)
+class _Calibrated:
+    """How a 4-bit calibrated checkpoint stores its layers: `method` ("gptq" or
+    "awq"), the group size, and the offset added to each stored zero point (GPTQ's
+    original format, `checkpoint_format` "gptq", stores zero - 1)."""
+
+    method: str
+    group: int
+    zero_offset: int
+
+    @classmethod
+    def read(cls, config: Mapping[str, object]) -> _Calibrated:
+        method = str(config.get("quant_method", "")).lower()
+        if method == "bitsandbytes":
+            raise LinnetError("bitsandbytes checkpoints hold NF4 blocks (Nf4Linear), which linnet_amd does not import")
+        if method not in ("gptq", "awq"):
+            raise LinnetError(f"quant_method {method!r}: linnet_amd imports GPTQ and AWQ checkpoints")
+        if _config_number(config, "bits", 4) != 4:
+            raise LinnetError(f"{method.upper()} checkpoint of {config.get('bits', config.get('w_bit'))} bits: "
+                              "only 4-bit layers become Int4GroupLinear")
+        version = str(config.get("version", "gemm")).lower()
+        if method == "awq" and version != "gemm":
+            raise LinnetError(f"AWQ version {version!r}: only the GEMM packing of the words is read")
+        original_gptq = method == "gptq" and config.get("checkpoint_format", "gptq") == "gptq"
+        return cls(method, _config_number(config, "group", 128), 1 if original_gptq else 0)
+
+
+def _config_beside(weights_path: str | Path) -> Mapping[str, object]:
+    where = Path(weights_path)
+    config_file = (where if where.is_dir() else where.parent) / "config.json"
+    if not config_file.is_file():
+        raise LinnetError(f"{config_file} does not exist: pass the quantization_config as `config`")
+    document = json.loads(config_file.read_text(encoding="utf-8"))
+    found = document.get("quantization_config") if isinstance(document, dict) else None
+    if not isinstance(found, Mapping):
+        raise LinnetError(f"{config_file} holds no quantization_config object")
+    return found
+
+
+# The tensors a calibrated layer `L` stores: `L.qweight`, `L.qzeros`, `L.scales`
+# and, for GPTQ, `L.g_idx` (each input's group).
+_LAYER_PARTS = ("qweight", "qzeros", "scales", "g_idx")
+
+
+def _calibrated_layers(index: Mapping[str, weights.StoredTensor]) -> dict[str, dict[str, weights.StoredTensor]]:
+    """Layer name -> its stored parts, for every layer with a `qweight`, by name."""
+    parts: dict[str, dict[str, weights.StoredTensor]] = {}
+    for name, stored in index.items():
+        layer, _, part = name.rpartition(".")
+        if part in _LAYER_PARTS:
+            parts.setdefault(layer, {})[part] = stored
+    return {layer: found for layer, found in sorted(parts.items()) if "qweight" in found}
+
+
+def input_order(g_idx: np.ndarray, group: int, in_features: int | None = None) -> np.ndarray | None:
+    """The order that makes each group's inputs contiguous, for a GPTQ layer
+    quantized in activation order: `order[k]` is the input at position k once the
+    inputs are sorted by group, ties kept in input order; None when every input
+    already sits in group `i // group`. Every group must hold exactly `group`
+    inputs. (`take_inputs(x, order)` then feeds the product, `stdlib/quant.linnet:163-174`.)"""
+    ids = np.asarray(g_idx).reshape(-1).astype(np.int64)
+    if in_features is not None and ids.size != in_features:
+        raise LinnetError(f"g_idx has {ids.size} entries for {in_features} inputs")
+    groups = ids.size // group
+    if np.array_equal(ids, np.arange(ids.size) // group):
+        return None
+    if ids.size % group or ids.min(initial=0) < 0 or ids.max(initial=0) >= groups:
+        raise LinnetError(f"g_idx names groups outside 0..{groups - 1}")
+    sizes = np.bincount(ids, minlength=groups)
+    if np.any(sizes != group):
+        raise LinnetError(f"g_idx puts {sizes.min()}..{sizes.max()} inputs in a group of {group}")
+    return np.argsort(ids, kind="stable").astype(np.int32)
 
 
 def import_quantized(
@@ -217,99 +303,67 @@ def import_quantized(
     config: Mapping[str, object] | None = None,
     device: torch.device | str | None = None,
 ) -> list[str]:
-    """Writes `output` with a 4-bit GPTQ or AWQ checkpoint's quantized linear layers
-    repacked on the GPU for `Int4GroupLinear` (`.weight`, `.scale` in `dtype`,
-    `.zero`, and `.order` for a GPTQ layer in activation order) and every other
-    tensor as it is, all under Linnet paths. `config` is the checkpoint's
-    `quantization_config` (by default read from the `config.json` beside
-    `weights_path`). Returns the quantized paths, as `.weight`. The reference's
-    `import_quantized` (`quant.py:255-354`) for GPTQ and AWQ; its bitsandbytes NF4
-    import (`Nf4Linear`) is not part of this build and raises."""
-    if config is None:
-        location = Path(weights_path)
-        directory = location if location.is_dir() else location.parent
-        try:
-            document = json.loads((directory / "config.json").read_text(encoding="utf-8"))
-        except FileNotFoundError:
-            raise LinnetError(f"no config.json beside {weights_path}; pass `config`") from None
-        config = document.get("quantization_config") if isinstance(document, dict) else None
-        if not isinstance(config, Mapping):
-            raise LinnetError(f"{directory / 'config.json'} has no quantization_config")
-    method = str(config.get("quant_method", "")).lower()
-    if method == "bitsandbytes":
-        raise LinnetError("bitsandbytes NF4 checkpoints (Nf4Linear) are not imported by linnet_amd")
-    if method not in ("gptq", "awq"):
-        raise LinnetError(f"a {method or 'unnamed'} checkpoint is not GPTQ, AWQ or bitsandbytes")
-    if _setting(config, "bits", "w_bit", 4) != 4:
-        raise LinnetError("only 4-bit GPTQ and AWQ checkpoints repack into Int4GroupLinear")
-    if method == "awq" and str(config.get("version", "gemm")).lower() != "gemm":
-        raise LinnetError(f"AWQ's {config.get('version')} packing is not read; GEMM's is")
-    group = _setting(config, "group_size", "q_group_size", 128)
-    _storage(dtype)
-    # GPTQ's first checkpoint format stores each zero point less one.
-    zero_offset = 1 if method == "gptq" and config.get("checkpoint_format", "gptq") == "gptq" else 0
-    target = _gpu(device)
-    index = weights.safetensors_index(weights_path)
-    paths_of = _paths_of(bindings)
-    out: list[Entry] = []
-    quantized: list[str] = []
-    parts = (".qweight", ".qzeros", ".scales", ".g_idx")
-    layers = sorted(name.removesuffix(".qweight") for name in index if name.endswith(".qweight"))
-    taken = {layer + part for layer in layers for part in parts}
+    """Converts a 4-bit GPTQ or AWQ checkpoint on the GPU: each calibrated layer
+    (`qweight`, `qzeros`, `scales`, and GPTQ's `g_idx`) becomes an
+    `Int4GroupLinear` block under its Linnet path -- `.weight`, `.scale` (stored in
+    `dtype`), `.zero`, and `.order` for activation order -- with the repack kernel
+    (`lnq_int4_repack`); every other tensor is copied. `config` is the
+    checkpoint's `quantization_config`, read from the `config.json` beside
+    `weights_path` when not given. Returns the layers' `.weight` paths. Replaces the
+    GPTQ / AWQ part of the reference's `import_quantized` (`quant.py:259-369`); NF4
+    (bitsandbytes) is outside this package and raises."""
+    calibrated = _Calibrated.read(config if config is not None else _config_beside(weights_path))
+    _scale_name(dtype)
+    target = _on_gpu(device)
+    index = weights.open_checkpoint(weights_path)
+    layers = _calibrated_layers(index)
+    paths = _bound(bindings)
+    writer = weights.CheckpointWriter()
+    done: list[str] = []
+    for layer, parts in layers.items():
+        blocks = _import_layer(layer, parts, calibrated, target)
+        name = layer + ".weight"
+        for path in paths.get(name) or [name]:
+            for entry in _block_tensors(siblings(path), dtype, *blocks):
+                writer.add(*entry)
+            done.append(path)
+    if not done:
+        raise LinnetError(f"{weights_path}: no `.qweight` tensor, so no {calibrated.method.upper()} layer to import")
+    consumed = {f"{layer}.{part}" for layer, parts in layers.items() for part in parts}
+    for name, stored in index.items():
+        if name not in consumed:
+            for path in paths.get(name) or [name]:
+                writer.add(path, stored.dtype, stored.shape, stored)
+    writer.write(output, {"format": "pt"})
+    return done
 
-    def load(name: str, dtype_: torch.dtype) -> torch.Tensor:
-        location = index[name]
-        raw = weights.RawTensor(name, location.dtype, location.shape, location.read())
-        return weights.tensor_from(raw, dtype_, target)
 
-    for layer in layers:
-        for part in (".qzeros", ".scales"):
-            if layer + part not in index:
-                raise LinnetError(f"{layer}: no `{part[1:]}` beside `qweight`")
-        qweight = load(layer + ".qweight", torch.int32)
-        qzeros = load(layer + ".qzeros", torch.int32)
-        stored = index[layer + ".scales"]
-        scales = weights.float_tensor(weights.RawTensor(layer + ".scales", stored.dtype, stored.shape, stored.read()), target)
-        if qweight.dim() != 2 or qzeros.dim() != 2 or scales.dim() != 2:
-            raise LinnetError(f"{layer}: qweight, qzeros and scales are 2-D")
-        if method == "gptq":
-            in_features, out_features = qweight.shape[0] * 8, qweight.shape[1]
-        else:
-            in_features, out_features = qweight.shape[0], qweight.shape[1] * 8
-        size = in_features if group <= 0 else group
-        groups = in_features // size if in_features % size == 0 else -1
-        if groups < 0 or tuple(qzeros.shape) != (groups, out_features // 8) or tuple(scales.shape) != (groups, out_features):
-            raise LinnetError(f"{layer}: {in_features} inputs do not make groups of {size}")
-        order: np.ndarray | None = None
-        if method == "gptq" and layer + ".g_idx" in index:
-            ids = load(layer + ".g_idx", torch.int32).cpu().numpy().reshape(-1)
-            group_of = np.arange(in_features) // size
-            if not np.array_equal(ids, group_of):
-                # Activation order: the groups hold inputs in another order. Taken
-                # in that order, each group is contiguous (`quant.py:314-325`).
-                order = np.argsort(ids, kind="stable").astype(np.int32)
-                if not np.array_equal(ids[order], group_of):
-                    raise LinnetError(f"{layer}: its groups are not all the same size")
-        order_t = torch.from_numpy(order).to(target) if order is not None else None
-        packed, zero = kernels.int4_repack(qweight, qzeros, method, size, zero_offset, order_t)
-        scale = scales.t().contiguous()
-        weight_name = layer + ".weight"
-        for path in paths_of.get(weight_name, [weight_name]):
-            prefix = _prefix(path)
-            out += _int4_tensors(prefix, packed, scale, zero, dtype)
-            if order is not None:
-                out.append((prefix + "order", "I32", (in_features,), order.tobytes()))
-            quantized.append(path)
-    if not quantized:
-        raise LinnetError(f"no {method.upper()} layer (`.qweight`) in {weights_path}")
-    # Every other tensor as it is, under its paths (`quant.py:357-369`).
-    for name, location in index.items():
-        if name in taken:
-            continue
-        for path in paths_of.get(name, [name]):
-            out.append((path, location.dtype, location.shape, location))
-    weights.write_safetensors(output, out, metadata={"format": "pt"})
-    return quantized
+def _import_layer(layer: str, parts: Mapping[str, weights.StoredTensor], calibrated: _Calibrated,
+                  target: torch.device) -> tuple:
+    """One calibrated layer as `(packed, "U8", scale [Out, Groups] f32, zero, order)`."""
+    absent = [p for p in ("qzeros", "scales") if p not in parts]
+    if absent:
+        raise LinnetError(f"{layer}: `qweight` without {' and '.join(absent)}")
+    words = weights.tensor_from(parts["qweight"], torch.int32, target)
+    zero_words = weights.tensor_from(parts["qzeros"], torch.int32, target)
+    scales = weights.float_tensor(parts["scales"], target)
+    if words.dim() != 2 or zero_words.dim() != 2 or scales.dim() != 2:
+        raise LinnetError(f"{layer}: qweight, qzeros and scales must be matrices")
+    gptq = calibrated.method == "gptq"
+    # GPTQ packs 8 inputs a word down the rows, AWQ 8 outputs a word along them.
+    in_features = words.shape[0] * 8 if gptq else words.shape[0]
+    out_features = words.shape[1] if gptq else words.shape[1] * 8
+    group = calibrated.group if calibrated.group > 0 else in_features
+    groups = in_features // group
+    if in_features % group or zero_words.shape != (groups, out_features // 8) or scales.shape != (groups, out_features):
+        raise LinnetError(f"{layer}: {in_features} inputs x {out_features} outputs do not fit groups of {group} "
+                          f"(qzeros {tuple(zero_words.shape)}, scales {tuple(scales.shape)})")
+    order = None
+    if gptq and "g_idx" in parts:
+        order = input_order(weights.tensor_from(parts["g_idx"], torch.int32, "cpu").numpy(), group, in_features)
+    packed, zero = kernels.int4_repack(words, zero_words, calibrated.method, group, calibrated.zero_offset,
+                                       None if order is None else torch.from_numpy(order).to(target))
+    return packed, "U8", scales.t().contiguous(), zero, order
 
 
 __all__ = [
@@ -318,8 +372,10 @@ __all__ = [
     "dequantize_int4_groups",
     "dequantize_int8_groups",
     "import_quantized",
+    "input_order",
     "pack_int4_groups",
     "quantize_checkpoint",
     "quantize_int4_groups",
     "quantize_int8_groups",
+    "siblings",
 ]

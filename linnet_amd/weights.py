@@ -1,235 +1,241 @@
-"""SafeTensors checkpoints read and written tensor by tensor, and the bindings
-that map Linnet parameter paths onto checkpoint tensor names, for the checkpoint
-tools of `linnet_amd.quant` (the reference's `python/linnet/src/linnet/weights.py`).
+"""SafeTensors checkpoints for the checkpoint tools of `linnet_amd.quant`: files
+memory-mapped and read tensor by tensor, new files streamed out, and the
+bindings that put Linnet parameter paths on checkpoint tensor names (the
+reference's tools read and write the same files, `python/linnet/src/linnet/weights.py`).
 
-A SafeTensors file is an 8-byte little-endian header length, a JSON header (each
-tensor's dtype name, shape and `data_offsets` into the data section, plus an
-optional `__metadata__` object of strings), padded with spaces to a multiple of 8
-bytes, then the tensors' bytes. Host code: bytes, JSON and PyTorch tensors, no
-kernels.
+The format, from the SafeTensors specification: a little-endian u64 N, N bytes
+of a JSON object mapping each tensor's name to `{"dtype", "shape",
+"data_offsets": [begin, end]}` (offsets into the data section that follows)
+plus an optional `"__metadata__"` object of strings, then the data section.
+`CheckpointWriter` writes the header as compact JSON (no spaces), in the order
+tensors were added, padded with spaces to a multiple of 8 bytes -- the bytes the
+reference's writer and the `safetensors` package produce for the same tensors.
+Host code: bytes, JSON and PyTorch tensors, no kernels.
 """
 
 from __future__ import annotations
 
+import itertools
 import json
+import mmap
 import struct
-from collections.abc import Iterable, Iterator, Mapping
-from dataclasses import dataclass
+from collections import defaultdict
+from collections.abc import Iterable, Mapping
+from dataclasses import dataclass, field
 from pathlib import Path
 
 import torch
 
 from .errors import LinnetError
 
-# SafeTensors floating-point dtype names and the torch dtypes that read them
-# (`decode_floats`, `weights.py:87-95`).
+# SafeTensors dtype names of the floating-point types the tools read, and the
+# torch dtypes that hold them.
 FLOAT_DTYPES = {"F64": torch.float64, "F32": torch.float32, "F16": torch.float16, "BF16": torch.bfloat16}
-# Linnet's scale storage dtypes by their SafeTensors names (`dtypes.py` `DTYPES[...].safetensors`).
+# A Linnet scale dtype's SafeTensors name.
 STORAGE = {"bf16": "BF16", "f16": "F16", "f32": "F32"}
 
+_LENGTH = struct.Struct("<Q")
+
+
+class _Mapping:
+    """One checkpoint file, mapped read-only for as long as a tensor of it is alive."""
+
+    def __init__(self, file: Path) -> None:
+        self.file = file
+        with file.open("rb") as handle:
+            size = handle.seek(0, 2)
+            self.bytes = mmap.mmap(handle.fileno(), 0, access=mmap.ACCESS_READ) if size else b""
+
+    def __len__(self) -> int:
+        return len(self.bytes)
+
 
 @dataclass(frozen=True)
-class RawTensor:
-    """One tensor of a SafeTensors file as bytes (`weights.py:232-239`)."""
+class StoredTensor:
+    """A tensor of a checkpoint file: its name, SafeTensors dtype and shape, and
+    where its bytes lie (absolute offsets `begin`..`end` in the mapped file)."""
 
     name: str
-    dtype: str  # the file's dtype name: BF16, F32, I32, U8, ...
-    shape: tuple[int, ...]
-    data: bytes
-
-
-@dataclass(frozen=True)
-class TensorLocation:
-    """Where a tensor's bytes lie in a file (`weights.py:242-258`), for copying a
-    tensor into a new file without holding it."""
-
-    file: Path
     dtype: str
     shape: tuple[int, ...]
-    start: int  # absolute byte offsets in the file
+    begin: int
     end: int
+    mapping: _Mapping = field(repr=False, compare=False)
 
     @property
     def nbytes(self) -> int:
-        return self.end - self.start
+        return self.end - self.begin
+
+    def view(self) -> memoryview:
+        """The bytes, without a copy (read-only)."""
+        return memoryview(self.mapping.bytes)[self.begin : self.end]
 
     def read(self) -> bytes:
-        with self.file.open("rb") as handle:
-            handle.seek(self.start)
-            data = handle.read(self.nbytes)
-        if len(data) != self.nbytes:
-            raise LinnetError(f"{self.file} ends inside a tensor")
-        return data
+        return bytes(self.view())
 
 
-def safetensors_files(weights: str | Path) -> list[Path]:
-    """One `.safetensors` file, or every one in a directory (`weights.py:38-44`)."""
-    path = Path(weights)
-    files = sorted(path.glob("*.safetensors")) if path.is_dir() else [path]
-    if not files or not all(file.exists() for file in files):
-        raise LinnetError(f"no .safetensors files under {weights}")
-    return files
+def checkpoint_files(weights: str | Path) -> list[Path]:
+    """A `.safetensors` file, or a directory's `.safetensors` files in name order."""
+    location = Path(weights)
+    found = sorted(location.glob("*.safetensors")) if location.is_dir() else [location]
+    missing = [str(f) for f in found if not f.is_file()]
+    if not found or missing:
+        raise LinnetError(f"{weights}: no SafeTensors file to read" + (f" ({', '.join(missing)})" if missing else ""))
+    return found
 
 
-def _header(file: Path) -> tuple[dict[str, object], int]:
-    """A file's JSON header and the offset where its data section starts."""
-    with file.open("rb") as handle:
-        head = handle.read(8)
-        if len(head) != 8:
-            raise LinnetError(f"{file} is not a SafeTensors file (no header length)")
-        (size,) = struct.unpack("<Q", head)
-        text = handle.read(size)
-    if len(text) != size:
-        raise LinnetError(f"{file} ends inside its header")
-    header = json.loads(text.decode("utf-8"))
+def _tensors_of(file: Path) -> Iterable[StoredTensor]:
+    mapped = _Mapping(file)
+    if len(mapped) < _LENGTH.size:
+        raise LinnetError(f"{file}: shorter than a SafeTensors header length")
+    (length,) = _LENGTH.unpack_from(mapped.bytes, 0)
+    data = _LENGTH.size + length
+    if data > len(mapped):
+        raise LinnetError(f"{file}: the header runs past the end of the file")
+    header = json.loads(bytes(mapped.bytes[_LENGTH.size : data]).decode("utf-8"))
     if not isinstance(header, dict):
         raise LinnetError(f"{file}: the header is not a JSON object")
-    return header, 8 + size
+    for name, spec in header.items():
+        if name == "__metadata__":
+            continue
+        try:
+            begin, end = (int(o) for o in spec["data_offsets"])
+            dtype, shape = str(spec["dtype"]), tuple(int(d) for d in spec["shape"])
+        except (KeyError, TypeError, ValueError):
+            raise LinnetError(f"{file}: tensor `{name}` lacks a dtype, shape or pair of data_offsets") from None
+        if begin < 0 or end < begin or data + end > len(mapped):
+            raise LinnetError(f"{file}: tensor `{name}` lies outside the data section ({begin}..{end})")
+        yield StoredTensor(str(name), dtype, shape, data + begin, data + end, mapped)
 
 
-def safetensors_index(weights: str | Path) -> dict[str, TensorLocation]:
-    """Every tensor of a checkpoint by name, from the headers alone (`weights.py:287-304`)."""
-    index: dict[str, TensorLocation] = {}
-    for file in safetensors_files(weights):
-        header, base = _header(file)
-        for name, entry in header.items():
-            if name == "__metadata__":
-                continue
-            if not isinstance(entry, dict) or not {"dtype", "shape", "data_offsets"} <= entry.keys():
-                raise LinnetError(f"{file}: `{name}` has no dtype, shape and data_offsets")
-            start, end = (int(o) for o in entry["data_offsets"])
-            if not 0 <= start <= end:
-                raise LinnetError(f"{file}: `{name}` has data_offsets {entry['data_offsets']}")
-            index[str(name)] = TensorLocation(
-                file=file,
-                dtype=str(entry["dtype"]),
-                shape=tuple(int(d) for d in entry["shape"]),
-                start=base + start,
-                end=base + end,
-            )
-    return index
+def open_checkpoint(weights: str | Path) -> dict[str, StoredTensor]:
+    """Every tensor of a checkpoint (a file or a directory of files) by name, in
+    the order the headers list them. Only headers are read; a tensor's bytes are
+    paged in when used."""
+    found: dict[str, StoredTensor] = {}
+    for file in checkpoint_files(weights):
+        for stored in _tensors_of(file):
+            if stored.name in found:
+                raise LinnetError(f"`{stored.name}` is in both {found[stored.name].mapping.file} and {file}")
+            found[stored.name] = stored
+    return found
 
 
-def iter_safetensors(weights: str | Path) -> Iterator[RawTensor]:
-    """A checkpoint's tensors one at a time, in header order (`weights.py:307-314`)."""
-    for name, location in safetensors_index(weights).items():
-        yield RawTensor(name, location.dtype, location.shape, location.read())
+Data = bytes | bytearray | memoryview | StoredTensor
 
 
-Data = bytes | TensorLocation
+class CheckpointWriter:
+    """Collects tensors, then writes them as one SafeTensors file in the order added."""
+
+    def __init__(self) -> None:
+        self._entries: list[tuple[str, str, tuple[int, ...], Data]] = []
+        self._names: set[str] = set()
+
+    def add(self, name: str, dtype: str, shape: Iterable[int], data: Data) -> None:
+        if name in self._names:
+            raise LinnetError(f"`{name}` would be written twice")
+        self._names.add(name)
+        self._entries.append((name, dtype, tuple(int(d) for d in shape), data))
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+    def write(self, path: str | Path, metadata: Mapping[str, str] | None = None) -> Path:
+        sizes = [d.nbytes if isinstance(d, (StoredTensor, memoryview)) else len(d) for _, _, _, d in self._entries]
+        ends = list(itertools.accumulate(sizes))
+        header: dict[str, object] = {"__metadata__": {str(k): str(v) for k, v in metadata.items()}} if metadata else {}
+        for (name, dtype, shape, _), end, size in zip(self._entries, ends, sizes):
+            header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [end - size, end]}
+        text = json.dumps(header, separators=(",", ":")).encode("utf-8")
+        text = text.ljust((len(text) + 7) // 8 * 8, b" ")
+        target = Path(path)
+        target.parent.mkdir(parents=True, exist_ok=True)
+        with target.open("wb") as out:
+            out.write(_LENGTH.pack(len(text)))
+            out.write(text)
+            for *_, data in self._entries:
+                # A stored tensor is written straight from its file's mapping.
+                out.write(data.view() if isinstance(data, StoredTensor) else data)
+        return target
 
 
-def write_safetensors(
+def write_checkpoint(
     path: str | Path,
-    tensors: Iterable[tuple[str, str, tuple[int, ...], Data]],
+    tensors: Iterable[tuple[str, str, Iterable[int], Data]],
     metadata: Mapping[str, str] | None = None,
 ) -> Path:
-    """Writes `(name, dtype, shape, data)` tensors in the order given, `data` the
-    bytes or a `TensorLocation` copied in 64 MiB pieces (`weights.py:325-373`)."""
-    entries = list(tensors)
-    header: dict[str, object] = {}
-    if metadata:
-        header["__metadata__"] = {str(k): str(v) for k, v in metadata.items()}
-    offset = 0
-    for name, dtype, shape, data in entries:
-        size = data.nbytes if isinstance(data, TensorLocation) else len(data)
-        if name in header:
-            raise LinnetError(f"`{name}` is written twice")
-        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [offset, offset + size]}
-        offset += size
-    encoded = json.dumps(header, separators=(",", ":")).encode("utf-8")
-    encoded += b" " * (-len(encoded) % 8)
-    target = Path(path)
-    target.parent.mkdir(parents=True, exist_ok=True)
-    with target.open("wb") as out:
-        out.write(struct.pack("<Q", len(encoded)))
-        out.write(encoded)
-        for _, _, _, data in entries:
-            if isinstance(data, TensorLocation):
-                with data.file.open("rb") as source:
-                    source.seek(data.start)
-                    remaining = data.nbytes
-                    while remaining:
-                        chunk = source.read(min(remaining, 64 << 20))
-                        if not chunk:
-                            raise LinnetError(f"{data.file} ends inside a tensor")
-                        out.write(chunk)
-                        remaining -= len(chunk)
-            else:
-                out.write(data)
-    return target
+    """Writes `(name, dtype, shape, data)` tensors, in order, as one SafeTensors file."""
+    writer = CheckpointWriter()
+    for name, dtype, shape, data in tensors:
+        writer.add(name, dtype, shape, data)
+    return writer.write(path, metadata)
 
 
 def read_bindings(bindings: str | Path) -> dict[str, str]:
-    """A JSON object of Linnet parameter path -> checkpoint tensor name (`weights.py:108-113`)."""
+    """A JSON file of `{Linnet parameter path: checkpoint tensor name}`."""
     loaded = json.loads(Path(bindings).read_text(encoding="utf-8"))
     if not isinstance(loaded, dict):
-        raise LinnetError("bindings must be a JSON object mapping parameter paths to tensor names")
-    return {str(path): str(name) for path, name in loaded.items()}
+        raise LinnetError(f"{bindings}: bindings are a JSON object of parameter paths to tensor names")
+    return {str(k): str(v) for k, v in loaded.items()}
 
 
 def paths_by_tensor(mapping: Mapping[str, str]) -> dict[str, list[str]]:
-    """The Linnet paths bound to each checkpoint tensor, in binding order (a tied
-    embedding and output head share one; `weights.py:124-130`)."""
-    paths: dict[str, list[str]] = {}
+    """Inverts bindings: each checkpoint tensor's paths, in binding order (a tied
+    embedding and output head name the same tensor)."""
+    inverse: defaultdict[str, list[str]] = defaultdict(list)
     for path, name in mapping.items():
-        paths.setdefault(name, []).append(path)
-    return paths
+        inverse[name].append(path)
+    return dict(inverse)
 
 
-def tensor_from(raw: RawTensor, dtype: torch.dtype, device: torch.device | str) -> torch.Tensor:
-    """A raw tensor's bytes as a torch tensor of `dtype`, shaped, on `device`."""
-    itemsize = torch.empty((), dtype=dtype).element_size()
+def tensor_from(stored: StoredTensor, dtype: torch.dtype, device: torch.device | str) -> torch.Tensor:
+    """A stored tensor's bytes read as `dtype`, in its shape, on `device`."""
     count = 1
-    for d in raw.shape:
+    for d in stored.shape:
         count *= d
-    if len(raw.data) != count * itemsize:
-        raise LinnetError(f"`{raw.name}`: {len(raw.data)} bytes for shape {list(raw.shape)} of {dtype}")
-    if count == 0:
-        return torch.empty(raw.shape, dtype=dtype, device=device)
-    host = torch.frombuffer(bytearray(raw.data), dtype=dtype).reshape(raw.shape)
-    return host.to(device)
+    width = torch.empty((), dtype=dtype).element_size()
+    if stored.nbytes != count * width:
+        raise LinnetError(f"`{stored.name}`: {stored.nbytes} bytes cannot hold {list(stored.shape)} of {dtype}")
+    if not count:
+        return torch.empty(stored.shape, dtype=dtype, device=device)
+    host = torch.frombuffer(bytearray(stored.view()), dtype=dtype)
+    return host.reshape(stored.shape).to(device)
 
 
-def float_tensor(raw: RawTensor, device: torch.device | str) -> torch.Tensor:
-    """A floating-point tensor (F64, F32, F16, BF16) as f32 on `device`: the values of
-    `decode_floats` (`weights.py:87-95`; F64 rounded to nearest f32, the others exact)."""
-    found = FLOAT_DTYPES.get(raw.dtype)
-    if found is None:
-        raise LinnetError(f"`{raw.name}` is {raw.dtype}, not a floating-point dtype")
-    return tensor_from(raw, found, device).to(torch.float32)
+def float_tensor(stored: StoredTensor, device: torch.device | str) -> torch.Tensor:
+    """A floating-point tensor (F64, F32, F16 or BF16) widened or rounded to f32
+    on `device` (round to nearest from F64; the others exactly)."""
+    if stored.dtype not in FLOAT_DTYPES:
+        raise LinnetError(f"`{stored.name}` holds {stored.dtype}, not floating-point values")
+    return tensor_from(stored, FLOAT_DTYPES[stored.dtype], device).to(torch.float32)
 
 
 def tensor_bytes(t: torch.Tensor) -> bytes:
-    """A tensor's bytes, row-major (any device)."""
-    flat = t.detach().contiguous().reshape(-1)
-    if flat.numel() == 0:
-        return b""
-    return flat.cpu().view(torch.uint8).numpy().tobytes()
+    """A tensor's elements as bytes in row-major order, from any device."""
+    flat = t.detach().reshape(-1).contiguous()
+    return flat.cpu().view(torch.uint8).numpy().tobytes() if flat.numel() else b""
 
 
 def encode_floats(values: torch.Tensor, dtype: str) -> bytes:
-    """f32 values as the bytes of SafeTensors dtype `dtype` (BF16, F16, F32), each
-    rounded to nearest, ties to even (`weights.py:98-105`)."""
-    found = FLOAT_DTYPES.get(dtype)
-    if found is None or found is torch.float64:
-        raise LinnetError(f"{dtype} is not a scale storage dtype")
-    return tensor_bytes(values.to(torch.float32).to(found))
+    """Values as SafeTensors dtype `dtype` (BF16, F16 or F32), each rounded to
+    nearest with ties to even."""
+    if dtype not in ("BF16", "F16", "F32"):
+        raise LinnetError(f"{dtype} is not a dtype scales are stored in")
+    return tensor_bytes(values.to(torch.float32).to(FLOAT_DTYPES[dtype]))
 
 
 __all__ = [
     "FLOAT_DTYPES",
     "STORAGE",
-    "RawTensor",
-    "TensorLocation",
+    "CheckpointWriter",
+    "StoredTensor",
+    "checkpoint_files",
     "encode_floats",
     "float_tensor",
-    "iter_safetensors",
+    "open_checkpoint",
     "paths_by_tensor",
     "read_bindings",
-    "safetensors_files",
-    "safetensors_index",
     "tensor_bytes",
     "tensor_from",
-    "write_safetensors",
+    "write_checkpoint",
 ]

@@ -4,31 +4,33 @@ from __future__ import annotations
 
 import numpy as np
 
-# GPTQ's and AWQ's int32 packings written from the formats' definitions, as the
-# reference's tests write them (`test_quant_groups.py:198-221`), not from the
-# importer: GPTQ `qweight[i // 8, o]` holds input i at bits 4 (i % 8) and
-# `qzeros[g, o // 8]` group g's zero point, less one in the first format, at bits
-# 4 (o % 8); AWQ `qweight[i, c]` and `qzeros[g, c]` hold output 8c + ORDER[k] at
-# bits 4k, zero points as they are.
-FORMAT_AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+# The two checkpoint formats' int32 words, built from their definitions:
+# - GPTQ: `qweight[i // 8, o]` holds input i of output o at bits 4 (i % 8);
+#   `qzeros[g, o // 8]` holds group g's zero point of output o at bits 4 (o % 8),
+#   less `offset` (1 in GPTQ's first checkpoint format), wrapped to 4 bits.
+# - AWQ (GEMM packing): `qweight[i, c]` and `qzeros[g, c]` hold output
+#   8c + AWQ_SLOTS[k] at bits 4k, zero points as they are.
+AWQ_SLOTS = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def _words(values: np.ndarray, slot_of: tuple[int, ...]) -> np.ndarray:
+    """Eight 4-bit values along the last axis as one int32: value j at bits 4 slot_of[j]."""
+    shifts = 4 * np.asarray(slot_of, dtype=np.uint32)
+    return np.bitwise_or.reduce((values.astype(np.uint32) & 15) << shifts, axis=-1).view(np.int32)
 
 
 def pack_gptq(q: np.ndarray, zero: np.ndarray, offset: int = 1) -> tuple[np.ndarray, np.ndarray]:
-    qweight = np.zeros((q.shape[0] // 8, q.shape[1]), np.uint32)
-    qzeros = np.zeros((zero.shape[0], zero.shape[1] // 8), np.uint32)
-    for k in range(8):
-        qweight |= q[k::8].astype(np.uint32) << (4 * k)
-        qzeros |= (zero[:, k::8] - offset).astype(np.uint32) << (4 * k)
-    return qweight.view(np.int32), qzeros.view(np.int32)
+    """`q` [In, Out] codes and `zero` [Groups, Out] as GPTQ's (qweight, qzeros)."""
+    inputs, outputs = q.shape
+    down_rows = np.moveaxis(q.reshape(inputs // 8, 8, outputs), 1, -1)  # [In/8, Out, 8]
+    along = (zero.astype(np.int64) - offset).reshape(zero.shape[0], outputs // 8, 8)
+    return _words(down_rows, tuple(range(8))), _words(along, tuple(range(8)))
 
 
 def pack_awq(q: np.ndarray, zero: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    qweight = np.zeros((q.shape[0], q.shape[1] // 8), np.uint32)
-    qzeros = np.zeros((zero.shape[0], zero.shape[1] // 8), np.uint32)
-    for k, column in enumerate(FORMAT_AWQ_ORDER):
-        qweight |= q[:, column::8].astype(np.uint32) << (4 * k)
-        qzeros |= zero[:, column::8].astype(np.uint32) << (4 * k)
-    return qweight.view(np.int32), qzeros.view(np.int32)
+    """`q` [In, Out] codes and `zero` [Groups, Out] as AWQ's (qweight, qzeros)."""
+    slot_of = tuple(AWQ_SLOTS.index(j) for j in range(8))
+    return (_words(q.reshape(q.shape[0], -1, 8), slot_of), _words(zero.reshape(zero.shape[0], -1, 8), slot_of))
 
 
 def calibrated_layer(method: str, act_order: bool, seed: int = 3, in_features: int = 256,

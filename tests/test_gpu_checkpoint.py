@@ -114,7 +114,7 @@ def test_import_quantized_rejects_unequal_groups(tmp_path: Path) -> None:
     save_file({"p.qweight": torch.from_numpy(layer["qweight"]), "p.qzeros": torch.from_numpy(layer["qzeros"]),
                "p.scales": torch.from_numpy(layer["scale"]), "p.g_idx": torch.from_numpy(g_idx)},
               str(tmp_path / "c.safetensors"))
-    with pytest.raises(LinnetError, match="not all the same size"):
+    with pytest.raises(LinnetError, match="inputs in a group of"):
         quant.import_quantized(tmp_path / "c.safetensors", tmp_path / "o.safetensors",
                                config={"quant_method": "gptq", "bits": 4, "group_size": 64})
 
@@ -150,7 +150,7 @@ def test_quantize_checkpoint_matches_the_oracle(tmp_path: Path, bits: int, dtype
         assert np.array_equal(stored.float().numpy(), oq.round_to_storage(scale, dtype))
     for name in ("model.layers.0.input_layernorm.weight", "model.embed_tokens.weight"):
         assert torch.equal(got[name], tensors[name])
-    with pytest.raises(LinnetError, match="no weight matched"):
+    with pytest.raises(LinnetError, match="path matched"):
         quant.quantize_checkpoint(tmp_path / "model.safetensors", tmp_path / "n.safetensors", patterns=["nothing*"])
 
 

@@ -36,7 +36,7 @@ _NAMES = {torch.bfloat16: "BF16", torch.float16: "F16", torch.int32: "I32", torc
 def test_written_files_read_back_through_safetensors(tmp_path: Path) -> None:
     tensors = _tensors()
     entries = [(n, _NAMES[t.dtype], tuple(t.shape), weights.tensor_bytes(t)) for n, t in tensors.items()]
-    path = weights.write_safetensors(tmp_path / "out.safetensors", entries, metadata={"format": "pt"})
+    path = weights.write_checkpoint(tmp_path / "out.safetensors", entries, metadata={"format": "pt"})
     raw = path.read_bytes()
     size = int.from_bytes(raw[:8], "little")
     assert size % 8 == 0
@@ -50,12 +50,12 @@ def test_written_files_read_back_through_safetensors(tmp_path: Path) -> None:
 def test_files_of_safetensors_read_back(tmp_path: Path) -> None:
     tensors = _tensors()
     save_file(tensors, str(tmp_path / "in.safetensors"))
-    seen = {raw.name: raw for raw in weights.iter_safetensors(tmp_path / "in.safetensors")}
+    seen = weights.open_checkpoint(tmp_path / "in.safetensors")
     assert set(seen) == set(tensors)
     for name, t in tensors.items():
         raw = seen[name]
         assert raw.dtype == _NAMES[t.dtype] and raw.shape == tuple(t.shape)
-        assert raw.data == weights.tensor_bytes(t)
+        assert raw.read() == weights.tensor_bytes(t)
         assert torch.equal(weights.tensor_from(raw, t.dtype, "cpu"), t)
     assert torch.equal(weights.float_tensor(seen["a.weight"], "cpu"), tensors["a.weight"].float())
 
@@ -63,9 +63,9 @@ def test_files_of_safetensors_read_back(tmp_path: Path) -> None:
 def test_copy_by_location_and_directories(tmp_path: Path) -> None:
     save_file({"x": torch.arange(10, dtype=torch.float32)}, str(tmp_path / "a.safetensors"))
     save_file({"y": torch.arange(6, dtype=torch.int32)}, str(tmp_path / "b.safetensors"))
-    index = weights.safetensors_index(tmp_path)
+    index = weights.open_checkpoint(tmp_path)
     assert list(index) == ["x", "y"]
-    out = weights.write_safetensors(
+    out = weights.write_checkpoint(
         tmp_path / "sub" / "c.safetensors",
         [(n, loc.dtype, loc.shape, loc) for n, loc in index.items()],
     )
@@ -73,9 +73,9 @@ def test_copy_by_location_and_directories(tmp_path: Path) -> None:
         assert torch.equal(f.get_tensor("x"), torch.arange(10, dtype=torch.float32))
         assert torch.equal(f.get_tensor("y"), torch.arange(6, dtype=torch.int32))
     with pytest.raises(LinnetError):
-        weights.safetensors_files(tmp_path / "missing.safetensors")
+        weights.checkpoint_files(tmp_path / "missing.safetensors")
     with pytest.raises(LinnetError):
-        weights.write_safetensors(tmp_path / "d.safetensors", [("x", "U8", (1,), b"\0"), ("x", "U8", (1,), b"\0")])
+        weights.write_checkpoint(tmp_path / "d.safetensors", [("x", "U8", (1,), b"\0"), ("x", "U8", (1,), b"\0")])
 
 
 def test_bf16_and_f16_encoding_rounds_to_nearest_even() -> None:
@@ -93,7 +93,7 @@ def test_bindings_and_prefixes(tmp_path: Path) -> None:
     path.write_text(json.dumps({"embed.weight": "model.embed", "head.weight": "model.embed", "p.weight": "q"}))
     mapping = weights.read_bindings(path)
     assert weights.paths_by_tensor(mapping) == {"model.embed": ["embed.weight", "head.weight"], "q": ["p.weight"]}
-    assert quant._prefix("weight") == "" and quant._prefix("a.b.weight") == "a.b." and quant._prefix("a") == "a."
+    assert quant.siblings("weight") == "" and quant.siblings("a.b.weight") == "a.b." and quant.siblings("a") == "a."
     path.write_text("[1, 2]")
     with pytest.raises(LinnetError):
         weights.read_bindings(path)
@@ -101,10 +101,17 @@ def test_bindings_and_prefixes(tmp_path: Path) -> None:
 
 def test_checkpoint_settings_and_errors(tmp_path: Path) -> None:
     """Host-side checks of the checkpoint tools that run before any GPU work."""
-    assert quant._setting({"w_bit": "4"}, "bits", "w_bit", 8) == 4
-    assert quant._setting({}, "group_size", "q_group_size", 128) == 128
+    assert quant._config_number({"w_bit": "4"}, "bits", 8) == 4
+    assert quant._config_number({}, "group", 128) == 128
+    assert quant._config_number({"q_group_size": 64.0}, "group", 128) == 64
     with pytest.raises(LinnetError):
-        quant._setting({"bits": [4]}, "bits", "w_bit", 4)
+        quant._config_number({"bits": [4]}, "bits", 4)
+    with pytest.raises(LinnetError):
+        quant._config_number({"bits": True}, "bits", 4)
+    assert quant._Calibrated.read({"quant_method": "GPTQ"}) == quant._Calibrated("gptq", 128, 1)
+    assert quant._Calibrated.read({"quant_method": "gptq", "checkpoint_format": "gptq_v2", "group_size": 32}) == \
+        quant._Calibrated("gptq", 32, 0)
+    assert quant._Calibrated.read({"quant_method": "awq", "w_bit": 4, "q_group_size": 64}) == quant._Calibrated("awq", 64, 0)
     with pytest.raises(LinnetError):
         quant.quantize_checkpoint(tmp_path / "x.safetensors", tmp_path / "y.safetensors", patterns=["*"], bits=3)
     with pytest.raises(LinnetError):
@@ -116,3 +123,33 @@ def test_checkpoint_settings_and_errors(tmp_path: Path) -> None:
             quant.import_quantized(tmp_path / "x.safetensors", tmp_path / "y.safetensors", config=config)
     with pytest.raises(LinnetError, match="config.json"):
         quant.import_quantized(tmp_path / "x.safetensors", tmp_path / "y.safetensors")
+
+
+def test_written_bytes_equal_the_safetensors_package(tmp_path: Path) -> None:
+    """Given the tensors in the order the `safetensors` package lays them out, the
+    file is byte for byte the package's own (compact JSON header, space padding)."""
+    from safetensors.torch import save
+
+    tensors = {k: v for k, v in _tensors().items() if v.numel()}
+    expected = save(tensors, metadata={"format": "pt"})
+    size = int.from_bytes(expected[:8], "little")
+    order = [name for name in json.loads(expected[8:8 + size]) if name != "__metadata__"]
+    entries = [(n, _NAMES[tensors[n].dtype], tuple(tensors[n].shape), weights.tensor_bytes(tensors[n])) for n in order]
+    got = weights.write_checkpoint(tmp_path / "same.safetensors", entries, metadata={"format": "pt"}).read_bytes()
+    assert got == expected
+
+
+def test_input_order_sorts_inputs_by_group() -> None:
+    """GPTQ's activation order: the stable sort of g_idx (each group's inputs in
+    input order), checked against a brute-force listing; equal-size groups only."""
+    rng = np.random.default_rng(6)
+    g_idx = (np.arange(96) // 32)[rng.permutation(96)].astype(np.int32)
+    order = quant.input_order(g_idx, 32, 96)
+    brute = [i for g in range(3) for i in range(96) if g_idx[i] == g]
+    assert order.dtype == np.int32 and order.tolist() == brute
+    assert quant.input_order(np.arange(64, dtype=np.int32) // 32, 32) is None
+    for bad in (np.r_[np.zeros(33), np.ones(31)], np.r_[np.zeros(32), np.full(32, 2)], np.full(64, -1)):
+        with pytest.raises(LinnetError):
+            quant.input_order(bad.astype(np.int32), 32)
+    with pytest.raises(LinnetError):
+        quant.input_order(g_idx, 32, 128)
