@@ -558,6 +558,7 @@ def cpu_baseline(k: int, n: int, budget_s: float) -> dict[str, object]:
     linear.int4_groups_linear_interpreter(x, p, s, z, None)
     interp = time.perf_counter() - t0
     nbytes = gemv_bytes(1, k, n)
+    del prepared, p, s, z
     return {
         "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
@@ -566,7 +567,49 @@ def cpu_baseline(k: int, n: int, budget_s: float) -> dict[str, object]:
         "sample": (f"full layer K={k} N={n} M=1, reference CPU generated-source path (bf16 F.linear over the "
                    f"prepared weight), median of {len(times)} calls = {med * 1e3:.2f} ms; interpreter path "
                    f"(dequantize per call) 1 call = {interp * 1e3:.1f} ms = {nbytes / interp / 1e9:.3f} GB/s"),
+        "configs": eight_bit_cpu(budget_s),
     }
+
+
+def eight_bit_cpu(budget_s: float) -> dict[str, object]:
+    """The reference's CPU branch of the 8-bit linears (`torch/quantized.py:133-134,
+    193`: the weight widened and scaled on every call, then a bf16 `F.linear`), at
+    config 1 (int8 per-row, 4096 x 4096, one token) and config 4 (FP8 E4M3 per-row,
+    K 8192 x N 28672, one token), on the host cores: median of the calls that fit
+    `budget_s` (at least 3, after 1 warmup). GB/s counts the weight, its scales and
+    the activations once, as the GPU figures do."""
+    import numpy as np
+    import torch
+
+    from oracle import linear
+
+    g = torch.Generator().manual_seed(0)
+    found: dict[str, object] = {}
+    for key, n, k, fp8 in (("C1_int8_M1", 4096, 4096, False), ("C4_fp8_M1", 28672, 8192, True)):
+        w = torch.randn(n, k, generator=g) * 0.02
+        if fp8:
+            s = (w.abs().max() / 448).expand(n).contiguous()
+            q = (w / s[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+            run = linear.fp8_linear_cpu
+        else:
+            s = w.abs().amax(1) / 127
+            q = torch.round(w / s[:, None]).clamp(-127, 127).to(torch.int8)
+            run = linear.int8_linear_cpu
+        del w
+        x = torch.randn(1, k, generator=g).to(torch.bfloat16)
+        run(x, q, s, None)
+        times: list[float] = []
+        start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 20):
+            t0 = time.perf_counter()
+            run(x, q, s, None)
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        nbytes = n * k + n * 4 + k * 2 + n * 2
+        found[key] = {"ms": round(med * 1e3, 3), "gbps": round(nbytes / med / 1e9, 3), "calls": len(times),
+                      "path": "per call: weight widened x scale -> bf16, F.linear"}
+        del q, s
+    return found
 
 
 if __name__ == "__main__":

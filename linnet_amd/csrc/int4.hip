@@ -77,11 +77,10 @@ __device__ inline void load_chunk(const uint8_t* __restrict__ chunk, int j, uint
 // The weights stream in batches of U chunks, double-buffered: batch b + 1 is
 // requested before batch b is multiplied. With one group a chunk (group % 128
 // == 0) a chunk's epilogue runs after the next chunk's MFMAs are issued, so the
-// MFMA latency is hidden. NW waves split K; ONE: M == 1, whose one output row
-// sits in register 0 of lanes 0..15, so the epilogue computes that alone.
+// MFMA latency is hidden. NW waves split K.
 // SV: the scales and zero points of a batch's 4 chunks (4 groups of 128) come
 // in one 8-byte and one 4-byte load per lane (aligned shapes, group 128).
-template <int DT, int LOADW, int MT, bool XL, bool SV, int NW, bool ONE>
+template <int DT, int LOADW, int MT, bool XL, bool SV, int NW>
 __global__ __launch_bounds__(64 * NW) void int4_skinny_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
@@ -92,7 +91,6 @@ __global__ __launch_bounds__(64 * NW) void int4_skinny_kernel(
   constexpr int GPC = 4 / tpg;      // groups a chunk spans
   constexpr int U = 4;              // chunks of weight a batch
   constexpr int PD = XL ? 1 : 2;    // chunks of x in flight ahead of use
-  constexpr int RR = ONE ? 1 : 4;   // accumulator registers that hold live rows
   __shared__ f32x4 red[NW][MT][64];
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
 
@@ -226,7 +224,7 @@ __global__ __launch_bounds__(64 * NW) void int4_skinny_kernel(
   };
   auto fold = [&](const f32x4& C, const f32x4& Cx, float s, float zz, f32x4& a) {
 #pragma unroll
-    for (int r = 0; r < RR; ++r) a[r] = fmaf(s, fmaf(-zz, Cx[r], C[r]), a[r]);
+    for (int r = 0; r < 4; ++r) a[r] = fmaf(s, fmaf(-zz, Cx[r], C[r]), a[r]);
   };
 
   auto run_batch = [&](int c0, const Batch& bt) {
@@ -543,18 +541,13 @@ static void launch_skinny_v(const uint16_t* xs, const uint8_t* packed, const uin
   const int rows = min(M, 16 * MT);
   const int per_wave = skinny_per_wave(chunks, nw);
   const size_t lds = XL ? static_cast<size_t>(nw) * rows * (128 * per_wave + 8) * 2 : 0;
-  // The one-row specialization (ONE) is not used: with its fewer live registers
-  // the compiler reuses MFMA operand registers early, and one row with group 32
-  // came out wrong on gfx950; the four-row epilogue is correct for one row too.
-  const bool one = false;
-#define LNQ_SKINNY(NW, ONE)                                                                        \
-  hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, XL, SV, NW, ONE>), grid, block, lds, stream, \
+  // Every row count runs the four-row epilogue (one row leaves rows 1..3 of the
+  // accumulators zero).
+#define LNQ_SKINNY(NW)                                                                        \
+  hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, XL, SV, NW>), grid, block, lds, stream, \
                      xs, packed, ss, zero, bs, ys, M, N, K, G)
-  if (eight) {
-    if (one && MT == 1) LNQ_SKINNY(8, true); else LNQ_SKINNY(8, false);
-  } else {
-    if (one && MT == 1) LNQ_SKINNY(4, true); else LNQ_SKINNY(4, false);
-  }
+  if (eight) LNQ_SKINNY(8);
+  else LNQ_SKINNY(4);
 #undef LNQ_SKINNY
 }
 

@@ -555,12 +555,15 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
 
 // A few tokens (2..MX rows, MX = 4 or 16): the one-token kernel's workgroup
 // shape and weight streams, with A-operand row m of every MFMA holding x row m
-// (lane col = m). Each lane loads its own 128 bytes of x (its row, its 32-input
-// slices of both halves) straight into registers, in pair order; the whole x
-// is read once per CU. The output registers of a tile then hold rows
+// (lane col = m). x is read contiguously, two rows of the wave's 256 inputs an
+// instruction (only the M real rows), and turned into A operands through a
+// wave-private LDS slot of 4 rows, 4 rows a round; the whole x is read once per
+// CU. (A lane loading its own A operand would touch 16 rows an instruction, 64
+// scattered 16-byte pieces, and its 8 such loads per wave held the weight loads
+// back by 1.4-3.3 us.) The output registers of a tile then hold rows
 // 4 (lane / 16) + i; the fold takes each row's sum of x from the lane that
 // loaded it, and after a barrier the 16 waves' partial sums are added through
-// LDS (the weight buffers, no longer read).
+// LDS (the weight buffers, no longer read), four lanes an output.
 template <int DT, int U8, bool G128, int MX>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
@@ -576,6 +579,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   // touches consecutive dwords (a stride of 16 dwords would put 16 lanes on one
   // bank).
   static_assert(gemv::MAX_WAVES * 256 * 4 <= gemv::tile_bytes(U8, NT - 1), "partial sums fit a tile array");
+  // Each wave's slot for 4 rows of its 256 inputs of x.
+  __shared__ __attribute__((aligned(16))) uint16_t Xst[gemv::MAX_WAVES][4 * 256];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -606,14 +611,18 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // Lane row col: rows M .. 15 read zeros through the range check.
-  u32x4 xr[2][4];
+  // Load i: x row 2 i (lanes 0..31) and 2 i + 1 (lanes 32..63), 8 inputs a lane;
+  // loads past row M are not issued, and a row M of an odd M reads zeros
+  // through the range check.
+  constexpr int XI = MX / 2;
+  u32x4 xc[XI];
 #pragma unroll
-  for (int H = 0; H < 2; ++H)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      xr[H][t] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (col * K + k0 + 128 * H + 32 * j + 8 * t) * 2, 0, 0));
+  for (int i = 0; i < XI; ++i) {
+    xc[i] = u32x4{0u, 0u, 0u, 0u};
+    if (2 * i < M)
+      xc[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rx, ((2 * i + (lane >> 5)) * K + k0 + 8 * (lane & 31)) * 2, 0, 0));
+  }
   __builtin_amdgcn_sched_barrier(0);
   {
     const int a = lane >> 4, b = lane & 15;
@@ -627,25 +636,48 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- x: wait for it (and the scales) alone; pair order; the sums of x row col
-  // over both halves.
+  // ---- x: wait for it (and the scales) alone; through the wave's LDS slot, 4
+  // rows a round, to A operands in pair order (lane col: x row col, inputs
+  // 128 H + 32 j + 8 t ..); the sums of x row col over both halves.
   wait_vm<U8>();
   __builtin_amdgcn_sched_barrier(0);
   u32x4 xa[2][4];
+  float part[2] = {0.f, 0.f};
+#pragma unroll
+  for (int H = 0; H < 2; ++H)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xa[H][t] = u32x4{0u, 0u, 0u, 0u};
+  uint16_t* Xw = Xst[wave];
+#pragma unroll
+  for (int r = 0; r < MX / 4; ++r) {
+    if (4 * r >= M) break;
+    // Unconditional stores: with a store under a condition the compiler could
+    // sink the x loads into it, behind the weight loads.
+    *reinterpret_cast<u32x4*>(Xw + 256 * (lane >> 5) + 8 * (lane & 31)) = xc[2 * r];
+    *reinterpret_cast<u32x4*>(Xw + 256 * (2 + (lane >> 5)) + 8 * (lane & 31)) = xc[2 * r + 1];
+    // Only the reads are under the lane condition: VALU work there would cost
+    // every round the full wave's cycles.
+    if ((col >> 2) == r) {
+#pragma unroll
+      for (int H = 0; H < 2; ++H)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          xa[H][t] = *reinterpret_cast<const u32x4*>(Xw + 256 * (col & 3) + 128 * H + 32 * j + 8 * t);
+    }
+  }
   float xsum[2];
 #pragma unroll
   for (int H = 0; H < 2; ++H) {
-    float sum = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const u32x4 v = xr[H][t];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t d = v[e];
-        sum += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
+        const uint32_t d = xa[H][t][e];
+        part[H] += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
       }
-      xa[H][t] = permute_x8(v);
+      xa[H][t] = permute_x8(xa[H][t]);
     }
+    float sum = part[H];
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     xsum[H] = sum;  // sum of x row col over half H of this wave's inputs
@@ -730,17 +762,25 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     }
   }
   __syncthreads();
+  // Output o = (T, m, c) of the NT * M * 16: four lanes, each adding a quarter of
+  // the waves (read unconditionally, the waves past nw masked), then two
+  // exchanges; a group of four lanes is active or inactive together.
+  const int per_tile = M * 16;
+  for (int t = threadIdx.x; t < 4 * NT * per_tile; t += blockDim.x) {
+    const int o = t >> 2, q = t & 3;
+    const int T = o / per_tile, m = (o - T * per_tile) >> 4, c = o & 15;
+    const float* red = reinterpret_cast<const float*>(tile_lds(T, 0)) + (m & 3) * 64 + (m >> 2) * 16 + c;
+    float v = 0.f;
 #pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    const float* red = reinterpret_cast<const float*>(tile_lds(T, 0));
-    for (int o = threadIdx.x; o < M * 16; o += blockDim.x) {
-      const int m = o >> 4, c = o & 15;
-      const int n = n0 + 16 * T + c;
-      if (16 * T + c >= R || n >= N) continue;
-      float v = 0.f;
-#pragma unroll
-      for (int w = 0; w < gemv::MAX_WAVES; ++w)
-        if (w < nw) v += red[w * 256 + (m & 3) * 64 + (m >> 2) * 16 + c];
+    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
+      const int wv = q * (gemv::MAX_WAVES / 4) + w;
+      const float r = red[wv * 256];
+      v += wv < nw ? r : 0.f;
+    }
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    const int n = n0 + 16 * T + c;
+    if (q == 0 && 16 * T + c < R && n < N) {
       uint16_t out = E::from_f32(v);
       if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
       y[static_cast<size_t>(m) * N + n] = out;
