@@ -20,6 +20,10 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = PACKAGE.parent / "include"
 LIBDIR = PACKAGE / "_lib"
 LIBRARY = LIBDIR / "liblinnet_quant_hip.so"
+# The diagnostic library of linnet_amd.timeline: the same objects, the one-token
+# GEMV compiled with per-wave timestamps (LNQ_GEMV_TIMELINE).
+TIMELINE = LIBDIR / "liblinnet_quant_timeline.so"
+TIMELINE_SOURCE = "int4_gemv.hip"
 ARCH = "gfx950"
 
 # -packed-fp32-ops keeps hipcc from emitting packed f32 VALU instructions (the
@@ -57,33 +61,43 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def _compile(source: Path, objdir: Path) -> Path:
-    obj = objdir / (source.stem + ".o")
+def _compile(source: Path, objdir: Path, defines: tuple[str, ...] = (), suffix: str = "") -> Path:
+    obj = objdir / (source.stem + suffix + ".o")
     lang = ["-x", "hip"] if source.suffix in (".hip", ".cpp") else []
-    cmd = [hipcc(), *FLAGS, *EXTRA.get(source.name, []), f"-I{INCLUDE}", *lang, "-c", str(source), "-o", str(obj)]
+    cmd = [hipcc(), *FLAGS, *EXTRA.get(source.name, []), *(f"-D{d}" for d in defines), f"-I{INCLUDE}", *lang, "-c",
+           str(source), "-o", str(obj)]
     done = subprocess.run(cmd, capture_output=True, text=True)
     if done.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source.name}:\n{done.stdout}\n{done.stderr}")
     return obj
 
 
+def _link(objects: list[Path], target: Path) -> None:
+    staged = LIBDIR / f".{target.name}.{os.getpid()}.tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(staged), *map(str, objects)]
+    done = subprocess.run(cmd, capture_output=True, text=True)
+    if done.returncode != 0:
+        raise RuntimeError(f"linking {target.name} failed:\n{done.stdout}\n{done.stderr}")
+    os.replace(staged, target)
+
+
 def build(verbose: bool = False) -> Path:
-    """Compiles every source under csrc/ and links the library; returns its path."""
+    """Compiles every source under csrc/ and links the library (and the timeline
+    diagnostic library beside it); returns the library's path."""
     LIBDIR.mkdir(parents=True, exist_ok=True)
     with tempfile.TemporaryDirectory(prefix="lnq_build_") as tmp:
         objdir = Path(tmp)
         srcs = sources()
-        workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+        timeline_src = CSRC / TIMELINE_SOURCE
+        jobs = [(src, (), "") for src in srcs] + [(timeline_src, ("LNQ_GEMV_TIMELINE",), "_timeline")]
+        workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
         with ThreadPoolExecutor(max_workers=workers) as pool:
-            objects = list(pool.map(lambda s: _compile(s, objdir), srcs))
-        staged = LIBDIR / f".{LIBRARY.name}.{os.getpid()}.tmp"
-        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(staged), *map(str, objects)]
-        done = subprocess.run(cmd, capture_output=True, text=True)
-        if done.returncode != 0:
-            raise RuntimeError(f"linking {LIBRARY.name} failed:\n{done.stdout}\n{done.stderr}")
-        os.replace(staged, LIBRARY)
+            built = list(pool.map(lambda job: _compile(job[0], objdir, job[1], job[2]), jobs))
+        objects, timeline_obj = built[:-1], built[-1]
+        _link(objects, LIBRARY)
+        _link([timeline_obj if o.name == timeline_src.stem + ".o" else o for o in objects], TIMELINE)
     if verbose:
-        print(f"built {LIBRARY}", file=sys.stderr)
+        print(f"built {LIBRARY} and {TIMELINE.name}", file=sys.stderr)
     return LIBRARY
 
 

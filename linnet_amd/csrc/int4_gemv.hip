@@ -41,6 +41,26 @@
 
 namespace lnq {
 
+// Per-wave timestamps of the one-token kernel, for the diagnostic build only
+// (compiled with LNQ_GEMV_TIMELINE into liblinnet_quant_timeline.so, read by
+// linnet_amd.timeline): lane 0 of each wave of the first 512 workgroups stores
+// s_memrealtime (100 MHz) at point e: 0 entry, 1 small loads issued, 2 past the
+// start barrier, 3 weights issued, 4 x landed, 5 + T tile T folded, 9 the half
+// tile folded, 10 / 11 before / after the final barrier, 12 end. The product
+// build compiles the points to nothing.
+#ifdef LNQ_GEMV_TIMELINE
+__device__ unsigned long long gemv_stamps[512][16][16];
+#define LNQ_STAMP(e)                                                                                   \
+  do {                                                                                                 \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < 512)                                                   \
+      gemv_stamps[blockIdx.x][threadIdx.x >> 6][e] = __builtin_amdgcn_s_memrealtime();                 \
+  } while (0)
+#else
+#define LNQ_STAMP(e) \
+  do {               \
+  } while (0)
+#endif
+
 namespace gemv {
 constexpr int MAX_WAVES = 16;  // K <= 4096
 constexpr int MAX_U8 = 8;      // R <= 64 rows per workgroup
@@ -99,6 +119,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t Xsm[gemv::MAX_WAVES][256];
   __shared__ float Rsm[gemv::MAX_WAVES][R];  // wave-major: consecutive lanes, consecutive dwords
 
+  LNQ_STAMP(0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
@@ -139,12 +160,14 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     ov1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
+  LNQ_STAMP(1);
   // Every wave's small loads enter the CU's memory pipeline before any weight
   // load: without this barrier the waves that reach their first load last find
   // it queued behind the other waves' weights (~100 KB), their x and scales land
   // late and their tiles are all multiplied after the stream has ended.
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
+  LNQ_STAMP(2);
   // Load u: rows n0 + 8u + (lane & 7) at 16-byte piece sigma of the wave's 128
   // bytes; sigma = 2 (lane / 16) + ((lane / 8) % 2 ^ u % 2) puts piece sigma of
   // row r at LDS slot 16 (sigma / 2) + 8 (sigma % 2 ^ u % 2) + r.
@@ -163,10 +186,12 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
 #pragma unroll
   for (int u = 0; u < PRE; ++u) load_weights(u);
   __builtin_amdgcn_sched_barrier(0);
+  LNQ_STAMP(3);
 
   // ---- x: wait for it (and the scales), stage it in pair order, sums of both halves.
   wait_vm<PRE>();
   __builtin_amdgcn_sched_barrier(0);
+  LNQ_STAMP(4);
   if constexpr (ORD) {
     // The workgroup's x in input order (Xsm holds exactly K values), then each
     // lane's 8 taken inputs; the second barrier keeps Xsm until all have read it.
@@ -264,6 +289,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const float c1 = chain(xa[1], w1, 0);
     const float acc = fmaf(fs0[T], fmaf(fz0[T], xs0, c0), fs1[T] * fmaf(fz1[T], xs1, c1));
     if (lane < 16) Rsm[wave][16 * T + lane] = acc;
+    LNQ_STAMP(5 + T);
   }
   if constexpr (HALF) {
     __builtin_amdgcn_sched_barrier(0);
@@ -279,8 +305,11 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const float part = H == 0 ? fs0[NF] * fmaf(fz0[NF], xs0, c) : fs1[NF] * fmaf(fz1[NF], xs1, c);
     const float acc = part + __shfl_xor(part, 8, 64);
     if (lane < 8) Rsm[wave][16 * NF + lane] = acc;
+    LNQ_STAMP(9);
   }
+  LNQ_STAMP(10);
   __syncthreads();
+  LNQ_STAMP(11);
   // Four lanes per output row, each adding a quarter of the waves, then two
   // exchanges (a fixed order: the result does not depend on timing). A group of
   // four lanes is always active or inactive together.
@@ -301,6 +330,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
       y[n] = out;
     }
   }
+  LNQ_STAMP(12);
 }
 
 // One token, K > 4096 (the down projection's 14336): the one-token kernel with
@@ -954,3 +984,14 @@ LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* sca
 }
 
 }  // namespace lnq
+
+#ifdef LNQ_GEMV_TIMELINE
+// The last launch's timestamps, [512 workgroups][16 waves][16 points] of u64.
+extern "C" LNQ_API LnqStatus lnq_gemv_timeline_read(unsigned long long* host) {
+  LNQ_REQUIRE(host != nullptr, "lnq_gemv_timeline_read: null pointer");
+  LNQ_HIP_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(lnq::gemv_stamps), sizeof(lnq::gemv_stamps), 0,
+                                    hipMemcpyDeviceToHost));
+  lnq::clear_error();
+  return LNQ_OK;
+}
+#endif

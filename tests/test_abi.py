@@ -208,3 +208,21 @@ def test_plan_queries_name_the_kernel_without_a_device() -> None:
     assert kernels.mm8_plan(256, 28672, 8192) == 128
     with pytest.raises(LinnetError, match="tile_n"):
         _lib.call("lnq_mm8_tiles", *[ctypes.c_void_p(256)] * 5, 4, 256, 128, 1, _lib.BF16, 64, None)
+
+
+def test_timeline_library_exports_the_stamp_reader() -> None:
+    """The diagnostic build (one-token GEMV with per-wave timestamps) links the
+    same entry points plus `lnq_gemv_timeline_read`; the product library has no
+    stamps."""
+    from linnet_amd import _build
+
+    stamped = ctypes.CDLL(str(_build.TIMELINE))
+    assert hasattr(stamped, "lnq_gemv_timeline_read") and hasattr(stamped, "lnq_int4_linear")
+    assert not hasattr(_lib.load(), "lnq_gemv_timeline_read")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the answer without a GPU")
+def test_timeline_needs_a_gpu() -> None:
+    from linnet_amd import timeline
+
+    assert timeline.main([]) == 2
