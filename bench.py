@@ -334,7 +334,8 @@ def eight_bit(torch, dev, timed_graph, steps: int) -> dict[str, object]:
 
 
 def llama_decode(torch, kernels, dev) -> dict[str, object]:
-    """Config 5: one decode step of the int4 Llama-3.1-8B-shaped stack at a
+    """Config 5: the 1024-token prompt's prefill (time to first token) and one
+    decode step of the int4 Llama-3.1-8B-shaped stack at a
     1024-token context, captured as one HIP graph and replayed; tokens/s =
     batch / step time. Batch 1 runs every linear on the one-token GEMV
     kernels, batch 32 on the few-token GEMV (gate, up) and the skinny kernel;
@@ -347,6 +348,28 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
     from linnet_amd.llama import Int4Llama
 
     model = Int4Llama(torch, kernels, dev)
+    # The 1024-token prompt (batch 1): `prefill` runs every projection at 1024 rows
+    # on the tiled GEMM, causal attention over the prompt, the head on the last row.
+    # Time to first token = the prefill's time on the GPU (eager, inputs resident).
+    prompt = (torch.randn(1024, 4096, device=dev) * 0.5).to(torch.bfloat16)
+    model.prefill(prompt)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ttft = []
+    for _ in range(5):
+        start.record()
+        first = model.prefill(prompt)
+        end.record()
+        torch.cuda.synchronize()
+        ttft.append(start.elapsed_time(end))
+    ttft_ms = sorted(ttft)[len(ttft) // 2]
+    linear_params = sum(p[name][0].numel() * 2 for p in model.layers for name in ("qkv", "o", "gate_up", "down"))
+    out["prefill_1024"] = {"ttft_ms": round(ttft_ms, 3), "tokens_per_s": round(1024e3 / ttft_ms, 1),
+                           "linear_tflops": round(2 * linear_params * 1024 / ttft_ms / 1e9, 1),
+                           "attention": "torch fused" if model._flash else "torch f32 math",
+                           "finite": bool(torch.isfinite(first).all().item())}
+    model.set_position(1024)
+    del prompt, first
     for batch in (1, 32):
         if batch != 1:
             model.kt = [t[:1].expand(batch, -1, -1, -1).contiguous() for t in model.kt]
@@ -361,7 +384,6 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         graph.replay()
         torch.cuda.synchronize()
         reps = 20
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(reps):
             graph.replay()

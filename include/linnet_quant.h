@@ -380,6 +380,22 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
                                        int64_t pos, int64_t q_stride,
                                        int64_t kv_stride, void* stream);
 
+/* lnq_decode_attention with the position in device memory (`pos`: one int32), so
+ * that a step recorded into a graph moves along the cache on each replay when the
+ * graph also advances the position. cos_table / sin_table are f32 [cap, head_dim/2]
+ * (row p: cos / sin of p times the rotary frequencies), read at row pos; the
+ * workspace is sized for position cap - 1 and the grid covers the whole cache
+ * (chunks past pos return at once). A position outside [0, cap) writes nothing to
+ * the caches and zeros to `out`.
+ * Replaces: the rotary-position bookkeeping of the generated decode step
+ * (python/linnet/src/linnet/torch/compiled.py:430-503), which passes the position
+ * from the host on every call. */
+LNQ_API LnqStatus lnq_decode_attention_at(const void* q, const void* k, const void* v, const float* cos_table,
+                                          const float* sin_table, void* kt_cache, void* v_cache, void* out,
+                                          float* workspace, int64_t workspace_floats, int64_t rows, int64_t heads,
+                                          int64_t kv_heads, int64_t head_dim, int64_t cap, const int32_t* pos,
+                                          int64_t q_stride, int64_t kv_stride, void* stream);
+
 /* Floats of lnq_decode_attention's workspace: rows * kv_heads * ceil((pos + 1) / 64)
  * * 8 * (head_dim + 2). */
 LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim,

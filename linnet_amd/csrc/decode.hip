@@ -190,7 +190,7 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const float* __restrict__ cosv, const float* __restrict__ sinv, uint16_t* __restrict__ kt,
     uint16_t* __restrict__ vc, float* __restrict__ work, int heads, int kv_heads, int cap, int pos, int chunks,
-    int64_t q_stride, int64_t kv_stride) {
+    int64_t q_stride, int64_t kv_stride, const int32_t* __restrict__ pos_dev) {
   constexpr int C = decode::CHUNK;       // 64 positions
   constexpr int DG = 16;                 // dimension groups of the scores
   constexpr int DPG = HD / DG;           // dimensions a score thread takes
@@ -210,6 +210,15 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   const int rk = blockIdx.x / chunks;  // row * kv_heads + kvh
   const int row = rk / kv_heads, kvh = rk % kv_heads;
   const int l0 = c * C;
+  if (pos_dev != nullptr) {
+    // The position in device memory (a captured step advances it on the device):
+    // the grid covers the whole cache, the chunks past pos have nothing to do, and
+    // cos / sin are tables [cap, HD / 2] read at row pos.
+    pos = *pos_dev;
+    if (pos < 0 || pos >= cap || l0 > pos) return;
+    cosv += static_cast<size_t>(pos) * (HD / 2);
+    sinv += static_cast<size_t>(pos) * (HD / 2);
+  }
   const int n = min(C, pos + 1 - l0);  // live positions of this chunk
   const int tid = threadIdx.x;
   constexpr int HALF = HD / 2;
@@ -365,7 +374,8 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
 // out[row, head] = sum_c acc_c exp(m_c - M) / sum_c s_c exp(m_c - M), chunks in order.
 template <int HD>
 __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restrict__ work, uint16_t* __restrict__ out,
-                                                            int heads, int kv_heads, int chunks) {
+                                                            int heads, int kv_heads, int chunks,
+                                                            const int32_t* __restrict__ pos_dev, int cap) {
   // The chunks' (m, s) are read by all threads at once (thread t: chunks t, t +
   // HD, ...), their weights exp(m - M) kept in LDS, and thread d sums its
   // dimension over the chunks in order, eight loads in flight.
@@ -379,6 +389,17 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
   const float* base = work + (static_cast<size_t>(row) * kv_heads + kvh) * chunks * decode::MAX_GROUP * (HD + 2) +
                       g * (HD + 2);
   const size_t stride = static_cast<size_t>(decode::MAX_GROUP) * (HD + 2);
+  // With the position in device memory, the chunks up to pos's (the workspace
+  // keeps the whole cache's chunk stride); a position outside the cache gives zeros.
+  int live = chunks;
+  if (pos_dev != nullptr) {
+    const int p = *pos_dev;
+    live = p >= 0 && p < cap ? p / decode::CHUNK + 1 : 0;
+    if (live == 0) {
+      out[(static_cast<size_t>(row) * heads + head) * HD + d] = 0;
+      return;
+    }
+  }
   auto block_reduce = [&](float v, bool is_max) {
     v = is_max ? wave_max(v) : wave_sum(v);
     __syncthreads();
@@ -390,10 +411,10 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
     return r;
   };
   float m = -INFINITY;
-  for (int c = d; c < chunks; c += HD) m = fmaxf(m, base[c * stride]);
+  for (int c = d; c < live; c += HD) m = fmaxf(m, base[c * stride]);
   const float M = block_reduce(m, true);
   float sp = 0.f;
-  for (int c = d; c < chunks; c += HD) {
+  for (int c = d; c < live; c += HD) {
     const float w = expf(base[c * stride] - M);
     wts[c] = w;
     sp = fmaf(base[c * stride + 1], w, sp);
@@ -401,14 +422,14 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
   const float S = block_reduce(sp, false);  // its barriers also publish wts
   float o = 0.f;
   int c = 0;
-  for (; c + 8 <= chunks; c += 8) {
+  for (; c + 8 <= live; c += 8) {
     float a[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) a[i] = base[(c + i) * stride + 2 + d];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o = fmaf(a[i], wts[c + i], o);
   }
-  for (; c < chunks; ++c) o = fmaf(base[c * stride + 2 + d], wts[c], o);
+  for (; c < live; ++c) o = fmaf(base[c * stride + 2 + d], wts[c], o);
   out[(static_cast<size_t>(row) * heads + head) * HD + d] = f32_to_bf16_bits(o / S);
 }
 
@@ -459,11 +480,13 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
   return launched("rmsnorm");
 }
 
-LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
-                                       const float* sin, void* kt_cache, void* v_cache, void* out, float* workspace,
-                                       int64_t workspace_floats, int64_t rows, int64_t heads, int64_t kv_heads,
-                                       int64_t head_dim, int64_t cap, int64_t pos, int64_t q_stride,
-                                       int64_t kv_stride, void* stream) {
+// pos_dev: nullptr (the position is `pos`) or the device address of the int32
+// position, the grid then sized for position `pos` = cap - 1 (the whole cache).
+static LnqStatus decode_attention(const void* q, const void* k, const void* v, const float* cos, const float* sin,
+                                  void* kt_cache, void* v_cache, void* out, float* workspace,
+                                  int64_t workspace_floats, int64_t rows, int64_t heads, int64_t kv_heads,
+                                  int64_t head_dim, int64_t cap, int64_t pos, int64_t q_stride, int64_t kv_stride,
+                                  const int32_t* pos_dev, void* stream) {
   LNQ_REQUIRE(head_dim == 64 || head_dim == 128, "lnq_decode_attention: head_dim is 64 or 128, not %lld",
               static_cast<long long>(head_dim));
   LNQ_REQUIRE(rows >= 0 && kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= decode::MAX_GROUP,
@@ -493,9 +516,10 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
                      static_cast<const uint16_t*>(v), cos, sin, static_cast<uint16_t*>(kt_cache),                    \
                      static_cast<uint16_t*>(v_cache), workspace,                                                    \
                      static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(cap), static_cast<int>(pos), \
-                     static_cast<int>(chunks), qs_, kvs_);                                                          \
+                     static_cast<int>(chunks), qs_, kvs_, pos_dev);                                                 \
   hipLaunchKernelGGL(decode_combine_kernel<HD_>, grid2, dim3(HD_), 0, s, workspace, static_cast<uint16_t*>(out),   \
-                     static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(chunks))
+                     static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(chunks), pos_dev,         \
+                     static_cast<int>(cap))
 #define LNQ_ATT(HD_)                                      \
   switch (group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8) { \
     case 1: LNQ_ATT_G(HD_, 1); break;                     \
@@ -521,6 +545,26 @@ LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void*
 #undef LNQ_ATT
 #undef LNQ_ATT_G
   return launched("decode_attention");
+}
+
+LNQ_API LnqStatus lnq_decode_attention(const void* q, const void* k, const void* v, const float* cos,
+                                       const float* sin, void* kt_cache, void* v_cache, void* out, float* workspace,
+                                       int64_t workspace_floats, int64_t rows, int64_t heads, int64_t kv_heads,
+                                       int64_t head_dim, int64_t cap, int64_t pos, int64_t q_stride,
+                                       int64_t kv_stride, void* stream) {
+  return decode_attention(q, k, v, cos, sin, kt_cache, v_cache, out, workspace, workspace_floats, rows, heads,
+                          kv_heads, head_dim, cap, pos, q_stride, kv_stride, nullptr, stream);
+}
+
+LNQ_API LnqStatus lnq_decode_attention_at(const void* q, const void* k, const void* v, const float* cos_table,
+                                          const float* sin_table, void* kt_cache, void* v_cache, void* out,
+                                          float* workspace, int64_t workspace_floats, int64_t rows, int64_t heads,
+                                          int64_t kv_heads, int64_t head_dim, int64_t cap, const int32_t* pos,
+                                          int64_t q_stride, int64_t kv_stride, void* stream) {
+  LNQ_REQUIRE(pos != nullptr || rows == 0, "lnq_decode_attention_at: null position");
+  LNQ_REQUIRE(cap > 0, "lnq_decode_attention_at: empty cache");
+  return decode_attention(q, k, v, cos_table, sin_table, kt_cache, v_cache, out, workspace, workspace_floats, rows,
+                          heads, kv_heads, head_dim, cap, cap - 1, q_stride, kv_stride, pos, stream);
 }
 
 LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim, int64_t pos) {

@@ -27,7 +27,7 @@ class Int4Llama:
     SiLU x up); otherwise as torch ops (the reference for the tests)."""
 
     def __init__(self, torch, kernels, dev, layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336,
-                 vocab=128256, ctx=1024, batch=1, seed=0, fused=True):
+                 vocab=128256, ctx=1024, batch=1, seed=0, fused=True, spare=0):
         self.torch, self.kernels, self.fused = torch, kernels, fused
         self.hidden, self.heads, self.kv_heads, self.hd = hidden, heads, kv_heads, hidden // heads
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -43,17 +43,20 @@ class Int4Llama:
                             n1=1 + 0.1 * torch.randn(hidden, generator=g, device=dev),
                             n2=1 + 0.1 * torch.randn(hidden, generator=g, device=dev)) for _ in range(layers)]
         # The decode kernels' step runs q, k and v as one joined projection (their
-        # int4 rows stacked: one launch, one weight stream) and reads q, k and v as
-        # column slices of its output; gate and up likewise.
+        # int4 rows stacked at prepare: one launch, one weight stream) and reads q, k
+        # and v as column slices of its output; gate and up likewise.
+        from linnet_amd.torch import generated
+
         for p in self.layers:
-            p["qkv"] = tuple(torch.cat([p["q"][i], p["k"][i], p["v"][i]], dim=0) for i in range(3))
-            p["gate_up"] = tuple(torch.cat([p["gate"][i], p["up"][i]], dim=0) for i in range(3))
+            p["qkv"], p["qkv_rows"] = generated._int4_join(p["q"], p["k"], p["v"])
+            p["gate_up"], p["gate_up_rows"] = generated._int4_join(p["gate"], p["up"])
         self.norm = 1 + 0.1 * torch.randn(hidden, generator=g, device=dev)
         self.head = lin(vocab, hidden)
         # KV caches, bf16 (the model's dtype), capacity ctx + 1 rounded up to 4: Kt
         # [batch, kv_heads, hd, cap] (transposed), V [batch, kv_heads, cap, hd].
-        # Position ctx is written by the step.
-        cap = (ctx + 4) // 4 * 4
+        # Position ctx is written by the step; `spare` more positions stay free for
+        # steps past it.
+        cap = (ctx + 1 + spare + 3) // 4 * 4
         self.kt = [torch.randn(batch, kv_heads, self.hd, cap, generator=g, device=dev).to(torch.bfloat16)
                    for _ in range(layers)]
         self.vc = [torch.randn(batch, kv_heads, cap, self.hd, generator=g, device=dev).to(torch.bfloat16)
@@ -62,7 +65,23 @@ class Int4Llama:
         inv = 1.0 / (500000.0 ** (torch.arange(0, self.hd, 2, device=dev, dtype=torch.float32) / self.hd))
         ang = ctx * inv
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)
+        # The position in device memory and the rotary tables of every cache
+        # position, for steps whose position lives on the device (`step_at`).
+        from linnet_amd.torch import decode
+
+        self.pos_t = torch.tensor([ctx], dtype=torch.int32, device=dev)
+        self.cos_tab, self.sin_tab = decode.rope_tables(self.hd, cap, 500000.0, dev)
         self.linear = lambda x, w: kernels.int4_linear(x, *w)
+        self._flash = None  # whether PyTorch's fused attention ran (None: not tried)
+
+    def set_position(self, pos):
+        """Moves the next step to cache position `pos` (host and device copies)."""
+        torch = self.torch
+        self.pos = pos
+        inv = 1.0 / (500000.0 ** (torch.arange(0, self.hd, 2, device=self.pos_t.device, dtype=torch.float32) / self.hd))
+        ang = pos * inv
+        self.cos, self.sin = torch.cos(ang), torch.sin(ang)
+        self.pos_t.fill_(pos)
 
     def _rms(self, x, w):
         torch = self.torch
@@ -106,31 +125,113 @@ class Int4Llama:
     def head_torch(self, x, linear=None):
         return (linear or self.linear)(self._rms(x, self.norm), self.head)
 
-    def layer_fused(self, i, x, delta, parts=None):
+    def layer_fused(self, i, x, delta, parts=None, device_pos=False):
         """Layer i on the decode kernels and the joined int4 projections. `x` is the
         residual stream, updated in place; `delta` the previous layer's MLP output,
         not yet added (the norm adds it). Returns this layer's MLP output; `parts`,
-        if a dict, receives the attention branch's output too."""
-        from linnet_amd.torch import decode
+        if a dict, receives the attention branch's output too. `device_pos`: the
+        position is read from `pos_t` on the device (with the rotary tables)."""
+        from linnet_amd.torch import decode, generated
 
         p = self.layers[i]
         h = decode.rmsnorm(x, p["n1"], 1e-5, delta)
-        qkv = self.linear(h, p["qkv"])
-        kvd = self.kv_heads * self.hd
-        q, k, v = qkv[:, : self.hidden], qkv[:, self.hidden : self.hidden + kvd], qkv[:, self.hidden + kvd :]
-        att = decode.decode_attention(q, k, v, self.cos, self.sin, self.kt[i], self.vc[i], self.pos)
+        q, k, v = generated._int4_split(self.linear(h, p["qkv"]), p["qkv_rows"])
+        if device_pos:
+            att = decode.decode_attention(q, k, v, self.cos_tab, self.sin_tab, self.kt[i], self.vc[i], self.pos_t)
+        else:
+            att = decode.decode_attention(q, k, v, self.cos, self.sin, self.kt[i], self.vc[i], self.pos)
         o = self.linear(att, p["o"])
         if parts is not None:
             parts["attn"] = o
         h = decode.rmsnorm(x, p["n2"], 1e-5, o)
-        gu = self.linear(h, p["gate_up"])
-        ffn = gu.shape[1] // 2
-        return self.linear(decode.silu_mul(gu[:, :ffn], gu[:, ffn:]), p["down"])
+        g, u = generated._int4_split(self.linear(h, p["gate_up"]), p["gate_up_rows"])
+        return self.linear(decode.silu_mul(g, u), p["down"])
 
     def head_fused(self, x, delta):
         from linnet_amd.torch import decode
 
         return self.linear(decode.rmsnorm(x, self.norm, 1e-5, delta), self.head)
+
+    def _attend_prompt(self, q, k, v):
+        """Causal grouped-query attention of a prompt, q [P, heads, hd], k and v
+        [P, kv_heads, hd] (bf16, rotated): PyTorch's fused attention (flash on this
+        GPU when present), otherwise the same math in f32. Returns [P, heads*hd] bf16."""
+        torch = self.torch
+        fn = torch.nn.functional.scaled_dot_product_attention
+        qh, kh, vh = (t.transpose(0, 1).unsqueeze(0).contiguous() for t in (q, k, v))  # [1, H, P, hd]
+        if self._flash is not False:
+            try:
+                from torch.nn.attention import SDPBackend, sdpa_kernel
+
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    att = fn(qh, kh, vh, is_causal=True, enable_gqa=True)
+                self._flash = True
+                return att[0].transpose(0, 1).reshape(q.shape[0], -1)
+            except RuntimeError:
+                self._flash = False
+        grp = self.heads // self.kv_heads
+        kf = kh.float().repeat_interleave(grp, dim=1)
+        vf = vh.float().repeat_interleave(grp, dim=1)
+        att = fn(qh.float(), kf, vf, is_causal=True)
+        return att[0].transpose(0, 1).reshape(q.shape[0], -1).to(torch.bfloat16)
+
+    def prefill_layer(self, i, x, delta):
+        """Layer i of a prompt (batch 1) on the residual stream x [P, hidden] (bf16,
+        updated in place; `delta`, the previous layer's MLP output, is added first):
+        the joined int4 projections at P rows, the rotary embedding at positions
+        0..P-1 from the tables, k and v written into cache positions 0..P-1 (k
+        rounded to bf16, as the decode step stores it), causal attention over the
+        prompt. Returns (attention output, MLP output); the latter is not added."""
+        from linnet_amd.torch import decode, generated
+
+        torch = self.torch
+        prompt = x.shape[0]
+        p = self.layers[i]
+        cos, sin = self.cos_tab[:prompt, None, :], self.sin_tab[:prompt, None, :]
+        half = self.hd // 2
+
+        def rope(t):  # [P, H, hd] -> f32
+            t = t.float()
+            a, b = t[..., :half], t[..., half:]
+            return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1)
+
+        h = decode.rmsnorm(x, p["n1"], 1e-5, delta)
+        q, k, v = generated._int4_split(self.linear(h, p["qkv"]), p["qkv_rows"])
+        q = rope(q.reshape(prompt, self.heads, self.hd)).to(torch.bfloat16)
+        k = rope(k.reshape(prompt, self.kv_heads, self.hd)).to(torch.bfloat16)
+        v = v.reshape(prompt, self.kv_heads, self.hd)
+        self.kt[i][0, :, :, :prompt] = k.permute(1, 2, 0)
+        self.vc[i][0, :, :prompt, :] = v.permute(1, 0, 2)
+        o = self.linear(self._attend_prompt(q, k, v), p["o"])
+        h = decode.rmsnorm(x, p["n2"], 1e-5, o)
+        g, u = generated._int4_split(self.linear(h, p["gate_up"]), p["gate_up_rows"])
+        return o, self.linear(decode.silu_mul(g, u), p["down"])
+
+    def prefill(self, x):
+        """The prompt x [P, hidden] (bf16, batch 1) through every layer
+        (`prefill_layer`), then the lm_head on the last row only; moves the next
+        step to position P. Returns the last row's logits [1, vocab]."""
+        if self.kt[0].shape[0] != 1 or x.shape[0] > self.kt[0].shape[-1]:
+            raise ValueError("prefill takes one sequence that fits the cache")
+        x = x.clone()  # the residual stream is updated in place
+        delta = None
+        for i in range(len(self.layers)):
+            _, delta = self.prefill_layer(i, x, delta)
+        logits = self.head_fused(x[-1:].contiguous(), delta[-1:].contiguous())
+        self.set_position(x.shape[0])
+        return logits
+
+    def step_at(self, x):
+        """One fused decode step at the position held in `pos_t` on the device,
+        which it then advances by one (a graph recording this step moves along the
+        cache on each replay). Returns the logits."""
+        x = x.clone()
+        delta = None
+        for i in range(len(self.layers)):
+            delta = self.layer_fused(i, x, delta, device_pos=True)
+        logits = self.head_fused(x, delta)
+        self.pos_t.add_(1)
+        return logits
 
     def step(self, x):
         if self.fused:

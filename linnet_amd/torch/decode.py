@@ -38,13 +38,27 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: tor
     return h
 
 
+def rope_tables(head_dim: int, positions: int, theta: float = 500000.0,
+                device: torch.device | str = "cuda") -> tuple[torch.Tensor, torch.Tensor]:
+    """`(cos, sin)` f32 [positions, head_dim/2]: row p holds cos / sin of p times the
+    rotary frequencies theta^(-2i/head_dim) (no frequency scaling), the values
+    `decode_attention` takes at one position, for every position of a cache."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
+    ang = torch.arange(positions, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+    return torch.cos(ang).contiguous(), torch.sin(ang).contiguous()
+
+
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                     kt_cache: torch.Tensor, v_cache: torch.Tensor, pos: int) -> torch.Tensor:
+                     kt_cache: torch.Tensor, v_cache: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
     """One decode step of grouped-query attention for q [rows, heads*hd], k, v
     [rows, kv_heads*hd] (bf16): rotary embedding (cos, sin f32 [hd/2] at `pos`) of
     q and k, k and v written (rounded) into the bf16 caches at `pos` (K transposed:
     kt_cache [rows, kv_heads, hd, cap]; v_cache [rows, kv_heads, cap, hd]), then
-    softmax(q K^T / sqrt(hd)) V over positions 0..pos. Returns [rows, heads*hd] bf16."""
+    softmax(q K^T / sqrt(hd)) V over positions 0..pos. Returns [rows, heads*hd] bf16.
+
+    `pos` may be a one-element int32 tensor on the device instead: the kernels then
+    read it there (a graph replaying the step follows the position as the device
+    advances it), and cos / sin are the whole tables [cap, hd/2] of `rope_tables`."""
     device = _on_gpu("decode_attention", q, k, v, cos, sin, kt_cache, v_cache)
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise LinnetError("decode_attention: q, k and v are bf16")
@@ -62,6 +76,20 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
     short = rows > 1 and (q.stride(0) < q.shape[1] or k.stride(0) < k.shape[1] or v.stride(0) < v.shape[1])
     if short or q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(0) != v.stride(0):
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if isinstance(pos, torch.Tensor):
+        if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != device:
+            raise LinnetError("decode_attention: a device position is one int32 on q's device")
+        if tuple(cos.shape) != (cap, hd // 2) or tuple(sin.shape) != (cap, hd // 2) or cos.dtype != torch.float32 \
+                or sin.dtype != torch.float32:
+            raise LinnetError(f"decode_attention: with a device position cos and sin are f32 [{cap}, {hd // 2}]")
+        out = torch.empty_like(q)
+        floats = _lib.load().lnq_decode_attention_workspace(rows, kvh, hd, cap - 1)
+        work = torch.empty(max(floats, 1), dtype=torch.float32, device=device)
+        with torch.cuda.device(device):
+            _lib.call("lnq_decode_attention_at", _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(kt_cache),
+                      _ptr(v_cache), _ptr(out), _ptr(work), work.numel(), rows, heads, kvh, hd, cap, _ptr(pos),
+                      q.stride(0), k.stride(0), _stream(device))
+        return out
     if cos.numel() != hd // 2 or sin.numel() != hd // 2 or cos.dtype != torch.float32 or sin.dtype != torch.float32:
         raise LinnetError("decode_attention: cos and sin are f32 [hd/2]")
     out = torch.empty_like(q)

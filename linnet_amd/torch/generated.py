@@ -13,7 +13,8 @@ reference's `_int4_pack` falls back (`torch_source.cpp:1501-1504`), and
 `_int4_linear` multiplies it with `F.linear`.
 
 `_int4_row_pack` / `_int4_row_linear` run `std.quant::Int4Linear` (per-row
-signed int4) on the same kernels.
+signed int4) on the same kernels; `_int4_join` / `_int4_split` join sibling
+int4 layers that read one input into one launch.
 
 `_mxfp4_experts(x, blocks, scales, experts)` is the helper for
 `std.quant::mxfp4_experts` (`torch_source.cpp:1579-1600`): the chosen experts'
@@ -117,6 +118,39 @@ def _int4_row_linear(x: torch.Tensor, packed: tuple[torch.Tensor, ...], bias: to
     weight = packed[0] if len(packed) == 1 else kernels.int4_weight(*packed)
     y = functional.linear(flat, weight.to(flat.dtype)).reshape(*x.shape[:-1], weight.shape[0])
     return y if bias is None else y + bias
+
+
+def _int4_join(*packs: tuple[torch.Tensor, ...]) -> tuple[tuple[torch.Tensor, ...], tuple[int, ...]]:
+    """Prepare-time join of sibling int4 layers that read one input (q, k and v;
+    gate and up): their `_int4_pack` tuples stacked along the outputs, so that one
+    kernel launch streams every sibling's weight, and each sibling's output count.
+    The int4 form of the reference's joins of sibling `F.linear` and 8-bit layers
+    (`src/backend/torch_source.cpp:77-158`, weights laid out one after another by
+    `_adjacent`). Fused 3-tuples join as one 3-tuple (same group; the joined copy
+    holds the siblings' bytes again, like `_adjacent` where the runtime did not
+    place them together); dequantized 1-tuples as one dequantized weight."""
+    if not packs:
+        raise LinnetError("_int4_join: no layers")
+    kinds = {len(p) for p in packs}
+    if len(kinds) != 1:
+        raise LinnetError("_int4_join: the siblings were prepared differently (fused and dequantized)")
+    rows = tuple(int(p[0].shape[0]) for p in packs)
+    if kinds == {3}:
+        if len({tuple(p[0].shape[1:]) for p in packs}) != 1 or len({p[1].dtype for p in packs}) != 1:
+            raise LinnetError("_int4_join: siblings share In, the group and the scale dtype")
+        return tuple(torch.cat([p[i] for p in packs], dim=0) for i in range(3)), rows
+    if len({p[0].shape[1] for p in packs}) != 1:
+        raise LinnetError("_int4_join: siblings share In")
+    return (torch.cat([p[0] for p in packs], dim=0),), rows
+
+
+def _int4_split(y: torch.Tensor, rows: tuple[int, ...]) -> list[torch.Tensor]:
+    """The siblings' outputs of a joined product (`y[..., a:b]` views, no copy)."""
+    out, start = [], 0
+    for n in rows:
+        out.append(y[..., start : start + n])
+        start += n
+    return out
 
 
 def _mxfp4_experts(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, experts: torch.Tensor) -> torch.Tensor:

@@ -131,6 +131,171 @@ def test_int4_decode_step_replays_as_a_graph(fused: bool) -> None:
         assert torch.equal(again, eager)
 
 
+@pytest.mark.parametrize("batch", [1, 3])
+def test_captured_step_advances_the_position(batch: int) -> None:
+    """A step recorded with the position in device memory (`step_at`) moves one
+    cache position a replay: three replays equal, bit for bit, three eager steps
+    of an identical model at positions 64, 65, 66 (host position, per-position
+    rotary values), each replay with eager work between, and every replay wrote
+    its own k / v cache column."""
+    x = (torch.randn(batch, SMALL["hidden"], generator=torch.Generator().manual_seed(5)) * 0.5).to(torch.bfloat16).to(DEV)
+    live = Int4Llama(torch, kernels, DEV, batch=batch, seed=7, spare=8, **SMALL)
+    twin = Int4Llama(torch, kernels, DEV, batch=batch, seed=7, spare=8, **SMALL)
+    graph = torch.cuda.CUDAGraph()
+    live.step_at(x)  # warm up at 64 (writes column 64, as the first eager step below does)
+    live.set_position(64)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        out = live.step_at(x)
+    torch.cuda.synchronize()
+    assert int(live.pos_t.item()) == 64, "recording a step does not run it"
+    for k in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        twin.set_position(64 + k)
+        want = twin.step(x)
+        torch.cuda.synchronize()
+        assert int(live.pos_t.item()) == 65 + k
+        assert torch.equal(out, want), f"replay {k}"
+        for i in range(SMALL["layers"]):
+            assert torch.equal(live.kt[i][..., 64 + k], twin.kt[i][..., 64 + k])
+            assert torch.equal(live.vc[i][:, :, 64 + k], twin.vc[i][:, :, 64 + k])
+
+
+def test_device_position_outside_the_cache_writes_nothing() -> None:
+    from linnet_amd.torch import decode
+
+    g = torch.Generator(device=DEV).manual_seed(2)
+    rows, heads, kvh, hd, cap = 2, 8, 2, 64, 16
+    q = torch.randn(rows, heads * hd, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(rows, kvh * hd, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(rows, kvh * hd, generator=g, device=DEV).to(torch.bfloat16)
+    kt = torch.randn(rows, kvh, hd, cap, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(rows, kvh, cap, hd, generator=g, device=DEV).to(torch.bfloat16)
+    cos, sin = decode.rope_tables(hd, cap, 500000.0, DEV)
+    kt0, vc0 = kt.clone(), vc.clone()
+    for bad in (cap, -1):
+        out = decode.decode_attention(q, k, v, cos, sin, kt, vc, torch.tensor([bad], dtype=torch.int32, device=DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(kt, kt0) and torch.equal(vc, vc0)
+        assert bool((out == 0).all())
+    # In range, the device position gives the host position's result.
+    pos = 11
+    want_kt, want_vc = kt.clone(), vc.clone()
+    want = decode.decode_attention(q, k, v, cos[pos], sin[pos], want_kt, want_vc, pos)
+    got = decode.decode_attention(q, k, v, cos, sin, kt, vc, torch.tensor([pos], dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(kt, want_kt) and torch.equal(vc, want_vc)
+
+
+def test_prefill_matches_token_by_token_reference_steps() -> None:
+    """A 64-token prompt through `prefill` (the joined int4 projections at 64 rows,
+    causal attention over the prompt) against the same tokens fed one at a time
+    through the torch-glue step whose linears multiply the exactly dequantized f32
+    weight, at positions 0..63 of an identical model: the last token's logits and
+    every layer's k / v cache columns 0..63 agree within 3e-2 of their largest
+    value (two chained layers of bf16 intermediates), and the next step starts at
+    position 64."""
+    prompt = (torch.randn(64, SMALL["hidden"], generator=torch.Generator().manual_seed(9)) * 0.5).to(torch.bfloat16).to(DEV)
+    model = Int4Llama(torch, kernels, DEV, batch=1, seed=4, **SMALL)
+    ref = Int4Llama(torch, kernels, DEV, batch=1, seed=4, fused=False, **SMALL)
+    ref.linear = _exact_linear
+    got = model.prefill(prompt).float()
+    for t in range(64):
+        ref.set_position(t)
+        want = ref.step(prompt[t : t + 1]).float()
+    torch.cuda.synchronize()
+    assert model.pos == 64 and int(model.pos_t.item()) == 64
+    rel, agree = _compare("prefill vs token-by-token reference", got, want)
+    assert rel <= 3e-2
+    for i in range(SMALL["layers"]):
+        for name, a, b in (("k", model.kt[i][..., :64], ref.kt[i][..., :64]), ("v", model.vc[i][:, :, :64], ref.vc[i][:, :, :64])):
+            err = (a.float() - b.float()).abs().max().item()
+            print(f"layer {i} {name} cache max abs err {err:.3e} (max |{name}| {b.float().abs().max().item():.3e})")
+            assert err <= 3e-2 * b.float().abs().max().item()
+
+
+def _prompt_layer_reference(model: Int4Llama, i: int, x: torch.Tensor, linear) -> tuple[torch.Tensor, torch.Tensor]:
+    """Layer i of a prompt as torch ops on the residual x [P, hidden] (bf16): RMSNorm,
+    q / k / v apart through `linear`, the rotary embedding in f32 (angles p * theta^(-2j/hd)
+    computed here), causal grouped-query attention in f32 with each kv head repeated
+    over its query heads, o, the residual add, RMSNorm, SiLU(gate) * up, down.
+    Writes no cache. Returns (attention output, MLP output)."""
+    p, prompt, hd = model.layers[i], x.shape[0], model.hd
+    inv = 1.0 / (500000.0 ** (torch.arange(0, hd, 2, device=DEV, dtype=torch.float32) / hd))
+    ang = torch.arange(prompt, device=DEV, dtype=torch.float32)[:, None, None] * inv
+    cos, sin = torch.cos(ang), torch.sin(ang)
+
+    def rope(t):
+        a, b = t[..., : hd // 2], t[..., hd // 2 :]
+        return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1)
+
+    h = model._rms(x, p["n1"])
+    q = rope(linear(h, p["q"]).float().view(prompt, model.heads, hd)).to(torch.bfloat16).float()
+    k = rope(linear(h, p["k"]).float().view(prompt, model.kv_heads, hd)).to(torch.bfloat16).float()
+    v = linear(h, p["v"]).float().view(prompt, model.kv_heads, hd)
+    grp = model.heads // model.kv_heads
+    qh = q.transpose(0, 1).contiguous()
+    kh = k.transpose(0, 1).repeat_interleave(grp, dim=0).contiguous()
+    vh = v.transpose(0, 1).repeat_interleave(grp, dim=0).contiguous()
+    scores = torch.matmul(qh, kh.transpose(1, 2).contiguous()) * hd ** -0.5  # [heads, P, P]
+    mask = torch.ones(prompt, prompt, dtype=torch.bool, device=DEV).triu(1)
+    att = torch.matmul(torch.softmax(scores.masked_fill(mask, float("-inf")), dim=-1), vh)
+    o = linear(att.transpose(0, 1).reshape(prompt, -1).to(torch.bfloat16), p["o"])
+    h = model._rms(x + o, p["n2"])
+    a = torch.nn.functional.silu(linear(h, p["gate"]).float()) * linear(h, p["up"]).float()
+    return o, linear(a.to(torch.bfloat16), p["down"])
+
+
+def test_full_size_prefill_matches_the_reference_layer_by_layer() -> None:
+    """Config 5's 1024-token prompt, layer by layer: each layer of `prefill` (the
+    joined int4 projections on the tiled GEMM at 1024 rows, PyTorch's fused
+    causal attention) takes the same residual input as the torch-op prompt layer
+    whose linears multiply the exactly dequantized f32 weight, and both branch
+    outputs agree within 1e-2 of their largest value. Then the same prompt fed
+    token by token through 1024 replays of the captured fused decode step
+    (`step_at`) writes layer 0's k / v cache columns 0..1023 within 1e-2 of their
+    largest value of what prefill wrote; the last logits after 32 chained random
+    layers are compared and reported (not bounded: chaotic, as for the step)."""
+    model = Int4Llama(torch, kernels, DEV, batch=1, seed=11)
+    prompt = (torch.randn(1024, 4096, generator=torch.Generator().manual_seed(3)) * 0.5).to(torch.bfloat16).to(DEV)
+    x, worst = prompt.clone(), {"attn": 0.0, "mlp": 0.0}
+    for i in range(len(model.layers)):
+        start = x.clone()
+        o, mlp = model.prefill_layer(i, x, None)
+        want_o, want_mlp = _prompt_layer_reference(model, i, start, _exact_linear)
+        for name, got, want in (("attn", o, want_o), ("mlp", mlp, want_mlp)):
+            rel = (got.float() - want.float()).abs().max().item() / want.float().abs().max().item()
+            worst[name] = max(worst[name], rel)
+            assert rel <= 1e-2, (i, name, rel)
+        x += mlp
+    print(f"attention: {'fused' if model._flash else 'f32 math'}; branch error rel to its max, worst layer: "
+          f"attn {worst['attn']:.3e}, mlp {worst['mlp']:.3e}", flush=True)
+    got = model.prefill(prompt).float()
+    assert model.pos == 1024 and torch.isfinite(got).all()
+    kt0, vc0 = model.kt[0][..., :1024].clone(), model.vc[0][:, :, :1024].clone()
+    model.set_position(0)
+    xin = prompt[:1].clone()
+    model.step_at(xin)
+    model.set_position(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = model.step_at(xin)
+    print("1024 decode steps", flush=True)
+    for t in range(1024):
+        xin.copy_(prompt[t : t + 1])
+        graph.replay()
+    torch.cuda.synchronize()
+    assert int(model.pos_t.item()) == 1024
+    for name, a, b in (("k", kt0, model.kt[0][..., :1024]), ("v", vc0, model.vc[0][:, :, :1024])):
+        err = (a.float() - b.float()).abs().max().item()
+        print(f"layer 0 {name} cache max abs err {err:.3e} (max |{name}| {b.float().abs().max().item():.3e})")
+        assert err <= 1e-2 * b.float().abs().max().item()
+    _compare("prefill vs 1024 decode steps, end to end", got, out.float())
+    del model, graph
+
+
 def test_decode_kernels_match_torch_ops() -> None:
     """Each decode kernel against the torch ops it replaces (f32 math, bf16 in and out)."""
     from linnet_amd.torch import decode
