@@ -104,6 +104,27 @@ LNQ_API LnqStatus lnq_int4_linear_ordered(const void* x, const int32_t* order, c
                                           void* taken, int64_t rows, int64_t in_features, int64_t out_features,
                                           int64_t group, int32_t dtype, int32_t kernel, void* stream);
 
+/* What lnq_int4_linear_prologue multiplies in place of x. */
+#define LNQ_PROLOGUE_RMSNORM 1  /* x * rsqrt(mean(x^2) + eps) * norm_weight, rounded to bf16 */
+#define LNQ_PROLOGUE_SILU_MUL 2 /* silu(x) * u = x / (1 + exp(-x)) * u, rounded to bf16 */
+
+/* lnq_int4_linear of the decode glue ahead of a projection (bf16): RMSNorm of x
+ * (weight norm_weight f32 [in], eps; what lnq_rmsnorm with no delta computes) or
+ * silu(x) * u (u [rows, in], as lnq_silu_mul), then the int4 product, + bias. One row
+ * at group 128 runs one kernel, the prologue folded into the one-token GEMV's staging
+ * of x (operand 16-byte aligned, kernel AUTO or GEMV), with the same bits as the two
+ * kernels; any other call writes the prologue's output to `staged` (rows * in bf16,
+ * 16-byte aligned; may be NULL when fused) and multiplies that. With one row and bias
+ * = the residual stream's row, y = residual + product rounded as a residual add.
+ * Replaces: the ops the generated module runs around a quantized linear in the
+ * decode step -- `torch.rms_norm` (src/backend/torch_source.cpp:686-689) or SiLU
+ * (:670) times up (stdlib/nn/mlp.linnet:22) -- then `_int4_linear` (:1553-1570). */
+LNQ_API LnqStatus lnq_int4_linear_prologue(const void* x, const void* u, const float* norm_weight, float eps,
+                                           int32_t prologue, const uint8_t* packed, const void* scale,
+                                           const uint8_t* zero, const void* bias, void* y, void* staged, int64_t rows,
+                                           int64_t in_features, int64_t out_features, int64_t group, int32_t dtype,
+                                           int32_t kernel, void* stream);
+
 /* The kernel lnq_int4_linear runs for these arguments on the current device, its
  * operands 16-byte aligned: *chosen = LNQ_KERNEL_GEMV, LNQ_KERNEL_SKINNY,
  * LNQ_KERNEL_TILED_128 or LNQ_KERNEL_TILED_256 (GEMV also for 17..64 rows run as

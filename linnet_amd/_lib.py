@@ -22,11 +22,13 @@ ABI_VERSION = 1
 LNQ_OK, LNQ_ERROR, LNQ_UNAVAILABLE = 0, 1, 2
 BF16, F16, F32 = 0, 1, 2
 KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV, KERNEL_TILED_128, KERNEL_TILED_256 = 0, 1, 2, 3, 4, 5
+PROLOGUE_RMSNORM, PROLOGUE_SILU_MUL = 1, 2
 PACKING_GPTQ, PACKING_AWQ = 0, 1
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
+_f32 = ctypes.c_float
 
 # Entry point -> argument types (the return type is always LnqStatus, int32).
 SIGNATURES: dict[str, list[object]] = {
@@ -41,6 +43,7 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_int4_row_prepare": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_take_inputs": [_p, _p, _p, _i64, _i64, _i32, _p],
     "lnq_int4_linear_ordered": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
+    "lnq_int4_linear_prologue": [_p, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
     "lnq_int4_repack": [_p, _p, _p, _i32, _i32, _i64, _i64, _i64, _p, _p, _p],
     "lnq_int8_quantize": [_p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_w8a16": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _i64, _i32, _p],

@@ -288,4 +288,63 @@ __device__ inline float wave_min(float v) {
   return v;
 }
 
+// ------------------------------------------------ decode glue on 8 bf16 values
+// The decode step's glue between linear layers, on one 16-byte chunk (8 bf16
+// values, two a dword, low first), shared by its own kernels (lnq_rmsnorm,
+// lnq_silu_mul) and the one-token GEMV's x staging, which computes the same bits.
+
+__device__ inline void unpack_bf16x8(u32x4 d, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[2 * e] = bf16_bits_to_f32(d[e] & 0xffffu);
+    v[2 * e + 1] = bf16_bits_to_f32(d[e] >> 16);
+  }
+}
+
+// RMSNorm's sum of squares runs in one order wherever it is computed: each
+// chunk's 8 squares in turn (chunk_squares), a butterfly over each 32
+// consecutive chunks held by lanes l..l+31 with lane & 31 = chunk % 32
+// (sum_over_32_lanes; every lane of the 32 gets the same bits), then the
+// 32-chunk group sums one after another in chunk order.
+__device__ inline float chunk_squares(const float (&v)[8]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+  return ss;
+}
+
+__device__ inline float sum_over_32_lanes(float v) {
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// RMSNorm's output for a chunk: v * scale * w rounded to bf16 (w: the chunk's 8
+// f32 weights), scale = rsqrt(sum of squares / hidden + eps).
+__device__ inline u32x4 norm_bf16x8(const float (&v)[8], float scale, f32x4 w0, f32x4 w1) {
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const f32x4& w = e < 2 ? w0 : w1;
+    const uint32_t lo = f32_to_bf16_bits(v[2 * e] * scale * w[(2 * e) & 3]);
+    const uint32_t hi = f32_to_bf16_bits(v[2 * e + 1] * scale * w[(2 * e + 1) & 3]);
+    out[e] = lo | (hi << 16);
+  }
+  return out;
+}
+
+// SiLU(g) * u, in f32, as the MLP computes it: g / (1 + e^-g) * u.
+__device__ inline float silu_times(float g, float u) { return g / (1.f + expf(-g)) * u; }
+
+__device__ inline u32x4 silu_mul_bf16x8(u32x4 g, u32x4 u) {
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t lo = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g[e] & 0xffffu), bf16_bits_to_f32(u[e] & 0xffffu)));
+    const uint32_t hi = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g[e] >> 16), bf16_bits_to_f32(u[e] >> 16)));
+    out[e] = lo | (hi << 16);
+  }
+  return out;
+}
+
 }  // namespace lnq

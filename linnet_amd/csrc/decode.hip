@@ -107,7 +107,7 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_kernel(uint16_t* __re
 }
 
 // The same with the row held in registers: thread t owns 16-byte chunks t,
-// t + 256, ... (CH of them: hidden <= 2048 CH, hidden % 8 == 0), every load of x,
+// t + 256, ... (CH of them, up to 8: hidden <= 2048 CH, hidden % 8 == 0), every load of x,
 // delta and the weight issued before any is used (the scalar loop above waits on
 // each of its 16 loads a thread in turn: 14 us for one 4096-wide row).
 template <int CH>
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
                                                                       const uint16_t* __restrict__ delta,
                                                                       const float* __restrict__ w,
                                                                       uint16_t* __restrict__ h, int hidden, float eps) {
-  __shared__ float red[4];
+  __shared__ float group_ss[CH * decode::THREADS / 32];
   uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * hidden;
   uint16_t* hr = h + static_cast<size_t>(blockIdx.x) * hidden;
   const uint16_t* dr = delta ? delta + static_cast<size_t>(blockIdx.x) * hidden : nullptr;
@@ -133,10 +133,11 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
     }
   }
   float v[CH][8];
-  float ss = 0.f;
+  float ss[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int i = threadIdx.x + c * decode::THREADS;
+    ss[c] = 0.f;
     if (i >= chunks) continue;
     u32x4 out;
 #pragma unroll
@@ -152,12 +153,20 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
       out[e] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
     }
     if (dr) *reinterpret_cast<u32x4*>(xr + 8 * i) = out;
-    // (The sum of squares runs chunk by chunk: another order of additions than
-    // the scalar kernel's, element by element.)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(v[c][e], v[c][e], ss);
+    ss[c] = chunk_squares(v[c]);
   }
-  const float scale = rsqrtf(block_sum(ss, red) / static_cast<float>(hidden) + eps);
+  // The sum of squares in the order the one-token GEMV's norm prologue uses (so
+  // both give the same bits): chunk i = t + 256 c sits in 32-chunk group i / 32 =
+  // t / 32 + 8 c at lane t % 32 of its half wave; chunks past the row add 0.
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const float g = sum_over_32_lanes(ss[c]);
+    if ((threadIdx.x & 31) == 0) group_ss[(threadIdx.x >> 5) + c * (decode::THREADS / 32)] = g;
+  }
+  __syncthreads();
+  float total = 0.f;
+  for (int g = 0; g < (chunks + 31) / 32; ++g) total += group_ss[g];
+  const float scale = rsqrtf(total / static_cast<float>(hidden) + eps);
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int i = threadIdx.x + c * decode::THREADS;
@@ -443,8 +452,7 @@ __global__ __launch_bounds__(decode::THREADS) void silu_mul_kernel(const uint16_
   for (int64_t i = blockIdx.x * static_cast<int64_t>(decode::THREADS) + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * decode::THREADS) {
     const int64_t r = i / width, c = i - r * width;
-    const float gv = bf16_bits_to_f32(g[r * g_stride + c]);
-    a[i] = f32_to_bf16_bits(gv / (1.f + expf(-gv)) * bf16_bits_to_f32(u[r * u_stride + c]));
+    a[i] = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g[r * g_stride + c]), bf16_bits_to_f32(u[r * u_stride + c])));
   }
 }
 
@@ -470,12 +478,13 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
   auto* hs = static_cast<uint16_t*>(h);
   const int H = static_cast<int>(hidden);
   const int ch = (H + 8 * decode::THREADS - 1) / (8 * decode::THREADS);
-  const bool vec = H % 8 == 0 && ch <= 4 && aligned(x, 16) && aligned(h, 16) && aligned(weight, 16) &&
+  const bool vec = H % 8 == 0 && ch <= 8 && aligned(x, 16) && aligned(h, 16) && aligned(weight, 16) &&
                    (delta == nullptr || aligned(delta, 16));
   const dim3 grid(static_cast<unsigned>(rows)), block(decode::THREADS);
   if (vec && ch == 1) hipLaunchKernelGGL(rmsnorm_vec_kernel<1>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
   else if (vec && ch == 2) hipLaunchKernelGGL(rmsnorm_vec_kernel<2>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
-  else if (vec) hipLaunchKernelGGL(rmsnorm_vec_kernel<4>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else if (vec && ch <= 4) hipLaunchKernelGGL(rmsnorm_vec_kernel<4>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else if (vec) hipLaunchKernelGGL(rmsnorm_vec_kernel<8>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
   else hipLaunchKernelGGL(rmsnorm_kernel, grid, block, 0, s, xs, ds, weight, hs, H, eps);
   return launched("rmsnorm");
 }

@@ -614,9 +614,12 @@ bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* p
                         const void* zero);
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                            const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream,
-                           const int32_t* order = nullptr);
+                           const int32_t* order = nullptr, int prologue = 0, const float* norm_weight = nullptr,
+                           const void* u = nullptr, float eps = 0.f);
 bool int4_gemv_takes_order(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
                            const void* zero, const void* order);
+bool int4_gemv_takes_prologue(int M, int N, int K, int G, int dtype, const void* x, const void* packed,
+                              const void* scale, const void* zero, int prologue, const void* operand);
 
 // The argument checks of lnq_int4_linear that do not look at the operands;
 // false (with the message set) when one fails.
@@ -936,6 +939,42 @@ LNQ_API LnqStatus lnq_int4_linear_ordered(const void* x, const int32_t* order, c
               "(the gather is fused only for one row, group 128)", M, K);
   if (lnq_take_inputs(x, order, taken, rows, in_features, dtype, stream) != LNQ_OK) return LNQ_ERROR;
   return lnq_int4_linear(taken, packed, scale, zero, bias, y, rows, in_features, out_features, group, dtype, kernel,
+                         stream);
+}
+
+LNQ_API LnqStatus lnq_int4_linear_prologue(const void* x, const void* u, const float* norm_weight, float eps,
+                                           int32_t prologue, const uint8_t* packed, const void* scale,
+                                           const uint8_t* zero, const void* bias, void* y, void* staged, int64_t rows,
+                                           int64_t in_features, int64_t out_features, int64_t group, int32_t dtype,
+                                           int32_t kernel, void* stream) {
+  LNQ_REQUIRE(prologue == LNQ_PROLOGUE_RMSNORM || prologue == LNQ_PROLOGUE_SILU_MUL,
+              "lnq_int4_linear_prologue: prologue is LNQ_PROLOGUE_RMSNORM or LNQ_PROLOGUE_SILU_MUL");
+  LNQ_REQUIRE(dtype == LNQ_BF16, "lnq_int4_linear_prologue: the prologues compute in bf16");
+  if (!check_int4_linear(rows, in_features, out_features, group, dtype, kernel, "lnq_int4_linear_prologue"))
+    return LNQ_ERROR;
+  LNQ_REQUIRE(x && packed && scale && zero && y, "lnq_int4_linear_prologue: null pointer");
+  LNQ_REQUIRE(prologue == LNQ_PROLOGUE_RMSNORM ? norm_weight != nullptr : u != nullptr,
+              "lnq_int4_linear_prologue: RMSNorm needs norm_weight, SiLU(x) * u needs u");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  const void* operand = prologue == LNQ_PROLOGUE_RMSNORM ? static_cast<const void*>(norm_weight) : u;
+  if ((kernel == LNQ_KERNEL_AUTO || kernel == LNQ_KERNEL_GEMV) &&
+      int4_gemv_takes_prologue(M, N, K, G, dtype, x, packed, scale, zero, prologue, operand))
+    return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, static_cast<hipStream_t>(stream),
+                            nullptr, prologue, norm_weight, u, eps);
+  LNQ_REQUIRE(staged != nullptr && aligned(staged, 16),
+              "lnq_int4_linear_prologue: %d rows x %d inputs need a 16-byte aligned `staged` buffer of as many "
+              "elements (the prologue is fused only for one row, group 128, on the one-token kernels)", M, K);
+  const LnqStatus st =
+      prologue == LNQ_PROLOGUE_RMSNORM
+          ? lnq_rmsnorm(const_cast<void*>(x), nullptr, norm_weight, staged, rows, in_features, eps, stream)
+          : lnq_silu_mul(x, u, staged, rows * in_features, stream);
+  if (st != LNQ_OK) return st;
+  return lnq_int4_linear(staged, packed, scale, zero, bias, y, rows, in_features, out_features, group, dtype, kernel,
                          stream);
 }
 

@@ -37,6 +37,14 @@
 //   they land, the workgroup's x slices sit in LDS in input order, each lane
 //   reads x[order[k]] for its 8 k, and the taken slice continues as x does
 //   above. The gather costs two LDS barriers and no extra HBM round trip.
+// * The decode glue ahead of a projection, folded into the x staging (PRO,
+//   bf16, group 128), so that it costs no launch of its own: RMSNorm (each wave
+//   loads its 256 weights of the norm with its x slice; the squares of its
+//   slice are summed, the waves' sums exchanged through LDS behind one barrier
+//   and added in a fixed order, and the slice is normalised in registers), or
+//   SiLU(g) * u (each wave loads its u slice beside g). Both compute the bits
+//   of lnq_rmsnorm / lnq_silu_mul (the helpers of common.hpp, one order of the
+//   sum of squares), so a fused call equals the two-kernel one exactly.
 #include "common.hpp"
 
 namespace lnq {
@@ -62,6 +70,9 @@ __device__ unsigned long long gemv_stamps[512][16][16];
 #endif
 
 namespace gemv {
+// What x the one-token kernels multiply: x itself; RMSNorm(x) with weights
+// pro.w and pro.eps; SiLU(x) * pro.u. Both prologues round to bf16.
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_SILU = 2 };
 constexpr int MAX_WAVES = 16;  // K <= 4096
 constexpr int MAX_U8 = 8;      // R <= 64 rows per workgroup
 
@@ -73,6 +84,13 @@ constexpr int MAX_U8 = 8;      // R <= 64 rows per workgroup
 constexpr int tile_wave_bytes(int u8, int t) { return 2 * t + 1 < u8 ? 2048 : 1024; }
 constexpr int tile_bytes(int u8, int t) { return 2 * t < u8 ? tile_wave_bytes(u8, t) * MAX_WAVES : 16; }
 }  // namespace gemv
+
+// The prologue's operands (PRO_NORM: w, eps; PRO_SILU: u), by value.
+struct GemvPrologue {
+  const float* w;
+  const uint16_t* u;
+  float eps;
+};
 
 // The tile arrays of a kernel with U8 loads, and tile_lds(T, wave): wave's part
 // of tile T (T a constant after unrolling).
@@ -104,20 +122,22 @@ __device__ inline void widen_pair(uint32_t lo, uint32_t hi, uint32_t mask, uint3
 // Workgroup: NW = K / 256 waves, R = 8 * U8 rows. G128: group 128 (a wave's two
 // halves have consecutive groups, scales loaded as one dword); otherwise G is
 // a multiple of 256 (both halves share one group).
-template <int DT, int U8, bool G128, bool ORD = false>
+template <int DT, int U8, bool G128, bool ORD = false, int PRO = gemv::PRO_NONE>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G,
-    const int32_t* __restrict__ order) {
+    const int32_t* __restrict__ order, GemvPrologue pro) {
   using E = Elem<DT>;
   static_assert(!ORD || G128, "inputs in another order: group 128");
+  static_assert(PRO == gemv::PRO_NONE || (DT == LNQ_BF16 && G128 && !ORD), "prologues: bf16, group 128, no order");
   constexpr int R = 8 * U8;
   constexpr int NF = U8 / 2;            // full 16-row tiles
   constexpr bool HALF = (U8 & 1) != 0;  // a last tile of 8 rows
   LNQ_GEMV_TILE_ARRAYS(U8);
   __shared__ __attribute__((aligned(16))) uint16_t Xsm[gemv::MAX_WAVES][256];
   __shared__ float Rsm[gemv::MAX_WAVES][R];  // wave-major: consecutive lanes, consecutive dwords
+  __shared__ float Nsm[PRO == gemv::PRO_NORM ? gemv::MAX_WAVES : 1];  // each wave's sum of squares
 
   LNQ_STAMP(0);
   const int lane = threadIdx.x & 63;
@@ -158,6 +178,16 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const int ob = (k0 + 8 * (lane & 31)) * 4;
     ov0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob, 0, 0));
     ov1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16, 0, 0));
+  }
+  u32x4 pv0{}, pv1{};  // PRO: the norm's 8 f32 weights of the lane's x, or its 8 values of u
+  if constexpr (PRO == gemv::PRO_NORM) {
+    const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(pro.w, static_cast<uint32_t>(K * 4));
+    const int pb = (k0 + 8 * (lane & 31)) * 4;
+    pv0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pb, 0, 0));
+    pv1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pb + 16, 0, 0));
+  } else if constexpr (PRO == gemv::PRO_SILU) {
+    const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(pro.u, static_cast<uint32_t>(K * 2));
+    pv0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ru, (k0 + 8 * (lane & 31)) * 2, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
   LNQ_STAMP(1);
@@ -205,6 +235,21 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
 #pragma unroll
     for (int u = PRE; u < U8; ++u) load_weights(u);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (PRO == gemv::PRO_NORM) {
+    // The wave's 256 inputs are 32-chunk group `wave` of the row (lanes 32..63
+    // hold lanes 0..31's chunks); the groups' sums are added in order.
+    float v[8];
+    unpack_bf16x8(xv, v);
+    const float g = sum_over_32_lanes(chunk_squares(v));
+    if (lane == 0) Nsm[wave] = g;
+    lds_barrier();
+    float total = 0.f;
+    for (int w = 0; w < nw; ++w) total += Nsm[w];
+    const float rs = rsqrtf(total / static_cast<float>(K) + pro.eps);
+    xv = norm_bf16x8(v, rs, __builtin_bit_cast(f32x4, pv0), __builtin_bit_cast(f32x4, pv1));
+  } else if constexpr (PRO == gemv::PRO_SILU) {
+    xv = silu_mul_bf16x8(xv, pv0);
   }
   if (lane < 32) *reinterpret_cast<u32x4*>(Xw + 8 * lane) = permute_x8(xv);
   float sum = 0.f;
@@ -348,14 +393,15 @@ constexpr int slice_tile_bytes(int u8, int t, int s) {
 }
 }  // namespace gemv
 
-template <int DT, int U8, bool G128, int S, bool ORD = false>
+template <int DT, int U8, bool G128, int S, bool ORD = false, int PRO = gemv::PRO_NONE>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int N, int K, int G,
-    const int32_t* __restrict__ order) {
+    const int32_t* __restrict__ order, GemvPrologue pro) {
   using E = Elem<DT>;
   static_assert(!ORD || G128, "inputs in another order: group 128");
+  static_assert(PRO == gemv::PRO_NONE || (DT == LNQ_BF16 && G128 && !ORD), "prologues: bf16, group 128, no order");
   constexpr int R = 8 * U8;
   constexpr int NF = U8 / 2;
   constexpr bool HALF = (U8 & 1) != 0;
@@ -365,6 +411,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t L1[gemv::slice_tile_bytes(U8, 1, S)];
   __shared__ __attribute__((aligned(16))) uint16_t Xsm[SW][256 * S];
   __shared__ float Rsm[SW][R];
+  __shared__ float Nsm[PRO == gemv::PRO_NORM ? SW * S : 1];  // each slice's sum of squares
   // Tile T's bytes of slice s of wave w (tiles 0 and 1 only: U8 <= 4).
   auto tile_lds = [&](int T, int w, int sl) -> uint8_t* {
     return (T == 0 ? L0 : L1) + (w * S + sl) * gemv::tile_wave_bytes(U8, T);
@@ -415,6 +462,22 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
       ov[sl][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16, 0, 0));
     }
   }
+  u32x4 pv[S][2];  // PRO: each slice's 8 norm weights (f32), or its 8 values of u
+  if constexpr (PRO == gemv::PRO_NORM) {
+    const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(pro.w, static_cast<uint32_t>(K * 4));
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) {
+      const int pb = (kw + 256 * sl + 8 * (lane & 31)) * 4;
+      pv[sl][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pb, 0, 0));
+      pv[sl][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pb + 16, 0, 0));
+    }
+  } else if constexpr (PRO == gemv::PRO_SILU) {
+    const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(pro.u, static_cast<uint32_t>(K * 2));
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl)
+      pv[sl][0] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(ru, (kw + 256 * sl + 8 * (lane & 31)) * 2, 0, 0));
+  }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -460,6 +523,27 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
     __builtin_amdgcn_sched_barrier(0);
     load_weights(PRE, S * U8);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (PRO == gemv::PRO_NORM) {
+    // Slice sl of wave w is 32-chunk group S w + sl of the row; the groups' sums
+    // are added in order.
+    float v[S][8];
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) {
+      unpack_bf16x8(xv[sl], v[sl]);
+      const float g = sum_over_32_lanes(chunk_squares(v[sl]));
+      if (lane == 0) Nsm[wave * S + sl] = g;
+    }
+    lds_barrier();
+    float total = 0.f;
+    for (int g = 0; g < nw * S; ++g) total += Nsm[g];
+    const float rs = rsqrtf(total / static_cast<float>(K) + pro.eps);
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl)
+      xv[sl] = norm_bf16x8(v[sl], rs, __builtin_bit_cast(f32x4, pv[sl][0]), __builtin_bit_cast(f32x4, pv[sl][1]));
+  } else if constexpr (PRO == gemv::PRO_SILU) {
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) xv[sl] = silu_mul_bf16x8(xv[sl], pv[sl][0]);
   }
   float xs0[S], xs1[S];
 #pragma unroll
@@ -862,38 +946,52 @@ bool int4_gemv_takes_order(int M, int N, int K, int G, const void* x, const void
 
 template <int DT, int U8>
 static void launch_gemv_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int N, int K, int G, const int32_t* order,
-                           hipStream_t stream) {
+                           const void* bias, void* y, int N, int K, int G, const int32_t* order, int kind,
+                           GemvPrologue pro, hipStream_t stream) {
   const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / 256));
   const auto* xs = static_cast<const uint16_t*>(x);
   const auto* ss = static_cast<const uint16_t*>(scale);
   const auto* bs = static_cast<const uint16_t*>(bias);
   auto* ys = static_cast<uint16_t*>(y);
+  if constexpr (DT == LNQ_BF16) {
+    if (kind == gemv::PRO_NORM) {
+      hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true, false, gemv::PRO_NORM>), grid, block, 0, stream, xs, packed, ss,
+                         zero, bs, ys, N, K, G, nullptr, pro);
+      return;
+    }
+    if (kind == gemv::PRO_SILU) {
+      hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true, false, gemv::PRO_SILU>), grid, block, 0, stream, xs, packed, ss,
+                         zero, bs, ys, N, K, G, nullptr, pro);
+      return;
+    }
+  }
   if (order != nullptr)
     hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N,
-                       K, G, order);
+                       K, G, order, pro);
   else if (G == 128)
     hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K, G,
-                       nullptr);
+                       nullptr, pro);
   else
     hipLaunchKernelGGL((int4_gemv_kernel<DT, U8, false>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys, N, K,
-                       G, nullptr);
+                       G, nullptr, pro);
 }
 
 template <int DT>
 static void launch_gemv_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                           const void* bias, void* y, int N, int K, int G, const int32_t* order,
-                           hipStream_t stream) {
+                           const void* bias, void* y, int N, int K, int G, const int32_t* order, int kind,
+                           GemvPrologue pro, hipStream_t stream) {
+#define LNQ_GEMV_U8(U_) launch_gemv_u8<DT, U_>(x, packed, scale, zero, bias, y, N, K, G, order, kind, pro, stream)
   switch ((N + 2047) / 2048) {
-    case 1: launch_gemv_u8<DT, 1>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
-    case 2: launch_gemv_u8<DT, 2>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
-    case 3: launch_gemv_u8<DT, 3>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
-    case 4: launch_gemv_u8<DT, 4>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
-    case 5: launch_gemv_u8<DT, 5>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
-    case 6: launch_gemv_u8<DT, 6>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
-    case 7: launch_gemv_u8<DT, 7>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
-    default: launch_gemv_u8<DT, 8>(x, packed, scale, zero, bias, y, N, K, G, order, stream); break;
+    case 1: LNQ_GEMV_U8(1); break;
+    case 2: LNQ_GEMV_U8(2); break;
+    case 3: LNQ_GEMV_U8(3); break;
+    case 4: LNQ_GEMV_U8(4); break;
+    case 5: LNQ_GEMV_U8(5); break;
+    case 6: LNQ_GEMV_U8(6); break;
+    case 7: LNQ_GEMV_U8(7); break;
+    default: LNQ_GEMV_U8(8); break;
   }
+#undef LNQ_GEMV_U8
 }
 
 template <int DT, int U8, int MX>
@@ -929,50 +1027,81 @@ static void launch_rows_dt(const void* x, const uint8_t* packed, const void* sca
 
 template <int DT, int U8, int S>
 static void launch_slices_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                             const void* bias, void* y, int N, int K, int G, const int32_t* order,
-                             hipStream_t stream) {
+                             const void* bias, void* y, int N, int K, int G, const int32_t* order, int kind,
+                             GemvPrologue pro, hipStream_t stream) {
   const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / (256 * S)));
   const auto* xs = static_cast<const uint16_t*>(x);
   const auto* ss = static_cast<const uint16_t*>(scale);
   const auto* bs = static_cast<const uint16_t*>(bias);
   auto* ys = static_cast<uint16_t*>(y);
+  if constexpr (DT == LNQ_BF16) {
+    if (kind == gemv::PRO_NORM) {
+      hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, true, S, false, gemv::PRO_NORM>), grid, block, 0, stream, xs, packed, ss,
+                         zero, bs, ys, N, K, G, nullptr, pro);
+      return;
+    }
+    if (kind == gemv::PRO_SILU) {
+      hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, true, S, false, gemv::PRO_SILU>), grid, block, 0, stream, xs, packed, ss,
+                         zero, bs, ys, N, K, G, nullptr, pro);
+      return;
+    }
+  }
   if (order != nullptr)
     hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, true, S, true>), grid, block, 0, stream, xs, packed, ss, zero,
-                       bs, ys, N, K, G, order);
+                       bs, ys, N, K, G, order, pro);
   else if (G == 128)
     hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, true, S>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
-                       N, K, G, nullptr);
+                       N, K, G, nullptr, pro);
   else
     hipLaunchKernelGGL((int4_gemv_slices_kernel<DT, U8, false, S>), grid, block, 0, stream, xs, packed, ss, zero, bs,
-                       ys, N, K, G, nullptr);
+                       ys, N, K, G, nullptr, pro);
 }
 
 template <int DT>
 static void launch_slices_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
-                             const void* bias, void* y, int N, int K, int G, const int32_t* order,
-                             hipStream_t stream) {
+                             const void* bias, void* y, int N, int K, int G, const int32_t* order, int kind,
+                             GemvPrologue pro, hipStream_t stream) {
   const int sl = gemv_slices(K), u8 = (N + 2047) / 2048;
 #define LNQ_SLICES(S_, U_) \
   if (sl == S_ && u8 == U_)  \
-    return launch_slices_u8<DT, U_, S_>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
+    return launch_slices_u8<DT, U_, S_>(x, packed, scale, zero, bias, y, N, K, G, order, kind, pro, stream);
   LNQ_SLICES(2, 1) LNQ_SLICES(2, 2) LNQ_SLICES(2, 3) LNQ_SLICES(2, 4)
   LNQ_SLICES(3, 1) LNQ_SLICES(3, 2) LNQ_SLICES(4, 1) LNQ_SLICES(4, 2)
 #undef LNQ_SLICES
 }
 
+// Whether the one-token kernels fold a prologue (1 RMSNorm, 2 SiLU(x) * u) into
+// their x staging for this shape: one row, bf16, group 128, the prologue's
+// operand 16-byte aligned.
+bool int4_gemv_takes_prologue(int M, int N, int K, int G, int dtype, const void* x, const void* packed,
+                              const void* scale, const void* zero, int prologue, const void* operand) {
+  return M == 1 && dtype == LNQ_BF16 && G == 128 && (prologue == gemv::PRO_NORM || prologue == gemv::PRO_SILU) &&
+         aligned(operand, 16) && int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
+}
+
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                            const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream,
-                           const int32_t* order) {
+                           const int32_t* order, int prologue, const float* norm_weight, const void* u, float eps) {
   if (order != nullptr && !int4_gemv_takes_order(M, N, K, G, x, packed, scale, zero, order)) {
     set_error("launch_int4_gemv: the one-token kernels take no input order for this shape");
     return LNQ_ERROR;
   }
+  if (prologue != gemv::PRO_NONE &&
+      (order != nullptr ||
+       !int4_gemv_takes_prologue(M, N, K, G, dtype, x, packed, scale, zero, prologue,
+                                 prologue == gemv::PRO_NORM ? static_cast<const void*>(norm_weight) : u))) {
+    set_error("launch_int4_gemv: the one-token kernels fold no such prologue for this shape");
+    return LNQ_ERROR;
+  }
+  const GemvPrologue pro{norm_weight, static_cast<const uint16_t*>(u), eps};
   if (M == 1 && gemv_slices_supports(N, K, G, x, packed, scale, zero)) {
-    if (dtype == LNQ_BF16) launch_slices_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
-    else launch_slices_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
+    if (dtype == LNQ_BF16)
+      launch_slices_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, order, prologue, pro, stream);
+    else launch_slices_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, order, prologue, pro, stream);
   } else if (M == 1) {
-    if (dtype == LNQ_BF16) launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
-    else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, order, stream);
+    if (dtype == LNQ_BF16)
+      launch_gemv_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, N, K, G, order, prologue, pro, stream);
+    else launch_gemv_dt<LNQ_F16>(x, packed, scale, zero, bias, y, N, K, G, order, prologue, pro, stream);
   } else if (M <= 4) {
     if (dtype == LNQ_BF16) launch_rows_dt<LNQ_BF16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
     else launch_rows_dt<LNQ_F16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);

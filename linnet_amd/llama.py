@@ -24,7 +24,9 @@ class Int4Llama:
     reference (dequantized weight and `F.linear`). `fused` runs the glue between
     the linear layers as this package's decode kernels (`torch/decode.py`: norm
     with the residual add, attention with the rotary embedding and cache write,
-    SiLU x up); otherwise as torch ops (the reference for the tests)."""
+    SiLU x up); otherwise as torch ops (the reference for the tests). With
+    `fused` and `fold` (the default), a one-token step folds that glue into the
+    linear layers' own kernels (`layer_folded`), with the same bits."""
 
     def __init__(self, torch, kernels, dev, layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336,
                  vocab=128256, ctx=1024, batch=1, seed=0, fused=True, spare=0):
@@ -72,6 +74,8 @@ class Int4Llama:
         self.pos_t = torch.tensor([ctx], dtype=torch.int32, device=dev)
         self.cos_tab, self.sin_tab = decode.rope_tables(self.hd, cap, 500000.0, dev)
         self.linear = lambda x, w: kernels.int4_linear(x, *w)
+        # One-token steps fold the glue into the linear layers (`layer_folded`).
+        self.fold = True
         self._flash = None  # whether PyTorch's fused attention ran (None: not tried)
 
     def set_position(self, pos):
@@ -147,6 +151,32 @@ class Int4Llama:
         g, u = generated._int4_split(self.linear(h, p["gate_up"]), p["gate_up_rows"])
         return self.linear(decode.silu_mul(g, u), p["down"])
 
+    def layer_folded(self, i, x, parts=None, device_pos=False):
+        """Layer i of a one-token step with the glue folded into the linear layers:
+        the RMSNorms into the staging of x of the q|k|v and gate|up GEMVs, SiLU(gate)
+        * up into the down projection's, each residual add into the epilogue of the
+        o and down GEMVs (the residual row as their bias). Five launches a layer
+        (four linears and the attention's two kernels, less the norm, residual and
+        SiLU kernels); the same bits as `layer_fused`. x: the residual stream [1,
+        hidden] with every earlier branch added; returns the next one (a new tensor)."""
+        from linnet_amd.torch import decode, generated
+
+        kernels, p = self.kernels, self.layers[i]
+        qkv = kernels.int4_linear_rmsnorm(x, p["n1"], 1e-5, *p["qkv"])
+        q, k, v = generated._int4_split(qkv, p["qkv_rows"])
+        if device_pos:
+            att = decode.decode_attention(q, k, v, self.cos_tab, self.sin_tab, self.kt[i], self.vc[i], self.pos_t)
+        else:
+            att = decode.decode_attention(q, k, v, self.cos, self.sin, self.kt[i], self.vc[i], self.pos)
+        x = kernels.int4_linear(att, *p["o"], bias=x[0])
+        if parts is not None:
+            parts["resid"] = x
+        g, u = generated._int4_split(kernels.int4_linear_rmsnorm(x, p["n2"], 1e-5, *p["gate_up"]), p["gate_up_rows"])
+        return kernels.int4_linear_silu_mul(g, u, *p["down"], bias=x[0])
+
+    def head_folded(self, x):
+        return self.kernels.int4_linear_rmsnorm(x, self.norm, 1e-5, *self.head)
+
     def head_fused(self, x, delta):
         from linnet_amd.torch import decode
 
@@ -221,19 +251,31 @@ class Int4Llama:
         self.set_position(x.shape[0])
         return logits
 
+    def _folds(self, x):
+        return self.fused and self.fold and x.shape[0] == 1
+
     def step_at(self, x):
         """One fused decode step at the position held in `pos_t` on the device,
         which it then advances by one (a graph recording this step moves along the
         cache on each replay). Returns the logits."""
-        x = x.clone()
-        delta = None
-        for i in range(len(self.layers)):
-            delta = self.layer_fused(i, x, delta, device_pos=True)
-        logits = self.head_fused(x, delta)
+        if self._folds(x):
+            for i in range(len(self.layers)):
+                x = self.layer_folded(i, x, device_pos=True)
+            logits = self.head_folded(x)
+        else:
+            x = x.clone()
+            delta = None
+            for i in range(len(self.layers)):
+                delta = self.layer_fused(i, x, delta, device_pos=True)
+            logits = self.head_fused(x, delta)
         self.pos_t.add_(1)
         return logits
 
     def step(self, x):
+        if self._folds(x):
+            for i in range(len(self.layers)):
+                x = self.layer_folded(i, x)
+            return self.head_folded(x)
         if self.fused:
             x = x.clone()  # the residual stream is updated in place
             delta = None

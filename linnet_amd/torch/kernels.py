@@ -136,6 +136,66 @@ def int4_linear(
     return y
 
 
+def _prologue_linear(what: str, prologue: int, x: torch.Tensor, operand: torch.Tensor, eps: float,
+                     packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, bias: torch.Tensor | None,
+                     out: torch.Tensor | None) -> torch.Tensor:
+    device = _on_gpu(what, x, operand, packed, scale, zero, bias)
+    if x.dim() != 2 or packed.dim() != 3 or x.dtype != torch.bfloat16:
+        raise LinnetError(f"{what}: x is [rows, In] bf16 and packed [Out, Groups, Group/2]")
+    rows, depth = x.shape
+    width, groups, half = packed.shape
+    if groups * 2 * half != depth or packed.dtype != torch.uint8 or zero.dtype != torch.uint8:
+        raise LinnetError(f"{what}: packed {tuple(packed.shape)} (uint8) does not hold In={depth}")
+    if scale.dtype != torch.bfloat16 or tuple(scale.shape) != (width, groups) or tuple(zero.shape) != (width, groups):
+        raise LinnetError(f"{what}: scale is [{width}, {groups}] bf16 and zero [{width}, {groups}] uint8")
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (width,)):
+        raise LinnetError(f"{what}: bias is [{width}] bf16")
+    x, operand = x.contiguous(), operand.contiguous()
+    packed, scale, zero = packed.contiguous(), scale.contiguous(), zero.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    if out is None:
+        y = torch.empty(rows, width, dtype=x.dtype, device=device)
+    elif tuple(out.shape) != (rows, width) or out.dtype != x.dtype or out.device != device or not out.is_contiguous():
+        raise LinnetError(f"{what}: out is a contiguous [{rows}, {width}] bf16 tensor on {device}")
+    else:
+        y = out
+    # The staging buffer, used where the prologue is not fused (more rows, another
+    # group, an In no one-token kernel takes); one row's is a few KB.
+    staged = torch.empty_like(x)
+    norm = prologue == _lib.PROLOGUE_RMSNORM
+    with torch.cuda.device(device):
+        _lib.call("lnq_int4_linear_prologue", _ptr(x), None if norm else _ptr(operand), _ptr(operand) if norm else None,
+                  float(eps), prologue, _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y), _ptr(staged),
+                  rows, depth, width, 2 * half, _lib.BF16, _lib.KERNEL_AUTO, _stream(device))
+    return y
+
+
+def int4_linear_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, packed: torch.Tensor,
+                        scale: torch.Tensor, zero: torch.Tensor, bias: torch.Tensor | None = None,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """`int4_linear(rmsnorm(x, norm_weight, eps), ...)` (bf16; norm_weight f32 [In]):
+    one row at group 128 in one kernel, the norm folded into the one-token GEMV's
+    staging of x, with the bits of the two calls; more rows normalise first. With
+    one row, `bias` = the residual stream's row gives residual + product (the
+    residual add of the next layer, rounded as it rounds)."""
+    if norm_weight.dtype != torch.float32 or tuple(norm_weight.shape) != (x.shape[-1],):
+        raise LinnetError("int4_linear_rmsnorm: norm_weight is f32 [In]")
+    return _prologue_linear("int4_linear_rmsnorm", _lib.PROLOGUE_RMSNORM, x, norm_weight, eps, packed, scale, zero,
+                            bias, out)
+
+
+def int4_linear_silu_mul(g: torch.Tensor, u: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor,
+                         zero: torch.Tensor, bias: torch.Tensor | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """`int4_linear(silu(g) * u, ...)` (bf16, g and u [rows, In]): the MLP's down
+    projection with SiLU(gate) * up folded into the one-token GEMV's staging of x
+    (one row, group 128; the bits of `decode.silu_mul` then `int4_linear`); more
+    rows compute the product first. `bias` as for `int4_linear_rmsnorm`."""
+    if u.shape != g.shape or u.dtype != torch.bfloat16:
+        raise LinnetError("int4_linear_silu_mul: u is bf16 of g's shape")
+    return _prologue_linear("int4_linear_silu_mul", _lib.PROLOGUE_SILU_MUL, g, u, 0.0, packed, scale, zero, bias, out)
+
+
 def take_inputs(x: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
     """`std.quant::take_inputs` (`stdlib/quant.linnet:142-149`): `x[..., order[k]]`
     over x's last axis, in one HIP gather kernel; `order` is [N] int32 (the

@@ -113,6 +113,15 @@ def test_other_entry_points_validate() -> None:
                                      NULL)[1]
     assert "taken" in _status("lnq_int4_linear_ordered", FAKE, FAKE, FAKE, FAKE, FAKE, NULL, FAKE, NULL, 4, 4096, 4096,
                               128, _lib.BF16, 0, NULL)[1]
+    pro = lambda kind, norm, u, rows, dtype=_lib.BF16, staged=NULL: _status(  # noqa: E731
+        "lnq_int4_linear_prologue", FAKE, u, norm, 1e-5, kind, FAKE, FAKE, FAKE, NULL, FAKE, staged, rows, 4096, 4096,
+        128, dtype, 0, NULL)
+    assert "prologue is" in pro(0, FAKE, NULL, 1)[1]
+    assert "compute in bf16" in pro(_lib.PROLOGUE_RMSNORM, FAKE, NULL, 1, _lib.F16)[1]
+    assert "needs norm_weight" in pro(_lib.PROLOGUE_RMSNORM, NULL, FAKE, 1)[1]
+    assert "needs u" in pro(_lib.PROLOGUE_SILU_MUL, FAKE, NULL, 1)[1]
+    assert "staged" in pro(_lib.PROLOGUE_SILU_MUL, NULL, FAKE, 4)[1]
+    assert pro(_lib.PROLOGUE_RMSNORM, FAKE, NULL, 0)[0] == _lib.LNQ_OK
     assert "bf16, f16 or f32" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, 9, NULL)[1]
     assert "must not be x" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, _lib.BF16, NULL)[1]
     assert "groups of 128" in _status("lnq_fp8_groups", FAKE, FAKE, FAKE, 2, 2, 256, 64, _lib.BF16, NULL)[1]

@@ -131,6 +131,36 @@ def test_int4_decode_step_replays_as_a_graph(fused: bool) -> None:
         assert torch.equal(again, eager)
 
 
+@pytest.mark.parametrize("shape", ["small", "config5"])
+def test_folded_step_equals_the_fused_step(shape: str) -> None:
+    """A one-token step with the glue folded into the linear layers' kernels
+    (`layer_folded`: RMSNorm and SiLU x up in the GEMVs' staging of x, the residual
+    adds in their epilogues) gives the bits of the step on the separate decode
+    kernels, eagerly and through the captured device-position step."""
+    dims = SMALL if shape == "small" else {}
+    model = Int4Llama(torch, kernels, DEV, batch=1, seed=6, spare=4, **dims)
+    hidden = dims.get("hidden", 4096)
+    x = (torch.randn(1, hidden, generator=torch.Generator().manual_seed(8)) * 0.5).to(torch.bfloat16).to(DEV)
+    model.fold = False
+    want = model.step(x)
+    model.fold = True
+    got = model.step(x)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    pos = model.pos
+    model.set_position(pos)
+    model.step_at(x)
+    model.set_position(pos)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = model.step_at(x)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    del model, graph
+
+
 @pytest.mark.parametrize("batch", [1, 3])
 def test_captured_step_advances_the_position(batch: int) -> None:
     """A step recorded with the position in device memory (`step_at`) moves one
@@ -301,9 +331,9 @@ def test_decode_kernels_match_torch_ops() -> None:
     from linnet_amd.torch import decode
 
     g = torch.Generator().manual_seed(5)
-    # hidden: two and four 16-byte chunks a thread (4096, 8192), a partial third
-    # (5120), and the element-wise kernel (1000, not a multiple of 8)
-    for hidden in (4096, 8192, 5120, 1000):
+    # hidden: two, four and seven 16-byte chunks a thread (4096, 8192, 14336), a
+    # partial third (5120), and the element-wise kernel (1000, not a multiple of 8)
+    for hidden in (4096, 8192, 14336, 5120, 1000):
         x = torch.randn(3, hidden, generator=g).to(torch.bfloat16).to(DEV)
         d = torch.randn(3, hidden, generator=g).to(torch.bfloat16).to(DEV)
         w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(DEV)
