@@ -112,10 +112,12 @@ LNQ_API LnqStatus lnq_int4_linear_ordered(const void* x, const int32_t* order, c
  * (weight norm_weight f32 [in], eps; what lnq_rmsnorm with no delta computes) or
  * silu(x) * u (u [rows, in], as lnq_silu_mul), then the int4 product, + bias. One row
  * at group 128 runs one kernel, the prologue folded into the one-token GEMV's staging
- * of x (operand 16-byte aligned, kernel AUTO or GEMV), with the same bits as the two
- * kernels; any other call writes the prologue's output to `staged` (rows * in bf16,
- * 16-byte aligned; may be NULL when fused) and multiplies that. With one row and bias
- * = the residual stream's row, y = residual + product rounded as a residual add.
+ * of x (operand 16-byte aligned, kernel AUTO or GEMV): SiLU with the bits of the two
+ * kernels; RMSNorm as r * (W (x * w)) with r = rsqrt(mean(x^2) + eps) the row's
+ * factor, x * w rounded to bf16 where lnq_rmsnorm rounds x * r * w (so the two
+ * differ by that rounding). Any other call writes the prologue's output to `staged`
+ * (rows * in bf16, 16-byte aligned) and multiplies that. With one row and bias = the
+ * residual stream's row, y = residual + product rounded as a residual add.
  * Replaces: the ops the generated module runs around a quantized linear in the
  * decode step -- `torch.rms_norm` (src/backend/torch_source.cpp:686-689) or SiLU
  * (:670) times up (stdlib/nn/mlp.linnet:22) -- then `_int4_linear` (:1553-1570). */

@@ -291,7 +291,7 @@ __device__ inline float wave_min(float v) {
 // ------------------------------------------------ decode glue on 8 bf16 values
 // The decode step's glue between linear layers, on one 16-byte chunk (8 bf16
 // values, two a dword, low first), shared by its own kernels (lnq_rmsnorm,
-// lnq_silu_mul) and the one-token GEMV's x staging, which computes the same bits.
+// lnq_silu_mul) and the one-token GEMV's x staging.
 
 __device__ inline void unpack_bf16x8(u32x4 d, float (&v)[8]) {
 #pragma unroll
@@ -301,11 +301,12 @@ __device__ inline void unpack_bf16x8(u32x4 d, float (&v)[8]) {
   }
 }
 
-// RMSNorm's sum of squares runs in one order wherever it is computed: each
-// chunk's 8 squares in turn (chunk_squares), a butterfly over each 32
-// consecutive chunks held by lanes l..l+31 with lane & 31 = chunk % 32
-// (sum_over_32_lanes; every lane of the 32 gets the same bits), then the
-// 32-chunk group sums one after another in chunk order.
+// RMSNorm's sum of squares runs in one order wherever it is computed (the row
+// kernel and the GEMV's norm prologue give the same factor): each chunk's 8
+// squares in turn (chunk_squares), a butterfly over each 32 consecutive chunks
+// held by lanes l..l+31 with lane & 31 = chunk % 32 (sum_over_32_lanes; every
+// lane of the 32 gets the same bits), then the 32-chunk group sums one after
+// another in chunk order.
 __device__ inline float chunk_squares(const float (&v)[8]) {
   float ss = 0.f;
 #pragma unroll
@@ -333,16 +334,46 @@ __device__ inline u32x4 norm_bf16x8(const float (&v)[8], float scale, f32x4 w0, 
   return out;
 }
 
-// SiLU(g) * u, in f32, as the MLP computes it: g / (1 + e^-g) * u.
-__device__ inline float silu_times(float g, float u) { return g / (1.f + expf(-g)) * u; }
+// SiLU(g) * u in f32, as the MLP computes it, g / (1 + e^-g) * u, with the
+// hardware's exp2 and reciprocal (v_exp_f32, v_rcp_f32; about 1 ulp each, far
+// below the bf16 rounding of the result): g * rcp(1 + exp2(-g log2 e)) * u. The
+// one-token GEMV evaluates it for every input in every workgroup, where the
+// IEEE divide and the library exp cost ~20 instructions an element.
+__device__ inline float silu_times(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.f + e) * u;
+}
 
-__device__ inline u32x4 silu_mul_bf16x8(u32x4 g, u32x4 u) {
+// SiLU(g) * u of one dword of each (two bf16 values, low first), rounded to bf16.
+__device__ inline uint32_t silu_mul_bf16x2(uint32_t g, uint32_t u) {
+  const uint32_t lo = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g & 0xffffu), bf16_bits_to_f32(u & 0xffffu)));
+  const uint32_t hi = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g >> 16), bf16_bits_to_f32(u >> 16)));
+  return lo | (hi << 16);
+}
+
+// The same for a chunk that lanes l and l + 32 of a wave both hold: each half
+// of the wave computes two of its four dwords (lanes 0..31 dwords 0 and 1,
+// lanes 32..63 dwords 2 and 3) and the halves exchange them, so every lane ends
+// with the whole chunk for half the arithmetic.
+__device__ inline u32x4 silu_mul_bf16x8_halves(u32x4 g, u32x4 u, int lane) {
+  const bool upper = lane >= 32;
+  const uint32_t m0 = silu_mul_bf16x2(upper ? g[2] : g[0], upper ? u[2] : u[0]);
+  const uint32_t m1 = silu_mul_bf16x2(upper ? g[3] : g[1], upper ? u[3] : u[1]);
+  const uint32_t o0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(m0), 32, 64));
+  const uint32_t o1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), 32, 64));
+  return upper ? u32x4{o0, o1, m0, m1} : u32x4{m0, m1, o0, o1};
+}
+
+// x * w rounded to bf16 for a chunk (w: its 8 f32 weights).
+__device__ inline u32x4 scale_bf16x8(u32x4 x, f32x4 w0, f32x4 w1) {
+  float v[8];
+  unpack_bf16x8(x, v);
   u32x4 out;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const uint32_t lo = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g[e] & 0xffffu), bf16_bits_to_f32(u[e] & 0xffffu)));
-    const uint32_t hi = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g[e] >> 16), bf16_bits_to_f32(u[e] >> 16)));
-    out[e] = lo | (hi << 16);
+    const f32x4& w = e < 2 ? w0 : w1;
+    out[e] = static_cast<uint32_t>(f32_to_bf16_bits(v[2 * e] * w[(2 * e) & 3])) |
+             (static_cast<uint32_t>(f32_to_bf16_bits(v[2 * e + 1] * w[(2 * e + 1) & 3])) << 16);
   }
   return out;
 }

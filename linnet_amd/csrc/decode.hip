@@ -171,14 +171,7 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
   for (int c = 0; c < CH; ++c) {
     const int i = threadIdx.x + c * decode::THREADS;
     if (i >= chunks) continue;
-    u32x4 out;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = f32_to_bf16_bits(v[c][2 * e] * scale * wv[c][e >> 1][(2 * e) & 3]);
-      const uint32_t hi = f32_to_bf16_bits(v[c][2 * e + 1] * scale * wv[c][e >> 1][(2 * e + 1) & 3]);
-      out[e] = lo | (hi << 16);
-    }
-    *reinterpret_cast<u32x4*>(hr + 8 * i) = out;
+    *reinterpret_cast<u32x4*>(hr + 8 * i) = norm_bf16x8(v[c], scale, wv[c][0], wv[c][1]);
   }
 }
 

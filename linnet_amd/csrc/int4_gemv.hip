@@ -38,13 +38,16 @@
 //   reads x[order[k]] for its 8 k, and the taken slice continues as x does
 //   above. The gather costs two LDS barriers and no extra HBM round trip.
 // * The decode glue ahead of a projection, folded into the x staging (PRO,
-//   bf16, group 128), so that it costs no launch of its own: RMSNorm (each wave
-//   loads its 256 weights of the norm with its x slice; the squares of its
-//   slice are summed, the waves' sums exchanged through LDS behind one barrier
-//   and added in a fixed order, and the slice is normalised in registers), or
-//   SiLU(g) * u (each wave loads its u slice beside g). Both compute the bits
-//   of lnq_rmsnorm / lnq_silu_mul (the helpers of common.hpp, one order of the
-//   sum of squares), so a fused call equals the two-kernel one exactly.
+//   bf16, group 128), so that it costs no launch of its own. RMSNorm: the
+//   per-row factor r = rsqrt(mean(x^2) + eps) is a scalar of the one row, so
+//   y = r * (W (x * w)): each wave loads its 256 norm weights with its x slice
+//   and stages x * w (rounded to bf16) as x; the squares of its raw slice are
+//   summed after its tiles, the waves' sums meet in LDS at the final barrier
+//   (added in a fixed order) and r scales the output sums. Nothing of the norm
+//   stands between x landing and the first MFMA; the staged values differ from
+//   lnq_rmsnorm's x * r * w rounded to bf16 by that rounding. SiLU(g) * u: each
+//   wave loads its u slice beside g; lanes l and l + 32 hold the same chunk, so
+//   each half computes half of it and they exchange (the bits of lnq_silu_mul).
 #include "common.hpp"
 
 namespace lnq {
@@ -71,7 +74,8 @@ __device__ unsigned long long gemv_stamps[512][16][16];
 
 namespace gemv {
 // What x the one-token kernels multiply: x itself; RMSNorm(x) with weights
-// pro.w and pro.eps; SiLU(x) * pro.u. Both prologues round to bf16.
+// pro.w and pro.eps (x * w staged, the row's factor applied to the sums);
+// SiLU(x) * pro.u rounded to bf16.
 enum { PRO_NONE = 0, PRO_NORM = 1, PRO_SILU = 2 };
 constexpr int MAX_WAVES = 16;  // K <= 4096
 constexpr int MAX_U8 = 8;      // R <= 64 rows per workgroup
@@ -236,20 +240,11 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     for (int u = PRE; u < U8; ++u) load_weights(u);
     __builtin_amdgcn_sched_barrier(0);
   }
+  const u32x4 xraw = xv;  // NORM: the raw slice, its squares summed after the tiles
   if constexpr (PRO == gemv::PRO_NORM) {
-    // The wave's 256 inputs are 32-chunk group `wave` of the row (lanes 32..63
-    // hold lanes 0..31's chunks); the groups' sums are added in order.
-    float v[8];
-    unpack_bf16x8(xv, v);
-    const float g = sum_over_32_lanes(chunk_squares(v));
-    if (lane == 0) Nsm[wave] = g;
-    lds_barrier();
-    float total = 0.f;
-    for (int w = 0; w < nw; ++w) total += Nsm[w];
-    const float rs = rsqrtf(total / static_cast<float>(K) + pro.eps);
-    xv = norm_bf16x8(v, rs, __builtin_bit_cast(f32x4, pv0), __builtin_bit_cast(f32x4, pv1));
+    xv = scale_bf16x8(xv, __builtin_bit_cast(f32x4, pv0), __builtin_bit_cast(f32x4, pv1));
   } else if constexpr (PRO == gemv::PRO_SILU) {
-    xv = silu_mul_bf16x8(xv, pv0);
+    xv = silu_mul_bf16x8_halves(xv, pv0, lane);
   }
   if (lane < 32) *reinterpret_cast<u32x4*>(Xw + 8 * lane) = permute_x8(xv);
   float sum = 0.f;
@@ -352,9 +347,23 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     if (lane < 8) Rsm[wave][16 * NF + lane] = acc;
     LNQ_STAMP(9);
   }
+  if constexpr (PRO == gemv::PRO_NORM) {
+    // The wave's 256 inputs are 32-chunk group `wave` of the row (lanes 32..63
+    // hold lanes 0..31's chunks).
+    float v[8];
+    unpack_bf16x8(xraw, v);
+    const float g = sum_over_32_lanes(chunk_squares(v));
+    if (lane == 0) Nsm[wave] = g;
+  }
   LNQ_STAMP(10);
   __syncthreads();
   LNQ_STAMP(11);
+  float rnorm = 1.f;  // NORM: the row's factor, the groups' sums added in order
+  if constexpr (PRO == gemv::PRO_NORM) {
+    float total = 0.f;
+    for (int w = 0; w < nw; ++w) total += Nsm[w];
+    rnorm = rsqrtf(total / static_cast<float>(K) + pro.eps);
+  }
   // Four lanes per output row, each adding a quarter of the waves, then two
   // exchanges (a fixed order: the result does not depend on timing). A group of
   // four lanes is always active or inactive together.
@@ -368,6 +377,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     }
     v += __shfl_xor(v, 1, 64);
     v += __shfl_xor(v, 2, 64);
+    if constexpr (PRO == gemv::PRO_NORM) v *= rnorm;
     const int n = n0 + r;
     if (part == 0 && n < N) {
       uint16_t out = E::from_f32(v);
@@ -524,26 +534,20 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
     load_weights(PRE, S * U8);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if constexpr (PRO == gemv::PRO_NORM) {
-    // Slice sl of wave w is 32-chunk group S w + sl of the row; the groups' sums
-    // are added in order.
-    float v[S][8];
 #pragma unroll
-    for (int sl = 0; sl < S; ++sl) {
-      unpack_bf16x8(xv[sl], v[sl]);
-      const float g = sum_over_32_lanes(chunk_squares(v[sl]));
+  for (int sl = 0; sl < S; ++sl) {
+    if constexpr (PRO == gemv::PRO_NORM) {
+      // Slice sl of wave w is 32-chunk group S w + sl of the row. (Summed here, not
+      // after the tiles as in the one-token kernel: kept across them, the partial
+      // sums would push this kernel's registers past its budget.)
+      float v[8];
+      unpack_bf16x8(xv[sl], v);
+      const float g = sum_over_32_lanes(chunk_squares(v));
       if (lane == 0) Nsm[wave * S + sl] = g;
+      xv[sl] = scale_bf16x8(xv[sl], __builtin_bit_cast(f32x4, pv[sl][0]), __builtin_bit_cast(f32x4, pv[sl][1]));
+    } else if constexpr (PRO == gemv::PRO_SILU) {
+      xv[sl] = silu_mul_bf16x8_halves(xv[sl], pv[sl][0], lane);
     }
-    lds_barrier();
-    float total = 0.f;
-    for (int g = 0; g < nw * S; ++g) total += Nsm[g];
-    const float rs = rsqrtf(total / static_cast<float>(K) + pro.eps);
-#pragma unroll
-    for (int sl = 0; sl < S; ++sl)
-      xv[sl] = norm_bf16x8(v[sl], rs, __builtin_bit_cast(f32x4, pv[sl][0]), __builtin_bit_cast(f32x4, pv[sl][1]));
-  } else if constexpr (PRO == gemv::PRO_SILU) {
-#pragma unroll
-    for (int sl = 0; sl < S; ++sl) xv[sl] = silu_mul_bf16x8(xv[sl], pv[sl][0]);
   }
   float xs0[S], xs1[S];
 #pragma unroll
@@ -648,6 +652,12 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
     if (lane < 8) Rsm[wave][16 * NF + lane] = acc;
   }
   __syncthreads();
+  float rnorm = 1.f;  // NORM: the row's factor, the groups' sums added in order
+  if constexpr (PRO == gemv::PRO_NORM) {
+    float total = 0.f;
+    for (int g = 0; g < nw * S; ++g) total += Nsm[g];
+    rnorm = rsqrtf(total / static_cast<float>(K) + pro.eps);
+  }
   for (int t = threadIdx.x; t < 4 * R; t += blockDim.x) {
     const int r = t >> 2, part = t & 3;
     float v = 0.f;
@@ -658,6 +668,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
     }
     v += __shfl_xor(v, 1, 64);
     v += __shfl_xor(v, 2, 64);
+    if constexpr (PRO == gemv::PRO_NORM) v *= rnorm;
     const int n = n0 + r;
     if (part == 0 && n < N) {
       uint16_t out = E::from_f32(v);
@@ -1072,11 +1083,14 @@ static void launch_slices_dt(const void* x, const uint8_t* packed, const void* s
 
 // Whether the one-token kernels fold a prologue (1 RMSNorm, 2 SiLU(x) * u) into
 // their x staging for this shape: one row, bf16, group 128, the prologue's
-// operand 16-byte aligned.
+// operand 16-byte aligned, and at most 32768 outputs. Every workgroup repeats
+// the prologue; past two rounds of 64-row workgroups on 256 CUs that costs more
+// than the separate kernel (measured on the lm_head, N = 128256: 64.1 us folded
+// against 60.0 for the norm kernel and the GEMV; N = 28672: 15.4 against 16.7).
 bool int4_gemv_takes_prologue(int M, int N, int K, int G, int dtype, const void* x, const void* packed,
                               const void* scale, const void* zero, int prologue, const void* operand) {
   return M == 1 && dtype == LNQ_BF16 && G == 128 && (prologue == gemv::PRO_NORM || prologue == gemv::PRO_SILU) &&
-         aligned(operand, 16) && int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
+         N <= 32768 && aligned(operand, 16) && int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
 }
 
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,

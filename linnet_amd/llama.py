@@ -26,7 +26,7 @@ class Int4Llama:
     with the residual add, attention with the rotary embedding and cache write,
     SiLU x up); otherwise as torch ops (the reference for the tests). With
     `fused` and `fold` (the default), a one-token step folds that glue into the
-    linear layers' own kernels (`layer_folded`), with the same bits."""
+    linear layers' own kernels (`layer_folded`)."""
 
     def __init__(self, torch, kernels, dev, layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336,
                  vocab=128256, ctx=1024, batch=1, seed=0, fused=True, spare=0):
@@ -155,10 +155,12 @@ class Int4Llama:
         """Layer i of a one-token step with the glue folded into the linear layers:
         the RMSNorms into the staging of x of the q|k|v and gate|up GEMVs, SiLU(gate)
         * up into the down projection's, each residual add into the epilogue of the
-        o and down GEMVs (the residual row as their bias). Five launches a layer
-        (four linears and the attention's two kernels, less the norm, residual and
-        SiLU kernels); the same bits as `layer_fused`. x: the residual stream [1,
-        hidden] with every earlier branch added; returns the next one (a new tensor)."""
+        o and down GEMVs (the residual row as their bias). Six launches a layer
+        (four linears and the attention's two kernels) against nine for
+        `layer_fused`, with its numbers up to the bf16 rounding of the normed
+        activations (the GEMV stages x * w and scales its sums by the row's norm
+        factor). x: the residual stream [1, hidden] with every earlier branch added;
+        returns the next one (a new tensor)."""
         from linnet_amd.torch import decode, generated
 
         kernels, p = self.kernels, self.layers[i]

@@ -174,9 +174,10 @@ def int4_linear_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, 
                         scale: torch.Tensor, zero: torch.Tensor, bias: torch.Tensor | None = None,
                         out: torch.Tensor | None = None) -> torch.Tensor:
     """`int4_linear(rmsnorm(x, norm_weight, eps), ...)` (bf16; norm_weight f32 [In]):
-    one row at group 128 in one kernel, the norm folded into the one-token GEMV's
-    staging of x, with the bits of the two calls; more rows normalise first. With
-    one row, `bias` = the residual stream's row gives residual + product (the
+    one row at group 128 in one kernel, the norm folded into the one-token GEMV as
+    `r * (W (x * w))` (r = rsqrt(mean(x^2) + eps), the row's factor; x * w rounded
+    to bf16 where `decode.rmsnorm` rounds x * r * w); more rows normalise first.
+    With one row, `bias` = the residual stream's row gives residual + product (the
     residual add of the next layer, rounded as it rounds)."""
     if norm_weight.dtype != torch.float32 or tuple(norm_weight.shape) != (x.shape[-1],):
         raise LinnetError("int4_linear_rmsnorm: norm_weight is f32 [In]")
