@@ -77,10 +77,13 @@ def main() -> int:
         """Seconds per call over exactly `steps` calls, cycling through
         `launches`: `warmup` untimed eager calls, then the `steps` calls recorded
         into one HIP graph and replayed untimed until about 20 ms of GPU time
-        have passed, then once between HIP events on the stream the kernels run
-        on (synchronized on both sides). The untimed replays put the GPU at the
-        clock a decode loop runs at: a burst of 20 one-token GEMVs (~0.16 ms)
-        from idle measures the clock's ramp instead (8.2 against 7.3 us a call)."""
+        have passed (the clock a decode loop runs at), then, after a
+        synchronization, one more untimed replay and the timed one between HIP
+        events on the stream the kernels run on, synchronized after. The untimed
+        replay queued ahead keeps the GPU busy while the timed replay is
+        submitted, so the events see the `steps` calls back to back, as in a
+        decode loop, and not the graph's submission from an idle queue (~20 us,
+        1 us a call when 20 calls are timed)."""
         for i in range(max(warmup, len(launches))):
             launches[i % len(launches)]()
         torch.cuda.synchronize()
@@ -98,6 +101,7 @@ def main() -> int:
         for _ in range(min(400, int(20.0 / max(start.elapsed_time(end), 1e-3)))):
             graph.replay()
         torch.cuda.synchronize()
+        graph.replay()
         start.record(stream)
         graph.replay()
         end.record(stream)
