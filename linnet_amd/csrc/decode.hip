@@ -232,26 +232,54 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   uint16_t* vcb = vc + static_cast<size_t>(rk) * cap * HD;
   const bool owner = pos >= l0 && pos < l0 + C;
 
-  // The chunk's keys and values: every load issued first (registers), the
-  // rotary embedding and the scores after. Key thread (dimension group dg,
-  // positions 4 p4 .. 4 p4 + 3); value thread (dimensions 4 d4 .. 4 d4 + 3,
-  // positions pg, pg + PG, ...). Position pos is the new key / value (from LDS).
+  // The new token's inputs first -- q of the G heads and k (pairs i, i + HD/2),
+  // cos / sin at pos, v -- so that the rotary embedding runs while the chunk's
+  // keys and values, loaded next, are in flight (loads retire in issue order).
+  constexpr int RT = ((decode::MAX_GROUP + 1) * HALF + decode::THREADS - 1) / decode::THREADS;
+  // (Every load is unconditional -- an item past the last reads the last one's
+  // inputs again -- so that they all issue together instead of each behind its
+  // own branch and wait.)
+  float ra_in[RT], rb_in[RT], rcos[RT], rsin[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int t = min(tid + r * decode::THREADS, (G + 1) * HALF - 1);
+    const int g = t / HALF, i = t % HALF;
+    const uint16_t* src = g < G ? qr + g * HD : kr;
+    ra_in[r] = bf16_bits_to_f32(src[i]);
+    rb_in[r] = bf16_bits_to_f32(src[i + HALF]);
+    rcos[r] = cosv[i];
+    rsin[r] = sinv[i];
+  }
+  const uint16_t vnew = vr[min(tid, HD - 1)];
+  // (A compiler barrier: the chunk's loads below may not move above these.)
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+
+  // The chunk's keys and values: every load issued before any is used
+  // (registers), the scores after. Key thread (dimension group dg, positions
+  // 4 p4 .. 4 p4 + 3); value thread (dimensions 4 d4 .. 4 d4 + 3, positions pg,
+  // pg + PG, ...). Position pos is the new key / value (from LDS).
   const int p4 = tid & 15, dg = tid >> 4;
   const int lp = l0 + 4 * p4;
   const int d4 = tid % DV, pg = tid / DV;
   constexpr int VJ = C / PG;  // value positions a thread takes
   // (bf16 caches: four values are 8 bytes.)
+  // Buffer loads, unconditional: keys past the cache's end read zeros through the
+  // range check of this (row, KV head)'s block (keys past pos are read and their
+  // scores masked); values from pos on read zeros (the range ends at pos: past it
+  // the cache may hold anything, and 0 * NaN would not vanish).
   u32x2 kreg[DPG], vreg[VJ];
+  const __amdgpu_buffer_rsrc_t rkt = buffer_rsrc(ktb, static_cast<uint32_t>(HD * cap * 2));
+  const __amdgpu_buffer_rsrc_t rvc = buffer_rsrc(vcb, static_cast<uint32_t>(pos * HD * 2));
 #pragma unroll
   for (int dd = 0; dd < DPG; ++dd) {
     const int d = dg * DPG + dd;
-    kreg[dd] = lp < cap ? *reinterpret_cast<const u32x2*>(ktb + static_cast<size_t>(d) * cap + lp) : u32x2{0u, 0u};
+    kreg[dd] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rkt, (d * cap + lp) * 2, 0, 0));
   }
 #pragma unroll
   for (int jj = 0; jj < VJ; ++jj) {
     const int j = pg + jj * PG;
-    vreg[jj] = j < n && l0 + j != pos ? *reinterpret_cast<const u32x2*>(vcb + static_cast<size_t>(l0 + j) * HD + 4 * d4)
-                                      : u32x2{0u, 0u};
+    vreg[jj] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rvc, ((l0 + j) * HD + 4 * d4) * 2, 0, 0));
   }
   auto widen = [](u32x2 w) {
     return make_float4(bf16_bits_to_f32(static_cast<uint16_t>(w.x & 0xffffu)), bf16_bits_to_f32(static_cast<uint16_t>(w.x >> 16)),
@@ -260,11 +288,13 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
 
   // Rotary embedding (pairs i, i + HD/2); the new key and value into LDS, and into
   // the caches by the chunk that holds pos.
-  for (int t = tid; t < (G + 1) * HALF; t += decode::THREADS) {
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    // (Items past the last repeat it: the same values to the same places.)
+    const int t = min(tid + r * decode::THREADS, (G + 1) * HALF - 1);
     const int g = t / HALF, i = t % HALF;
-    const uint16_t* src = g < G ? qr + g * HD : kr;
-    const float a = bf16_bits_to_f32(src[i]), b = bf16_bits_to_f32(src[i + HALF]);
-    const float ra = a * cosv[i] - b * sinv[i], rb = b * cosv[i] + a * sinv[i];
+    const float a = ra_in[r], b = rb_in[r];
+    const float ra = a * rcos[r] - b * rsin[r], rb = b * rcos[r] + a * rsin[r];
     if (g < G) {
       qs[g][i] = ra * scale;
       qs[g][i + HALF] = rb * scale;
@@ -279,9 +309,13 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
       }
     }
   }
-  for (int d = tid; d < HD; d += decode::THREADS) {
-    vn[d] = bf16_bits_to_f32(vr[d]);
-    if (owner) vcb[static_cast<size_t>(pos) * HD + d] = vr[d];
+  // Heads past G (G < G8) hold zeros: the score and value loops below then run
+  // over all G8 heads without a branch (their LDS reads issue together).
+  for (int t = G * HD + tid; t < G8 * HD; t += decode::THREADS) qs[t / HD][t % HD] = 0.f;
+  static_assert(HD <= decode::THREADS, "a thread stores one value of the new token");
+  if (tid < HD) {
+    vn[tid] = bf16_bits_to_f32(vnew);
+    if (owner) vcb[static_cast<size_t>(pos) * HD + tid] = vnew;
   }
   __syncthreads();
 
@@ -302,9 +336,8 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
         if (lp + e == pos) kk[e] = kn[d];
 #pragma unroll
       for (int g = 0; g < G8; ++g)
-        if (g < G)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(qs[g][d], kk[e], acc[g][e]);
+        for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(qs[g][d], kk[e], acc[g][e]);
     }
 #pragma unroll
     for (int g = 0; g < G8; ++g)
@@ -315,8 +348,12 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   // Scores (16 groups added in order); a wave holds one head's 64 positions
   // (C = 64), so its max and its sum of exp(score - max) are wave reductions.
   static_assert(C == 64, "one head's chunk a wave");
-  for (int t = tid; t < G * C; t += decode::THREADS) {
+  for (int t = tid; t < G8 * C; t += decode::THREADS) {
     const int g = t / C, j = t % C;
+    if (g >= G) {  // (wave-uniform: a wave holds one head)
+      p[g][j] = 0.f;
+      continue;
+    }
     float sc = 0.f;
 #pragma unroll
     for (int q = 0; q < DG; ++q) sc += sp[q][g][j];
@@ -340,19 +377,17 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
       for (int e = 0; e < 4; ++e) acc[g][e] = 0.f;
 #pragma unroll
     for (int jj = 0; jj < VJ; ++jj) {
-      const int j = pg + jj * PG;
-      if (j >= n) break;
+      const int j = pg + jj * PG;  // past pos: p is 0 and the value read 0
       const float4 vv =
           l0 + j == pos ? make_float4(vn[4 * d4], vn[4 * d4 + 1], vn[4 * d4 + 2], vn[4 * d4 + 3]) : widen(vreg[jj]);
 #pragma unroll
-      for (int g = 0; g < G8; ++g)
-        if (g < G) {
-          const float pj = p[g][j];
-          acc[g][0] = fmaf(pj, vv.x, acc[g][0]);
-          acc[g][1] = fmaf(pj, vv.y, acc[g][1]);
-          acc[g][2] = fmaf(pj, vv.z, acc[g][2]);
-          acc[g][3] = fmaf(pj, vv.w, acc[g][3]);
-        }
+      for (int g = 0; g < G8; ++g) {
+        const float pj = p[g][j];
+        acc[g][0] = fmaf(pj, vv.x, acc[g][0]);
+        acc[g][1] = fmaf(pj, vv.y, acc[g][1]);
+        acc[g][2] = fmaf(pj, vv.z, acc[g][2]);
+        acc[g][3] = fmaf(pj, vv.w, acc[g][3]);
+      }
     }
 #pragma unroll
     for (int g = 0; g < G8; ++g)
@@ -378,10 +413,13 @@ template <int HD>
 __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restrict__ work, uint16_t* __restrict__ out,
                                                             int heads, int kv_heads, int chunks,
                                                             const int32_t* __restrict__ pos_dev, int cap) {
-  // The chunks' (m, s) are read by all threads at once (thread t: chunks t, t +
-  // HD, ...), their weights exp(m - M) kept in LDS, and thread d sums its
-  // dimension over the chunks in order, eight loads in flight.
+  // One round trip to memory: every load is issued as the kernel starts -- the
+  // chunks' (m, s) (thread t: chunks t, t + HD, ...) and thread d's dimension
+  // of the first PRE chunks' sums -- then the max and the sum of the weights
+  // (block reductions, the weights exp(m - M) kept in LDS), then thread d adds
+  // its dimension over the chunks in order.
   constexpr int WAVES = HD / 64;
+  constexpr int PRE = 32;  // chunks whose sums a thread holds in registers (context 2048)
   __shared__ float wts[decode::MAX_CHUNKS];
   __shared__ float red[WAVES];
   const int G = heads / kv_heads;
@@ -402,6 +440,16 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
       return;
     }
   }
+  // (Loads past the live chunks read the last live chunk again and are unused:
+  // unconditional, so that they issue together.)
+  float a_pre[PRE];
+#pragma unroll
+  for (int i = 0; i < PRE; ++i) a_pre[i] = base[static_cast<size_t>(min(i, live - 1)) * stride + 2 + d];
+  float m_own = -INFINITY, s_own = 0.f;  // thread d's first chunk (d < live)
+  if (d < live) {
+    m_own = base[static_cast<size_t>(d) * stride];
+    s_own = base[static_cast<size_t>(d) * stride + 1];
+  }
   auto block_reduce = [&](float v, bool is_max) {
     v = is_max ? wave_max(v) : wave_sum(v);
     __syncthreads();
@@ -412,26 +460,26 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
     for (int i = 1; i < WAVES; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
     return r;
   };
-  float m = -INFINITY;
-  for (int c = d; c < live; c += HD) m = fmaxf(m, base[c * stride]);
+  float m = m_own;
+  for (int c = d + HD; c < live; c += HD) m = fmaxf(m, base[c * stride]);
   const float M = block_reduce(m, true);
   float sp = 0.f;
-  for (int c = d; c < live; c += HD) {
+  if (d < live) {
+    const float w = expf(m_own - M);
+    wts[d] = w;
+    sp = s_own * w;
+  }
+  for (int c = d + HD; c < live; c += HD) {
     const float w = expf(base[c * stride] - M);
     wts[c] = w;
     sp = fmaf(base[c * stride + 1], w, sp);
   }
   const float S = block_reduce(sp, false);  // its barriers also publish wts
   float o = 0.f;
-  int c = 0;
-  for (; c + 8 <= live; c += 8) {
-    float a[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = base[(c + i) * stride + 2 + d];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o = fmaf(a[i], wts[c + i], o);
-  }
-  for (; c < live; ++c) o = fmaf(base[c * stride + 2 + d], wts[c], o);
+  for (int i = 0; i < PRE; ++i)
+    if (i < live) o = fmaf(a_pre[i], wts[i], o);
+  for (int c = PRE; c < live; ++c) o = fmaf(base[c * stride + 2 + d], wts[c], o);
   out[(static_cast<size_t>(row) * heads + head) * HD + d] = f32_to_bf16_bits(o / S);
 }
 
