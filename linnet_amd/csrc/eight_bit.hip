@@ -225,16 +225,21 @@ __global__ __launch_bounds__(256) void w8_skinny_kernel(
 // of the same 8 rows, so A row 0 takes x at the even pieces and A row 1 at the
 // odd ones, and row r's sum is C[0][r] + C[1][8 + r]. Two loads (rows 0-7 and
 // 8-15) per 128 inputs, each two MFMA 16x16x32 (bytes 0-7 and 8-15 of a piece).
-template <int DT, int FP8>
-__global__ __launch_bounds__(256) void w8_row_kernel(const uint16_t* __restrict__ x,
-                                                     const uint8_t* __restrict__ weight,
-                                                     const float* __restrict__ scale,
-                                                     uint16_t* __restrict__ y, int N, int K, int G,
-                                                     int row_block, int scale_cols) {
+//
+// NW waves split K (4, or 16 for K = 4096: every CU then holds 16 waves of 2
+// steps, their loads all in flight at once, and a wave's steps are multiplied as
+// soon as its own loads land instead of after a quarter of K); D loads in flight
+// per wave.
+template <int DT, int FP8, int NW = 4, int D = 16>
+__global__ __launch_bounds__(64 * NW) void w8_row_kernel(const uint16_t* __restrict__ x,
+                                                         const uint8_t* __restrict__ weight,
+                                                         const float* __restrict__ scale,
+                                                         uint16_t* __restrict__ y, int N, int K, int G,
+                                                         int row_block, int scale_cols) {
   using E = Elem<DT>;
   constexpr float offset = FP8 ? 0.0f : 128.0f;
-  constexpr int D = 16;  // loads in flight per wave (8 steps of 128 inputs)
-  __shared__ float red[4][16];
+  constexpr int THREADS = 64 * NW;
+  __shared__ float red[NW][16];
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
 
   const int lane = threadIdx.x & 63;
@@ -243,7 +248,7 @@ __global__ __launch_bounds__(256) void w8_row_kernel(const uint16_t* __restrict_
   const int j = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int steps = K >> 7;  // 128 inputs a step
-  const int per_wave = steps >> 2;
+  const int per_wave = steps / NW;
   const int sb = wave * per_wave, se = sb + per_wave;
   const int steps_per_group = G >> 7;
 
@@ -271,12 +276,34 @@ __global__ __launch_bounds__(256) void w8_row_kernel(const uint16_t* __restrict_
   auto fetch = [&](int slot, int step) {
     rw[slot] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[slot & 1] + 128 * step));
   };
-  // x first (it lands ahead of the weight loads issued after it), then the ring.
-  for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
-    *reinterpret_cast<u32x4*>(&xl[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
+  // x and the scales of the wave's first group into registers first, then the
+  // ring's weight loads, and only then x into LDS: a store of x right after its
+  // load would hold every weight load back by x's round trip. (Loads retire in
+  // issue order, so x and the scales land ahead of the weights.)
+  constexpr int XR = 8192 / (8 * THREADS);  // x chunks a thread loads (K <= 8192 from registers)
+  u32x4 xr[XR];
 #pragma unroll
-  for (int i = 0; i < D; ++i)
-    if (sb + (i >> 1) < se) fetch(i, sb + (i >> 1));
+  for (int r = 0; r < XR; ++r) {
+    const int i = 8 * (threadIdx.x + THREADS * r);
+    xr[r] = i < K ? *reinterpret_cast<const u32x4*>(&x[i]) : u32x4{0u, 0u, 0u, 0u};
+  }
+  const int g_first = sb / steps_per_group;
+  float s_first[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) s_first[h] = srow[h][g_first];
+  __asm__ volatile("" ::: "memory");
+  // (Unconditional: a wave with fewer than D / 2 steps re-reads its last one,
+  // unused, so that the number of loads in flight is known where x is stored.)
+#pragma unroll
+  for (int i = 0; i < D; ++i) fetch(i, min(sb + (i >> 1), se - 1));
+  __asm__ volatile("" ::: "memory");
+#pragma unroll
+  for (int r = 0; r < XR; ++r) {
+    const int i = 8 * (threadIdx.x + THREADS * r);
+    if (i < K) *reinterpret_cast<u32x4*>(&xl[i]) = xr[r];
+  }
+  for (int i = 8 * (threadIdx.x + THREADS * XR); i < K; i += 8 * THREADS)
+    *reinterpret_cast<u32x4*>(&xl[i]) = *reinterpret_cast<const u32x4*>(&x[i]);
   __syncthreads();
   // A row m (lane m = l % 16): x at piece 2 j + (m & 1); rows 2..15 repeat rows
   // 0 / 1 and their outputs are not used.
@@ -311,7 +338,13 @@ __global__ __launch_bounds__(256) void w8_row_kernel(const uint16_t* __restrict_
         const int g = step / steps_per_group;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const float sc = srow[h][g];
+          float sc = s_first[h];
+          if (g != g_first) {
+            // (The asm keeps this load in its branch: loaded speculatively, the
+            // wait for it would add a round trip to every group's end.)
+            __asm__ volatile("" ::: "memory");
+            sc = srow[h][g];
+          }
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float d = FP8 ? C[h][r] : fmaf(-offset, Cx[r], C[h][r]);
@@ -334,7 +367,9 @@ __global__ __launch_bounds__(256) void w8_row_kernel(const uint16_t* __restrict_
   __syncthreads();
   if (threadIdx.x < 16) {
     const int n = n0 + threadIdx.x;
-    const float v = red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] + red[3][threadIdx.x];
+    float v = red[0][threadIdx.x];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[w][threadIdx.x];
     if (n < N) y[n] = E::from_f32(v);
   }
 }
@@ -515,7 +550,10 @@ static void launch_w8_skinny(const void* x, const uint8_t* w, const float* s, vo
                              int N, int K, int G, int rb, int cols, hipStream_t stream) {
   const auto* xs = static_cast<const uint16_t*>(x);
   auto* ys = static_cast<uint16_t*>(y);
-  if (M == 1 && K <= 32768 && K % 512 == 0 && G % 128 == 0)
+  if (M == 1 && K == 4096 && G % 128 == 0)
+    hipLaunchKernelGGL((w8_row_kernel<DT, FP8, 16, 4>), dim3((N + 15) / 16), dim3(1024), K * 2, stream, xs, w, s, ys, N,
+                       K, G, rb, cols);
+  else if (M == 1 && K <= 32768 && K % 512 == 0 && G % 128 == 0)
     hipLaunchKernelGGL((w8_row_kernel<DT, FP8>), dim3((N + 15) / 16), dim3(256), K * 2, stream, xs, w, s, ys, N, K, G,
                        rb, cols);
   else if (M == 1 && K <= 32768)
