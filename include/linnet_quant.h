@@ -444,6 +444,23 @@ LNQ_API LnqStatus lnq_decode_attention_noalloc(const void* q, const void* k, con
                                                int64_t pos, int64_t q_stride, int64_t kv_stride,
                                                void* stream);
 
+/* A prompt's rotary embedding and cache writes (bf16): for positions 0..positions-1,
+ * q [positions, heads*head_dim], k and v [positions, kv_heads*head_dim] (rows
+ * in_stride elements apart: column slices of a joined q|k|v output); q and k
+ * rotated in f32 (pairs i, i + head_dim/2, cos / sin tables f32 [cap, head_dim/2]
+ * read at each position) and rounded to bf16; q_out [heads, positions, head_dim],
+ * k_out and v_out [kv_heads, positions, head_dim]; k also into kt_cache [kv_heads,
+ * head_dim, cap] (transposed) and v into v_cache [kv_heads, cap, head_dim] at
+ * positions 0..positions-1. One sequence (one row of the caches).
+ * Replaces: the rotary embedding (examples/01-llama/src/rope.linnet:11), the
+ * head split and the cache writes of the decoder card's prompt attention
+ * (examples/01-llama/src/attention.linnet:35-56, 114-119), which the generated
+ * module runs as framework ops. */
+LNQ_API LnqStatus lnq_prefill_rope(const void* q, const void* k, const void* v, int64_t in_stride,
+                                   const float* cos_table, const float* sin_table, void* q_out, void* k_out,
+                                   void* v_out, void* kt_cache, void* v_cache, int64_t positions, int64_t heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t cap, void* stream);
+
 /* a = silu(g) * u = g / (1 + exp(-g)) * u for n bf16 elements, f32 math. */
 LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n, void* stream);
 

@@ -59,6 +59,7 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_decode_attention": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "lnq_decode_attention_at": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p],
     "lnq_decode_attention_noalloc": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "lnq_prefill_rope": [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "lnq_silu_mul": [_p, _p, _p, _i64, _p],
     "lnq_silu_mul_rows": [_p, _p, _p, _i64, _i64, _i64, _i64, _p],
 }

@@ -483,6 +483,73 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
   out[(static_cast<size_t>(row) * heads + head) * HD + d] = f32_to_bf16_bits(o / S);
 }
 
+// A prompt's rotary embedding and cache writes, one kernel for what the torch
+// glue does in ~15: workgroup (head slot hs, 64-position tile). Slots 0..heads-1
+// are q heads, then the kv_heads k heads, then the v heads. A tile of 64
+// positions x HD values moves through LDS (coalesced loads along each
+// position's HD values); q and k are rotated in f32 (pairs i, i + HD/2, cos / sin
+// tables [cap, HD/2] at each position) and rounded to bf16, as the decode kernel
+// and the torch reference round them; q, k and v go out head-major [head, P, HD]
+// (the fused attention's layout), k also transposed into Kt [kv_heads, HD, cap]
+// and v into V [kv_heads, cap, HD] at positions 0..P-1.
+template <int HD>
+__global__ __launch_bounds__(decode::THREADS) void prefill_rope_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t in_stride,
+    const float* __restrict__ cosv, const float* __restrict__ sinv, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out, uint16_t* __restrict__ kt, uint16_t* __restrict__ vc,
+    int P, int heads, int kv_heads, int cap) {
+  constexpr int C = 64;                  // positions a tile
+  constexpr int HALF = HD / 2;
+  constexpr int CH = HD / 8;             // 16-byte chunks a position
+  __shared__ uint16_t tile[C][HD + 2];   // (+2: the transposed reads of Kt hit distinct banks)
+  const int hs = blockIdx.y;
+  const int p0 = blockIdx.x * C;
+  const int tid = threadIdx.x;
+  const bool is_q = hs < heads, is_k = !is_q && hs < heads + kv_heads;
+  const int h = is_q ? hs : is_k ? hs - heads : hs - heads - kv_heads;
+  const uint16_t* src = (is_q ? q : is_k ? k : v) + static_cast<size_t>(h) * HD;
+  for (int c = tid; c < C * CH; c += decode::THREADS) {
+    const int pl = c / CH, dc = c % CH;
+    u32x4 val{0u, 0u, 0u, 0u};
+    if (p0 + pl < P) val = *reinterpret_cast<const u32x4*>(src + static_cast<size_t>(p0 + pl) * in_stride + 8 * dc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[pl][8 * dc + 2 * e] = static_cast<uint16_t>(val[e] & 0xffffu);
+      tile[pl][8 * dc + 2 * e + 1] = static_cast<uint16_t>(val[e] >> 16);
+    }
+  }
+  __syncthreads();
+  if (is_q || is_k) {
+    for (int t = tid; t < C * HALF; t += decode::THREADS) {
+      const int pl = t / HALF, i = t % HALF;
+      if (p0 + pl >= P) continue;
+      const float a = bf16_bits_to_f32(tile[pl][i]), b = bf16_bits_to_f32(tile[pl][i + HALF]);
+      const float c = cosv[static_cast<size_t>(p0 + pl) * HALF + i], sn = sinv[static_cast<size_t>(p0 + pl) * HALF + i];
+      tile[pl][i] = f32_to_bf16_bits(a * c - b * sn);
+      tile[pl][i + HALF] = f32_to_bf16_bits(b * c + a * sn);
+    }
+    __syncthreads();
+  }
+  uint16_t* out = (is_q ? q_out : is_k ? k_out : v_out) + static_cast<size_t>(h) * P * HD;
+  for (int c = tid; c < C * HD; c += decode::THREADS) {
+    const int pl = c / HD, d = c % HD;
+    if (p0 + pl < P) out[static_cast<size_t>(p0 + pl) * HD + d] = tile[pl][d];
+  }
+  if (is_k) {
+    uint16_t* ktb = kt + static_cast<size_t>(h) * HD * cap;
+    for (int c = tid; c < HD * C; c += decode::THREADS) {
+      const int d = c / C, pl = c % C;  // consecutive threads: consecutive positions of one dimension
+      if (p0 + pl < P) ktb[static_cast<size_t>(d) * cap + p0 + pl] = tile[pl][d];
+    }
+  } else if (!is_q) {
+    uint16_t* vcb = vc + static_cast<size_t>(h) * cap * HD;
+    for (int c = tid; c < C * HD; c += decode::THREADS) {
+      const int pl = c / HD, d = c % HD;
+      if (p0 + pl < P) vcb[static_cast<size_t>(p0 + pl) * HD + d] = tile[pl][d];
+    }
+  }
+}
+
 __global__ __launch_bounds__(decode::THREADS) void silu_mul_kernel(const uint16_t* __restrict__ g,
                                                                    const uint16_t* __restrict__ u,
                                                                    uint16_t* __restrict__ a, int64_t n, int64_t width,
@@ -648,6 +715,43 @@ LNQ_API LnqStatus lnq_decode_attention_noalloc(const void* q, const void* k, con
   // nothing in `scratch` has to start at zero.
   return lnq_decode_attention(q, k, v, cos, sin, kt_cache, v_cache, out, work, LNQ_DECODE_ATTENTION_SCRATCH_FLOATS,
                               rows, heads, kv_heads, head_dim, cap, pos, q_stride, kv_stride, stream);
+}
+
+LNQ_API LnqStatus lnq_prefill_rope(const void* q, const void* k, const void* v, int64_t in_stride,
+                                   const float* cos_table, const float* sin_table, void* q_out, void* k_out,
+                                   void* v_out, void* kt_cache, void* v_cache, int64_t positions, int64_t heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t cap, void* stream) {
+  LNQ_REQUIRE(head_dim == 64 || head_dim == 128, "lnq_prefill_rope: head_dim is 64 or 128, not %lld",
+              static_cast<long long>(head_dim));
+  LNQ_REQUIRE(positions >= 0 && positions <= cap && cap <= INT32_MAX && heads > 0 && kv_heads > 0 &&
+                  heads % kv_heads == 0 && heads + 2 * kv_heads <= 65535,
+              "lnq_prefill_rope: bad shape (positions <= cap, heads a multiple of kv_heads)");
+  LNQ_REQUIRE(in_stride >= head_dim && in_stride % 8 == 0, "lnq_prefill_rope: in_stride is a multiple of 8 elements");
+  if (positions == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(q && k && v && cos_table && sin_table && q_out && k_out && v_out && kt_cache && v_cache,
+              "lnq_prefill_rope: null pointer");
+  LNQ_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16), "lnq_prefill_rope: q, k and v 16-byte aligned");
+  const dim3 grid(static_cast<unsigned>((positions + 63) / 64), static_cast<unsigned>(heads + 2 * kv_heads));
+  const auto s = static_cast<hipStream_t>(stream);
+  const auto* qs = static_cast<const uint16_t*>(q);
+  const auto* ks = static_cast<const uint16_t*>(k);
+  const auto* vs = static_cast<const uint16_t*>(v);
+  auto* qo = static_cast<uint16_t*>(q_out);
+  auto* ko = static_cast<uint16_t*>(k_out);
+  auto* vo = static_cast<uint16_t*>(v_out);
+  auto* kt = static_cast<uint16_t*>(kt_cache);
+  auto* vc = static_cast<uint16_t*>(v_cache);
+  const int P = static_cast<int>(positions), H = static_cast<int>(heads), KVH = static_cast<int>(kv_heads);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(prefill_rope_kernel<128>, grid, dim3(decode::THREADS), 0, s, qs, ks, vs, in_stride, cos_table,
+                       sin_table, qo, ko, vo, kt, vc, P, H, KVH, static_cast<int>(cap));
+  else
+    hipLaunchKernelGGL(prefill_rope_kernel<64>, grid, dim3(decode::THREADS), 0, s, qs, ks, vs, in_stride, cos_table,
+                       sin_table, qo, ko, vo, kt, vc, P, H, KVH, static_cast<int>(cap));
+  return launched("prefill_rope");
 }
 
 LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n, void* stream) {

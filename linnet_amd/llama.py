@@ -184,13 +184,14 @@ class Int4Llama:
 
         return self.linear(decode.rmsnorm(x, self.norm, 1e-5, delta), self.head)
 
-    def _attend_prompt(self, q, k, v):
-        """Causal grouped-query attention of a prompt, q [P, heads, hd], k and v
-        [P, kv_heads, hd] (bf16, rotated): PyTorch's fused attention (flash on this
-        GPU when present), otherwise the same math in f32. Returns [P, heads*hd] bf16."""
+    def _attend_prompt(self, qh, kh, vh):
+        """Causal grouped-query attention of a prompt, q [1, heads, P, hd], k and v
+        [1, kv_heads, P, hd] (bf16, rotated): PyTorch's fused attention (flash on
+        this GPU when present), otherwise the same math in f32. Returns [P,
+        heads*hd] bf16."""
         torch = self.torch
         fn = torch.nn.functional.scaled_dot_product_attention
-        qh, kh, vh = (t.transpose(0, 1).unsqueeze(0).contiguous() for t in (q, k, v))  # [1, H, P, hd]
+        prompt = qh.shape[2]
         if self._flash is not False:
             try:
                 from torch.nn.attention import SDPBackend, sdpa_kernel
@@ -198,43 +199,30 @@ class Int4Llama:
                 with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                     att = fn(qh, kh, vh, is_causal=True, enable_gqa=True)
                 self._flash = True
-                return att[0].transpose(0, 1).reshape(q.shape[0], -1)
+                return att[0].transpose(0, 1).reshape(prompt, -1)
             except RuntimeError:
                 self._flash = False
         grp = self.heads // self.kv_heads
         kf = kh.float().repeat_interleave(grp, dim=1)
         vf = vh.float().repeat_interleave(grp, dim=1)
         att = fn(qh.float(), kf, vf, is_causal=True)
-        return att[0].transpose(0, 1).reshape(q.shape[0], -1).to(torch.bfloat16)
+        return att[0].transpose(0, 1).reshape(prompt, -1).to(torch.bfloat16)
 
     def prefill_layer(self, i, x, delta):
         """Layer i of a prompt (batch 1) on the residual stream x [P, hidden] (bf16,
         updated in place; `delta`, the previous layer's MLP output, is added first):
         the joined int4 projections at P rows, the rotary embedding at positions
-        0..P-1 from the tables, k and v written into cache positions 0..P-1 (k
-        rounded to bf16, as the decode step stores it), causal attention over the
-        prompt. Returns (attention output, MLP output); the latter is not added."""
+        0..P-1 from the tables and k and v written into cache positions 0..P-1 (one
+        kernel, `decode.prefill_rope`; k rounded to bf16, as the decode step stores
+        it), causal attention over the prompt. Returns (attention output, MLP
+        output); the latter is not added."""
         from linnet_amd.torch import decode, generated
 
-        torch = self.torch
-        prompt = x.shape[0]
         p = self.layers[i]
-        cos, sin = self.cos_tab[:prompt, None, :], self.sin_tab[:prompt, None, :]
-        half = self.hd // 2
-
-        def rope(t):  # [P, H, hd] -> f32
-            t = t.float()
-            a, b = t[..., :half], t[..., half:]
-            return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1)
-
         h = decode.rmsnorm(x, p["n1"], 1e-5, delta)
         q, k, v = generated._int4_split(self.linear(h, p["qkv"]), p["qkv_rows"])
-        q = rope(q.reshape(prompt, self.heads, self.hd)).to(torch.bfloat16)
-        k = rope(k.reshape(prompt, self.kv_heads, self.hd)).to(torch.bfloat16)
-        v = v.reshape(prompt, self.kv_heads, self.hd)
-        self.kt[i][0, :, :, :prompt] = k.permute(1, 2, 0)
-        self.vc[i][0, :, :prompt, :] = v.permute(1, 0, 2)
-        o = self.linear(self._attend_prompt(q, k, v), p["o"])
+        qh, kh, vh = decode.prefill_rope(q, k, v, self.cos_tab, self.sin_tab, self.kt[i][0], self.vc[i][0])
+        o = self.linear(self._attend_prompt(qh, kh, vh), p["o"])
         h = decode.rmsnorm(x, p["n2"], 1e-5, o)
         g, u = generated._int4_split(self.linear(h, p["gate_up"]), p["gate_up_rows"])
         return o, self.linear(decode.silu_mul(g, u), p["down"])

@@ -38,6 +38,42 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: tor
     return h
 
 
+def prefill_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                 kt_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """A prompt's rotary embedding and cache writes (`lnq_prefill_rope`): q [P,
+    heads*hd], k and v [P, kv_heads*hd] (bf16; column slices of a joined q|k|v
+    output are read in place); `cos`, `sin` f32 [cap, hd/2] (`rope_tables`);
+    `kt_cache` [kv_heads, hd, cap] and `v_cache` [kv_heads, cap, hd] bf16 (one
+    sequence's caches) receive positions 0..P-1. Returns q, k and v head-major,
+    [1, heads, P, hd] and [1, kv_heads, P, hd], with q and k rotated and rounded
+    to bf16."""
+    device = _on_gpu("prefill_rope", q, k, v, cos, sin, kt_cache, v_cache)
+    _bf16("prefill_rope", kt_cache, v_cache)
+    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+        raise LinnetError("prefill_rope: q, k and v are bf16")
+    if q.dim() != 2 or k.shape != v.shape or k.dim() != 2 or q.shape[0] != k.shape[0]:
+        raise LinnetError("prefill_rope: q [P, heads*hd], k and v [P, kv_heads*hd]")
+    kvh, hd, cap = kt_cache.shape
+    prompt = q.shape[0]
+    if tuple(v_cache.shape) != (kvh, cap, hd) or k.shape[1] != kvh * hd or q.shape[1] % hd != 0:
+        raise LinnetError("prefill_rope: caches [kv_heads, hd, cap] and [kv_heads, cap, hd] matching k")
+    if tuple(cos.shape) != (cap, hd // 2) or cos.shape != sin.shape or cos.dtype != torch.float32:
+        raise LinnetError(f"prefill_rope: cos and sin are f32 [{cap}, {hd // 2}]")
+    if not (kt_cache.is_contiguous() and v_cache.is_contiguous() and cos.is_contiguous() and sin.is_contiguous()):
+        raise LinnetError("prefill_rope: contiguous caches and tables")
+    stride = q.stride(0)
+    if q.stride(1) != 1 or k.stride(1) != 1 or v.stride(1) != 1 or k.stride(0) != stride or v.stride(0) != stride:
+        raise LinnetError("prefill_rope: q, k and v rows share one stride, each row contiguous")
+    heads = q.shape[1] // hd
+    q_out = torch.empty(1, heads, prompt, hd, dtype=q.dtype, device=device)
+    k_out = torch.empty(1, kvh, prompt, hd, dtype=q.dtype, device=device)
+    v_out = torch.empty(1, kvh, prompt, hd, dtype=q.dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_prefill_rope", _ptr(q), _ptr(k), _ptr(v), stride, _ptr(cos), _ptr(sin), _ptr(q_out),
+                  _ptr(k_out), _ptr(v_out), _ptr(kt_cache), _ptr(v_cache), prompt, heads, kvh, hd, cap, _stream(device))
+    return q_out, k_out, v_out
+
+
 def rope_tables(head_dim: int, positions: int, theta: float = 500000.0,
                 device: torch.device | str = "cuda") -> tuple[torch.Tensor, torch.Tensor]:
     """`(cos, sin)` f32 [positions, head_dim/2]: row p holds cos / sin of p times the

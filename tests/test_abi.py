@@ -122,6 +122,13 @@ def test_other_entry_points_validate() -> None:
     assert "needs u" in pro(_lib.PROLOGUE_SILU_MUL, FAKE, NULL, 1)[1]
     assert "staged" in pro(_lib.PROLOGUE_SILU_MUL, NULL, FAKE, 4)[1]
     assert pro(_lib.PROLOGUE_RMSNORM, FAKE, NULL, 0)[0] == _lib.LNQ_OK
+    rope = lambda positions, hd, cap, stride=4096: _status(  # noqa: E731
+        "lnq_prefill_rope", FAKE, FAKE, FAKE, stride, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, positions, 32, 8, hd, cap,
+        NULL)
+    assert "head_dim is 64 or 128" in rope(10, 96, 16)[1]
+    assert "positions <= cap" in rope(20, 128, 16)[1]
+    assert "multiple of 8" in rope(10, 128, 16, stride=100)[1]
+    assert rope(0, 128, 16)[0] == _lib.LNQ_OK
     assert "bf16, f16 or f32" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, 9, NULL)[1]
     assert "must not be x" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, _lib.BF16, NULL)[1]
     assert "groups of 128" in _status("lnq_fp8_groups", FAKE, FAKE, FAKE, 2, 2, 256, 64, _lib.BF16, NULL)[1]

@@ -337,6 +337,41 @@ def test_full_size_prefill_matches_the_reference_layer_by_layer() -> None:
     del model, graph
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_prefill_rope_matches_torch_ops(hd: int) -> None:
+    """`decode.prefill_rope` (one kernel) against the torch ops it replaces, bit for
+    bit: q and k rotated in f32 from the tables and rounded to bf16, head-major
+    q / k / v, k transposed into Kt and v into V at positions 0..P-1 (a ragged P of
+    100 over a 136-position cache; q, k and v read as column slices of a joined
+    output), the rest of the caches untouched."""
+    from linnet_amd.torch import decode
+
+    g = torch.Generator(device=DEV).manual_seed(hd)
+    heads, kvh, prompt, cap = 8, 2, 100, 136
+    joined = torch.randn(prompt, (heads + 2 * kvh) * hd, generator=g, device=DEV).to(torch.bfloat16)
+    q, k, v = joined[:, : heads * hd], joined[:, heads * hd : (heads + kvh) * hd], joined[:, (heads + kvh) * hd :]
+    cos, sin = decode.rope_tables(hd, cap, 500000.0, DEV)
+    kt = torch.randn(kvh, hd, cap, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(kvh, cap, hd, generator=g, device=DEV).to(torch.bfloat16)
+    kt0, vc0 = kt.clone(), vc.clone()
+    qh, kh, vh = decode.prefill_rope(q, k, v, cos, sin, kt, vc)
+    c, sn = cos[:prompt, None, :], sin[:prompt, None, :]
+
+    def rope(t):
+        t = t.float()
+        a, b = t[..., : hd // 2], t[..., hd // 2 :]
+        return torch.cat([a * c - b * sn, b * c + a * sn], dim=-1).to(torch.bfloat16)
+
+    want_q = rope(q.reshape(prompt, heads, hd))
+    want_k = rope(k.reshape(prompt, kvh, hd))
+    want_v = v.reshape(prompt, kvh, hd)
+    assert torch.equal(qh[0], want_q.transpose(0, 1))
+    assert torch.equal(kh[0], want_k.transpose(0, 1))
+    assert torch.equal(vh[0], want_v.transpose(0, 1))
+    assert torch.equal(kt[:, :, :prompt], want_k.permute(1, 2, 0)) and torch.equal(kt[:, :, prompt:], kt0[:, :, prompt:])
+    assert torch.equal(vc[:, :prompt], want_v.transpose(0, 1)) and torch.equal(vc[:, prompt:], vc0[:, prompt:])
+
+
 def test_decode_kernels_match_torch_ops() -> None:
     """Each decode kernel against the torch ops it replaces (f32 math, bf16 in and out)."""
     from linnet_amd.torch import decode
