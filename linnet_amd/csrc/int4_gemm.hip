@@ -408,20 +408,25 @@ constexpr int WAVES = 4;
 constexpr int THREADS = 64 * WAVES;
 constexpr int WB = 32;            // columns of W a wave owns
 constexpr int BN = WAVES * WB;    // 128
-constexpr int FA = gemm::BM / 32;  // 8 row fragments of 32
 constexpr int NS = 4;             // x stages
-constexpr int LPS = 3 + 8;        // loads a wave issues a step: weights, scale, zero, 8 x DMAs
 }  // namespace narrow
 
-template <int DT>
+// BM: rows of x a tile (256, or 128 where 256-row tiles would leave more than
+// half the CUs without one: twice the tiles, each a wave's weights dequantized
+// for half the rows).
+template <int DT, int BM = gemm::BM>
 __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scale,
     const uint8_t* __restrict__ zero, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
     int gshift) {
   using namespace narrow;
   using gemm::BK;
-  using gemm::BM;
   using E = Elem<DT>;
+  constexpr int FA = BM / 32;     // row fragments of 32 (8 or 4)
+  constexpr int XL = FA;          // x DMAs a wave issues a step (1 KB each)
+  constexpr int LPS = 3 + XL;     // loads a wave issues a step: weights, scale, zero, x DMAs
+  constexpr int PPS = 8 / FA;     // dequantization positions a slot runs
+  static_assert(FA == 8 || FA == 4, "256- or 128-row tiles");
   __shared__ __attribute__((aligned(16))) uint16_t XS[NS * BM * BK];
   LNQ_MFMA_IN_AGPRS();
 
@@ -446,7 +451,7 @@ __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
   const __amdgpu_buffer_rsrc_t rnull = buffer_rsrc(packed, 0);
 
-  // x: DMA i (0..7) of wave w writes rows 32 i + 8 w .. + 7 of a stage, in the
+  // x: DMA i (0..FA-1) of wave w writes rows 32 i + 8 w .. + 7 of a stage, in the
   // swizzled layout of int4_tiled_kernel (the key (row >> 1) & 7 = (4 w + l /
   // 16) & 7 does not depend on i).
   const int xrow = 8 * wave + (lane >> 3);
@@ -530,16 +535,17 @@ __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
   u32x4 b0[4], b1[4];
 
   // Region kk: FA MFMA slots on (ca, bc[kk]); slot s reads the next x fragment
-  // s, runs dequantization position s of dword kk of the next step's weights
-  // (registers dn, into bn[kk]) and the loads vm(s). Each slot is its own
-  // scheduling region, which pins the interleave.
+  // s, runs dequantization positions PPS s .. PPS s + PPS - 1 of dword kk of the
+  // next step's weights (registers dn, into bn[kk]) and the loads vm(s). Each
+  // slot is its own scheduling region, which pins the interleave.
   auto region = [&](int kk, const u32x4* ca, u32x4* na, int nstage, int nkk, const u32x4* bc, u32x4* bn,
                     const WRegs& dn, auto&& vm) {
 #pragma unroll
     for (int s = 0; s < FA; ++s) {
       acc[s] = mfma32x32x16<DT>(bc[kk], ca[s], acc[s]);
       na[s] = rd(nstage, nkk, s);
-      deq_slot(dn.w[kk], s, bn[kk]);
+#pragma unroll
+      for (int q2 = 0; q2 < PPS; ++q2) deq_slot(dn.w[kk], PPS * s + q2, bn[kk]);
       vm(s);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -557,7 +563,7 @@ __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
     const int xst = (st + 3) % NS;
     auto vm = [&](int r, int s) {
       if (r == 0 && s == 0) load_w(req, ks + 4);
-      if (r < 2 && (s & 1)) load_x(xst, xr, xk0, 4 * r + s / 2);
+      if (r < 2 && (s & 1)) load_x(xst, xr, xk0, (XL / 2) * r + s / 2);  // XL / 2 a region
     };
     set_scale(dn);
     region(0, a0, a1, st, 1, bc, bn, dn, [&](int s) { vm(0, s); });
@@ -577,13 +583,13 @@ __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
   WRegs w0, w1, w2, w3;
   load_w(w0, 0);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) load_x(0, rx, 0, i);
+  for (int i = 0; i < XL; ++i) load_x(0, rx, 0, i);
   load_w(w1, 1);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) load_x(1, steps > 1 ? rx : rnull, steps > 1 ? BK : 0, i);
+  for (int i = 0; i < XL; ++i) load_x(1, steps > 1 ? rx : rnull, steps > 1 ? BK : 0, i);
   load_w(w2, 2);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) load_x(2, steps > 2 ? rx : rnull, steps > 2 ? 2 * BK : 0, i);
+  for (int i = 0; i < XL; ++i) load_x(2, steps > 2 ? rx : rnull, steps > 2 ? 2 * BK : 0, i);
   load_w(w3, 3);
   wait_vm<0>();
   set_scale(w0);
@@ -663,19 +669,26 @@ static int compute_units() {
   return cached[dev];
 }
 
+
 template <int DT>
 static void launch_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                          const void* bias, void* y, int M, int N, int K, int gshift, bool wide, hipStream_t stream) {
   const int bn = wide ? 256 : narrow::BN;
   const int tiles = ((M + gemm::BM - 1) / gemm::BM) * ((N + bn - 1) / bn);
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* ys = static_cast<uint16_t*>(y);
   if (wide)
-    hipLaunchKernelGGL((int4_tiled_kernel<DT, 256>), dim3(tiles), dim3(gemm::THREADS), 0, stream,
-                       static_cast<const uint16_t*>(x), packed, static_cast<const uint16_t*>(scale), zero,
-                       static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, K, gshift);
+    hipLaunchKernelGGL((int4_tiled_kernel<DT, 256>), dim3(tiles), dim3(gemm::THREADS), 0, stream, xs, packed, ss, zero,
+                       bs, ys, M, N, K, gshift);
+  else if (2 * tiles <= compute_units())
+    // 256-row tiles would leave more than half the CUs idle: 128-row ones.
+    hipLaunchKernelGGL((int4_narrow_kernel<DT, 128>), dim3(((M + 127) / 128) * ((N + bn - 1) / bn)),
+                       dim3(narrow::THREADS), 0, stream, xs, packed, ss, zero, bs, ys, M, N, K, gshift);
   else
-    hipLaunchKernelGGL((int4_narrow_kernel<DT>), dim3(tiles), dim3(narrow::THREADS), 0, stream,
-                       static_cast<const uint16_t*>(x), packed, static_cast<const uint16_t*>(scale), zero,
-                       static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, K, gshift);
+    hipLaunchKernelGGL((int4_narrow_kernel<DT>), dim3(tiles), dim3(narrow::THREADS), 0, stream, xs, packed, ss, zero,
+                       bs, ys, M, N, K, gshift);
 }
 
 // 256-column tiles read half the x bytes per FLOP of 128-column ones, but only

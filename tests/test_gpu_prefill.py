@@ -1,8 +1,8 @@
 """Parity of the prefill products at BASELINE's full shapes, on the GPU, with the
 kernel instance that ran pinned by the library's own plan query.
 
-- Config 3 (int4 g128, M = 2048, bf16 x N(0, 1) with 0.1% of the input channels
-  scaled x20): a sampled block of 64 rows against the f64 product with the
+- Config 3 (int4 g128, M = 2048, and config 5's prompt, M = 1024, bf16 x N(0, 1)
+  with 0.1% of the input channels scaled x20): a sampled block of 64 rows against the f64 product with the
   exactly dequantized weight (the oracle) within `1e-2 * max|y|`
   (`python/linnet/tests/test_quant_groups.py:194-195`), and the whole output
   against hipBLASLt over the HIP-dequantized weight (the reference's own prefill
@@ -59,9 +59,13 @@ def _sample_rows(rows: int, seed: int) -> np.ndarray:
     return np.sort(np.random.default_rng(seed).choice(rows, size=min(SAMPLE, rows), replace=False))
 
 
-@pytest.mark.parametrize(("k", "n", "want_kernel"), [(4096, 14336, "tiled256"), (4096, 4096, "tiled128"), (14336, 4096, "tiled128")])
-def test_config3_prefill_matches_the_oracle(k: int, n: int, want_kernel: str) -> None:
-    rows = 2048
+# At 1024 rows the 128-column kernel runs 128-row tiles (256-row tiles would
+# leave more than half the compute units idle); at 2048 rows, 256-row tiles.
+@pytest.mark.parametrize(("rows", "k", "n", "want_kernel"), [
+    (2048, 4096, 14336, "tiled256"), (2048, 4096, 4096, "tiled128"), (2048, 14336, 4096, "tiled128"),
+    (1024, 14336, 4096, "tiled128"),
+])
+def test_config3_prefill_matches_the_oracle(rows: int, k: int, n: int, want_kernel: str) -> None:
     print(f"config 3 rows={rows} k={k} n={n}", flush=True)
     assert kernels.int4_linear_plan(rows, k, n, 128) == want_kernel
     packed, scale, zero = _layer(n, k, seed=k + n)
