@@ -680,15 +680,17 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
 
 // A few tokens (2..MX rows, MX = 4 or 16): the one-token kernel's workgroup
 // shape and weight streams, with A-operand row m of every MFMA holding x row m
-// (lane col = m). x is read contiguously, two rows of the wave's 256 inputs an
-// instruction (only the M real rows), and turned into A operands through a
-// wave-private LDS slot of 4 rows, 4 rows a round; the whole x is read once per
-// CU. (A lane loading its own A operand would touch 16 rows an instruction, 64
-// scattered 16-byte pieces, and its 8 such loads per wave held the weight loads
-// back by 1.4-3.3 us.) The output registers of a tile then hold rows
-// 4 (lane / 16) + i; the fold takes each row's sum of x from the lane that
-// loaded it, and after a barrier the 16 waves' partial sums are added through
-// LDS (the weight buffers, no longer read), four lanes an output.
+// (lane col = m). The order of the inputs within a wave's 256 is free as long
+// as A and B agree, so MFMA t of half H takes inputs 128 H + 32 t + 8 j .. + 7
+// in lane (col, j): at 16 rows each lane loads its own A operands straight from
+// x, an instruction reading 16 rows x 64 contiguous bytes (rows past M read
+// zeros through the range check; up to 4 rows the loads are two rows x 512
+// bytes, put in operand order through LDS). The B operands follow: lane (col,
+// j) reads dword j of the 16-byte pieces 4 H + t of its weight row. The output
+// registers of a tile hold rows 4 (lane / 16) + i; the fold takes each row's sum
+// of x from the lanes that loaded it, and after a barrier the 16 waves' partial
+// sums are added through LDS (the weight buffers, no longer read), four lanes an
+// output.
 template <int DT, int U8, bool G128, int MX>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
@@ -699,13 +701,11 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   constexpr int NT = (U8 + 1) / 2;  // 16-row tiles (an odd U8: the last one has 8 rows)
   LNQ_GEMV_TILE_ARRAYS(U8);
   // After the barrier, tile T's array holds the waves' partial sums of its 16
-  // output rows in output-register order, red[wave][i][lane] (x row 4 (lane / 16)
-  // + i, output row 16 T + lane % 16): each store and each read of the final sum
-  // touches consecutive dwords (a stride of 16 dwords would put 16 lanes on one
-  // bank).
+  // output rows in output-register order: element e = 64 i + lane (x row
+  // 4 (lane / 16) + i, output row 16 T + lane % 16) of wave w at
+  // 256 w + (e + 4 w) % 256. The rotation by 4 w puts the four waves a read
+  // instruction touches (lanes 16 q + c read wave 4 q + w) in distinct banks.
   static_assert(gemv::MAX_WAVES * 256 * 4 <= gemv::tile_bytes(U8, NT - 1), "partial sums fit a tile array");
-  // Each wave's slot for 4 rows of its 256 inputs of x.
-  __shared__ __attribute__((aligned(16))) uint16_t Xst[gemv::MAX_WAVES][4 * 256];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -722,8 +722,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
 
   // ---- loads: scales and zeros (first: they are few, and the compiler may copy
-  // them out of their registers early), x (row col, inputs k0 + 128 H + 32 j +
-  // 8 t), weights.
+  // them out of their registers early), x (row col, inputs k0 + 128 H + 32 t +
+  // 8 j), weights.
   const int srow = n0 + (lane < R ? lane : R - 1);
   const int g0 = k0 / G;
   uint32_t sv;
@@ -736,15 +736,22 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // Load i: x row 2 i (lanes 0..31) and 2 i + 1 (lanes 32..63), 8 inputs a lane;
-  // loads past row M are not issued, and a row M of an odd M reads zeros
-  // through the range check.
-  constexpr int XI = MX / 2;
-  u32x4 xc[XI];
+  // 16 rows: each lane loads its A operands. Up to 4 rows, loads of two rows
+  // x 256 inputs (lanes 0..31 row 2 i, 32..63 row 2 i + 1) move x to registers
+  // with fewer instructions, and one pass through a wave-private LDS slot puts
+  // it in operand order (A rows past 4 are zeros).
+  u32x4 xa[2][4];
+  u32x4 xc[2];
+  if constexpr (MX == 16) {
 #pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    xc[i] = u32x4{0u, 0u, 0u, 0u};
-    if (2 * i < M)
+    for (int H = 0; H < 2; ++H)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        xa[H][t] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (col * K + k0 + 128 * H + 32 * t + 8 * j) * 2, 0, 0));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
       xc[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             rx, ((2 * i + (lane >> 5)) * K + k0 + 8 * (lane & 31)) * 2, 0, 0));
   }
@@ -761,51 +768,45 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- x: wait for it (and the scales) alone; through the wave's LDS slot, 4
-  // rows a round, to A operands in pair order (lane col: x row col, inputs
-  // 128 H + 32 j + 8 t ..); the sums of x row col over both halves.
+  // ---- x: wait for it (and the scales) alone; the sums of x row col over both
+  // halves, then the A operands in pair order.
   wait_vm<U8>();
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 xa[2][4];
-  float part[2] = {0.f, 0.f};
+  if constexpr (MX != 16) {
+    static_assert(MX == 4, "4 or 16 rows");
+    __shared__ __attribute__((aligned(16))) uint16_t Xst[gemv::MAX_WAVES][4 * 256];
+    uint16_t* Xw = Xst[wave];
+    *reinterpret_cast<u32x4*>(Xw + 256 * (lane >> 5) + 8 * (lane & 31)) = xc[0];
+    *reinterpret_cast<u32x4*>(Xw + 256 * (2 + (lane >> 5)) + 8 * (lane & 31)) = xc[1];
 #pragma unroll
-  for (int H = 0; H < 2; ++H)
+    for (int H = 0; H < 2; ++H)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xa[H][t] = u32x4{0u, 0u, 0u, 0u};
-  uint16_t* Xw = Xst[wave];
-#pragma unroll
-  for (int r = 0; r < MX / 4; ++r) {
-    if (4 * r >= M) break;
-    // Unconditional stores: with a store under a condition the compiler could
-    // sink the x loads into it, behind the weight loads.
-    *reinterpret_cast<u32x4*>(Xw + 256 * (lane >> 5) + 8 * (lane & 31)) = xc[2 * r];
-    *reinterpret_cast<u32x4*>(Xw + 256 * (2 + (lane >> 5)) + 8 * (lane & 31)) = xc[2 * r + 1];
-    // Only the reads are under the lane condition: VALU work there would cost
-    // every round the full wave's cycles.
-    if ((col >> 2) == r) {
+      for (int t = 0; t < 4; ++t) xa[H][t] = u32x4{0u, 0u, 0u, 0u};
+    // Only the reads are under the lane condition.
+    if (col < 4) {
 #pragma unroll
       for (int H = 0; H < 2; ++H)
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          xa[H][t] = *reinterpret_cast<const u32x4*>(Xw + 256 * (col & 3) + 128 * H + 32 * j + 8 * t);
+          xa[H][t] = *reinterpret_cast<const u32x4*>(Xw + 256 * col + 128 * H + 32 * t + 8 * j);
     }
   }
   float xsum[2];
 #pragma unroll
   for (int H = 0; H < 2; ++H) {
+    float part = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t d = xa[H][t][e];
-        part[H] += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
+        part += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
       }
       xa[H][t] = permute_x8(xa[H][t]);
     }
-    float sum = part[H];
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    xsum[H] = sum;  // sum of x row col over half H of this wave's inputs
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    xsum[H] = part;  // sum of x row col over half H of this wave's inputs
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -813,8 +814,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   hide_in_vgpr(nib_mask);
   hide_in_vgpr(nib_magic);
   const int r7 = col & 7;
-  // One MFMA chain over a lane's 16 bytes of weights; the operand registers stay
-  // allocated until the result has been read.
+  // One MFMA chain over four packed dwords (MFMA t takes dword t); the operand
+  // registers stay allocated until the result has been read.
   auto chain = [&](const u32x4 (&a)[4], const u32x4 w) -> f32x4 {
     u32x4 b0, b1, b2, b3;
     widen_pair<DT>(w.x, w.y, nib_mask, nib_magic, b0, b1);
@@ -828,7 +829,10 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     return C;
   };
   // ---- tiles as their loads land; tile T covers rows 16 T .. 16 T + 15 (the
-  // last of an odd U8 only its first 8, the other 8 columns read again and dropped).
+  // last of an odd U8 only its first 8, the other 8 columns read again and
+  // dropped). Piece sigma of row r7 of load u sits at 16-byte position
+  // 16 (sigma / 2) + 8 ((sigma % 2) ^ (u % 2)) + r7; pieces t and t + 2 are 256
+  // bytes apart, one ds_read2 a pair.
   f32x4 cf[NT][2];
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
@@ -839,13 +843,20 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     const int h = col >> 3;
     const int u = min(2 * T + h, U8 - 1);
     const int hh = u & 1;  // the piece order of load u (and its half of the tile array)
-    const int p0 = 16 * (j >> 1) + 8 * ((j & 1) ^ hh) + r7;
-    const int p1 = 16 * (2 + (j >> 1)) + 8 * ((j & 1) ^ hh) + r7;
-    const uint8_t* Wt = tile_lds(T, wave) + 1024 * hh;
-    const u32x4 w0 = *reinterpret_cast<const u32x4*>(Wt + 16 * p0);
-    const u32x4 w1 = *reinterpret_cast<const u32x4*>(Wt + 16 * p1);
-    cf[T][0] = chain(xa[0], w0);
-    cf[T][1] = chain(xa[1], w1);
+    const uint32_t* Wt = reinterpret_cast<const uint32_t*>(tile_lds(T, wave) + 1024 * hh);
+    u32x4 w[2];
+#pragma unroll
+    for (int H = 0; H < 2; ++H)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        // pieces 4 H + t and 4 H + t + 2
+        const int p = 16 * (2 * H) + 8 * ((t & 1) ^ hh) + r7;
+        const uint32_t* at = Wt + 4 * p + j;
+        w[H][t] = at[0];
+        w[H][t + 2] = at[64];
+      }
+    cf[T][0] = chain(xa[0], w[0]);
+    cf[T][1] = chain(xa[1], w[1]);
   }
   // ---- scales / zeros (landed before x), the fold.
   __builtin_amdgcn_sched_barrier(0);
@@ -879,36 +890,56 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   __syncthreads();
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
-    float* red = reinterpret_cast<float*>(tile_lds(T, 0));
+    float* red = reinterpret_cast<float*>(tile_lds(T, 0)) + 256 * wave;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 4 * j + i;
-      if (m < MX) red[wave * 256 + i * 64 + lane] = acc[T][i];
+      if (m < MX) red[(64 * i + lane + 4 * wave) & 255] = acc[T][i];
     }
   }
   __syncthreads();
-  // Output o = (T, m, c) of the NT * M * 16: four lanes, each adding a quarter of
-  // the waves (read unconditionally, the waves past nw masked), then two
-  // exchanges; a group of four lanes is active or inactive together.
-  const int per_tile = M * 16;
-  for (int t = threadIdx.x; t < 4 * NT * per_tile; t += blockDim.x) {
-    const int o = t >> 2, q = t & 3;
-    const int T = o / per_tile, m = (o - T * per_tile) >> 4, c = o & 15;
-    const float* red = reinterpret_cast<const float*>(tile_lds(T, 0)) + (m & 3) * 64 + (m >> 2) * 16 + c;
-    float v = 0.f;
+  // Output (T, m, c): lanes 16 q + c of a wave add waves 4 q .. 4 q + 3 (the
+  // waves past nw masked), two exchanges finish the sum. Pass o (T = o / MX,
+  // m = o % MX) covers 16 outputs; wave w takes passes w, w + nw, .., all its
+  // reads issued before the first sum.
+  constexpr int PASSES = NT * MX;
+  constexpr int PW = (PASSES + gemv::MAX_WAVES - 1) / gemv::MAX_WAVES;  // passes a wave at 16 waves
+  const int q = j;
+  auto pass = [&](const int o, float (&r)[4]) {
+    const int T = min(o / MX, NT - 1), m = o % MX;
+    const float* red = reinterpret_cast<const float*>(tile_lds(T, 0));
+    const int e = 64 * (m & 3) + 16 * (m >> 2) + col;
 #pragma unroll
     for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
-      const int wv = q * (gemv::MAX_WAVES / 4) + w;
-      const float r = red[wv * 256];
-      v += wv < nw ? r : 0.f;
+      const int wv = 4 * q + w;
+      r[w] = red[256 * wv + ((e + 4 * wv) & 255)];
     }
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    const int n = n0 + 16 * T + c;
-    if (q == 0 && 16 * T + c < R && n < N) {
+  };
+  auto finish = [&](const int o, const float (&r)[4]) {
+    const int T = o / MX, m = o % MX;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) v += 4 * q + w < nw ? r[w] : 0.f;
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    const int n = n0 + 16 * T + col;
+    if (q == 0 && o < PASSES && m < M && 16 * T + col < R && n < N) {
       uint16_t out = E::from_f32(v);
       if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
       y[static_cast<size_t>(m) * N + n] = out;
+    }
+  };
+  if (nw == gemv::MAX_WAVES) {
+    float r[PW][4];
+#pragma unroll
+    for (int p = 0; p < PW; ++p) pass(wave + gemv::MAX_WAVES * p, r[p]);
+#pragma unroll
+    for (int p = 0; p < PW; ++p) finish(wave + gemv::MAX_WAVES * p, r[p]);
+  } else {
+    for (int o = wave; o < PASSES; o += nw) {
+      float r[4];
+      pass(o, r);
+      finish(o, r);
     }
   }
 }
