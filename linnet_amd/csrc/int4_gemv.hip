@@ -700,12 +700,13 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   constexpr int R = 8 * U8;
   constexpr int NT = (U8 + 1) / 2;  // 16-row tiles (an odd U8: the last one has 8 rows)
   LNQ_GEMV_TILE_ARRAYS(U8);
-  // After the barrier, tile T's array holds the waves' partial sums of its 16
-  // output rows in output-register order: element e = 64 i + lane (x row
-  // 4 (lane / 16) + i, output row 16 T + lane % 16) of wave w at
-  // 256 w + (e + 4 w) % 256. The rotation by 4 w puts the four waves a read
-  // instruction touches (lanes 16 q + c read wave 4 q + w) in distinct banks.
-  static_assert(gemv::MAX_WAVES * 256 * 4 <= gemv::tile_bytes(U8, NT - 1), "partial sums fit a tile array");
+  // Once a wave has folded its tiles it writes its partial sums of tile T (16
+  // output rows) over its own part of tile T's array, which only it reads:
+  // element e = 64 i + lane (x row 4 (lane / 16) + i, output row 16 T +
+  // lane % 16) at float (e + 4 w) % 256 of wave w's part. The rotation by 4 w
+  // puts the four waves a read instruction touches (lanes 16 q + c read wave
+  // 4 q + w, parts 2048 or 1024 bytes apart) in distinct banks.
+  static_assert(gemv::tile_wave_bytes(U8, NT - 1) >= 256 * 4, "partial sums fit a wave's part of a tile");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -886,11 +887,10 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     for (int i = 0; i < 4; ++i)
       acc[T][i] = fmaf(s0, fmaf(-z0, xs[0][i], cf[T][0][i]), s1 * fmaf(-z1, xs[1][i], cf[T][1][i]));
   }
-  // ---- the cross-wave sum through the (now unread) tile arrays.
-  __syncthreads();
+  // ---- the cross-wave sum through the wave's own (now unread) tile parts.
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
-    float* red = reinterpret_cast<float*>(tile_lds(T, 0)) + 256 * wave;
+    float* red = reinterpret_cast<float*>(tile_lds(T, wave));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 4 * j + i;
@@ -907,12 +907,11 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   const int q = j;
   auto pass = [&](const int o, float (&r)[4]) {
     const int T = min(o / MX, NT - 1), m = o % MX;
-    const float* red = reinterpret_cast<const float*>(tile_lds(T, 0));
     const int e = 64 * (m & 3) + 16 * (m >> 2) + col;
 #pragma unroll
     for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
       const int wv = 4 * q + w;
-      r[w] = red[256 * wv + ((e + 4 * wv) & 255)];
+      r[w] = reinterpret_cast<const float*>(tile_lds(T, wv))[(e + 4 * wv) & 255];
     }
   };
   auto finish = [&](const int o, const float (&r)[4]) {
