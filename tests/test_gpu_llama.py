@@ -403,14 +403,17 @@ def test_decode_kernels_match_torch_ops() -> None:
     joined = torch.cat([gg, uu], dim=1)
     assert torch.equal(decode.silu_mul(joined[:, :1000], joined[:, 1000:]), decode.silu_mul(gg, uu))
     for rows, heads, kvh, hd, cap, pos in ((2, 8, 2, 128, 40, 37), (2, 8, 2, 128, 2048, 1999), (1, 8, 2, 128, 704, 700),
-                                           (2, 8, 1, 128, 132, 130), (3, 6, 2, 64, 100, 64), (1, 4, 4, 64, 68, 3)):
+                                           (2, 8, 1, 128, 132, 130), (3, 6, 2, 64, 100, 64), (1, 4, 4, 64, 68, 3),
+                                           (32, 32, 8, 128, 1088, 1000), (32, 32, 8, 128, 1088, 512),
+                                           (48, 16, 2, 128, 1088, 700), (24, 16, 4, 64, 1028, 1027)):
         _attention_case(decode, g, rows, heads, kvh, hd, cap, pos)
 
 
 def _attention_case(decode, g, rows: int, heads: int, kvh: int, hd: int, cap: int, pos: int) -> None:
     """One attention step against torch (bf16 caches, f32 math): group sizes 4, 8,
     3 and 1 (the LDS arrays sized 4, 8, 4, 1), head sizes 128 and 64, chunks from
-    1 to 32 (the merge's eight-at-a-time loop and its tail)."""
+    1 to 32 (the merge's eight-at-a-time loop and its tail), and batches of 24 to
+    48 rows (up to 4352 workgroups)."""
     print(f"attention rows={rows} heads={heads} kv_heads={kvh} hd={hd} cap={cap} pos={pos}", flush=True)
     q = torch.randn(rows, heads * hd, generator=g).to(torch.bfloat16).to(DEV)
     k = torch.randn(rows, kvh * hd, generator=g).to(torch.bfloat16).to(DEV)
