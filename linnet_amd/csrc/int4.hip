@@ -675,14 +675,16 @@ static int choose_int4_kernel(int M, int N, int K, int G, int dtype, int kernel,
     // holds up to 56-row workgroups (N = 14336: 11.4 against 11.7 us) and the
     // skinny kernel is ahead past them (N = 16384: 10.9 against 11.9 us; 28672:
     // 17.5 against 22.2).
-    // From 5 rows over a wide output the few-token GEMV wins (N = 14336: 13.7
-    // against 21.7 us at 16 rows), and at 17..64 rows it still does once per 16-row
-    // chunk, each chunk streaming the weight again (26.7 against 35.6 us at 32 rows,
-    // 51.9 against 69.2 at 64; N = 128256: 197 against 264): the skinny kernel's
-    // 16-feature workgroups each read all of x. Over N < 8192 the skinny kernel is
-    // ahead from 16 rows on (N = 4096: 7.2 against 7.9 us; N = 1024: 6.3 against 7.3).
-    const bool wide = N >= 8192;
-    const bool few = M <= 4 && N <= 14336;
+    // From 5 rows over a wide output the few-token GEMV wins (N = 14336: 11.9
+    // against 21.2 us at 16 rows; N = 6144: 8.5 against 11.6), and at 17..64 rows it
+    // still does once per 16-row chunk, each chunk streaming the weight again
+    // (N = 6144: 16.5 against 18.9 us at 32 rows, 32.8 against 34.8 at 64; N =
+    // 128256: 197 against 264): the skinny kernel's 16-feature workgroups each read
+    // all of x. Over N <= 4096 the GEMV holds at 5 rows (N = 4096: 5.6 against 6.0
+    // us; N = 1024: 5.1 against 5.5), the two are level at 8 and the skinny kernel is
+    // ahead from 16 rows on (N = 4096: 7.1 against 7.4 us; 32 rows: 10.7 against 14.5).
+    const bool wide = N >= 6144;
+    const bool few = M <= 6 && N <= 14336;
     if (gemv_ok && (M == 1 || few || (M > 4 && wide))) return LNQ_KERNEL_GEMV;
     if (wide && M > 16 && M <= 64 && int4_gemv_supports(16, N, K, G, x, packed, scale, zero)) return LNQ_KERNEL_GEMV;
     if (M > 64 && int4_tiled_supports(M, N, K, G, dtype))
