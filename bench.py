@@ -278,6 +278,12 @@ def main() -> int:
     return 0
 
 
+def _rows(kernels, x):
+    """Per-token FP8 rows of x and their scales as `torch._scaled_mm` takes them."""
+    qx, xs = kernels.fp8_rows(x)
+    return qx, xs.reshape(-1, 1)
+
+
 def eight_bit(torch, dev, timed_graph, steps: int) -> dict[str, object]:
     """Configs 1 and 4 through the `linnet.torch.quantized` operands/linear entry
     points (`quantized.py:113-194`), weights rotated past the Infinity Cache.
@@ -322,6 +328,24 @@ def eight_bit(torch, dev, timed_graph, steps: int) -> dict[str, object]:
                         "frac_hbm_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
                         "tflops": round(flops / sec / 1e12, 1),
                         "frac_fp8_peak": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4)}
+        if m > 1:
+            # The vendor library beside it: the reference's own fast path is the
+            # per-token rounding then torch._scaled_mm (hipBLASLt's FP8 GEMM here;
+            # `quantized.py:129`) -- timed on rows rounded once (the product
+            # alone) and with the rounding in each call; null where torch's FP8
+            # GEMM does not run.
+            try:
+                qx, sa = _rows(kernels, x)
+                ws = [o[1] for o in ops]  # the FP8 views of the weight copies
+                sb = ops[0][2]  # the scales, f32 [1, Out]
+                mm = lambda qx, sa, w: torch._scaled_mm(qx, w.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)  # noqa: E731
+                t_mm = timed_graph([lambda w=w: mm(qx, sa, w) for w in ws], calls, 2)
+                t_both = timed_graph([lambda w=w, x=x: mm(*_rows(kernels, x), w) for w in ws], calls, 2)
+                fp8[f"M{m}"]["scaled_mm_tflops"] = round(flops / t_mm / 1e12, 1)
+                fp8[f"M{m}"]["rows_scaled_mm_tflops"] = round(flops / t_both / 1e12, 1)
+            except (RuntimeError, TypeError) as e:
+                fp8[f"M{m}"]["scaled_mm_tflops"] = None
+                fp8[f"M{m}"]["scaled_mm_error"] = str(e)[:200]
         del x
     out["fp8_C4_K8192_N28672"] = fp8
     del ops
