@@ -213,36 +213,54 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   };
 
   // The dequantization of one step's weights as a stream of 4 * NMF positions,
-  // 8 per packed dword (8 weights -> one 16-byte column of row brow): position
-  // j of a dword does its share of 2 masks, 8 conversions, 8 FMAs and 4 packs.
+  // 8 per packed dword (8 weights -> one 16-byte column of row brow): (q - z) s
+  // in f32 (exact), one rounding. The codes become f16 halves without a
+  // conversion -- (0x6400 | q) is 1024 + q, (0x6400 | 16 q) is 1024 + 16 q --
+  // and v_fma_mix_f32 (an f16 half times an f32) gives (1024 + q) s -
+  // (1024 + z) s and (1024 + 16 q) (s / 16) - (64 + z) s, each exactly
+  // (q - z) s: codes 0 and 4 from w & 0x000f000f, 1 and 5 from w & 0x00f000f0,
+  // 2, 6 and 3, 7 the same of w >> 8; 17 instructions a dword (4 and-or, 1
+  // shift, 8 FMAs, 4 packs), spread over its 8 positions.
   struct Deq {
-    uint32_t lo, hi;
-    float f0, f1, v0, v1;
+    uint32_t m0, m1, m2, m3, t;
+    float v[8];
     u32x4 o;
   };
   Deq q;
-  float sv = 0.f, nzs = 0.f;  // scale and -zero * scale of the weights being dequantized
-  auto cvtb = [](uint32_t v, int byte) -> float { return static_cast<float>((v >> (8 * byte)) & 0xffu); };
+  // scale, -(1024 + zero) * scale, scale / 16, -(64 + zero) * scale
+  float sv = 0.f, cv = 0.f, sv16 = 0.f, cv16 = 0.f;
+  uint32_t mlo = 0x000f000fu, mhi = 0x00f000f0u, magic = 0x64006400u;
+  hide_in_vgpr(mlo);
+  hide_in_vgpr(mhi);
+  hide_in_vgpr(magic);
+  auto half_of = [](uint32_t m, int h) -> float { return static_cast<float>(__builtin_bit_cast(f16x2, m)[h]); };
   auto set_scale = [&](const WRegs& r) {
     sv = E::to_f32(static_cast<uint16_t>(r.s));
-    nzs = -static_cast<float>(r.z & 0xffu) * sv;
+    const float z = static_cast<float>(r.z & 0xffu);
+    cv = -(1024.f + z) * sv;
+    sv16 = sv * 0.0625f;
+    cv16 = -(64.f + z) * sv;
   };
   auto deq_slot = [&](const WRegs& r, int pos, uint16_t* dst) {
     const int d = pos >> 3;
     switch (pos & 7) {
-      case 0:
-        q.lo = opaque(r.w[d] & 0x0f0f0f0fu);
-        q.hi = opaque((r.w[d] >> 4) & 0x0f0f0f0fu);
+      case 0: q.m0 = and_or(r.w[d], mlo, magic); q.t = r.w[d] >> 8; break;
+      case 1: q.m1 = and_or(r.w[d], mhi, magic); q.v[0] = fmaf(half_of(q.m0, 0), sv, cv); break;
+      case 2: q.v[4] = fmaf(half_of(q.m0, 1), sv, cv); q.v[1] = fmaf(half_of(q.m1, 0), sv16, cv16); break;
+      case 3: q.v[5] = fmaf(half_of(q.m1, 1), sv16, cv16); q.o.x = pack2<DT>(q.v[0], q.v[1]); break;
+      case 4: q.m2 = and_or(q.t, mlo, magic); q.m3 = and_or(q.t, mhi, magic); break;
+      case 5:
+        q.v[2] = fmaf(half_of(q.m2, 0), sv, cv);
+        q.v[3] = fmaf(half_of(q.m3, 0), sv16, cv16);
+        q.o.y = pack2<DT>(q.v[2], q.v[3]);
         break;
-      case 1: q.f0 = cvtb(q.lo, 0); q.f1 = cvtb(q.hi, 0); q.v0 = fmaf(q.f0, sv, nzs); break;
-      case 2: q.v1 = fmaf(q.f1, sv, nzs); q.o.x = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 1); break;
-      case 3: q.f1 = cvtb(q.hi, 1); q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); break;
-      case 4: q.o.y = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 2); q.f1 = cvtb(q.hi, 2); break;
-      case 5: q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); q.o.z = pack2<DT>(q.v0, q.v1); break;
-      case 6: q.f0 = cvtb(q.lo, 3); q.f1 = cvtb(q.hi, 3); q.v0 = fmaf(q.f0, sv, nzs); break;
+      case 6:
+        q.v[6] = fmaf(half_of(q.m2, 1), sv, cv);
+        q.v[7] = fmaf(half_of(q.m3, 1), sv16, cv16);
+        q.o.z = pack2<DT>(q.v[4], q.v[5]);
+        break;
       default:
-        q.v1 = fmaf(q.f1, sv, nzs);
-        q.o.w = pack2<DT>(q.v0, q.v1);
+        q.o.w = pack2<DT>(q.v[6], q.v[7]);
         *reinterpret_cast<u32x4*>(&dst[swz(brow, DW * bpart + d)]) = q.o;
         break;
     }
@@ -484,32 +502,51 @@ __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
   };
 
   // A dword's 8 codes dequantized into one operand fragment, as 8 positions of
-  // about three VALU instructions: (q - z) * s = fma(q, s, -z * s) in f32
-  // (exact), one rounding to the 16-bit type, as int4_tiled_kernel does.
+  // about two VALU instructions: (q - z) * s in f32 (exact), one rounding to the
+  // 16-bit type, as int4_tiled_kernel does. The codes become f16 halves without
+  // a conversion: (0x6400 | q) is 1024 + q and (0x6400 | 16 q) is 1024 + 16 q,
+  // both exact, so v_fma_mix_f32 (an f16 half of a register times an f32)
+  // gives (1024 + q) s - (1024 + z) s and (1024 + 16 q) (s / 16) - (64 + z) s,
+  // each exactly (q - z) s: codes 0 and 4 come from w & 0x000f000f, 1 and 5
+  // from w & 0x00f000f0, 2, 6 and 3, 7 the same of w >> 8.
   struct Deq {
-    uint32_t lo, hi;
-    float f0, f1, v0, v1;
+    uint32_t m0, m1, m2, m3, t;
+    float v[8];
   };
   Deq q;
-  float sv = 0.f, nzs = 0.f;
-  auto cvtb = [](uint32_t v, int byte) -> float { return static_cast<float>((v >> (8 * byte)) & 0xffu); };
+  float sv = 0.f, cv = 0.f, sv16 = 0.f, cv16 = 0.f;
+  uint32_t mlo = 0x000f000fu, mhi = 0x00f000f0u, magic = 0x64006400u;
+  hide_in_vgpr(mlo);
+  hide_in_vgpr(mhi);
+  hide_in_vgpr(magic);
+  auto half_of = [](uint32_t m, int h) -> float {
+    return static_cast<float>(__builtin_bit_cast(f16x2, m)[h]);
+  };
   auto set_scale = [&](const WRegs& r) {
     sv = E::to_f32(static_cast<uint16_t>(r.s));
-    nzs = -static_cast<float>(r.z & 0xffu) * sv;
+    const float z = static_cast<float>(r.z & 0xffu);
+    cv = -(1024.f + z) * sv;
+    sv16 = sv * 0.0625f;
+    cv16 = -(64.f + z) * sv;
   };
   auto deq_slot = [&](uint32_t w, int pos, u32x4& o) {
     switch (pos) {
-      case 0:
-        q.lo = opaque(w & 0x0f0f0f0fu);
-        q.hi = opaque((w >> 4) & 0x0f0f0f0fu);
+      case 0: q.m0 = and_or(w, mlo, magic); q.t = w >> 8; break;
+      case 1: q.m1 = and_or(w, mhi, magic); q.v[0] = fmaf(half_of(q.m0, 0), sv, cv); break;
+      case 2: q.v[4] = fmaf(half_of(q.m0, 1), sv, cv); q.v[1] = fmaf(half_of(q.m1, 0), sv16, cv16); break;
+      case 3: q.v[5] = fmaf(half_of(q.m1, 1), sv16, cv16); o.x = pack2<DT>(q.v[0], q.v[1]); break;
+      case 4: q.m2 = and_or(q.t, mlo, magic); q.m3 = and_or(q.t, mhi, magic); break;
+      case 5:
+        q.v[2] = fmaf(half_of(q.m2, 0), sv, cv);
+        q.v[3] = fmaf(half_of(q.m3, 0), sv16, cv16);
+        o.y = pack2<DT>(q.v[2], q.v[3]);
         break;
-      case 1: q.f0 = cvtb(q.lo, 0); q.f1 = cvtb(q.hi, 0); q.v0 = fmaf(q.f0, sv, nzs); break;
-      case 2: q.v1 = fmaf(q.f1, sv, nzs); o.x = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 1); break;
-      case 3: q.f1 = cvtb(q.hi, 1); q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); break;
-      case 4: o.y = pack2<DT>(q.v0, q.v1); q.f0 = cvtb(q.lo, 2); q.f1 = cvtb(q.hi, 2); break;
-      case 5: q.v0 = fmaf(q.f0, sv, nzs); q.v1 = fmaf(q.f1, sv, nzs); o.z = pack2<DT>(q.v0, q.v1); break;
-      case 6: q.f0 = cvtb(q.lo, 3); q.f1 = cvtb(q.hi, 3); q.v0 = fmaf(q.f0, sv, nzs); break;
-      default: q.v1 = fmaf(q.f1, sv, nzs); o.w = pack2<DT>(q.v0, q.v1); break;
+      case 6:
+        q.v[6] = fmaf(half_of(q.m2, 1), sv, cv);
+        q.v[7] = fmaf(half_of(q.m3, 1), sv16, cv16);
+        o.z = pack2<DT>(q.v[4], q.v[5]);
+        break;
+      default: o.w = pack2<DT>(q.v[6], q.v[7]); break;
     }
   };
 
