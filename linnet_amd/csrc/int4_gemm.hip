@@ -729,10 +729,14 @@ static void launch_tiled(const void* x, const uint8_t* packed, const void* scale
 }
 
 // 256-column tiles read half the x bytes per FLOP of 128-column ones, but only
-// pay while they still give every compute unit a tile.
+// pay while they still give nearly every compute unit a tile.
 int int4_tiled_width(int M, int N) {
+  // 256-column tiles once they fill at least 7/8 of the CUs: at M = 1024, N =
+  // 14336 (224 tiles on 256 CUs) they take 114 us against 124 us for 448 tiles
+  // of 256 x 128; at 128 tiles (N = 4096, M = 2048) the 128-column ones win (72
+  // against 97 us).
   const long tiles256 = static_cast<long>((M + gemm::BM - 1) / gemm::BM) * ((N + 255) / 256);
-  return tiles256 >= compute_units() ? 256 : 128;
+  return 8 * tiles256 >= 7L * compute_units() ? 256 : 128;
 }
 
 LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,

@@ -61,9 +61,11 @@ def _sample_rows(rows: int, seed: int) -> np.ndarray:
 
 # At 1024 rows the 128-column kernel runs 128-row tiles (256-row tiles would
 # leave more than half the compute units idle); at 2048 rows, 256-row tiles.
+# 224 tiles of 256 x 256 (1024 rows, N = 14336) fill 7/8 of the CUs: the
+# 256-column kernel.
 @pytest.mark.parametrize(("rows", "k", "n", "want_kernel"), [
     (2048, 4096, 14336, "tiled256"), (2048, 4096, 4096, "tiled128"), (2048, 14336, 4096, "tiled128"),
-    (1024, 14336, 4096, "tiled128"),
+    (1024, 14336, 4096, "tiled128"), (1024, 4096, 14336, "tiled256"),
 ])
 def test_config3_prefill_matches_the_oracle(rows: int, k: int, n: int, want_kernel: str) -> None:
     print(f"config 3 rows={rows} k={k} n={n}", flush=True)
