@@ -533,9 +533,11 @@ template <int DT, int LOADW, int MT, bool XL, bool SV>
 static void launch_skinny_v(const uint16_t* xs, const uint8_t* packed, const uint16_t* ss,
                             const uint8_t* zero, const uint16_t* bs, uint16_t* ys, int M, int N,
                             int K, int G, hipStream_t stream) {
-  // Eight waves split K when each still gets at least one batch of chunks.
+  // Eight waves split K when each still gets at least one batch of chunks, up
+  // to 32 rows: at 64 rows (MT = 4) two waves a SIMD leave 256 registers a
+  // wave, which spills, while one wave a SIMD holds all of its tile.
   const int chunks = K >> 7;
-  const bool eight = chunks >= 64;
+  const bool eight = chunks >= 64 && MT < 4;
   const int nw = eight ? 8 : 4;
   const dim3 grid((N + 15) / 16, (M + 16 * MT - 1) / (16 * MT)), block(64 * nw);
   const int rows = min(M, 16 * MT);
