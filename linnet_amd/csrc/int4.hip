@@ -548,8 +548,13 @@ static void launch_skinny_v(const uint16_t* xs, const uint8_t* packed, const uin
 #define LNQ_SKINNY(NW)                                                                        \
   hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, XL, SV, NW>), grid, block, lds, stream, \
                      xs, packed, ss, zero, bs, ys, M, N, K, G)
-  if (eight) LNQ_SKINNY(8);
-  else LNQ_SKINNY(4);
+  if constexpr (MT < 4) {
+    if (eight) {
+      LNQ_SKINNY(8);
+      return;
+    }
+  }
+  LNQ_SKINNY(4);
 #undef LNQ_SKINNY
 }
 
