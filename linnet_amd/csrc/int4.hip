@@ -534,10 +534,12 @@ static void launch_skinny_v(const uint16_t* xs, const uint8_t* packed, const uin
                             const uint8_t* zero, const uint16_t* bs, uint16_t* ys, int M, int N,
                             int K, int G, hipStream_t stream) {
   // Eight waves split K when each still gets at least one batch of chunks, up
-  // to 32 rows: at 64 rows (MT = 4) two waves a SIMD leave 256 registers a
-  // wave, which spills, while one wave a SIMD holds all of its tile.
+  // to 16 rows. At 64 rows (MT = 4) two waves a SIMD leave 256 registers a wave,
+  // which spills, while one wave a SIMD holds all of its tile; at 17-32 rows
+  // four waves are as fast or a little faster (K = 14336: 31.0 against 31.4 us
+  // at 32 rows).
   const int chunks = K >> 7;
-  const bool eight = chunks >= 64 && MT < 4;
+  const bool eight = chunks >= 64 && MT < 2;
   const int nw = eight ? 8 : 4;
   const dim3 grid((N + 15) / 16, (M + 16 * MT - 1) / (16 * MT)), block(64 * nw);
   const int rows = min(M, 16 * MT);
@@ -548,7 +550,7 @@ static void launch_skinny_v(const uint16_t* xs, const uint8_t* packed, const uin
 #define LNQ_SKINNY(NW)                                                                        \
   hipLaunchKernelGGL((int4_skinny_kernel<DT, LOADW, MT, XL, SV, NW>), grid, block, lds, stream, \
                      xs, packed, ss, zero, bs, ys, M, N, K, G)
-  if constexpr (MT < 4) {
+  if constexpr (MT < 2) {
     if (eight) {
       LNQ_SKINNY(8);
       return;
