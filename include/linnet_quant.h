@@ -371,6 +371,48 @@ LNQ_API LnqStatus lnq_mxfp4_experts(const void* x, int64_t x_row_stride, int64_t
                                     int64_t num_experts, int64_t out_features,
                                     int64_t in_features, int32_t dtype, void* stream);
 
+/* ------------------------------------------------------------------------- NF4
+ * std.quant::Nf4Linear (stdlib/quant.linnet:177-215): codes [out, in/2] bytes of
+ * QLoRA's 4-bit NormalFloat, the first input of a pair in the low nibble, and
+ * absmax [out, in/block] f32, one scale for each `block` consecutive inputs of a
+ * row: weight[o, i] = nf4(q[o, i]) * absmax[o, i / block]. All three enqueue on
+ * `stream` and return at once.
+ */
+
+/* The weight in `dtype` (bf16, f16 or f32), [out, in]: the code's f32 value times
+ * its scale in f32, rounded once to nearest even -- bit for bit the reference's
+ * `dequantize_nf4` (stdlib/quant.linnet:180-187). block even, in % block == 0.
+ * Replaces: the generated torch module's lowering of `dequantize_nf4` (the
+ * codebook cast, src/emit/source.cpp:120-143, then the multiply). */
+LNQ_API LnqStatus lnq_nf4_dequant(const uint8_t* codes, const float* absmax, void* out,
+                                  int64_t out_features, int64_t in_features, int64_t block,
+                                  int32_t dtype, void* stream);
+
+/* y[r, o] = sum_i x[r, i] * weight[o, i] (+ bias[o]) for `rows` rows of x
+ * (row strides in elements), x / bias / y of `dtype` (bf16 or f16). The weight
+ * is read as stored: each code's value, rounded once to `dtype`, meets x in an
+ * f32 dot product; a block's sum is scaled by its absmax and the blocks added in
+ * f32, the row rounded once. Up to 4 rows of x a pass over the weight. block %
+ * 16 == 0, in % block == 0, in <= 32768, the codes under 2 GiB; x 16-byte aligned
+ * with x_stride % 8 == 0. Replaces: `linear_nf4`'s body, the widened weight and
+ * its product (stdlib/quant.linnet:189-199), for the few-row calls. */
+LNQ_API LnqStatus lnq_nf4_linear(const void* x, int64_t x_stride, int64_t rows, const uint8_t* codes,
+                                 const float* absmax, const void* bias, void* y, int64_t y_stride,
+                                 int64_t out_features, int64_t in_features, int64_t block,
+                                 int32_t dtype, void* stream);
+
+/* A bitsandbytes 4-bit NF4 layer as Nf4Linear holds it: `codes` = `packed`
+ * ([out * in / 2] bytes, the first code of a pair in the high nibble) with each
+ * byte's nibbles swapped; `absmax` [out * in / block] f32 = `absmax_in` (f32)
+ * as it is, or, with double quantization (nested_map and nested_absmax given),
+ * absmax_in's uint8 codes decoded as nested_map[code] * nested_absmax[i /
+ * nested_block] + offset, in f32 (two roundings). Replaces: quant.py:414-466
+ * `_bnb_nf4` (numpy). */
+LNQ_API LnqStatus lnq_nf4_repack(const uint8_t* packed, const void* absmax_in, const float* nested_absmax,
+                                 const float* nested_map, int64_t nested_block, float offset,
+                                 uint8_t* codes, float* absmax, int64_t out_features,
+                                 int64_t in_features, int64_t block, void* stream);
+
 /* ------------------------------------------------------- decode-step glue (bf16)
  * What a decoder layer runs between its quantized linear layers, for the int4
  * Llama-shaped decode step of BASELINE config 5. No counterpart in the reference's

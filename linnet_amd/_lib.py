@@ -55,6 +55,9 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_fp8_groups": [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "lnq_mm8_block": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_mxfp4_experts": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "lnq_nf4_dequant": [_p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "lnq_nf4_linear": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p],
+    "lnq_nf4_repack": [_p, _p, _p, _p, _i64, _f32, _p, _p, _i64, _i64, _i64, _p],
     "lnq_rmsnorm": [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p],
     "lnq_decode_attention": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "lnq_decode_attention_at": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p],

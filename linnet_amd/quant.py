@@ -233,8 +233,6 @@ class _Calibrated:
     @classmethod
     def read(cls, config: Mapping[str, object]) -> _Calibrated:
         method = str(config.get("quant_method", "")).lower()
-        if method == "bitsandbytes":
-            raise LinnetError("bitsandbytes checkpoints hold NF4 blocks (Nf4Linear), which linnet_amd does not import")
         if method not in ("gptq", "awq"):
             raise LinnetError(f"quant_method {method!r}: linnet_amd imports GPTQ and AWQ checkpoints")
         if _config_number(config, "bits", 4) != 4:
@@ -310,9 +308,14 @@ def import_quantized(
     (`lnq_int4_repack`); every other tensor is copied. `config` is the
     checkpoint's `quantization_config`, read from the `config.json` beside
     `weights_path` when not given. Returns the layers' `.weight` paths. Replaces the
-    GPTQ / AWQ part of the reference's `import_quantized` (`quant.py:259-369`); NF4
-    (bitsandbytes) is outside this package and raises."""
-    calibrated = _Calibrated.read(config if config is not None else _config_beside(weights_path))
+    GPTQ / AWQ part of the reference's `import_quantized` (`quant.py:259-369`). A
+    bitsandbytes 4-bit NF4 checkpoint (`quant_method` "bitsandbytes") becomes
+    `Nf4Linear` blocks instead (`.weight` [Out, In/2] U8, `.absmax` [Out, In/block]
+    F32), through `lnq_nf4_repack` (`quant.py:402-499`); `dtype` is then unused."""
+    config = config if config is not None else _config_beside(weights_path)
+    if str(config.get("quant_method", "")).lower() == "bitsandbytes":
+        return _import_nf4(weights_path, output, config, _bound(bindings), _on_gpu(device))
+    calibrated = _Calibrated.read(config)
     _scale_name(dtype)
     target = _on_gpu(device)
     index = weights.open_checkpoint(weights_path)
@@ -367,6 +370,7 @@ def _import_layer(layer: str, parts: Mapping[str, weights.StoredTensor], calibra
 
 
 __all__ = [
+    "NF4",
     "FEW_ROWS",
     "TILED_ROWS",
     "dequantize_int4_groups",
@@ -379,3 +383,133 @@ __all__ = [
     "quantize_int8_groups",
     "siblings",
 ]
+
+
+# ------------------------------------------------------- bitsandbytes NF4 import
+#
+# A bitsandbytes 4-bit layer `L` stores `L.weight` (two codes a byte, the first
+# in the high nibble, the weight flattened), `L.weight.absmax` (one scale a
+# block, or its uint8 code under double quantization), `L.weight.quant_map` (the
+# 16 values), for double quantization `L.weight.nested_absmax` and
+# `L.weight.nested_quant_map`, and its state -- shape, block size, nested block
+# size and offset -- as JSON bytes in `L.weight.quant_state.bitsandbytes__<type>`.
+_NF4_STATE = ".quant_state.bitsandbytes__"
+_NF4_SIDE = (".absmax", ".quant_map", ".nested_absmax", ".nested_quant_map")
+
+# NF4's 16 values by code (QLoRA's normal quantiles, as bitsandbytes' map holds
+# them; the reference's `NF4`, quant.py:373-394).
+NF4 = np.array(
+    [-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453, -0.28444138169288635,
+     -0.18477343022823334, -0.09105003625154495, 0.0, 0.07958029955625534, 0.16093020141124725,
+     0.2461123019456863, 0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
+     0.7229568362236023, 1.0],
+    dtype=np.float32,
+)
+
+
+@dataclass(frozen=True)
+class _Nf4Layer:
+    """What a bitsandbytes NF4 layer's state says: its [Out, In] shape, the
+    block size, and for double quantization the nested block size and offset."""
+
+    weight: str
+    out_features: int
+    in_features: int
+    block: int
+    nested_block: int = 0
+    offset: float = 0.0
+
+    @classmethod
+    def parse(cls, weight: str, stored: weights.StoredTensor) -> _Nf4Layer:
+        try:
+            state = json.loads(bytes(stored.view()).decode("utf-8"))
+        except (UnicodeDecodeError, json.JSONDecodeError):
+            state = None
+        if not isinstance(state, dict):
+            raise LinnetError(f"`{stored.name}` holds no quantization state")
+        shape, block = state.get("shape"), state.get("blocksize")
+        dims = [d for d in shape if isinstance(d, int) and not isinstance(d, bool)] if isinstance(shape, list) else []
+        if len(dims) != 2 or len(shape) != 2 or not isinstance(block, int) or isinstance(block, bool):
+            raise LinnetError(f"{weight}: its quantization state has no 2-d shape and block size")
+        out_features, in_features = dims
+        if block <= 0 or block % 2 or in_features % block:
+            raise LinnetError(f"{weight}: {in_features} inputs do not make blocks of {block}")
+        nested_block, offset = state.get("nested_blocksize"), state.get("nested_offset")
+        if nested_block is None and offset is None:
+            return cls(weight, out_features, in_features, block)
+        if (not isinstance(nested_block, int) or isinstance(nested_block, bool) or nested_block <= 0
+                or not isinstance(offset, (int, float)) or isinstance(offset, bool)):
+            raise LinnetError(f"{weight}: its nested quantization state is incomplete")
+        return cls(weight, out_features, in_features, block, nested_block, float(offset))
+
+
+def _import_nf4(weights_path: str | Path, output: str | Path, config: Mapping[str, object],
+                paths: Mapping[str, list[str]], target: torch.device) -> list[str]:
+    """`import_quantized` for a bitsandbytes 4-bit NF4 checkpoint: each layer's
+    codes repacked low nibble first and its absmax decoded on the GPU
+    (`kernels.nf4_repack`), every other tensor copied."""
+    from .torch import kernels
+
+    if not config.get("load_in_4bit", config.get("_load_in_4bit", False)):
+        raise LinnetError("bitsandbytes checkpoint without `load_in_4bit`: only its 4-bit layers import")
+    kind = str(config.get("bnb_4bit_quant_type", "fp4")).lower()
+    if kind != "nf4":
+        raise LinnetError(f"bitsandbytes 4-bit type {kind!r}: only NF4 imports")
+    index = weights.open_checkpoint(weights_path)
+    writer = weights.CheckpointWriter()
+    consumed: set[str] = set()
+    done: list[str] = []
+    for name in sorted(n for n in index if _NF4_STATE in n):
+        weight, _, layer_kind = name.partition(_NF4_STATE)
+        if layer_kind != "nf4":
+            raise LinnetError(f"{weight}: bitsandbytes 4-bit type {layer_kind!r}: only NF4 imports")
+        layer = _Nf4Layer.parse(weight, index[name])
+        codes, absmax = _nf4_layer(layer, index, target, kernels)
+        consumed |= {name, weight, *(weight + side for side in _NF4_SIDE)}
+        for path in paths.get(weight) or [weight]:
+            prefix = siblings(path)
+            writer.add(prefix + "weight", "U8", tuple(codes.shape), weights.tensor_bytes(codes))
+            writer.add(prefix + "absmax", "F32", tuple(absmax.shape), weights.tensor_bytes(absmax))
+            done.append(path)
+    if not done:
+        raise LinnetError(f"{weights_path}: no bitsandbytes 4-bit layer (`{_NF4_STATE}nf4`)")
+    for name, stored in index.items():
+        if name not in consumed:
+            for path in paths.get(name) or [name]:
+                writer.add(path, stored.dtype, stored.shape, stored)
+    writer.write(output, {"format": "pt"})
+    return done
+
+
+def _nf4_layer(layer: _Nf4Layer, index: Mapping[str, weights.StoredTensor], target: torch.device,
+               kernels) -> tuple[torch.Tensor, torch.Tensor]:
+    """One NF4 layer as `Nf4Linear` holds it: (codes [Out, In/2], absmax [Out, In/block])."""
+    w = layer.weight
+    missing = [w + side for side in (".absmax", ".quant_map") if w + side not in index]
+    if w not in index or missing:
+        raise LinnetError(f"{w}: the layer lacks {', '.join(missing) or 'its weight'}")
+    quant_map = weights.float_tensor(index[w + ".quant_map"], "cpu").numpy().reshape(-1)
+    if quant_map.shape != (16,) or not np.allclose(quant_map, NF4, rtol=0, atol=1e-6):
+        raise LinnetError(f"{w}: its quantization map is not NF4's")
+    stored = index[w]
+    if stored.nbytes * 2 != layer.out_features * layer.in_features:
+        raise LinnetError(f"{w}: {stored.nbytes} bytes for a [{layer.out_features}, {layer.in_features}] weight")
+    packed = weights.tensor_from(stored, torch.uint8, target).reshape(-1)
+    scales = layer.out_features * layer.in_features // layer.block
+    nested = w + ".nested_absmax" in index
+    if nested != bool(layer.nested_block):
+        raise LinnetError(f"{w}: its nested quantization state is incomplete")
+    if nested:
+        if w + ".nested_quant_map" not in index:
+            raise LinnetError(f"{w}: `.nested_absmax` without `.nested_quant_map`")
+        scale_codes = weights.tensor_from(index[w + ".absmax"], torch.uint8, target).reshape(-1)
+        outer = weights.float_tensor(index[w + ".nested_absmax"], target).reshape(-1)
+        table = weights.float_tensor(index[w + ".nested_quant_map"], target).reshape(-1)
+        if scale_codes.numel() != scales:
+            raise LinnetError(f"{w}: {scale_codes.numel()} scales for blocks of {layer.block}")
+        return kernels.nf4_repack(packed, scale_codes, layer.out_features, layer.in_features, layer.block,
+                                  outer, table, layer.nested_block, layer.offset)
+    absmax = weights.float_tensor(index[w + ".absmax"], target).reshape(-1)
+    if absmax.numel() != scales:
+        raise LinnetError(f"{w}: {absmax.numel()} scales for blocks of {layer.block}")
+    return kernels.nf4_repack(packed, absmax, layer.out_features, layer.in_features, layer.block)

@@ -618,3 +618,127 @@ def quantize_int8(weight: torch.Tensor, group: int, dtype: str) -> tuple[torch.T
     with torch.cuda.device(device):
         _lib.call("lnq_int8_quantize", _ptr(w), _ptr(q), _ptr(scale), width, depth, group, codes[dtype], _stream(device))
     return q, scale
+
+
+# ------------------------------------------------------------------------- NF4
+
+
+def _nf4_operands(what: str, codes: torch.Tensor, absmax: torch.Tensor, block: int) -> tuple[int, int]:
+    """(Out, In) of an `Nf4Linear` weight: codes [Out, In/2] uint8, absmax
+    [Out, In/block] float32 (`stdlib/quant.linnet:201-215`)."""
+    if codes.dtype != torch.uint8 or codes.dim() != 2:
+        raise LinnetError(f"{what}: the weight is [Out, In/2] uint8 bytes of NF4 codes")
+    out_features, in_features = codes.shape[0], 2 * codes.shape[1]
+    if block <= 0 or block % 2 or in_features % block:
+        raise LinnetError(f"{what}: {in_features} inputs do not make even blocks of {block}")
+    if absmax.dtype != torch.float32 or absmax.shape != (out_features, in_features // block):
+        raise LinnetError(f"{what}: absmax is [{out_features}, {in_features // block}] float32, "
+                          f"got {tuple(absmax.shape)} {absmax.dtype}")
+    return out_features, in_features
+
+
+def nf4_dequantize(codes: torch.Tensor, absmax: torch.Tensor, block: int, dtype: torch.dtype) -> torch.Tensor:
+    """`dequantize_nf4` (`stdlib/quant.linnet:180-187`): the [Out, In] weight in
+    `dtype`, `nf4(q) * absmax` in f32 rounded once, bit for bit."""
+    device = _on_gpu("nf4_dequantize", codes, absmax)
+    out_features, in_features = _nf4_operands("nf4_dequantize", codes, absmax, block)
+    code = _code(dtype, "nf4_dequantize", (torch.bfloat16, torch.float16, torch.float32))
+    codes, absmax = codes.contiguous(), absmax.contiguous()
+    out = torch.empty(out_features, in_features, dtype=dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_nf4_dequant", _ptr(codes), _ptr(absmax), _ptr(out), out_features, in_features, block, code,
+                  _stream(device))
+    return out
+
+
+# Rows of x up to which `nf4_linear` reads the stored weight with the NF4 GEMV
+# (4 rows a pass over the weight); more rows widen the weight and multiply. At
+# 4096 -> 14336 (bf16, graph-replayed): 1 row 12.1 us, 4 rows 15.9, 8 rows 31.2,
+# 16 rows 61 us, against 57-59 us for the widened weight and its product.
+NF4_GEMV_ROWS = 8
+NF4_GEMV_MAX_IN = 32768
+
+
+def nf4_gemv_fits(rows: int, in_features: int, block: int, dtype: torch.dtype) -> bool:
+    """Whether `nf4_linear` takes the GEMV for this call."""
+    return (dtype in _HALF and rows <= NF4_GEMV_ROWS and block % 16 == 0 and in_features % block == 0
+            and 0 < in_features <= NF4_GEMV_MAX_IN)
+
+
+def nf4_gemv(x: torch.Tensor, codes: torch.Tensor, absmax: torch.Tensor, block: int,
+             bias: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., In] (bf16 / f16) times the NF4 weight's transpose (+ bias), the
+    weight read as stored (`lnq_nf4_linear`)."""
+    device = _on_gpu("nf4_gemv", x, codes, absmax, bias)
+    out_features, in_features = _nf4_operands("nf4_gemv", codes, absmax, block)
+    code = _code(x.dtype, "nf4_gemv")
+    if x.shape[-1] != in_features:
+        raise LinnetError(f"nf4_gemv: x has {x.shape[-1]} inputs, the weight {in_features}")
+    if bias is not None and (bias.dtype != x.dtype or bias.numel() != out_features):
+        raise LinnetError(f"nf4_gemv: bias is [{out_features}] {x.dtype}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, in_features)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) < in_features):
+        x2 = x2.contiguous()
+        if in_features % 8:
+            raise LinnetError("nf4_gemv: In must be a multiple of 8")
+    codes, absmax = codes.contiguous(), absmax.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    y = torch.empty(x2.shape[0], out_features, dtype=x.dtype, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_nf4_linear", _ptr(x2), max(x2.stride(0), in_features), x2.shape[0], _ptr(codes), _ptr(absmax),
+                  _ptr(bias), _ptr(y), out_features, out_features, in_features, block, code, _stream(device))
+    return y.reshape(*lead, out_features)
+
+
+def nf4_linear(x: torch.Tensor, codes: torch.Tensor, absmax: torch.Tensor, block: int,
+               bias: torch.Tensor | None = None) -> torch.Tensor:
+    """`linear_nf4` (`stdlib/quant.linnet:189-199`): up to `NF4_GEMV_ROWS` rows of
+    bf16 / f16 x on the NF4 GEMV; otherwise the weight widened by the HIP
+    dequantize kernel, then multiplied in x's type (the reference's own body)."""
+    _on_gpu("nf4_linear", x, codes, absmax, bias)
+    out_features, in_features = _nf4_operands("nf4_linear", codes, absmax, block)
+    rows = x.numel() // max(in_features, 1) if x.dim() else 0
+    if nf4_gemv_fits(rows, in_features, block, x.dtype):
+        return nf4_gemv(x, codes, absmax, block, bias)
+    weight = nf4_dequantize(codes, absmax, block, x.dtype)
+    return torch.nn.functional.linear(x, weight, bias)
+
+
+def nf4_repack(packed: torch.Tensor, absmax: torch.Tensor, out_features: int, in_features: int, block: int,
+               nested_absmax: torch.Tensor | None = None, nested_map: torch.Tensor | None = None,
+               nested_block: int = 0, offset: float = 0.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """A bitsandbytes NF4 layer as `Nf4Linear` holds it (`quant.py:414-466`):
+    (codes [Out, In/2] uint8 with the first input in the low nibble, absmax
+    [Out, In/block] float32). `packed` is bitsandbytes' byte array (first code of
+    a pair in the high nibble); `absmax` its f32 scales, or, with double
+    quantization, their uint8 codes decoded through `nested_map` [256] and
+    `nested_absmax` (one a `nested_block` scales) plus `offset`, in f32."""
+    device = _on_gpu("nf4_repack", packed, absmax, nested_absmax, nested_map)
+    if block <= 0 or block % 2 or in_features % block:
+        raise LinnetError(f"nf4_repack: {in_features} inputs do not make even blocks of {block}")
+    if packed.dtype != torch.uint8 or packed.numel() * 2 != out_features * in_features:
+        raise LinnetError(f"nf4_repack: {packed.numel()} bytes for a [{out_features}, {in_features}] weight")
+    scales = out_features * in_features // block
+    nested = nested_map is not None or nested_absmax is not None
+    if nested:
+        if nested_map is None or nested_absmax is None or nested_block <= 0:
+            raise LinnetError("nf4_repack: double quantization takes nested_absmax, nested_map and nested_block")
+        if nested_map.dtype != torch.float32 or nested_map.numel() != 256:
+            raise LinnetError("nf4_repack: nested_map is 256 float32 values")
+        if nested_absmax.dtype != torch.float32 or nested_absmax.numel() < -(-scales // nested_block):
+            raise LinnetError(f"nf4_repack: {nested_absmax.numel()} nested scales for {scales} blocks of {nested_block}")
+        if absmax.dtype != torch.uint8 or absmax.numel() != scales:
+            raise LinnetError(f"nf4_repack: {absmax.numel()} absmax codes for {scales} blocks")
+    elif absmax.dtype != torch.float32 or absmax.numel() != scales:
+        raise LinnetError(f"nf4_repack: {absmax.numel()} absmax values for {scales} blocks of {block}")
+    packed, absmax = packed.contiguous(), absmax.contiguous()
+    nested_absmax = None if nested_absmax is None else nested_absmax.contiguous()
+    nested_map = None if nested_map is None else nested_map.contiguous()
+    codes = torch.empty(out_features, in_features // 2, dtype=torch.uint8, device=device)
+    scale = torch.empty(out_features, in_features // block, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_nf4_repack", _ptr(packed), _ptr(absmax), _ptr(nested_absmax), _ptr(nested_map),
+                  nested_block, ctypes.c_float(offset), _ptr(codes), _ptr(scale), out_features, in_features, block,
+                  _stream(device))
+    return codes, scale

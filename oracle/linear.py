@@ -131,3 +131,11 @@ def mxfp4_experts_f64(x: np.ndarray, blocks: np.ndarray, scales: np.ndarray, exp
     weight = quant.dequantize_mxfp4(blocks, scales).astype(np.float64)  # [E, Out, In]
     chosen = weight[np.asarray(experts)]  # [R, K, Out, In]
     return np.einsum("rki,rkoi->rko", np.asarray(x, dtype=np.float64), chosen)
+
+
+def nf4_reference_f64(x: np.ndarray, codes: np.ndarray, absmax: np.ndarray, block: int,
+                      bias: np.ndarray | None = None) -> np.ndarray:
+    """`linear_nf4` (`stdlib/quant.linnet:189-199`) in f64 over the exact f32
+    weight `quant.nf4_weight`: the tolerance reference of the NF4 GEMV."""
+    y = product_f64(x, quant.nf4_weight(codes, absmax, block))
+    return y if bias is None else y + np.asarray(bias, dtype=np.float64)

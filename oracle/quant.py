@@ -380,3 +380,63 @@ def dequantize_mxfp4(blocks: np.ndarray, scales: np.ndarray) -> np.ndarray:
     values = values.reshape(*b.shape[:-1], 32)
     factor = np.ldexp(np.float32(1.0), np.asarray(scales).astype(np.int32) - 127).astype(np.float32)
     return (values * factor[..., None]).reshape(*b.shape[:-2], b.shape[-2] * 32)
+
+
+# ------------------------------------------------------------------------ NF4
+
+# QLoRA's NormalFloat-4 values by code, as bitsandbytes' map holds them (the
+# reference's `NF4`, `python/linnet/src/linnet/quant.py:373-394`, and
+# `std.dtypes::nf4`, `stdlib/dtypes.linnet:32-52`).
+NF4_VALUES = np.array(
+    [-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453, -0.28444138169288635,
+     -0.18477343022823334, -0.09105003625154495, 0.0, 0.07958029955625534, 0.16093020141124725,
+     0.2461123019456863, 0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
+     0.7229568362236023, 1.0],
+    dtype=np.float32,
+)
+
+
+def nf4_weight(codes: np.ndarray, absmax: np.ndarray, block: int) -> np.ndarray:
+    """`dequantize_nf4` in f32 (`stdlib/quant.linnet:180-187`): codes [Out, In/2]
+    bytes, the first input of a pair in the low nibble; absmax [Out, In/block];
+    `weight[o, i] = NF4_VALUES[q[o, i]] * absmax[o, i // block]`, one f32 product.
+
+    Pin: `NF4_VALUES` against QLoRA's construction (normal quantiles, scipy), and
+    the nibble and block order against a hand-built layer whose every element
+    is told apart (tests/test_oracle.py::test_nf4_table_is_qloras_normal_quantiles,
+    ::test_nf4_weight_from_the_layout_definition)."""
+    q = np.asarray(codes, dtype=np.uint8)
+    values = np.stack([NF4_VALUES[q & 15], NF4_VALUES[q >> 4]], axis=-1).reshape(q.shape[0], 2 * q.shape[1])
+    scale = np.asarray(absmax, dtype=np.float32)
+    return (values.reshape(q.shape[0], -1, block) * scale[:, :, None]).reshape(values.shape).astype(np.float32)
+
+
+def dequantize_nf4(codes: np.ndarray, absmax: np.ndarray, block: int, dtype: str) -> np.ndarray:
+    """`dequantize_nf4<..., T>`: the f32 weight rounded to `dtype`, as the raw
+    storage array of `encode_storage` (`cast<T>` of quant.linnet:186)."""
+    return encode_storage(nf4_weight(codes, absmax, block), dtype)
+
+
+def bnb_nf4_layer(packed: np.ndarray, absmax: np.ndarray, out_features: int, in_features: int, block: int,
+                  nested_absmax: np.ndarray | None = None, nested_map: np.ndarray | None = None,
+                  nested_block: int = 0, offset: float = 0.0) -> tuple[np.ndarray, np.ndarray]:
+    """A bitsandbytes 4-bit NF4 layer as `Nf4Linear` holds it: (codes [Out, In/2]
+    with each byte's nibbles swapped, absmax [Out, In/block] f32). Restates
+    `_bnb_nf4` (`quant.py:414-466`): bitsandbytes keeps the first code of a pair in
+    the high nibble; with double quantization a block's absmax is
+    `nested_map[code] * nested_absmax[i // nested_block] + float32(offset)` in f32.
+
+    Pin: a layer packed the way the reference's test writes bitsandbytes'
+    (`codes[1::2] | codes[0::2] << 4`, `python/linnet/tests/test_nf4.py:49-75`)
+    comes back as its codes, and nested scales built from exact binary values
+    decode to their known sums (tests/test_oracle.py::test_bnb_nf4_layer)."""
+    raw = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    swapped = ((raw >> 4) | (raw << 4)).astype(np.uint8)
+    if nested_map is not None:
+        codes = np.asarray(absmax, dtype=np.uint8).reshape(-1)
+        outer = np.asarray(nested_absmax, dtype=np.float32).reshape(-1)
+        scale = np.asarray(nested_map, dtype=np.float32).reshape(-1)[codes] * outer[np.arange(codes.size) // nested_block]
+        scale = (scale + np.float32(offset)).astype(np.float32)
+    else:
+        scale = np.asarray(absmax, dtype=np.float32).reshape(-1)
+    return swapped.reshape(out_features, in_features // 2), scale.reshape(out_features, in_features // block)

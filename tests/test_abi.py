@@ -242,3 +242,25 @@ def test_timeline_needs_a_gpu() -> None:
     from linnet_amd import timeline
 
     assert timeline.main([]) == 2
+
+
+def test_nf4_entry_points_validate() -> None:
+    """The NF4 entries refuse what their kernels do not take, before any device
+    call: odd or non-dividing blocks, the GEMV's blocks that are no multiple of
+    16, inputs past 32768, x's dtype, a half-given double quantization."""
+    def linear(rows: int, out_f: int, in_f: int, block: int, dtype: int = _lib.BF16) -> str:
+        return _status("lnq_nf4_linear", FAKE, in_f, rows, FAKE, FAKE, NULL, FAKE, out_f, out_f, in_f, block, dtype,
+                       NULL)[1]
+
+    assert "multiple of 16" in linear(1, 8, 128, 8)
+    assert "multiple of 16" in linear(1, 8, 96, 64)
+    assert "past the product's 32768" in linear(1, 8, 65536, 64)
+    assert "bf16 or f16" in linear(1, 8, 128, 64, _lib.F32)
+    assert "negative" in linear(-1, 8, 128, 64)
+    assert "aligned" in _status("lnq_nf4_linear", ctypes.c_void_p(4098), 128, 1, FAKE, FAKE, NULL, FAKE, 8, 8, 128, 64,
+                                _lib.BF16, NULL)[1]
+    assert "even" in _status("lnq_nf4_dequant", FAKE, FAKE, FAKE, 4, 126, 63, _lib.BF16, NULL)[1]
+    assert "dtype 5" in _status("lnq_nf4_dequant", FAKE, FAKE, FAKE, 4, 128, 64, 5, NULL)[1]
+    assert "both" in _status("lnq_nf4_repack", FAKE, FAKE, FAKE, NULL, 256, ctypes.c_float(0.0), FAKE, FAKE, 4, 128,
+                             64, NULL)[1]
+    assert _status("lnq_nf4_linear", NULL, 128, 0, NULL, NULL, NULL, NULL, 8, 8, 128, 64, _lib.BF16, NULL)[0] == _lib.LNQ_OK

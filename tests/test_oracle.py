@@ -442,3 +442,85 @@ def test_mxfp4_product_reference_against_a_loop() -> None:
             for o in range(4):
                 assert np.isclose(got[r, k, o], sum(x[r, k, i] * float(w[experts[r, k], o, i]) for i in range(64)),
                                   rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------------ NF4
+
+
+def test_nf4_table_is_qloras_normal_quantiles() -> None:
+    """QLoRA's NF4 (Dettmers et al. 2023, bitsandbytes' `create_normal_map` with
+    offset 0.9677083): 8 positive quantiles of N(0, 1) at float32 linspace(offset,
+    0.5, 9)[:-1], 7 negative ones at linspace(offset, 0.5, 8)[:-1], and 0, sorted
+    and divided by the largest. Catches a mistyped or reordered entry."""
+    from scipy.stats import norm
+
+    offset = 0.9677083
+    positive = norm.ppf(torch.linspace(offset, 0.5, 9)[:-1].numpy())
+    negative = -norm.ppf(torch.linspace(offset, 0.5, 8)[:-1].numpy())
+    values = np.sort(np.concatenate([positive, [0.0], negative]))
+    values = values / values.max()
+    np.testing.assert_array_equal(values.astype(np.float32), quant.NF4_VALUES)
+
+
+def test_nf4_weight_from_the_layout_definition() -> None:
+    """Byte j of a row holds inputs 2j (low nibble) and 2j + 1 (high); absmax
+    [o, b] scales inputs b*block .. b*block + block - 1 of row o. Every element
+    gets its own code and power-of-two scale, so a swapped nibble order, a block
+    index along the wrong axis or a transposed scale fails."""
+    out_features, in_features, block = 3, 16, 4
+    codes = np.array([[(5 * o + 3 * i) % 16 for i in range(in_features)] for o in range(out_features)], np.uint8)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    absmax = np.array([[2.0 ** (4 * o + b - 3) for b in range(in_features // block)] for o in range(out_features)],
+                      np.float32)
+    got = quant.nf4_weight(packed, absmax, block)
+    for o in range(out_features):
+        for i in range(in_features):
+            assert got[o, i] == np.float32(float(quant.NF4_VALUES[(5 * o + 3 * i) % 16]) * 2.0 ** (4 * o + i // block - 3))
+    rng = np.random.default_rng(21)
+    packed = rng.integers(0, 256, (5, 32)).astype(np.uint8)
+    absmax = rng.uniform(0.01, 3.0, (5, 2)).astype(np.float32)
+    weight = quant.nf4_weight(packed, absmax, 32)
+    for dtype, torch_dtype in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        want = torch.from_numpy(weight).to(torch_dtype).float().numpy()
+        np.testing.assert_array_equal(quant.decode_storage(quant.dequantize_nf4(packed, absmax, 32, dtype), dtype), want)
+
+
+def test_bnb_nf4_layer() -> None:
+    """bitsandbytes packs the first code of a pair in the high nibble (the
+    reference's test writes `codes[1::2] | codes[0::2] << 4`); double quantization
+    decodes `nested_map[code] * nested_absmax[i // nested_block] + offset`. With
+    exact binary values the decoded scales are known sums; a missed swap, a wrong
+    nested index or a dropped offset fails."""
+    rng = np.random.default_rng(3)
+    out_features, in_features, block, nested_block = 4, 64, 16, 5
+    codes = rng.integers(0, 16, out_features * in_features).astype(np.uint8)
+    packed = (codes[1::2] | (codes[0::2] << 4)).astype(np.uint8)
+    plain = rng.uniform(0.1, 2.0, out_features * in_features // block).astype(np.float32)
+    got_codes, got_scale = quant.bnb_nf4_layer(packed, plain, out_features, in_features, block)
+    unpacked = np.stack([got_codes & 15, got_codes >> 4], axis=-1).reshape(-1)
+    np.testing.assert_array_equal(unpacked, codes)
+    np.testing.assert_array_equal(got_scale.reshape(-1), plain)
+    blocks = out_features * in_features // block
+    scale_codes = rng.integers(0, 256, blocks).astype(np.uint8)
+    nested_map = (np.arange(256, dtype=np.float32) - 128) / 64
+    nested_absmax = np.array([0.5, 2.0, 4.0, 0.25], np.float32)
+    _, decoded = quant.bnb_nf4_layer(packed, scale_codes, out_features, in_features, block, nested_absmax,
+                                     nested_map, nested_block, 0.75)
+    want = [(int(c) - 128) / 64 * float(nested_absmax[i // nested_block]) + 0.75 for i, c in enumerate(scale_codes)]
+    np.testing.assert_array_equal(decoded.reshape(-1), np.array(want, np.float32))
+
+
+def test_nf4_reference_against_a_loop() -> None:
+    rng = np.random.default_rng(4)
+    packed = rng.integers(0, 256, (3, 16)).astype(np.uint8)
+    absmax = rng.uniform(0.5, 1.5, (3, 2)).astype(np.float32)
+    x = rng.standard_normal((2, 32))
+    bias = rng.standard_normal(3)
+    got = linear.nf4_reference_f64(x, packed, absmax, 16, bias)
+    for r in range(2):
+        for o in range(3):
+            want = bias[o]
+            for i in range(32):
+                code = int(packed[o, i // 2] >> (4 * (i % 2))) & 15
+                want += x[r, i] * float(quant.NF4_VALUES[code] * absmax[o, i // 16])  # the weight is f32
+            assert np.isclose(got[r, o], want, rtol=1e-12, atol=1e-12)
