@@ -18,7 +18,7 @@ and fp8 MFMA peaks), the int4 Llama-shaped decode step (config 5), the GPTQ /
 AWQ checkpoint repack kernel, gpt-oss-20B's MXFP4 expert projections at decode, a measured copy-bandwidth ceiling, and the
 reference's CPU path timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|8bit|llama|checkpoint|mxfp4|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemv|gemm|8bit|llama|checkpoint|mxfp4|nf4|all]
 
 The default K = 2000 GEMV calls (~16 ms) times the steady state of a decode
 loop; 200 calls (~1.8 ms) read 10-15% slower, the clock still ramping.
@@ -51,7 +51,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=2000)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "llama", "checkpoint", "mxfp4", "all"), default="all")
+    p.add_argument("--only", choices=("gemv", "gemm", "8bit", "llama", "checkpoint", "mxfp4", "nf4", "all"), default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
@@ -211,6 +211,10 @@ def main() -> int:
         extra["int4_repack_K4096_N14336"] = checkpoint_repack(torch, kernels, dev, timed_graph, not args.no_cpu)
     torch.cuda.synchronize()
 
+    if args.only in ("nf4", "all"):
+        extra["nf4_K4096_N14336"] = nf4_decode(torch, kernels, dev, timed_graph, not args.no_cpu)
+    torch.cuda.synchronize()
+
     # --- CPU baseline: the reference's CPU path (generated source: the weight
     # dequantized once at prepare, then bf16 F.linear per call), on host cores.
     cpu = None
@@ -247,6 +251,12 @@ def main() -> int:
         entry = extra["mxfp4_experts_gpt_oss_20b"]["gate_up_B1"]
         metric_value, unit, ms = entry["gbps"], "GB/s", entry["us"] / 1e3
         config = {"workload": "MXFP4 experts (gpt-oss-20B gate/up, 32 experts, top 4), batch 1"}
+        roofline = {"bound": "hbm", "achieved": entry["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": entry["frac_hbm_peak"], "traffic": None}
+    elif "nf4_K4096_N14336" in extra and args.only == "nf4":  # --only nf4: the NF4 GEMV at one row
+        entry = extra["nf4_K4096_N14336"]["M1"]
+        metric_value, unit, ms = entry["gbps"], "GB/s", entry["us"] / 1e3
+        config = {"workload": "NF4 (Nf4Linear, block 64) decode GEMV, M=1 K=4096 N=14336"}
         roofline = {"bound": "hbm", "achieved": entry["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": entry["frac_hbm_peak"], "traffic": None}
     else:  # --only checkpoint: the GPTQ repack of one layer
@@ -523,6 +533,48 @@ def mxfp4_decode(torch, kernels, dev, timed_graph, with_cpu: bool) -> dict[str, 
             found[f"{name}_B{batch}"] = entry
             del x
         del copies
+    return found
+
+
+def nf4_decode(torch, kernels, dev, timed_graph, with_cpu: bool) -> dict[str, object]:
+    """`Nf4Linear` (block 64, bf16) on Llama-3.1-8B's 4096 -> 14336 at 1, 4 and 8
+    rows: the NF4 GEMV (`lnq_nf4_linear`) and the reference's body (the weight
+    widened by `lnq_nf4_dequant`, then bf16 `F.linear`, hipBLASLt), over 8 copies
+    of random codes and absmax (265 MB > the Infinity Cache). Bytes: codes,
+    absmax, x and y. The CPU leg times the reference's body on the host
+    (codebook lookup, scale, bf16 `F.linear`) at one row."""
+    n, k, block, copies = 14336, 4096, 64, 8
+    g = torch.Generator(device=dev).manual_seed(0)
+    layers = [(torch.randint(0, 256, (n, k // 2), generator=g, device=dev, dtype=torch.uint8),
+               torch.rand(n, k // block, generator=g, device=dev) * 0.1 + 0.01) for _ in range(copies)]
+    found: dict[str, object] = {}
+    for m in (1, 4, 8):
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        gemv = [lambda c=c, a=a: kernels.nf4_linear(x, c, a, block) for c, a in layers]
+        wide = [lambda c=c, a=a: torch.nn.functional.linear(x, kernels.nf4_dequantize(c, a, block, torch.bfloat16))
+                for c, a in layers]
+        nbytes = n * k // 2 + n * (k // block) * 4 + m * k * 2 + m * n * 2
+        sec = timed_graph(gemv, 200, 10)
+        sec_wide = timed_graph(wide, 80, 10)
+        entry = {"us": round(sec * 1e6, 2), "gbps": round(nbytes / sec / 1e9, 1),
+                 "frac_hbm_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4), "bytes_per_call": nbytes,
+                 "dequant_linear_us": round(sec_wide * 1e6, 2)}
+        if with_cpu and m == 1:
+            table = torch.tensor([-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+                                  -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+                                  0.07958029955625534, 0.16093020141124725, 0.2461123019456863, 0.33791524171829224,
+                                  0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0])
+            codes, absmax, xc = layers[0][0].cpu(), layers[0][1].cpu(), x.cpu()
+            t0 = time.perf_counter()
+            values = torch.stack([table[(codes & 15).long()], table[(codes >> 4).long()]], dim=-1).reshape(n, k)
+            weight = (values.reshape(n, k // block, block) * absmax[:, :, None]).reshape(n, k).to(torch.bfloat16)
+            torch.nn.functional.linear(xc, weight)
+            cpu_s = time.perf_counter() - t0
+            entry["cpu_reference_body_ms"] = round(cpu_s * 1e3, 1)
+            entry["cpu_reference_body_gbps"] = round(nbytes / cpu_s / 1e9, 3)
+            del codes, absmax, values, weight
+        found[f"M{m}"] = entry
+    del layers
     return found
 
 
