@@ -13,7 +13,7 @@
 //   16-bit patterns (bf16 or f16, x's type) are held as two 16-byte planes (low
 //   bytes, high bytes) in 8 SGPRs, and v_perm_b32 selects four codes' bytes from
 //   a plane at once (two perms over the 8-entry halves, v_bfi_b32 on the code's
-//   bit 3). Each pair of values meets a pair of x in one v_dot2_f32_{bf16,f16};
+//   bit 3, itself spread to a byte mask by a v_perm_b32). Each pair of values meets a pair of x in one v_dot2_f32_{bf16,f16};
 //   a block's sum is scaled by its absmax and added in f32. The values are
 //   rounded to x's type once (as the reference's body rounds the scaled weight
 //   to T before its product), so the result is within T's rounding of the
@@ -108,19 +108,29 @@ __global__ __launch_bounds__(256) void nf4_dequant_kernel(const uint8_t* __restr
 }
 
 // ---------------------------------------------------------------------- GEMV
-// Values of the four codes in sel's bytes (each 0..15) as two pairs of 16-bit
-// patterns: a = (value of byte 0, value of byte 1), b = (byte 2, byte 3), the
-// first of each pair in the low half.
-__device__ inline void nf4_lookup4(uint32_t sel, const Nf4Planes& p, uint32_t& a, uint32_t& b) {
-  const uint32_t s7 = sel & 0x07070707u;
-  const uint32_t b3 = sel & 0x08080808u;
-  const uint32_t upper = (b3 << 5) - (b3 >> 3);  // 0xff in the bytes whose code is 8..15
-  const uint32_t lo = (upper & __builtin_amdgcn_perm(p.lo[3], p.lo[2], s7)) |
-                      (~upper & __builtin_amdgcn_perm(p.lo[1], p.lo[0], s7));
-  const uint32_t hi = (upper & __builtin_amdgcn_perm(p.hi[3], p.hi[2], s7)) |
-                      (~upper & __builtin_amdgcn_perm(p.hi[1], p.hi[0], s7));
-  a = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-  b = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+// Values of the eight codes of w (nibble j is input j of the 8) as four pairs
+// of 16-bit patterns, the first of each pair in the low half: v[0] = (0, 2),
+// v[1] = (4, 6), v[2] = (1, 3), v[3] = (5, 7). For the four codes of one nibble
+// position (low nibbles, then high), v_perm_b32 looks up their low and high
+// bytes in the 8-entry halves of the planes (selector = code & 7), and v_bfi_b32
+// keeps the upper half's bytes where the code's bit 3 is set. That mask comes
+// from one more v_perm_b32: its selectors 8..11 replicate bit 15, 31, 47 or 63
+// of the 8-byte source, and shifts of w put bit 3 of the four codes there
+// (selector dword 0x090B080A: byte 0 <- bit 47, 1 <- 15, 2 <- 63, 3 <- 31).
+__device__ inline void nf4_lookup8(uint32_t w, const Nf4Planes& p, uint32_t v[4]) {
+  const uint32_t upper_lo = __builtin_amdgcn_perm(w << 12, w << 4, 0x090B080Au);  // bits 3, 11, 19, 27
+  const uint32_t upper_hi = __builtin_amdgcn_perm(w << 8, w, 0x090B080Au);        // bits 7, 15, 23, 31
+  const uint32_t sel[2] = {w & 0x07070707u, (w >> 4) & 0x07070707u};
+  const uint32_t upper[2] = {upper_lo, upper_hi};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t lo = (upper[h] & __builtin_amdgcn_perm(p.lo[3], p.lo[2], sel[h])) |
+                        (~upper[h] & __builtin_amdgcn_perm(p.lo[1], p.lo[0], sel[h]));
+    const uint32_t hi = (upper[h] & __builtin_amdgcn_perm(p.hi[3], p.hi[2], sel[h])) |
+                        (~upper[h] & __builtin_amdgcn_perm(p.hi[1], p.hi[0], sel[h]));
+    v[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+    v[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+  }
 }
 
 template <int DT>
@@ -229,11 +239,7 @@ __global__ __launch_bounds__(nf4::THREADS) void nf4_gemv_kernel(const uint16_t* 
     for (int s = 0; s < SLOTS; ++s) {
       uint32_t wv[8];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t c = e == 0 ? q[i][s].x : q[i][s].y;
-        nf4_lookup4(c & 0x0f0f0f0fu, planes, wv[4 * e + 0], wv[4 * e + 1]);
-        nf4_lookup4((c >> 4) & 0x0f0f0f0fu, planes, wv[4 * e + 2], wv[4 * e + 3]);
-      }
+      for (int e = 0; e < 2; ++e) nf4_lookup8(e == 0 ? q[i][s].x : q[i][s].y, planes, wv + 4 * e);
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         float part = 0.0f;
