@@ -9,7 +9,10 @@ points as they are stored, so `prepare` converts nothing and the executable
 holds no bytes of its own (Marlin keeps a repacked copy). A layer in GPTQ's
 activation order (`take_inputs(x, order)` right before the product,
 `stdlib/quant.linnet:163-174`) is taken as one region of both calls and runs on
-`lnq_int4_linear_ordered`, the gather fused into the one-token GEMV. `execute` enqueues on
+`lnq_int4_linear_ordered`, the gather fused into the one-token GEMV. A
+`std.quant::linear_nf4` call (an `Nf4Linear`, which the reference leaves to "a
+backend with a 4-bit product", `stdlib/quant.linnet:189-199`) runs on the NF4
+kernels the same way, its codes and absmax read as stored. `execute` enqueues on
 the caller's stream and never waits, allocates its output with PyTorch, and may
 be recorded into a HIP graph.
 
@@ -36,6 +39,7 @@ from .torch import kernels
 
 CALLEE = "std.quant::linear_int4_groups"
 TAKE = "std.quant::take_inputs"
+NF4_CALLEE = "std.quant::linear_nf4"
 DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16}
 
 
@@ -119,26 +123,59 @@ class MI355XInt4:
             region = self._t.Region.of(graph, call.start, call.stop, call.index)
             if tuple(region.inputs) == (x.value,):
                 yield region
+        yield from self._match_nf4(graph, persistent)
 
-    def compile(self, region: Any, target: Any, options: Any) -> _Int4Linear:
+    def _match_nf4(self, graph: Any, persistent: set[int]) -> Iterable[Any]:
+        """Each `linear_nf4<Block>(x, q, absmax, bias)` call (`stdlib/quant.linnet:189-199`,
+        an `Nf4Linear`): bf16 / f16 x, q [Out, In] nf4 and absmax [Out, In / Block]
+        f32 parameters, an even Block; `nf4_linear` runs it (the NF4 GEMV up to 8
+        rows, the widened weight and its product beyond)."""
+        for call in graph.semantic_calls(NF4_CALLEE):
+            if len(call.arguments) != 4:
+                continue
+            x, q, absmax, bias = call.arguments
+            if len(q.shape) != 2 or len(absmax.shape) != 2 or absmax.shape[0] != q.shape[0] or not absmax.shape[1]:
+                continue
+            in_features, blocks = q.shape[1], absmax.shape[1]
+            block = in_features // blocks
+            if not (
+                x.dtype in DTYPES
+                and absmax.dtype == "f32"
+                and block * blocks == in_features
+                and block % 2 == 0
+                and q.value in persistent
+                and absmax.value in persistent
+                and (bias.value is None or bias.value in persistent)
+            ):
+                continue
+            region = self._t.Region.of(graph, call.start, call.stop, call.index)
+            if tuple(region.inputs) == (x.value,):
+                yield region
+
+    def compile(self, region: Any, target: Any, options: Any) -> _Int4Linear | _Nf4Linear:
         graph = region.graph
         if region.call is None:
             raise self._t.PlanError("linnet-amd takes a `linear_int4_groups` call")
         call = graph.calls[region.call]
-        x, q, scale, zero, bias = call.arguments
         path = {value: p for p, value in graph.parameters.items()}
-        order = None
-        if region.start != call.start:
-            take = _takes(graph, set(path)).get(x.value)
-            if take is None or region.start != take.start:
-                raise self._t.PlanError("linnet-amd takes `take_inputs` only right before `linear_int4_groups`")
-            order = path[take.arguments[1].value]
         values = graph.values
         meta = self._t.ExecutableMeta(
             tuple(self._t.TensorSpec(values[v].shape, values[v].dtype) for v in region.inputs),
             tuple(self._t.TensorSpec(values[v].shape, values[v].dtype) for v in region.outputs),
             holds=0,
         )
+        if call.callee == NF4_CALLEE:
+            x, q, absmax, bias = call.arguments
+            return _Nf4Linear(meta, (path[q.value], path[absmax.value]),
+                              path[bias.value] if bias.value is not None else None, DTYPES[x.dtype],
+                              q.shape[1] // absmax.shape[1])
+        x, q, scale, zero, bias = call.arguments
+        order = None
+        if region.start != call.start:
+            take = _takes(graph, set(path)).get(x.value)
+            if take is None or region.start != take.start:
+                raise self._t.PlanError("linnet-amd takes `take_inputs` only right before `linear_int4_groups`")
+            order = path[take.arguments[1].value]
         return _Int4Linear(meta, (path[q.value], path[scale.value], path[zero.value]),
                            path[bias.value] if bias.value is not None else None, DTYPES[x.dtype], order)
 
@@ -195,4 +232,33 @@ class _Int4Linear:
         return [y.reshape(*x.shape[:-1], y.shape[-1])]
 
 
-__all__ = ["CALLEE", "TAKE", "MI355XInt4"]
+class _Nf4Linear:
+    """One `linear_nf4` call on `kernels.nf4_linear`: the codes ([Out, In/2]
+    bytes, as the model binds an nf4 parameter) and absmax read as stored."""
+
+    def __init__(self, meta: Any, paths: tuple[str, str], bias: str | None, dtype: torch.dtype, block: int) -> None:
+        self._meta = meta
+        self._paths = paths
+        self._bias = bias
+        self._dtype = dtype
+        self._block = block
+
+    @property
+    def meta(self) -> Any:
+        return self._meta
+
+    def prepare(self, context: Any) -> None:
+        q, absmax = (context.parameters[p] for p in self._paths)
+        if not (q.is_cuda and absmax.is_cuda):
+            raise LinnetError("linnet-amd: the NF4 parameters are not on the GPU")
+        if q.dtype != torch.uint8 or absmax.dtype != torch.float32:
+            raise LinnetError("linnet-amd: NF4 codes are uint8 bytes and absmax float32")
+
+    def execute(self, inputs: Sequence[torch.Tensor], outputs: Sequence[torch.Tensor], context: Any) -> Sequence[torch.Tensor]:
+        q, absmax = (context.parameters[p] for p in self._paths)
+        bias = context.parameters[self._bias] if self._bias is not None else None
+        (x,) = inputs
+        return [kernels.nf4_linear(x, q, absmax, self._block, bias)]
+
+
+__all__ = ["CALLEE", "NF4_CALLEE", "TAKE", "MI355XInt4"]

@@ -135,6 +135,18 @@ class Graph:
         self.calls.append(Call(n, "std.quant::linear_int4_groups", True, args, (y,), start, start + 1))
         return self.calls[-1]
 
+    def nf4(self, name, rows, out, inp, block, dtype="bf16", bias=False, persistent=True, absmax_dtype="f32"):
+        """`std.quant::linear_nf4<block>(x, q, absmax, bias)`."""
+        x = self.value((rows, inp), dtype)
+        q = self.value((out, inp), "nf4", f"{name}.weight" if persistent else None)
+        a = self.value((out, inp // block), absmax_dtype, f"{name}.absmax")
+        b = self.value((out,), dtype, f"{name}.bias") if bias else Operand(None, (), dtype)
+        y = self.value((rows, out), dtype)
+        n = len(self.calls)
+        start = self.calls[-1].stop if self.calls else 0
+        self.calls.append(Call(n, "std.quant::linear_nf4", True, (x, q, a, b), (y,), start, start + 1))
+        return self.calls[-1]
+
     def read(self, operand):
         """A later call (another op) that reads `operand`."""
         n = len(self.calls)

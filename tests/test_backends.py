@@ -162,3 +162,71 @@ def test_ordered_executable_conforms_to_the_fallback() -> None:
         err = (got.float() - want.float()).abs().max().item()
         print(f"region {region.call}: max abs err {err:.3e}")
         assert got.shape == want.shape and err <= 1e-2 * want.float().abs().max().item(), err
+
+
+def _nf4_graph() -> tuple[Graph, list[bool]]:
+    g = Graph()
+    cases = [
+        (dict(name="n1", rows=1, out=96, inp=512, block=64), True),
+        (dict(name="n2", rows=12, out=40, inp=256, block=32, dtype="f16", bias=True), True),
+        (dict(name="n3", rows=2, out=32, inp=512, block=64, dtype="f32"), False),  # f32 x
+        (dict(name="n4", rows=2, out=32, inp=512, block=64, persistent=False), False),  # codes not a parameter
+        (dict(name="n5", rows=2, out=32, inp=510, block=85), False),  # odd block
+        (dict(name="n6", rows=2, out=32, inp=512, block=64, absmax_dtype="bf16"), False),  # absmax not f32
+    ]
+    for kwargs, _ in cases:
+        g.nf4(**kwargs)
+    return g, [ok for _, ok in cases]
+
+
+def test_match_takes_the_nf4_calls() -> None:
+    from linnet_amd.backends import NF4_CALLEE
+
+    g, ok = _nf4_graph()
+    backend = MI355XInt4(types=TYPES)
+    regions = list(backend.match(g, SimpleNamespace(kind="cuda", index=0)))
+    assert {r.call for r in regions} == {i for i, good in enumerate(ok) if good}
+    assert all(g.calls[r.call].callee == NF4_CALLEE for r in regions)
+    made = backend.compile(regions[0], SimpleNamespace(kind="cuda"), None)
+    assert made.meta.holds == 0 and [s.shape for s in made.meta.inputs] == [(1, 512)]
+    assert [s.shape for s in made.meta.outputs] == [(1, 96)]
+
+
+@pytest.mark.gpu
+def test_nf4_executable_conforms_to_the_fallback() -> None:
+    """The reference's body for `linear_nf4` (the widened weight, then the
+    product) against the executable, region by region."""
+    from linnet_amd.torch import kernels
+
+    backend = MI355XInt4(types=TYPES)
+    g, _ = _nf4_graph()
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    params = {}
+    for call in g.calls:
+        x, q, a, b = call.arguments
+        out, inp = q.shape
+        params[[p for p, v in g.parameters.items() if v == a.value][0].removesuffix("absmax") + "weight"] = torch.randint(
+            0, 256, (out, inp // 2), generator=gen, device="cuda", dtype=torch.uint8)
+        params[[p for p, v in g.parameters.items() if v == a.value][0]] = torch.rand(
+            *a.shape, generator=gen, device="cuda") * 0.1
+        if b.value is not None:
+            params[[p for p, v in g.parameters.items() if v == b.value][0]] = torch.randn(
+                out, generator=gen, device="cuda").to(torch.float16 if x.dtype == "f16" else torch.bfloat16)
+    context = SimpleNamespace(parameters=params, target=SimpleNamespace(kind="cuda", index=0))
+    regions = list(backend.match(g, context.target))
+    assert len(regions) == 2
+    for region in regions:
+        made = backend.compile(region, context.target, None)
+        made.prepare(context)
+        x, q, a, b = g.calls[region.call].arguments
+        dtype = torch.bfloat16 if x.dtype == "bf16" else torch.float16
+        xin = torch.randn(*x.shape, generator=gen, device="cuda").to(dtype)
+        (got,) = made.execute([xin], [], context)
+        prefix = [p for p, v in g.parameters.items() if v == a.value][0].removesuffix("absmax")
+        block = q.shape[1] // a.shape[1]
+        weight = kernels.nf4_dequantize(params[prefix + "weight"], params[prefix + "absmax"], block, torch.float32)
+        want = xin.float() @ weight.T
+        if b.value is not None:
+            want = want + params[prefix + "bias"].float()
+        err = (got.float() - want).abs().max().item()
+        assert got.shape == want.shape and err <= 1e-2 * want.abs().max().item(), err
