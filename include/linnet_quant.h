@@ -392,7 +392,8 @@ LNQ_API LnqStatus lnq_nf4_dequant(const uint8_t* codes, const float* absmax, voi
  * (row strides in elements), x / bias / y of `dtype` (bf16 or f16). The weight
  * is read as stored: each code's value, rounded once to `dtype`, meets x in an
  * f32 dot product; a block's sum is scaled by its absmax and the blocks added in
- * f32, the row rounded once. Up to 4 rows of x a pass over the weight. block %
+ * f32, the row rounded once. Up to 8 rows of x a pass over the weight (4 past
+ * in = 8192). block %
  * 16 == 0, in % block == 0, in <= 32768, the codes under 2 GiB; x 16-byte aligned
  * with x_stride % 8 == 0. Replaces: `linear_nf4`'s body, the widened weight and
  * its product (stdlib/quant.linnet:189-199), for the few-row calls. */

@@ -7,7 +7,7 @@
 // Three kernels:
 // - nf4_dequant_kernel: the weight in T, the f32 product of the code's value and
 //   the scale rounded once (`dequantize_nf4`, quant.linnet:180-187), bit for bit.
-// - nf4_gemv_kernel: y = x W^T (+ bias) for up to 4 rows of x, the weight read
+// - nf4_gemv_kernel: y = x W^T (+ bias) for up to 8 rows of x, the weight read
 //   once from HBM as it is stored. NF4's values are no affine function of the
 //   code, so the widening is a table lookup done in registers: the 16 values'
 //   16-bit patterns (bf16 or f16, x's type) are held as two 16-byte planes (low
@@ -49,7 +49,7 @@ constexpr float VALUES[16] = {
 constexpr int UNIT = 16;       // inputs of a lane's unit
 constexpr int THREADS = 256;   // lanes of a GEMV workgroup
 constexpr int MAX_SLOTS = 8;   // In <= 16 * 256 * 8 = 32768 for the GEMV
-constexpr int MAX_ROWS_X = 4;  // rows of x a GEMV launch takes
+constexpr int MAX_ROWS_X = 8;  // rows of x a GEMV launch takes (In <= 8192; 4 past that)
 }  // namespace nf4
 
 __constant__ float kNf4Values[16] = {
@@ -398,10 +398,13 @@ LNQ_API LnqStatus lnq_nf4_linear(const void* x, int64_t x_stride, int64_t rows, 
   const Nf4Planes planes = planes_for(dtype);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int O = static_cast<int>(out_features), K = static_cast<int>(in_features), B = static_cast<int>(block);
-  // Up to 4 rows of x a launch; more rows take more launches over the same weight.
-  for (int64_t r0 = 0; r0 < rows; r0 += nf4::MAX_ROWS_X) {
-    const int part = static_cast<int>(rows - r0 < nf4::MAX_ROWS_X ? rows - r0 : nf4::MAX_ROWS_X);
-    const int mr = part == 1 ? 1 : part == 2 ? 2 : 4;
+  // Up to 8 rows of x a launch (4 past In = 8192); more rows take more launches
+  // over the same weight.
+  // x's registers grow with rows x slots: 8 rows a pass up to 2 slots, else 4.
+  const int per_pass = slots <= 2 ? nf4::MAX_ROWS_X : 4;
+  for (int64_t r0 = 0; r0 < rows; r0 += per_pass) {
+    const int part = static_cast<int>(rows - r0 < per_pass ? rows - r0 : per_pass);
+    const int mr = part == 1 ? 1 : part == 2 ? 2 : part <= 4 ? 4 : 8;
     LNQ_REQUIRE((part - 1) * x_stride + in_features < (int64_t{1} << 30), "lnq_nf4_linear: x past 1 GiB");
     const auto* xs = static_cast<const uint16_t*>(x) + r0 * x_stride;
     auto* ys = static_cast<uint16_t*>(y) + r0 * y_stride;
@@ -420,11 +423,17 @@ LNQ_API LnqStatus lnq_nf4_linear(const void* x, int64_t x_stride, int64_t rows, 
     case 4: LNQ_NF4_GO(DT, M, 4); break; \
     default: LNQ_NF4_GO(DT, M, 8); break; \
   }
+#define LNQ_NF4_SL8(DT)                 \
+  switch (slots) {                      \
+    case 1: LNQ_NF4_GO(DT, 8, 1); break; \
+    default: LNQ_NF4_GO(DT, 8, 2); break; \
+  }
 #define LNQ_NF4_MR(DT)                  \
   switch (mr) {                         \
     case 1: LNQ_NF4_SL(DT, 1); break;   \
     case 2: LNQ_NF4_SL(DT, 2); break;   \
-    default: LNQ_NF4_SL(DT, 4); break;  \
+    case 4: LNQ_NF4_SL(DT, 4); break;   \
+    default: LNQ_NF4_SL8(DT); break;    \
   }
     if (dtype == LNQ_BF16) {
       LNQ_NF4_MR(LNQ_BF16)
@@ -432,6 +441,7 @@ LNQ_API LnqStatus lnq_nf4_linear(const void* x, int64_t x_stride, int64_t rows, 
       LNQ_NF4_MR(LNQ_F16)
     }
 #undef LNQ_NF4_MR
+#undef LNQ_NF4_SL8
 #undef LNQ_NF4_SL
 #undef LNQ_NF4_GO
     const LnqStatus st = launched("nf4_gemv");

@@ -652,16 +652,19 @@ def nf4_dequantize(codes: torch.Tensor, absmax: torch.Tensor, block: int, dtype:
 
 
 # Rows of x up to which `nf4_linear` reads the stored weight with the NF4 GEMV
-# (4 rows a pass over the weight); more rows widen the weight and multiply. At
-# 4096 -> 14336 (bf16, graph-replayed): 1 row 12.1 us, 4 rows 15.9, 8 rows 31.2,
-# 16 rows 61 us, against 57-59 us for the widened weight and its product.
-NF4_GEMV_ROWS = 8
+# (8 rows a pass over the weight up to In = 8192, 4 past it); more rows widen
+# the weight and multiply. bf16, graph-replayed, against 57 us for the widened
+# weight and its product: 4096 -> 14336 at 1 / 8 / 16 rows 12.0 / 21.6 / 41.8
+# us; 14336 -> 4096 at 1 / 8 / 12 rows 11.5 / 35.3 / 52.5 us.
+NF4_GEMV_ROWS = 16
+NF4_GEMV_ROWS_WIDE = 8  # In > 8192
 NF4_GEMV_MAX_IN = 32768
 
 
 def nf4_gemv_fits(rows: int, in_features: int, block: int, dtype: torch.dtype) -> bool:
     """Whether `nf4_linear` takes the GEMV for this call."""
-    return (dtype in _HALF and rows <= NF4_GEMV_ROWS and block % 16 == 0 and in_features % block == 0
+    limit = NF4_GEMV_ROWS if in_features <= 8192 else NF4_GEMV_ROWS_WIDE
+    return (dtype in _HALF and rows <= limit and block % 16 == 0 and in_features % block == 0
             and 0 < in_features <= NF4_GEMV_MAX_IN)
 
 
@@ -694,7 +697,7 @@ def nf4_gemv(x: torch.Tensor, codes: torch.Tensor, absmax: torch.Tensor, block: 
 def nf4_linear(x: torch.Tensor, codes: torch.Tensor, absmax: torch.Tensor, block: int,
                bias: torch.Tensor | None = None) -> torch.Tensor:
     """`linear_nf4` (`stdlib/quant.linnet:189-199`): up to `NF4_GEMV_ROWS` rows of
-    bf16 / f16 x on the NF4 GEMV; otherwise the weight widened by the HIP
+    bf16 / f16 x (`NF4_GEMV_ROWS_WIDE` past In = 8192) on the NF4 GEMV; otherwise the weight widened by the HIP
     dequantize kernel, then multiplied in x's type (the reference's own body)."""
     _on_gpu("nf4_linear", x, codes, absmax, bias)
     out_features, in_features = _nf4_operands("nf4_linear", codes, absmax, block)

@@ -4,8 +4,8 @@ The layer holds what `linnet_amd.quant.import_quantized` writes for a
 bitsandbytes NF4 checkpoint: `weight` [Out, In/2] uint8 (QLoRA's 4-bit
 NormalFloat codes, the first input of a pair in the low nibble), `absmax`
 [Out, In/block] float32 and an optional `bias` in the activation dtype. Its
-forward is `linear_nf4`: up to 8 rows of bf16 / f16 x read the stored weight
-once every 4 rows with the NF4 GEMV; other calls widen the weight with the HIP
+forward is `linear_nf4`: up to 16 rows of bf16 / f16 x (8 past In = 8192) read
+the stored weight with the NF4 GEMV, once every 8 rows (4 past In = 8192); other calls widen the weight with the HIP
 dequantize kernel (bit for bit the reference's `dequantize_nf4`) and multiply
 in x's type, as the reference's body does.
 """

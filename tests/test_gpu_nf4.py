@@ -3,7 +3,7 @@
 - `lnq_nf4_dequant` is bit-exact against the oracle's `dequantize_nf4` (the f32
   product of the code's value and its block's absmax, rounded once) for bf16,
   f16 and f32, with rows whose bytes do and do not split in 8.
-- The NF4 GEMV (`lnq_nf4_linear`, 1-16 rows of bf16 / f16 x, 4 a pass) is checked against
+- The NF4 GEMV (`lnq_nf4_linear`, 1-16 rows of bf16 / f16 x, 8 a pass up to In = 8192) is checked against
   the oracle's f64 product over the exact f32 weight, within 1e-2 of the
   largest output plus the 16-bit rounding of each one (the reference's
   tolerance for its quantized products, `python/linnet/tests/test_quant_groups.py:165-195`):
@@ -11,7 +11,7 @@
   rounds the scaled weight to T. Shapes cover In below one unit a lane, a
   ragged last unit slot, In = 32768 (8 slots), blocks of 16 to 256, a bias,
   and Llama-3.1-8B's 4096 -> 14336 and 14336 -> 4096.
-- More rows, f32 and blocks the GEMV does not take go through the dequantize
+- More rows (past 16, or 8 past In = 8192), f32 and blocks the GEMV does not take go through the dequantize
   kernel and the product in x's type (the reference's body); f32 is held to
   1e-5 as the reference's NF4 test holds its f32 layer
   (`python/linnet/tests/test_nf4.py:103-115`).
@@ -76,12 +76,13 @@ def _check(got: torch.Tensor, want: np.ndarray) -> None:
 def test_gemv_against_f64(dtype: torch.dtype, rows: int, out_features: int, in_features: int, block: int,
                           bias: bool) -> None:
     print(f"nf4 gemv rows {rows} {out_features}x{in_features} block {block} bias {bias} {dtype}", flush=True)
-    assert kernels.nf4_gemv_fits(rows, in_features, block, dtype) == (rows <= kernels.NF4_GEMV_ROWS)
+    limit = kernels.NF4_GEMV_ROWS if in_features <= 8192 else kernels.NF4_GEMV_ROWS_WIDE
+    assert kernels.nf4_gemv_fits(rows, in_features, block, dtype) == (rows <= limit)
     codes, absmax = _layer(out_features, in_features, block, rows * 7 + out_features)
     gen = torch.Generator().manual_seed(rows + in_features)
     x = torch.randn(rows, in_features, generator=gen).to(dtype)
     b = torch.randn(out_features, generator=gen).to(dtype) if bias else None
-    # The GEMV itself at every row count (4 rows a pass), whatever nf4_linear picks.
+    # The GEMV itself at every row count (several passes past 8 rows), whatever nf4_linear picks.
     got = kernels.nf4_gemv(x.to(DEV), torch.from_numpy(codes).to(DEV), torch.from_numpy(absmax).to(DEV), block,
                            None if b is None else b.to(DEV))
     want = linear.nf4_reference_f64(x.float().numpy(), codes, absmax, block, None if b is None else b.float().numpy())
@@ -99,7 +100,7 @@ def test_gemv_takes_strided_rows_and_leading_axes() -> None:
 
 
 @pytest.mark.parametrize(("dtype", "rows", "block"), [
-    (torch.bfloat16, 9, 64), (torch.float16, 33, 64), (torch.bfloat16, 3, 8), (torch.float32, 1, 64),
+    (torch.bfloat16, 17, 64), (torch.float16, 33, 64), (torch.bfloat16, 3, 8), (torch.float32, 1, 64),
     (torch.float32, 40, 64)])
 def test_wider_calls_widen_then_multiply(dtype: torch.dtype, rows: int, block: int) -> None:
     print(f"nf4 linear rows {rows} block {block} {dtype}", flush=True)
