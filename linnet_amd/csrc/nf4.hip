@@ -144,10 +144,13 @@ __device__ inline float nf4_dot2(uint32_t w, uint32_t x, float c) {
   }
 }
 
-// Output rows a GEMV workgroup takes: about 16 units of codes in flight a lane,
-// and 4..32 partial sums a lane (ROWS * MR) for the reduction's lane groups.
+// Output rows a GEMV workgroup takes: 8 at one unit slot (In <= 4096), about 16
+// units of codes in flight a lane past it, and 4..32 partial sums a lane
+// (ROWS * MR) for the reduction's lane groups. 4096 -> 14336 at one row of x:
+// 8 rows 11.6 us, 16 rows 12.0, 32 rows 12.9; at 14336 -> 4096, 2 rows of x, 16
+// units in flight 13.4 us against 15.8 with 8.
 constexpr int nf4_rows(int mr, int slots) {
-  int r = 16 / slots;
+  int r = slots == 1 ? 8 : 16 / slots;
   if (r > 32 / mr) r = 32 / mr;
   if (r < 4 / mr) r = 4 / mr;
   return r < 1 ? 1 : r;
