@@ -20,10 +20,6 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = PACKAGE.parent / "include"
 LIBDIR = PACKAGE / "_lib"
 LIBRARY = LIBDIR / "liblinnet_quant_hip.so"
-# The diagnostic library of linnet_amd.timeline: the same objects, the one-token
-# GEMV compiled with per-wave timestamps (LNQ_GEMV_TIMELINE).
-TIMELINE = LIBDIR / "liblinnet_quant_timeline.so"
-TIMELINE_SOURCE = "int4_gemv.hip"
 ARCH = "gfx950"
 
 # -packed-fp32-ops keeps hipcc from emitting packed f32 VALU instructions (the
@@ -61,10 +57,10 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def _compile(source: Path, objdir: Path, defines: tuple[str, ...] = (), suffix: str = "") -> Path:
-    obj = objdir / (source.stem + suffix + ".o")
+def _compile(source: Path, objdir: Path) -> Path:
+    obj = objdir / (source.stem + ".o")
     lang = ["-x", "hip"] if source.suffix in (".hip", ".cpp") else []
-    cmd = [hipcc(), *FLAGS, *EXTRA.get(source.name, []), *(f"-D{d}" for d in defines), f"-I{INCLUDE}", *lang, "-c",
+    cmd = [hipcc(), *FLAGS, *EXTRA.get(source.name, []), f"-I{INCLUDE}", *lang, "-c",
            str(source), "-o", str(obj)]
     done = subprocess.run(cmd, capture_output=True, text=True)
     if done.returncode != 0:
@@ -82,22 +78,17 @@ def _link(objects: list[Path], target: Path) -> None:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compiles every source under csrc/ and links the library (and the timeline
-    diagnostic library beside it); returns the library's path."""
+    """Compiles every source under csrc/ and links the library; returns its path."""
     LIBDIR.mkdir(parents=True, exist_ok=True)
     with tempfile.TemporaryDirectory(prefix="lnq_build_") as tmp:
         objdir = Path(tmp)
         srcs = sources()
-        timeline_src = CSRC / TIMELINE_SOURCE
-        jobs = [(src, (), "") for src in srcs] + [(timeline_src, ("LNQ_GEMV_TIMELINE",), "_timeline")]
-        workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
+        workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
         with ThreadPoolExecutor(max_workers=workers) as pool:
-            built = list(pool.map(lambda job: _compile(job[0], objdir, job[1], job[2]), jobs))
-        objects, timeline_obj = built[:-1], built[-1]
+            objects = list(pool.map(lambda src: _compile(src, objdir), srcs))
         _link(objects, LIBRARY)
-        _link([timeline_obj if o.name == timeline_src.stem + ".o" else o for o in objects], TIMELINE)
     if verbose:
-        print(f"built {LIBRARY} and {TIMELINE.name}", file=sys.stderr)
+        print(f"built {LIBRARY}", file=sys.stderr)
     return LIBRARY
 
 

@@ -727,6 +727,11 @@ LNQ_API LnqStatus lnq_prefill_rope(const void* q, const void* k, const void* v, 
                   heads % kv_heads == 0 && heads + 2 * kv_heads <= 65535,
               "lnq_prefill_rope: bad shape (positions <= cap, heads a multiple of kv_heads)");
   LNQ_REQUIRE(in_stride >= head_dim && in_stride % 8 == 0, "lnq_prefill_rope: in_stride is a multiple of 8 elements");
+  // A position's q row spans heads * head_dim elements (k and v rows kv_heads *
+  // head_dim <= that): a shorter stride would read rows that overlap.
+  LNQ_REQUIRE(positions <= 1 || in_stride >= heads * head_dim,
+              "lnq_prefill_rope: row stride %lld is shorter than a q row of %lld elements",
+              static_cast<long long>(in_stride), static_cast<long long>(heads * head_dim));
   if (positions == 0) {
     clear_error();
     return LNQ_OK;

@@ -52,26 +52,6 @@
 
 namespace lnq {
 
-// Per-wave timestamps of the one-token kernel, for the diagnostic build only
-// (compiled with LNQ_GEMV_TIMELINE into liblinnet_quant_timeline.so, read by
-// linnet_amd.timeline): lane 0 of each wave of the first 512 workgroups stores
-// s_memrealtime (100 MHz) at point e: 0 entry, 1 small loads issued, 2 past the
-// start barrier, 3 weights issued, 4 x landed, 5 + T tile T folded, 9 the half
-// tile folded, 10 / 11 before / after the final barrier, 12 end. The product
-// build compiles the points to nothing.
-#ifdef LNQ_GEMV_TIMELINE
-__device__ unsigned long long gemv_stamps[512][16][16];
-#define LNQ_STAMP(e)                                                                                   \
-  do {                                                                                                 \
-    if ((threadIdx.x & 63) == 0 && blockIdx.x < 512)                                                   \
-      gemv_stamps[blockIdx.x][threadIdx.x >> 6][e] = __builtin_amdgcn_s_memrealtime();                 \
-  } while (0)
-#else
-#define LNQ_STAMP(e) \
-  do {               \
-  } while (0)
-#endif
-
 namespace gemv {
 // What x the one-token kernels multiply: x itself; RMSNorm(x) with weights
 // pro.w and pro.eps (x * w staged, the row's factor applied to the sums);
@@ -143,7 +123,6 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   __shared__ float Rsm[gemv::MAX_WAVES][R];  // wave-major: consecutive lanes, consecutive dwords
   __shared__ float Nsm[PRO == gemv::PRO_NORM ? gemv::MAX_WAVES : 1];  // each wave's sum of squares
 
-  LNQ_STAMP(0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
@@ -194,14 +173,12 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     pv0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ru, (k0 + 8 * (lane & 31)) * 2, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
-  LNQ_STAMP(1);
   // Every wave's small loads enter the CU's memory pipeline before any weight
   // load: without this barrier the waves that reach their first load last find
   // it queued behind the other waves' weights (~100 KB), their x and scales land
   // late and their tiles are all multiplied after the stream has ended.
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  LNQ_STAMP(2);
   // Load u: rows n0 + 8u + (lane & 7) at 16-byte piece sigma of the wave's 128
   // bytes; sigma = 2 (lane / 16) + ((lane / 8) % 2 ^ u % 2) puts piece sigma of
   // row r at LDS slot 16 (sigma / 2) + 8 (sigma % 2 ^ u % 2) + r.
@@ -220,12 +197,10 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
 #pragma unroll
   for (int u = 0; u < PRE; ++u) load_weights(u);
   __builtin_amdgcn_sched_barrier(0);
-  LNQ_STAMP(3);
 
   // ---- x: wait for it (and the scales), stage it in pair order, sums of both halves.
   wait_vm<PRE>();
   __builtin_amdgcn_sched_barrier(0);
-  LNQ_STAMP(4);
   if constexpr (ORD) {
     // The workgroup's x in input order (Xsm holds exactly K values), then each
     // lane's 8 taken inputs; the second barrier keeps Xsm until all have read it.
@@ -274,9 +249,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
   hide_in_vgpr(nib_magic);
   const int r7 = col & 7;
   // One MFMA chain over a lane's 16 bytes of weights; returns output register
-  // `reg`. The operand registers stay allocated until the result has been read
-  // (an empty asm uses them), so no later instruction reuses a register that an
-  // MFMA still in flight reads.
+  // `reg`.
   auto chain = [&](const u32x4 (&a)[4], const u32x4 w, int reg) -> float {
     u32x4 b0, b1, b2, b3;
     widen_pair<DT>(w.x, w.y, nib_mask, nib_magic, b0, b1);
@@ -286,9 +259,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     C = mfma16x16x32<DT>(a[1], b1, C);
     C = mfma16x16x32<DT>(a[2], b2, C);
     C = mfma16x16x32<DT>(a[3], b3, C);
-    float c = reg == 0 ? C[0] : C[1];
-    __asm__ volatile("" : "+v"(c) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
-    return c;
+    return reg == 0 ? C[0] : C[1];
   };
   // ---- scales and zero points of each tile's rows (landed with x), so that a
   // tile's fold follows its MFMAs at once: acc = s0 (C0 - z0 xs0) + s1 (C1 - z1 xs1).
@@ -329,7 +300,6 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const float c1 = chain(xa[1], w1, 0);
     const float acc = fmaf(fs0[T], fmaf(fz0[T], xs0, c0), fs1[T] * fmaf(fz1[T], xs1, c1));
     if (lane < 16) Rsm[wave][16 * T + lane] = acc;
-    LNQ_STAMP(5 + T);
   }
   if constexpr (HALF) {
     __builtin_amdgcn_sched_barrier(0);
@@ -345,7 +315,6 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const float part = H == 0 ? fs0[NF] * fmaf(fz0[NF], xs0, c) : fs1[NF] * fmaf(fz1[NF], xs1, c);
     const float acc = part + __shfl_xor(part, 8, 64);
     if (lane < 8) Rsm[wave][16 * NF + lane] = acc;
-    LNQ_STAMP(9);
   }
   if constexpr (PRO == gemv::PRO_NORM) {
     // The wave's 256 inputs are 32-chunk group `wave` of the row (lanes 32..63
@@ -355,9 +324,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
     const float g = sum_over_32_lanes(chunk_squares(v));
     if (lane == 0) Nsm[wave] = g;
   }
-  LNQ_STAMP(10);
   __syncthreads();
-  LNQ_STAMP(11);
   float rnorm = 1.f;  // NORM: the row's factor, the groups' sums added in order
   if constexpr (PRO == gemv::PRO_NORM) {
     float total = 0.f;
@@ -385,7 +352,6 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_kernel(
       y[n] = out;
     }
   }
-  LNQ_STAMP(12);
 }
 
 // One token, K > 4096 (the down projection's 14336): the one-token kernel with
@@ -585,9 +551,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_slices_kernel(
     C = mfma16x16x32<DT>(a[1], b1, C);
     C = mfma16x16x32<DT>(a[2], b2, C);
     C = mfma16x16x32<DT>(a[3], b3, C);
-    float c = reg == 0 ? C[0] : C[1];
-    __asm__ volatile("" : "+v"(c) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
-    return c;
+    return reg == 0 ? C[0] : C[1];
   };
   // Scale / zero point of output row n (workgroup-local) in slice sl: (s0, s1, -(M + z0), -(M + z1)).
   auto coeff = [&](int n, int sl, float& s0, float& s1, float& nz0, float& nz1) {
@@ -815,8 +779,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   hide_in_vgpr(nib_mask);
   hide_in_vgpr(nib_magic);
   const int r7 = col & 7;
-  // One MFMA chain over four packed dwords (MFMA t takes dword t); the operand
-  // registers stay allocated until the result has been read.
+  // One MFMA chain over four packed dwords (MFMA t takes dword t).
   auto chain = [&](const u32x4 (&a)[4], const u32x4 w) -> f32x4 {
     u32x4 b0, b1, b2, b3;
     widen_pair<DT>(w.x, w.y, nib_mask, nib_magic, b0, b1);
@@ -826,7 +789,6 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
     C = mfma16x16x32<DT>(a[1], b1, C);
     C = mfma16x16x32<DT>(a[2], b2, C);
     C = mfma16x16x32<DT>(a[3], b3, C);
-    __asm__ volatile("" : "+v"(C) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
     return C;
   };
   // ---- tiles as their loads land; tile T covers rows 16 T .. 16 T + 15 (the
@@ -1157,14 +1119,3 @@ LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* sca
 }
 
 }  // namespace lnq
-
-#ifdef LNQ_GEMV_TIMELINE
-// The last launch's timestamps, [512 workgroups][16 waves][16 points] of u64.
-extern "C" LNQ_API LnqStatus lnq_gemv_timeline_read(unsigned long long* host) {
-  LNQ_REQUIRE(host != nullptr, "lnq_gemv_timeline_read: null pointer");
-  LNQ_HIP_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(lnq::gemv_stamps), sizeof(lnq::gemv_stamps), 0,
-                                    hipMemcpyDeviceToHost));
-  lnq::clear_error();
-  return LNQ_OK;
-}
-#endif

@@ -10,6 +10,7 @@ from collections.abc import Callable, Sequence
 
 import torch
 
+from ..errors import LinnetError
 from . import generated, kernels, quantized
 
 Native = Callable[[Sequence[object]], torch.Tensor]
@@ -60,11 +61,31 @@ def _int8_group_linear(args: Sequence[object]) -> torch.Tensor:
     return quantized.int8_group_linear(x, quantized.int8_group_operands(weight, scale), bias)  # type: ignore[arg-type]
 
 
+_GATHERED = (torch.bfloat16, torch.float16, torch.float32)
+
+
 def _index_select(args: Sequence[object]) -> torch.Tensor:
-    """`std.quant::take_inputs` (`native.py:269-271`): `x[..., order[k]]`, on the HIP
-    gather kernel."""
+    """`std.quant::take_inputs` (`native.py:269-271`): `x[..., order[k]]`.
+
+    The interpreter's entry is generic (any dtype, and an index outside the axis
+    raises). bf16 / f16 / f32 GPU tensors run the HIP gather kernel, whose
+    out-of-range index would read 0, so the order is range-checked first (one
+    host read of its extremes; skipped under graph capture, where the caller's
+    order was checked when the layer was built). Other dtypes, and an order that
+    is not a permutation-sized [n] vector, go to torch's own `index_select` on
+    the GPU, which is what the reference calls. CPU tensors raise, as every
+    entry of this package does."""
     x, order = args
     assert isinstance(x, torch.Tensor) and isinstance(order, torch.Tensor)
+    if not x.is_cuda:
+        raise LinnetError(f"linnet_amd runs on the GPU; take_inputs got x on {x.device}")
+    if x.dtype not in _GATHERED or x.dim() == 0 or tuple(order.shape) != (x.shape[-1],):
+        return x.index_select(-1, order.long())
+    n = x.shape[-1]
+    if order.numel() and not torch.cuda.is_current_stream_capturing():
+        low, high = torch.aminmax(order)
+        if int(low) < 0 or int(high) >= n:
+            raise LinnetError(f"take_inputs: order holds indices outside [0, {n}): {int(low)}..{int(high)}")
     return kernels.take_inputs(x, order if order.dtype == torch.int32 else order.to(torch.int32))
 
 

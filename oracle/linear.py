@@ -84,6 +84,21 @@ def fp8_linear_cpu(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, b
     return y if bias is None else y + bias
 
 
+def fp8_block_linear_cpu(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """`quantized.fp8_block_linear`'s CPU branch (`torch/quantized.py:167-172`): the
+    FP8 weight widened, each `B x B` block times its scale `scale[o / B, i / B]`
+    in f32, cast to x's dtype, `F.linear`, then the bias. The CPU path does not
+    round the activations."""
+    flat = x.reshape(-1, x.shape[-1])
+    out_features, in_features = weight.shape
+    block = out_features // scale.shape[0]
+    decoded = weight.contiguous().view(torch.uint8).view(torch.float8_e4m3fn).float()
+    decoded = decoded.reshape(out_features // block, block, in_features // block, block) * scale.float()[:, None, :, None]
+    y = functional.linear(flat, decoded.reshape(out_features, in_features).to(flat.dtype))
+    y = y.reshape(*x.shape[:-1], out_features)
+    return y if bias is None else y + bias
+
+
 # ------------------------------------------------------------ fp64 references
 
 

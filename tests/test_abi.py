@@ -128,6 +128,8 @@ def test_other_entry_points_validate() -> None:
     assert "head_dim is 64 or 128" in rope(10, 96, 16)[1]
     assert "positions <= cap" in rope(20, 128, 16)[1]
     assert "multiple of 8" in rope(10, 128, 16, stride=100)[1]
+    # 32 heads of 128: a q row is 4096 elements, so a 1024-element stride overlaps rows.
+    assert "shorter than a q row" in rope(10, 128, 16, stride=1024)[1]
     assert rope(0, 128, 16)[0] == _lib.LNQ_OK
     assert "bf16, f16 or f32" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, 9, NULL)[1]
     assert "must not be x" in _status("lnq_take_inputs", FAKE, FAKE, FAKE, 1, 8, _lib.BF16, NULL)[1]
@@ -224,24 +226,6 @@ def test_plan_queries_name_the_kernel_without_a_device() -> None:
     assert kernels.mm8_plan(256, 28672, 8192) == 128
     with pytest.raises(LinnetError, match="tile_n"):
         _lib.call("lnq_mm8_tiles", *[ctypes.c_void_p(256)] * 5, 4, 256, 128, 1, _lib.BF16, 64, None)
-
-
-def test_timeline_library_exports_the_stamp_reader() -> None:
-    """The diagnostic build (one-token GEMV with per-wave timestamps) links the
-    same entry points plus `lnq_gemv_timeline_read`; the product library has no
-    stamps."""
-    from linnet_amd import _build
-
-    stamped = ctypes.CDLL(str(_build.TIMELINE))
-    assert hasattr(stamped, "lnq_gemv_timeline_read") and hasattr(stamped, "lnq_int4_linear")
-    assert not hasattr(_lib.load(), "lnq_gemv_timeline_read")
-
-
-@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the answer without a GPU")
-def test_timeline_needs_a_gpu() -> None:
-    from linnet_amd import timeline
-
-    assert timeline.main([]) == 2
 
 
 def test_nf4_entry_points_validate() -> None:

@@ -256,3 +256,26 @@ def test_fp8_baseline_shape(rows: int) -> None:
     top = want.abs().max().item()
     print(f"rows {rows}: max abs err {err:.3e} rel {err / top:.3e}")
     assert err <= (0.06 if rows > 32 else 0.01) * top
+
+
+def test_config1_int8_per_row_gemv() -> None:
+    """BASELINE config 1 exactly: W [4096, 4096] ~ N(0, 0.02) (f32, seed 0) quantized
+    per row to int8 with f32 scales (`quantize_int8_groups(W, 4096, "f32")`), one bf16
+    row of x ~ N(0, 1), through `Int8Linear`'s call (`int8_operands` / `int8_linear`,
+    one row -> `gemv8`, the one-scale-a-row form of the one-row kernel), against the
+    f64 product with the exactly dequantized weight within `1e-2 * max|want|`, and
+    against the reference's CPU path (`quantized.py:193`) within the same bound."""
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(4096, 4096, generator=g) * 0.02).numpy()
+    q, scale = quant.quantize_int8_groups(w, 4096, "f32")
+    assert scale.shape == (4096, 1)
+    x = torch.randn(1, 4096, generator=g).to(torch.bfloat16)
+    qt, st = torch.from_numpy(q), torch.from_numpy(scale)
+    got = quantized.int8_linear(x.to(DEV), quantized.int8_operands(qt.to(DEV), st.to(DEV), 0), None)
+    y = got.float().cpu().numpy()
+    want = linear.product_f64(x.float().numpy(), quant.dequantize_int8_groups(q, scale))
+    err, top = _err(y, want)
+    assert err <= 0.01 * top
+    cpu = linear.int8_linear_cpu(x, qt, st, None).float().numpy()
+    err, top = _err(y, cpu)
+    assert err <= 0.01 * top

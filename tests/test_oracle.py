@@ -302,6 +302,110 @@ def test_cpu_8bit_paths_agree_with_fp64() -> None:
     assert np.abs(got.float().numpy() - ref).max() <= 1e-2 * np.abs(ref).max()
 
 
+def _decoded_by_loop(q: np.ndarray, scale: np.ndarray, group: int) -> np.ndarray:
+    """Brute force over (output, input): `bf16(f32(q[o, i]) * f32(s[o, i // group]))`,
+    the weight `Int8GroupLinear` decodes (`stdlib/quant.linnet:60-72`), element by
+    element, no reshape."""
+    out_features, in_features = q.shape
+    w = np.zeros((out_features, in_features), np.float32)
+    for o in range(out_features):
+        for i in range(in_features):
+            w[o, i] = np.float32(q[o, i]) * np.float32(scale[o, i // group])
+    return quant.from_bf16_bits(quant.to_bf16_bits(w))
+
+
+def test_int8_group_cpu_path_against_a_loop() -> None:
+    """`quantized.int8_group_linear`'s CPU branch on a layer with Out != In and 3
+    groups, each scale a different power of two: rows of the identity read the
+    decoded weight back exactly (one nonzero product per output), so a scale
+    taken along the wrong axis, a transposed weight or a group index off by one
+    changes the bits; a random x then matches the f64 loop sum to bf16's
+    rounding, and the bias is added after the product."""
+    rng = np.random.default_rng(11)
+    out_features, in_features, group = 5, 96, 32
+    q = rng.integers(-127, 128, size=(out_features, in_features)).astype(np.int8)
+    scale = np.exp2(rng.integers(-6, 3, size=(out_features, in_features // group))).astype(np.float32)
+    assert len(np.unique(scale)) > 3
+    qt, st = torch.from_numpy(q), torch.from_numpy(scale)
+    eye = torch.eye(in_features, dtype=torch.bfloat16)
+    got = linear.int8_group_linear_cpu(eye, qt, st, None).float().numpy()
+    np.testing.assert_array_equal(got, _decoded_by_loop(q, scale, group).T)
+
+    x = rng.standard_normal((3, in_features)).astype(np.float32)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    bias = torch.from_numpy(rng.standard_normal(out_features).astype(np.float32) * 50).to(torch.bfloat16)
+    got = linear.int8_group_linear_cpu(xb, qt, st, bias).float().numpy()
+    xs = xb.float().numpy().astype(np.float64)
+    want = np.zeros((3, out_features))
+    for r in range(3):
+        for o in range(out_features):
+            want[r, o] = sum(xs[r, i] * float(q[o, i]) * float(scale[o, i // group]) for i in range(in_features))
+    want += bias.float().numpy()
+    assert np.abs(got - want).max() <= 1e-2 * np.abs(want).max()
+
+
+def test_int8_cpu_path_against_a_loop_with_bias() -> None:
+    """`quantized.int8_linear`'s CPU branch, one scale a row: the identity reads back
+    `bf16(q * s[o])` bit for bit (a scale per input instead of per output fails),
+    and with a bias of the product's size the output is the loop sum plus the bias
+    (a dropped or doubled bias fails)."""
+    rng = np.random.default_rng(12)
+    out_features, in_features = 6, 64
+    q = rng.integers(-127, 128, size=(out_features, in_features)).astype(np.int8)
+    scale = np.exp2(rng.integers(-7, 0, size=out_features)).astype(np.float32)
+    qt, st = torch.from_numpy(q), torch.from_numpy(scale)
+    eye = torch.eye(in_features, dtype=torch.bfloat16)
+    got = linear.int8_linear_cpu(eye, qt, st, None).float().numpy()
+    np.testing.assert_array_equal(got, _decoded_by_loop(q, scale[:, None], in_features).T)
+
+    x = rng.standard_normal((2, in_features)).astype(np.float32)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    plain = linear.int8_linear_cpu(xb, qt, st, None).float().numpy()
+    bias = torch.from_numpy(np.abs(plain).max() * rng.standard_normal(out_features).astype(np.float32)).to(torch.bfloat16)
+    got = linear.int8_linear_cpu(xb, qt, st, bias).float().numpy()
+    xs = xb.float().numpy().astype(np.float64)
+    want = np.array([[sum(xs[r, i] * float(q[o, i]) * float(scale[o]) for i in range(in_features))
+                      for o in range(out_features)] for r in range(2)]) + bias.float().numpy()
+    assert np.abs(got - want).max() <= 1e-2 * np.abs(want).max()
+    # 3-d input: the leading axes are kept.
+    got3 = linear.int8_linear_cpu(xb.reshape(2, 1, in_features), qt, st, bias)
+    assert got3.shape == (2, 1, out_features)
+    np.testing.assert_array_equal(got3.reshape(2, out_features).float().numpy(), got)
+
+
+def test_fp8_block_cpu_path_against_a_loop() -> None:
+    """`quantized.fp8_block_linear`'s CPU branch with 4 x 4 blocks on a 8 x 12
+    weight (2 x 3 blocks, each scale a different power of two): the identity
+    reads back `bf16(decode(w[o, i]) * s[o / 4, i / 4])` bit for bit (a block
+    index on the wrong axis or a transposed scale fails), and a random x with a
+    bias matches the f64 loop sum within bf16's rounding."""
+    rng = np.random.default_rng(13)
+    out_features, in_features, block = 8, 12, 4
+    codes = rng.integers(0, 256, size=(out_features, in_features)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x38  # no NaN bytes (1.0 instead)
+    scale = np.exp2(rng.permutation(np.arange(-3, 3))).astype(np.float32).reshape(2, 3)
+    wt = torch.from_numpy(codes).view(torch.float8_e4m3fn)
+    st = torch.from_numpy(scale)
+    values = quant.decode_fp8(codes)
+    loop = np.zeros((out_features, in_features), np.float32)
+    for o in range(out_features):
+        for i in range(in_features):
+            loop[o, i] = np.float32(values[o, i]) * scale[o // block, i // block]
+    loop = quant.from_bf16_bits(quant.to_bf16_bits(loop))
+    eye = torch.eye(in_features, dtype=torch.bfloat16)
+    got = linear.fp8_block_linear_cpu(eye, wt, st, None).float().numpy()
+    np.testing.assert_array_equal(got, loop.T)
+
+    xb = torch.from_numpy(rng.standard_normal((3, in_features)).astype(np.float32)).to(torch.bfloat16)
+    bias = torch.from_numpy(rng.standard_normal(out_features).astype(np.float32) * 100).to(torch.bfloat16)
+    got = linear.fp8_block_linear_cpu(xb, wt, st, bias).float().numpy()
+    xs = xb.float().numpy().astype(np.float64)
+    want = np.array([[sum(xs[r, i] * float(values[o, i]) * float(scale[o // block, i // block])
+                          for i in range(in_features)) for o in range(out_features)] for r in range(3)])
+    want += bias.float().numpy()
+    assert np.abs(got - want).max() <= 1e-2 * np.abs(want).max()
+
+
 @pytest.mark.parametrize("fp8", [True, False])
 def test_rows8_product_reference(fp8: bool) -> None:
     """The 8-bit product reference equals the dequantized operands' product."""
