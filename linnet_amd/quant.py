@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import fnmatch
 import json
+import re
 from collections.abc import Iterable, Mapping
 from dataclasses import dataclass
 from pathlib import Path
@@ -387,14 +388,24 @@ __all__ = [
 
 # ------------------------------------------------------- bitsandbytes NF4 import
 #
-# A bitsandbytes 4-bit layer `L` stores `L.weight` (two codes a byte, the first
-# in the high nibble, the weight flattened), `L.weight.absmax` (one scale a
-# block, or its uint8 code under double quantization), `L.weight.quant_map` (the
-# 16 values), for double quantization `L.weight.nested_absmax` and
-# `L.weight.nested_quant_map`, and its state -- shape, block size, nested block
-# size and offset -- as JSON bytes in `L.weight.quant_state.bitsandbytes__<type>`.
-_NF4_STATE = ".quant_state.bitsandbytes__"
-_NF4_SIDE = (".absmax", ".quant_map", ".nested_absmax", ".nested_quant_map")
+# bitsandbytes saves a 4-bit `Linear4bit` layer under its weight's name W:
+#   W                                   uint8: the weight flattened row-major, two
+#                                       codes a byte, the earlier one in the high
+#                                       nibble
+#   W.absmax                            one scale per `blocksize` codes: float32, or
+#                                       under double quantization a uint8 code
+#   W.quant_map                         the 16 values the codes stand for
+#   W.nested_absmax, W.nested_quant_map double quantization only: a float32 scale
+#                                       per `nested_blocksize` absmax codes, and the
+#                                       256 values those codes stand for
+#   W.quant_state.bitsandbytes__<type>  uint8: the UTF-8 bytes of a JSON object with
+#                                       "shape" and "blocksize" (and, under double
+#                                       quantization, "nested_blocksize" and
+#                                       "nested_offset")
+_BNB_STATE = re.compile(r"(?P<weight>.+)\.quant_state\.bitsandbytes__(?P<codes>\w+)")
+# The code type a `quantization_config` without `bnb_4bit_quant_type` means
+# (BitsAndBytesConfig's default).
+_BNB_DEFAULT_CODES = "fp4"
 
 # NF4's 16 values by code (QLoRA's normal quantiles, as bitsandbytes' map holds
 # them; the reference's `NF4`, quant.py:373-394).
@@ -407,109 +418,151 @@ NF4 = np.array(
 )
 
 
-@dataclass(frozen=True)
-class _Nf4Layer:
-    """What a bitsandbytes NF4 layer's state says: its [Out, In] shape, the
-    block size, and for double quantization the nested block size and offset."""
+def _four_bit_codes(config: Mapping[str, object]) -> str:
+    """The code type of a bitsandbytes checkpoint's 4-bit layers, refusing a
+    configuration that has none (8-bit LLM.int8 layers) or whose codes are not
+    NF4 (bitsandbytes' FP4 has no kernel here)."""
+    if True not in (config.get("load_in_4bit"), config.get("_load_in_4bit")):
+        raise LinnetError("bitsandbytes quantization_config without load_in_4bit: its layers are not 4-bit")
+    codes = str(config.get("bnb_4bit_quant_type", _BNB_DEFAULT_CODES)).lower()
+    if codes != "nf4":
+        raise LinnetError(f"bitsandbytes 4-bit layers of {codes!r} codes: only NF4 codes have a kernel here")
+    return codes
 
-    weight: str
+
+def _state_int(state: Mapping[str, object], key: str, weight: str) -> int | None:
+    value = state.get(key)
+    if value is None:
+        return None
+    if isinstance(value, bool) or not isinstance(value, int) or value <= 0:
+        raise LinnetError(f"{weight}: quantization state field {key} = {value!r}, expected a positive integer")
+    return value
+
+
+@dataclass(frozen=True)
+class _Nf4State:
+    """A bitsandbytes 4-bit layer's saved state: the [Out, In] weight shape, the
+    codes a scale covers, and, under double quantization, the absmax codes a
+    nested scale covers and the offset added back to every decoded scale."""
+
     out_features: int
     in_features: int
     block: int
     nested_block: int = 0
-    offset: float = 0.0
+    nested_offset: float = 0.0
+
+    @property
+    def blocks(self) -> int:
+        return self.out_features * self.in_features // self.block
 
     @classmethod
-    def parse(cls, weight: str, stored: weights.StoredTensor) -> _Nf4Layer:
+    def decode(cls, stored: weights.StoredTensor, weight: str) -> _Nf4State:
         try:
-            state = json.loads(bytes(stored.view()).decode("utf-8"))
-        except (UnicodeDecodeError, json.JSONDecodeError):
-            state = None
+            state = json.loads(bytes(stored.view()))
+        except ValueError as err:  # bad UTF-8 or bad JSON
+            raise LinnetError(f"{weight}: `{stored.name}` does not decode as JSON ({err})") from None
         if not isinstance(state, dict):
-            raise LinnetError(f"`{stored.name}` holds no quantization state")
-        shape, block = state.get("shape"), state.get("blocksize")
-        dims = [d for d in shape if isinstance(d, int) and not isinstance(d, bool)] if isinstance(shape, list) else []
-        if len(dims) != 2 or len(shape) != 2 or not isinstance(block, int) or isinstance(block, bool):
-            raise LinnetError(f"{weight}: its quantization state has no 2-d shape and block size")
-        out_features, in_features = dims
-        if block <= 0 or block % 2 or in_features % block:
-            raise LinnetError(f"{weight}: {in_features} inputs do not make blocks of {block}")
-        nested_block, offset = state.get("nested_blocksize"), state.get("nested_offset")
-        if nested_block is None and offset is None:
-            return cls(weight, out_features, in_features, block)
-        if (not isinstance(nested_block, int) or isinstance(nested_block, bool) or nested_block <= 0
-                or not isinstance(offset, (int, float)) or isinstance(offset, bool)):
-            raise LinnetError(f"{weight}: its nested quantization state is incomplete")
-        return cls(weight, out_features, in_features, block, nested_block, float(offset))
+            raise LinnetError(f"{weight}: `{stored.name}` decodes to a JSON {type(state).__name__}, not an object")
+        shape = state.get("shape")
+        if not (isinstance(shape, list) and len(shape) == 2
+                and all(isinstance(d, int) and not isinstance(d, bool) and d > 0 for d in shape)):
+            raise LinnetError(f"{weight}: quantization state shape {shape!r}, expected [out_features, in_features]")
+        block = _state_int(state, "blocksize", weight)
+        if block is None:
+            raise LinnetError(f"{weight}: the quantization state gives no blocksize")
+        out_features, in_features = shape
+        if block % 2 or in_features % block:
+            raise LinnetError(f"{weight}: rows of {in_features} inputs are not whole blocks of {block} codes, "
+                              "which Nf4Linear's [Out, In / block] absmax needs")
+        nested_block = _state_int(state, "nested_blocksize", weight)
+        offset = state.get("nested_offset")
+        if (nested_block is None) != (offset is None):
+            raise LinnetError(f"{weight}: double quantization needs both nested_blocksize and nested_offset")
+        if nested_block is None:
+            return cls(out_features, in_features, block)
+        if isinstance(offset, bool) or not isinstance(offset, (int, float)):
+            raise LinnetError(f"{weight}: nested_offset = {offset!r}, expected a number")
+        return cls(out_features, in_features, block, nested_block, float(offset))
+
+    def tensors(self, weight: str) -> dict[str, str]:
+        """The checkpoint names of the layer's tensors, by role."""
+        names = {"codes": weight, "absmax": weight + ".absmax", "values": weight + ".quant_map"}
+        if self.nested_block:
+            names |= {"outer": weight + ".nested_absmax", "table": weight + ".nested_quant_map"}
+        return names
+
+
+def _holds_nf4(stored: weights.StoredTensor) -> bool:
+    """Whether a stored quant_map is NF4's 16 values in code order, exactly as its
+    own dtype holds them (a 16-bit map as those values rounded to it, an f32 or
+    f64 map as their f32 values)."""
+    if stored.dtype not in weights.FLOAT_DTYPES or int(np.prod(stored.shape)) != 16:
+        return False
+    held = weights.tensor_from(stored, weights.FLOAT_DTYPES[stored.dtype], "cpu").reshape(-1)
+    width = held.dtype if held.element_size() < 4 else torch.float32
+    return torch.equal(held.to(width), torch.from_numpy(NF4).to(width))
 
 
 def _import_nf4(weights_path: str | Path, output: str | Path, config: Mapping[str, object],
                 paths: Mapping[str, list[str]], target: torch.device) -> list[str]:
-    """`import_quantized` for a bitsandbytes 4-bit NF4 checkpoint: each layer's
-    codes repacked low nibble first and its absmax decoded on the GPU
-    (`kernels.nf4_repack`), every other tensor copied."""
-    from .torch import kernels
-
-    if not config.get("load_in_4bit", config.get("_load_in_4bit", False)):
-        raise LinnetError("bitsandbytes checkpoint without `load_in_4bit`: only its 4-bit layers import")
-    kind = str(config.get("bnb_4bit_quant_type", "fp4")).lower()
-    if kind != "nf4":
-        raise LinnetError(f"bitsandbytes 4-bit type {kind!r}: only NF4 imports")
+    """`import_quantized` for a bitsandbytes 4-bit NF4 checkpoint: each layer,
+    in checkpoint order, becomes `Nf4Linear`'s `.weight` (codes [Out, In/2], the
+    first input in the low nibble) and `.absmax` ([Out, In/block] f32, nested
+    scales decoded), through the HIP repack (`kernels.nf4_repack`); every other
+    tensor is copied."""
+    _four_bit_codes(config)
     index = weights.open_checkpoint(weights_path)
     writer = weights.CheckpointWriter()
-    consumed: set[str] = set()
+    layer_tensors: set[str] = set()
     done: list[str] = []
-    for name in sorted(n for n in index if _NF4_STATE in n):
-        weight, _, layer_kind = name.partition(_NF4_STATE)
-        if layer_kind != "nf4":
-            raise LinnetError(f"{weight}: bitsandbytes 4-bit type {layer_kind!r}: only NF4 imports")
-        layer = _Nf4Layer.parse(weight, index[name])
-        codes, absmax = _nf4_layer(layer, index, target, kernels)
-        consumed |= {name, weight, *(weight + side for side in _NF4_SIDE)}
+    for name, stored in index.items():
+        found = _BNB_STATE.fullmatch(name)
+        if found is None:
+            continue
+        weight = found["weight"]
+        if found["codes"].lower() != "nf4":
+            raise LinnetError(f"{weight}: a layer of {found['codes']!r} codes: only NF4 codes have a kernel here")
+        state = _Nf4State.decode(stored, weight)
+        if not state.nested_block and weight + ".nested_absmax" in index:
+            raise LinnetError(f"{weight}: the checkpoint holds nested scales, but the state has no nested_blocksize")
+        names = state.tensors(weight)
+        codes, absmax = _repack_nf4(weight, state, {role: index.get(n) for role, n in names.items()}, target)
+        layer_tensors |= {name, *names.values()}
         for path in paths.get(weight) or [weight]:
             prefix = siblings(path)
             writer.add(prefix + "weight", "U8", tuple(codes.shape), weights.tensor_bytes(codes))
             writer.add(prefix + "absmax", "F32", tuple(absmax.shape), weights.tensor_bytes(absmax))
             done.append(path)
     if not done:
-        raise LinnetError(f"{weights_path}: no bitsandbytes 4-bit layer (`{_NF4_STATE}nf4`)")
+        raise LinnetError(f"{weights_path}: no tensor is a bitsandbytes 4-bit state "
+                          "(`<weight>.quant_state.bitsandbytes__nf4`)")
     for name, stored in index.items():
-        if name not in consumed:
+        if name not in layer_tensors:
             for path in paths.get(name) or [name]:
                 writer.add(path, stored.dtype, stored.shape, stored)
     writer.write(output, {"format": "pt"})
     return done
 
 
-def _nf4_layer(layer: _Nf4Layer, index: Mapping[str, weights.StoredTensor], target: torch.device,
-               kernels) -> tuple[torch.Tensor, torch.Tensor]:
-    """One NF4 layer as `Nf4Linear` holds it: (codes [Out, In/2], absmax [Out, In/block])."""
-    w = layer.weight
-    missing = [w + side for side in (".absmax", ".quant_map") if w + side not in index]
-    if w not in index or missing:
-        raise LinnetError(f"{w}: the layer lacks {', '.join(missing) or 'its weight'}")
-    quant_map = weights.float_tensor(index[w + ".quant_map"], "cpu").numpy().reshape(-1)
-    if quant_map.shape != (16,) or not np.allclose(quant_map, NF4, rtol=0, atol=1e-6):
-        raise LinnetError(f"{w}: its quantization map is not NF4's")
-    stored = index[w]
-    if stored.nbytes * 2 != layer.out_features * layer.in_features:
-        raise LinnetError(f"{w}: {stored.nbytes} bytes for a [{layer.out_features}, {layer.in_features}] weight")
-    packed = weights.tensor_from(stored, torch.uint8, target).reshape(-1)
-    scales = layer.out_features * layer.in_features // layer.block
-    nested = w + ".nested_absmax" in index
-    if nested != bool(layer.nested_block):
-        raise LinnetError(f"{w}: its nested quantization state is incomplete")
-    if nested:
-        if w + ".nested_quant_map" not in index:
-            raise LinnetError(f"{w}: `.nested_absmax` without `.nested_quant_map`")
-        scale_codes = weights.tensor_from(index[w + ".absmax"], torch.uint8, target).reshape(-1)
-        outer = weights.float_tensor(index[w + ".nested_absmax"], target).reshape(-1)
-        table = weights.float_tensor(index[w + ".nested_quant_map"], target).reshape(-1)
-        if scale_codes.numel() != scales:
-            raise LinnetError(f"{w}: {scale_codes.numel()} scales for blocks of {layer.block}")
-        return kernels.nf4_repack(packed, scale_codes, layer.out_features, layer.in_features, layer.block,
-                                  outer, table, layer.nested_block, layer.offset)
-    absmax = weights.float_tensor(index[w + ".absmax"], target).reshape(-1)
-    if absmax.numel() != scales:
-        raise LinnetError(f"{w}: {absmax.numel()} scales for blocks of {layer.block}")
-    return kernels.nf4_repack(packed, absmax, layer.out_features, layer.in_features, layer.block)
+def _repack_nf4(weight: str, state: _Nf4State, parts: Mapping[str, weights.StoredTensor | None],
+                target: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """One layer's tensors, checked against its state, repacked on `target`."""
+    from .torch import kernels
+
+    absent = [role for role, stored in parts.items() if stored is None]
+    if absent:
+        raise LinnetError(f"{weight}: the checkpoint lacks the layer's {', '.join(absent)} "
+                          f"({', '.join(state.tensors(weight)[role] for role in absent)})")
+    if not _holds_nf4(parts["values"]):
+        raise LinnetError(f"{weight}: `{parts['values'].name}` is not NF4's 16 values in code order")
+    codes = weights.tensor_from(parts["codes"], torch.uint8, target).reshape(-1)
+    if not state.nested_block:
+        absmax = weights.float_tensor(parts["absmax"], target).reshape(-1)
+        return kernels.nf4_repack(codes, absmax, state.out_features, state.in_features, state.block)
+    if parts["absmax"].dtype != "U8":
+        raise LinnetError(f"{weight}: double quantization stores absmax as U8 codes, not {parts['absmax'].dtype}")
+    absmax_codes = weights.tensor_from(parts["absmax"], torch.uint8, target).reshape(-1)
+    outer = weights.float_tensor(parts["outer"], target).reshape(-1)
+    table = weights.float_tensor(parts["table"], target).reshape(-1)
+    return kernels.nf4_repack(codes, absmax_codes, state.out_features, state.in_features, state.block, outer, table,
+                              state.nested_block, state.nested_offset)

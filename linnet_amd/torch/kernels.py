@@ -719,9 +719,10 @@ def nf4_repack(packed: torch.Tensor, absmax: torch.Tensor, out_features: int, in
     `nested_absmax` (one a `nested_block` scales) plus `offset`, in f32."""
     device = _on_gpu("nf4_repack", packed, absmax, nested_absmax, nested_map)
     if block <= 0 or block % 2 or in_features % block:
-        raise LinnetError(f"nf4_repack: {in_features} inputs do not make even blocks of {block}")
+        raise LinnetError(f"nf4_repack: block {block} is not an even divisor of in_features {in_features}")
     if packed.dtype != torch.uint8 or packed.numel() * 2 != out_features * in_features:
-        raise LinnetError(f"nf4_repack: {packed.numel()} bytes for a [{out_features}, {in_features}] weight")
+        raise LinnetError(f"nf4_repack: packed holds {packed.numel()} {packed.dtype} elements; "
+                          f"{out_features} x {in_features} codes take {out_features * in_features // 2} uint8")
     scales = out_features * in_features // block
     nested = nested_map is not None or nested_absmax is not None
     if nested:
@@ -732,9 +733,11 @@ def nf4_repack(packed: torch.Tensor, absmax: torch.Tensor, out_features: int, in
         if nested_absmax.dtype != torch.float32 or nested_absmax.numel() < -(-scales // nested_block):
             raise LinnetError(f"nf4_repack: {nested_absmax.numel()} nested scales for {scales} blocks of {nested_block}")
         if absmax.dtype != torch.uint8 or absmax.numel() != scales:
-            raise LinnetError(f"nf4_repack: {absmax.numel()} absmax codes for {scales} blocks")
+            raise LinnetError(f"nf4_repack: absmax holds {absmax.numel()} {absmax.dtype} elements; "
+                              f"{scales} blocks take as many uint8 codes")
     elif absmax.dtype != torch.float32 or absmax.numel() != scales:
-        raise LinnetError(f"nf4_repack: {absmax.numel()} absmax values for {scales} blocks of {block}")
+        raise LinnetError(f"nf4_repack: absmax holds {absmax.numel()} {absmax.dtype} elements; "
+                          f"{scales} blocks take as many float32 scales")
     packed, absmax = packed.contiguous(), absmax.contiguous()
     nested_absmax = None if nested_absmax is None else nested_absmax.contiguous()
     nested_map = None if nested_map is None else nested_map.contiguous()

@@ -212,7 +212,7 @@ def test_import_bitsandbytes_then_multiply(tmp_path: Path, nested: bool) -> None
 
 def test_import_rejects_other_bitsandbytes_types(tmp_path: Path) -> None:
     _bnb_checkpoint(tmp_path / "bnb.safetensors", False)
-    with pytest.raises(lquant.LinnetError, match="only NF4"):
+    with pytest.raises(lquant.LinnetError, match="only NF4 codes"):
         lquant.import_quantized(tmp_path / "bnb.safetensors", tmp_path / "o.safetensors",
                                 config=CONFIG | {"bnb_4bit_quant_type": "fp4"})
     with pytest.raises(lquant.LinnetError, match="load_in_4bit"):
