@@ -665,11 +665,11 @@ static bool check_int4_linear(int64_t rows, int64_t in_features, int64_t out_fea
 
 // The kernel lnq_int4_linear runs (LNQ_KERNEL_GEMV, _SKINNY, _TILED_128 or
 // _TILED_256), or -1 with the message set when the one asked for does not take
-// the shape. GEMV at 17..64 rows means the few-token GEMV per 16-row chunk.
+// the shape. GEMV at 33..64 rows means the few-token GEMV per 32-row chunk.
 static int choose_int4_kernel(int M, int N, int K, int G, int dtype, int kernel, const void* x,
                               const void* packed, const void* scale, const void* zero) {
-  // The one-workgroup-per-CU GEMV takes 1..16 rows (1: one x row broadcast; 2..16:
-  // x row m in MFMA A row m).
+  // The one-workgroup-per-CU GEMV takes 1..32 rows (1: one x row broadcast; 2..32:
+  // x row m in MFMA A row m of one or two A blocks).
   const bool gemv_ok = int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
   if (kernel == LNQ_KERNEL_GEMV) {
     if (!gemv_ok) {
@@ -679,23 +679,22 @@ static int choose_int4_kernel(int M, int N, int K, int G, int dtype, int kernel,
     return LNQ_KERNEL_GEMV;
   }
   if (kernel == LNQ_KERNEL_AUTO) {
-    // Measured (bf16, group 128, K = 4096): one row always takes the GEMV (N =
-    // 128256: 56 against 69 us; 16384: 7.8 against 9.4). At 2..4 rows the GEMV
-    // holds up to 56-row workgroups (N = 14336: 11.4 against 11.7 us) and the
-    // skinny kernel is ahead past them (N = 16384: 10.9 against 11.9 us; 28672:
-    // 17.5 against 22.2).
-    // From 5 rows over a wide output the few-token GEMV wins (N = 14336: 11.9
-    // against 21.2 us at 16 rows; N = 6144: 8.5 against 11.6), and at 17..64 rows it
-    // still does once per 16-row chunk, each chunk streaming the weight again
-    // (N = 6144: 16.5 against 18.9 us at 32 rows, 32.8 against 34.8 at 64; N =
-    // 128256: 197 against 264): the skinny kernel's 16-feature workgroups each read
-    // all of x. Over N <= 4096 the GEMV holds at 5 rows (N = 4096: 5.6 against 6.0
-    // us; N = 1024: 5.1 against 5.5), the two are level at 8 and the skinny kernel is
-    // ahead from 16 rows on (N = 4096: 7.1 against 7.4 us; 32 rows: 10.7 against 14.5).
+    // Measured (bf16, group 128, K = 4096, graphs over rotating weight copies):
+    // one row always takes the GEMV (N = 128256: 56 against 69 us; 16384: 7.8
+    // against 9.4). Up to 6 rows the GEMV is ahead at every width (4 rows: N =
+    // 4096 4.7 against 6.3 us; 14336 9.5 against 11.7; 28672 16.2 against 19.7;
+    // 128256 60.7 against 73.1). Over a wide output (N >= 6144) it stays ahead
+    // at 5..32 rows in one launch -- up to 16 rows one A block, 17..32 two
+    // blocks over each weight tile (N = 14336: 12.0 against 21.7 us at 16 rows,
+    // 18.0 against 35.7 at 32; 128256: 128 against 264 at 32) -- and at 33..64
+    // rows once per 32-row chunk (N = 14336: 35.6 against 68.9 at 64). Over N
+    // <= 4096 the two are level from 16 to 32 rows (N = 4096: 7.2 / 7.5 us at
+    // 16, 11.3 / 11.2 at 32) and the skinny kernel is ahead at 64 (18.6 against
+    // 22.5 for two 32-row launches).
     const bool wide = N >= 6144;
-    const bool few = M <= 6 && N <= 14336;
+    const bool few = M <= 6;
     if (gemv_ok && (M == 1 || few || (M > 4 && wide))) return LNQ_KERNEL_GEMV;
-    if (wide && M > 16 && M <= 64 && int4_gemv_supports(16, N, K, G, x, packed, scale, zero)) return LNQ_KERNEL_GEMV;
+    if (wide && M > 32 && M <= 64 && int4_gemv_supports(32, N, K, G, x, packed, scale, zero)) return LNQ_KERNEL_GEMV;
     if (M > 64 && int4_tiled_supports(M, N, K, G, dtype))
       return int4_tiled_width(M, N) == 256 ? LNQ_KERNEL_TILED_256 : LNQ_KERNEL_TILED_128;
     return LNQ_KERNEL_SKINNY;
@@ -735,11 +734,11 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
   const int code = choose_int4_kernel(M, N, K, G, dtype, kernel, x, packed, scale, zero);
   if (code < 0) return LNQ_ERROR;
   if (code == LNQ_KERNEL_GEMV) {
-    if (M <= 16) return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
-    // 17..64 rows over a wide output: the few-token GEMV once per 16-row chunk.
+    if (M <= 32) return launch_int4_gemv(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
+    // 33..64 rows over a wide output: the few-token GEMV once per 32-row chunk.
     const size_t xrow = static_cast<size_t>(K) * 2, yrow = static_cast<size_t>(N) * 2;
-    for (int c = 0; c < M; c += 16) {
-      const int rc = M - c < 16 ? M - c : 16;
+    for (int c = 0; c < M; c += 32) {
+      const int rc = M - c < 32 ? M - c : 32;
       const LnqStatus st = launch_int4_gemv(static_cast<const uint8_t*>(x) + c * xrow, packed, scale, zero, bias,
                                             static_cast<uint8_t*>(y) + c * yrow, rc, N, K, G, dtype, s);
       if (st != LNQ_OK) return st;

@@ -59,6 +59,7 @@ namespace gemv {
 enum { PRO_NONE = 0, PRO_NORM = 1, PRO_SILU = 2 };
 constexpr int MAX_WAVES = 16;  // K <= 4096
 constexpr int MAX_U8 = 8;      // R <= 64 rows per workgroup
+constexpr int MAX_ROWS = 32;   // tokens of one few-token launch
 
 // Weight tile T (loads 2T and 2T + 1, 1 KB each per wave) has an LDS array of
 // its own. The compiler tracks buffer_load ... lds writes per LDS variable, so a
@@ -756,22 +757,20 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
           xa[H][t] = *reinterpret_cast<const u32x4*>(Xw + 256 * col + 128 * H + 32 * t + 8 * j);
     }
   }
-  float xsum[2];
+  // The sums of x over each half on the matrix core (A = x, B = ones): lane
+  // (col, j) register i is the sum of x row 4 j + i, the row its output
+  // register i holds.
+  u32x4 ones;
+  ones.x = ones.y = ones.z = ones.w = E::ONE2;
+  f32x4 xsum[2];
 #pragma unroll
   for (int H = 0; H < 2; ++H) {
-    float part = 0.f;
+    xsum[H] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t d = xa[H][t][e];
-        part += E::to_f32(static_cast<uint16_t>(d & 0xffffu)) + E::to_f32(static_cast<uint16_t>(d >> 16));
-      }
+      xsum[H] = mfma16x16x32<DT>(xa[H][t], ones, xsum[H]);
       xa[H][t] = permute_x8(xa[H][t]);
     }
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
-    xsum[H] = part;  // sum of x row col over half H of this wave's inputs
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -834,7 +833,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
 #pragma unroll
   for (int H = 0; H < 2; ++H)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xs[H][i] = __shfl(xsum[H], 4 * j + i, 64);
+    for (int i = 0; i < 4; ++i) xs[H][i] = xsum[H][i];
   float acc[NT][4];
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
@@ -905,6 +904,222 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   }
 }
 
+// 17..32 tokens: the few-token kernel with two 16-row A blocks per weight
+// tile, so that each packed byte is read and widened once for all 32 rows.
+// Lane (col, j) holds the A operands of x rows col and 16 + col (inputs k0 +
+// 128 H + 32 t + 8 j, rows past M read zeros), 64 registers; a wave may use 128
+// in a 16-wave workgroup, so nothing else is held across tiles: the sums of
+// each x row (MFMAs against ones) go to LDS once (XS), and each tile is folded
+// with its scales and zero points as soon as its two MFMA chains end, its
+// partial sums written over the
+// wave's own part of the tile array (2 KB: 16 outputs x 32 rows, output-minor;
+// the 8-row last tile of an odd U8 1 KB: its 8 outputs x 32 rows). The 16
+// waves' sums are then added as in int4_gemv_rows_kernel.
+template <int DT, int U8, bool G128>
+__global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
+    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G) {
+  using E = Elem<DT>;
+  constexpr int MX = 32;
+  constexpr int R = 8 * U8;
+  constexpr int NT = (U8 + 1) / 2;
+  constexpr bool HALF = (U8 & 1) != 0;
+  LNQ_GEMV_TILE_ARRAYS(U8);
+  // Outputs of tile T a wave part holds (its floats: 32 times as many).
+  auto outs = [](int T) { return HALF && T == NT - 1 ? 8 : 16; };
+  static_assert(gemv::tile_wave_bytes(U8, NT - 1) == (HALF ? 1024 : 2048), "tile parts hold the partial sums");
+  // Sums of x rows (block b, half H): XS[wave][b][H][row within the block].
+  __shared__ __attribute__((aligned(16))) float XS[gemv::MAX_WAVES][2][2][16];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int col = lane & 15, j = lane >> 4;
+  const int n0 = blockIdx.x * R;
+  const int k0 = wave * 256;
+  const int rowb = K >> 1;
+  const int groups = K / G;
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * rowb));
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint32_t>(static_cast<size_t>(M) * K * 2));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
+
+  // ---- loads: scales and zeros, x (16 per lane), weights.
+  const int srow = n0 + (lane < R ? lane : R - 1);
+  const int g0 = k0 / G;
+  uint32_t sv;
+  uint16_t zv16;
+  if constexpr (G128) {
+    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);
+    zv16 = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);
+  } else {
+    sv = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
+    zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 xa[2][2][4];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int H = 0; H < 2; ++H)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        xa[b][H][t] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rx, ((16 * b + col) * K + k0 + 128 * H + 32 * t + 8 * j) * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    const int a = lane >> 4, bb = lane & 15;
+#pragma unroll
+    for (int u = 0; u < U8; ++u) {
+      const int sigma = 2 * a + ((bb >> 3) ^ (u & 1));
+      const int row = n0 + 8 * u + (bb & 7);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(tile_lds(u >> 1, wave) + 1024 * (u & 1)), 16,
+                                               row * rowb + (k0 >> 1) + 16 * sigma, 0, 0, 2 /* non-temporal */);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- x (and the scales) landed: each row's sums over both halves on the
+  // matrix core (A = x, B = ones: lane (col, j) register i is the sum of x row
+  // 16 b + 4 j + i, the row its output register i holds), then the A operands
+  // in pair order.
+  wait_vm<U8>();
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 ones;
+  ones.x = ones.y = ones.z = ones.w = E::ONE2;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int H = 0; H < 2; ++H) {
+      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        sum = mfma16x16x32<DT>(xa[b][H][t], ones, sum);
+        xa[b][H][t] = permute_x8(xa[b][H][t]);
+      }
+      if (col == 0) *reinterpret_cast<f32x4*>(&XS[wave][b][H][4 * j]) = sum;
+    }
+  __builtin_amdgcn_sched_barrier(0);
+
+  __asm__ volatile("" : "+v"(sv), "+v"(zv16));
+  uint32_t zv = zv16;
+  if constexpr (!G128) {
+    sv = (sv & 0xffffu) | (sv << 16);
+    zv = (zv & 0xffu) | (zv << 8);
+  }
+  uint32_t nib_mask = 0x000f000fu, nib_magic = E::MAGIC2;
+  hide_in_vgpr(nib_mask);
+  hide_in_vgpr(nib_magic);
+  const int r7 = col & 7;
+
+  // ---- tiles as their loads land (the piece layout of int4_gemv_rows_kernel).
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (2 * T + 1 < U8) wait_vm_rt(U8 - 1 - (2 * T + 1));
+    else wait_vm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    const int h = col >> 3;
+    const int u = min(2 * T + h, U8 - 1);
+    const int hh = u & 1;
+    const uint32_t* Wt = reinterpret_cast<const uint32_t*>(tile_lds(T, wave) + 1024 * hh);
+    u32x4 w[2];
+#pragma unroll
+    for (int H = 0; H < 2; ++H)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int p = 16 * (2 * H) + 8 * ((t & 1) ^ hh) + r7;
+        const uint32_t* at = Wt + 4 * p + j;
+        w[H][t] = at[0];
+        w[H][t + 2] = at[64];
+      }
+    f32x4 C[2][2];
+#pragma unroll
+    for (int H = 0; H < 2; ++H) {
+      u32x4 b0, b1;
+      C[0][H] = C[1][H] = f32x4{0.f, 0.f, 0.f, 0.f};
+      widen_pair<DT>(w[H].x, w[H].y, nib_mask, nib_magic, b0, b1);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        C[b][H] = mfma16x16x32<DT>(xa[b][H][0], b0, C[b][H]);
+        C[b][H] = mfma16x16x32<DT>(xa[b][H][1], b1, C[b][H]);
+      }
+      widen_pair<DT>(w[H].z, w[H].w, nib_mask, nib_magic, b0, b1);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        C[b][H] = mfma16x16x32<DT>(xa[b][H][2], b0, C[b][H]);
+        C[b][H] = mfma16x16x32<DT>(xa[b][H][3], b1, C[b][H]);
+      }
+    }
+    // Fold: output row 16 T + col, x rows 16 b + 4 j + i.
+    const int n = 16 * T + col;
+    const int src = n < R ? n : R - 1;
+    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(sv)));
+    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(zv)));
+    const float s0 = E::to_f32(static_cast<uint16_t>(sp & 0xffffu)), s1 = E::to_f32(static_cast<uint16_t>(sp >> 16));
+    const float z0 = E::MAGIC_VALUE + static_cast<float>(zp & 0xffu);
+    const float z1 = E::MAGIC_VALUE + static_cast<float>((zp >> 8) & 0xffu);
+    const int CW = outs(T);
+    float* red = reinterpret_cast<float*>(tile_lds(T, wave));
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&XS[wave][b][0][4 * j]);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&XS[wave][b][1][4 * j]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = fmaf(s0, fmaf(-z0, x0[i], C[b][0][i]), s1 * fmaf(-z1, x1[i], C[b][1][i]));
+        if (col < CW) red[((((b * 4 + i) * 4 + j) * CW + col) + 4 * wave) & (32 * CW - 1)] = v;
+      }
+    }
+  }
+  __syncthreads();
+  // Output (T, m, c): lanes 16 q + c of a wave add waves 4 q .. 4 q + 3, two
+  // exchanges finish the sum; wave w takes passes w, w + nw, .. .
+  constexpr int PASSES = NT * MX;
+  constexpr int PW = (PASSES + gemv::MAX_WAVES - 1) / gemv::MAX_WAVES;
+  const int q = j;
+  auto pass = [&](const int o, float (&r)[4]) {
+    const int T = min(o / MX, NT - 1), m = o % MX;
+    const int cw = outs(T);
+    const int b = m >> 4, i = m & 3, jj = (m >> 2) & 3;
+    const int e = ((b * 4 + i) * 4 + jj) * cw + min(col, cw - 1);
+#pragma unroll
+    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
+      const int wv = 4 * q + w;
+      r[w] = reinterpret_cast<const float*>(tile_lds(T, wv))[(e + 4 * wv) & (32 * cw - 1)];
+    }
+  };
+  auto finish = [&](const int o, const float (&r)[4]) {
+    const int T = o / MX, m = o % MX;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) v += 4 * q + w < nw ? r[w] : 0.f;
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    const int n = n0 + 16 * T + col;
+    if (q == 0 && o < PASSES && m < M && 16 * T + col < R && n < N) {
+      uint16_t out = E::from_f32(v);
+      if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
+      y[static_cast<size_t>(m) * N + n] = out;
+    }
+  };
+  if (nw == gemv::MAX_WAVES) {
+    float r[PW][4];
+#pragma unroll
+    for (int p = 0; p < PW; ++p) pass(wave + gemv::MAX_WAVES * p, r[p]);
+#pragma unroll
+    for (int p = 0; p < PW; ++p) finish(wave + gemv::MAX_WAVES * p, r[p]);
+  } else {
+    for (int o = wave; o < PASSES; o += nw) {
+      float r[4];
+      pass(o, r);
+      finish(o, r);
+    }
+  }
+}
+
 // Whether the one-token kernel takes this shape (else the caller uses the
 // general skinny kernel).
 // Slices a wave takes in the K > 4096 one-token kernel (0: it does not take K):
@@ -928,7 +1143,7 @@ static bool gemv_slices_supports(int N, int K, int G, const void* x, const void*
 
 bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
                         const void* zero) {
-  if (M < 1 || M > 16) return false;
+  if (M < 1 || M > gemv::MAX_ROWS) return false;
   if (M == 1 && gemv_slices_supports(N, K, G, x, packed, scale, zero)) return true;
   if (K % 256 != 0 || K < 256 || K > 256 * gemv::MAX_WAVES) return false;
   if (!(G == 128 || G % 256 == 0) || K % G != 0) return false;
@@ -1028,6 +1243,37 @@ static void launch_rows_dt(const void* x, const uint8_t* packed, const void* sca
   }
 }
 
+template <int DT, int U8>
+static void launch_rows32_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                             const void* bias, void* y, int M, int N, int K, int G, hipStream_t stream) {
+  const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / 256));
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* ys = static_cast<uint16_t*>(y);
+  if (G == 128)
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
+                       M, N, K, G);
+  else
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, false>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
+                       M, N, K, G);
+}
+
+template <int DT>
+static void launch_rows32_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                             const void* bias, void* y, int M, int N, int K, int G, hipStream_t stream) {
+  switch ((N + 2047) / 2048) {
+    case 1: launch_rows32_u8<DT, 1>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 2: launch_rows32_u8<DT, 2>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 3: launch_rows32_u8<DT, 3>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 4: launch_rows32_u8<DT, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 5: launch_rows32_u8<DT, 5>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 6: launch_rows32_u8<DT, 6>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 7: launch_rows32_u8<DT, 7>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    default: launch_rows32_u8<DT, 8>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+  }
+}
+
 template <int DT, int U8, int S>
 static void launch_slices_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                              const void* bias, void* y, int N, int K, int G, const int32_t* order, int kind,
@@ -1111,9 +1357,12 @@ LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* sca
   } else if (M <= 4) {
     if (dtype == LNQ_BF16) launch_rows_dt<LNQ_BF16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
     else launch_rows_dt<LNQ_F16, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
-  } else {
+  } else if (M <= 16) {
     if (dtype == LNQ_BF16) launch_rows_dt<LNQ_BF16, 16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
     else launch_rows_dt<LNQ_F16, 16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+  } else {
+    if (dtype == LNQ_BF16) launch_rows32_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+    else launch_rows32_dt<LNQ_F16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
   }
   return launched("int4_gemv");
 }

@@ -228,9 +228,9 @@ def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, 
 
 @pytest.mark.parametrize(("rows", "out"), [(17, 8192), (32, 8192), (45, 8192), (64, 8192), (5, 20000), (32, 20000),
                                            (34, 20000), (19, 28672)])
-def test_wide_outputs_run_the_gemv_per_16_rows(rows: int, out: int) -> None:
+def test_wide_outputs_run_the_gemv_per_32_rows(rows: int, out: int) -> None:
     """5..64 rows over N >= 8192: the automatic choice runs the few-token GEMV
-    once per 16-row chunk (with a ragged last chunk and the bias in each); past
+    once per 32-row chunk (with a ragged last chunk and the bias in each); past
     16384 outputs with more workgroups than CUs."""
     packed, scale, zero = _layer(out, 1024, 128, seed=rows)
     x = torch.randn(rows, 1024, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
@@ -239,8 +239,8 @@ def test_wide_outputs_run_the_gemv_per_16_rows(rows: int, out: int) -> None:
     assert kernels.int4_linear_plan(rows, 1024, out, 128) == "gemv"
     y = kernels.int4_linear(x.to(DEV), *args)
     _check_linear(x, packed, scale, zero, y)
-    for c in range(0, rows, 16):
-        assert torch.equal(y[c:c + 16], kernels.int4_linear(x[c:c + 16].to(DEV), *args, kernel="gemv"))
+    for c in range(0, rows, 32):
+        assert torch.equal(y[c:c + 32], kernels.int4_linear(x[c:c + 32].to(DEV), *args, kernel="gemv"))
     assert torch.equal(kernels.int4_linear(x.to(DEV), *args, bias), y + bias)
 
 
@@ -275,9 +275,9 @@ def test_one_token_gemv_is_chosen_for_one_row_and_refuses_other_shapes() -> None
     # group 32 at one row: auto falls back to the skinny kernel
     _check_linear(x.cpu(), packed, scale, zero, kernels.int4_linear(x, packed.to(DEV), scale.to(DEV), zero.to(DEV)))
     packed, scale, zero = _layer(64, 512, 128, seed=2)
-    x17 = torch.randn(17, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
+    x33 = torch.randn(33, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
     with pytest.raises(LinnetError, match="one-token kernel"):
-        kernels.int4_linear(x17, packed.to(DEV), scale.to(DEV), zero.to(DEV), kernel="gemv")
+        kernels.int4_linear(x33, packed.to(DEV), scale.to(DEV), zero.to(DEV), kernel="gemv")
 
 
 @pytest.mark.parametrize(
@@ -291,11 +291,20 @@ def test_one_token_gemv_is_chosen_for_one_row_and_refuses_other_shapes() -> None
         (8, 6144, 1280, 256, torch.bfloat16),  # group 256, U8 = 3, 5 waves
         (16, 16384, 256, 128, torch.float16),  # U8 = 8, one wave
         (12, 100, 4096, 128, torch.bfloat16),  # one short workgroup
+        (17, 14336, 4096, 128, torch.bfloat16),  # 32-row form: config 2 shape, U8 = 7
+        (32, 14336, 4096, 128, torch.bfloat16),
+        (24, 4096, 4096, 128, torch.float16),  # U8 = 2
+        (32, 2049, 1024, 128, torch.bfloat16),  # ragged last workgroup
+        (20, 6144, 1280, 256, torch.bfloat16),  # group 256, U8 = 3, 5 waves
+        (32, 16384, 256, 128, torch.float16),  # U8 = 8, one wave
+        (31, 100, 4096, 128, torch.bfloat16),  # one short workgroup
+        (29, 28672, 4096, 128, torch.bfloat16),  # past 16384 outputs: more workgroups than CUs
     ],
 )
 def test_few_token_gemv_multiplies_the_dequantized_weight(rows: int, out: int, width: int, group: int, dtype: torch.dtype) -> None:
-    """2..16 rows through the one-workgroup-per-CU GEMV (x row m in MFMA A row m),
-    against the f64 product and against the skinny kernel on the same inputs."""
+    """2..32 rows through the one-workgroup-per-CU GEMV (x row m in MFMA A row m;
+    past 16 rows two A blocks per weight tile), against the f64 product and
+    against the skinny kernel on the same inputs."""
     packed, scale, zero = _layer(out, width, group, seed=out + rows, dtype=dtype)
     x = torch.randn(rows, width, generator=torch.Generator().manual_seed(rows)).to(dtype)
     args = (x.to(DEV), packed.to(DEV), scale.to(DEV), zero.to(DEV))
@@ -317,7 +326,7 @@ def _baseline_layer(n: int, k: int, seed: int = 0):
     return packed, scale.to(torch.bfloat16), zero
 
 
-@pytest.mark.parametrize(("rows", "k", "n"), [(1, 4096, 14336), (4, 4096, 14336), (16, 4096, 14336), (2048, 4096, 4096), (2048, 14336, 4096)])
+@pytest.mark.parametrize(("rows", "k", "n"), [(1, 4096, 14336), (4, 4096, 14336), (16, 4096, 14336), (32, 4096, 14336), (2048, 4096, 4096), (2048, 14336, 4096)])
 def test_baseline_sizes_agree_with_dequantize_then_gemm(rows: int, k: int, n: int) -> None:
     """At the BASELINE shapes: the fused kernel equals hipBLASLt over the HIP
     dequantized weight (the reference's own prefill strategy) within bf16 rounding,
