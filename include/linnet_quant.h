@@ -314,19 +314,23 @@ LNQ_API LnqStatus lnq_mm8(const uint8_t* q, const uint8_t* weight, const float* 
                           const float* scale, void* y, int64_t rows, int64_t out_features,
                           int64_t in_features, int32_t fp8, int32_t dtype, void* stream);
 
-/* lnq_mm8 with the tile width named: tile_n 128 or 256 output columns a workgroup,
- * 0 for lnq_mm8's own choice (256 while that still gives every compute unit a
- * tile). No counterpart in the reference (`torch._scaled_mm` / `int8_mm` choose
+/* lnq_mm8 with the kernel named: tile_n 128 or 256 output columns a workgroup,
+ * LNQ_MM8_PERSISTENT (1) the persistent form (256 x 256 tiles, one workgroup a
+ * compute unit walking its tiles; out % 256 == 0, in % 256 == 0), 0 for lnq_mm8's
+ * own choice.
+ * No counterpart in the reference (`torch._scaled_mm` / `int8_mm` choose
  * internally): lets a test run each instance. */
+#define LNQ_MM8_PERSISTENT 1
 LNQ_API LnqStatus lnq_mm8_tiles(const uint8_t* q, const uint8_t* weight, const float* x_scale,
                                 const float* scale, void* y, int64_t rows, int64_t out_features,
                                 int64_t in_features, int32_t fp8, int32_t dtype, int32_t tile_n,
                                 void* stream);
 
-/* The tile width (128 or 256) lnq_mm8 takes for rows x out_features on the current
- * device. */
+/* The kernel lnq_mm8 takes for rows x out_features x in_features (fp8 1: e4m3
+ * operands, 0: int8) on the current device, as lnq_mm8_tiles names it (1, 128
+ * or 256). */
 LNQ_API LnqStatus lnq_mm8_plan(int64_t rows, int64_t out_features, int64_t in_features,
-                               int32_t* tile_n);
+                               int32_t fp8, int32_t* tile_n);
 
 /* Each 128 inputs (group = 128) of each row of x [rows, in] (`dtype`: bf16, f16 or f32)
  * rounded to FP8 E4M3 with a scale of their own: scale = max(max|x|, 1e-12) / 448

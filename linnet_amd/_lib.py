@@ -51,7 +51,7 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_rows8": [_p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "lnq_mm8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
     "lnq_mm8_tiles": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p],
-    "lnq_mm8_plan": [_i64, _i64, _i64, ctypes.POINTER(_i32)],
+    "lnq_mm8_plan": [_i64, _i64, _i64, _i32, ctypes.POINTER(_i32)],
     "lnq_fp8_groups": [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "lnq_mm8_block": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_mxfp4_experts": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p],

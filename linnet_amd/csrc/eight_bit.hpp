@@ -363,4 +363,248 @@ __global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
   }
 }
 
+// ------------------------------------------------- persistent 256 x 256 form
+// mm8p_kernel: one workgroup per CU walks its tiles (tile b, b + G, b + 2G, ..
+// of the grid's XCD-grouped order, G workgroups), and the k-steps of all its
+// tiles form one stream: the loads of step g + 2 -- the next tile's near a
+// tile's end -- are issued while step g multiplies.
+//
+// 4 waves, one per SIMD, each owning 128 x 128 outputs (4 x 4 MFMA 32x32
+// tiles, 256 accumulator registers): per MFMA a wave reads half the operand
+// bytes of mm8_kernel's 128 x 64 waves. 128 input bytes a step in two stages
+// of 64 KB (rows of 128 bytes, A rows 0..255 then B rows), filled by
+// buffer_load ... lds, 8 rows x 128 bytes an instruction so that every L2
+// request is a whole line (64-byte steps split each line in two requests and
+// doubled the L2 traffic); 16-byte columns XOR-swizzled by bits 1..3 of the
+// row (swz8). Per step, a region per kk: MFMAs on kk's operands while kk + 1's
+// are read. One barrier, before the last kk: past it every wave's loads of
+// step g + 1 have landed and no wave reads step g's stage again, so the last
+// region reads step g + 1's first operands and issues step g + 2's loads into
+// step g's stage -- a whole step ahead of their use. At a tile's end the wave
+// folds the row and column scales into its tile and stores it; the next
+// tile's first MFMAs start from C = 0.
+namespace mm8p {
+constexpr int BM = 256, BN = 256, BK = 128, NW = 4, THREADS = 64 * NW;
+constexpr int FA = 4, FB = 4;                    // 32-row / 32-column fragments of a wave
+constexpr int STAGE = (BM + BN) * BK;            // bytes of a stage
+constexpr int LPW = (BM + BN) * BK / 1024 / NW;  // 1 KB loads of a wave a step
+static_assert(LPW == 16, "a wave's loads a step");
+}  // namespace mm8p
+
+template <int DT, int FP8>
+__global__ __launch_bounds__(mm8p::THREADS, 1) void mm8p_kernel(
+    const uint8_t* __restrict__ qx, const uint8_t* __restrict__ weight,
+    const float* __restrict__ x_scale, const float* __restrict__ scale,
+    uint16_t* __restrict__ y, int M, int N, int K) {
+  using namespace mm8p;
+  using E = Elem<DT>;
+  constexpr int KPM = FP8 ? 64 : 32;  // inputs per MFMA
+  constexpr int KK = BK / KPM;        // MFMAs of a fragment pair a step (2 or 4)
+  constexpr int CPL = KPM / 32;       // 16-byte columns of a lane's operand
+  using Op = typename std::conditional<FP8, i32x8, i32x4>::type;
+  using Acc = typename std::conditional<FP8, f32x16, i32x16>::type;
+  // One array per stage: the compiler then waits, before reading a stage, for
+  // that stage's loads only.
+  __shared__ __attribute__((aligned(16))) uint8_t L0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t L1[STAGE];
+  LNQ_MFMA_IN_AGPRS();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
+  const int total = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int b0 = blockIdx.x;
+  if (b0 >= total) return;
+  const int mine = (total - 1 - b0) / G + 1;  // tiles b0, b0 + G, ..
+  const int steps = K / BK;                   // even (K % 256 == 0)
+  const int nsteps = mine * steps;
+
+  // Rows past M read zeros through the range check: a load's whole row offset
+  // is in its lane offset (VGPR), only the step's k offset in the uniform one,
+  // so a row past M is out of range whether or not the uniform offset is
+  // range-checked. Steps past the stream read through a 0-byte descriptor (no
+  // traffic, the same count of loads).
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(qx, static_cast<uint32_t>(static_cast<size_t>(M) * K));
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(weight, static_cast<uint32_t>(static_cast<size_t>(N) * K));
+  const __amdgpu_buffer_rsrc_t rnull = buffer_rsrc(weight, 0);
+
+  // Load i (0..15) of wave w fills stage rows 8 (4 i + w) .. + 7 (i < 8: A rows
+  // 32 i + 8 w + l / 8 of the tile; else B rows 32 (i - 8) + 8 w + l / 8): lane
+  // l at byte 16 l of the 1 KB, stored column l % 8 holding source column
+  // (l % 8) ^ key(row), key = (row >> 1) & 7, the same for every i.
+  const int lr = 8 * wave + (lane >> 3);
+  const int lane_off = lr * K + 16 * ((lane & 7) ^ ((lr >> 1) & 7));
+  // The lane offsets of tile r's rows (r past this workgroup's tiles: any
+  // offsets, their loads go through the 0-byte descriptor).
+  uint32_t voff[LPW];
+  auto tile_offsets = [&](int r) {
+    int tm, tn;
+    mm8_tile_of(b0 + r * G, tiles_m, tiles_n, tm, tn);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      voff[i] = static_cast<uint32_t>((tm * BM + 32 * i) * K + lane_off);
+      voff[8 + i] = static_cast<uint32_t>((tn * BN + 32 * i) * K + lane_off);
+    }
+  };
+  // Load i of k-step ks (tile offsets in voff) into stage st.
+  auto load_one = [&](uint8_t* st, bool in, int ks, int i) {
+    const __amdgpu_buffer_rsrc_t q = in ? (i < 8 ? ra : rb) : rnull;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(q, (lds_ptr)(st + (4 * i + wave) * 1024), 16, voff[i],
+                                              in ? ks * BK : 0, 0, 0);
+  };
+
+  // Each tile's first step starts its accumulators with C = 0 (no clearing:
+  // a zeroed register would make the compiler keep the accumulators in VGPRs).
+  Acc acc[FA][FB];
+
+  // Operand offsets within a stage per (kk, column j): fragments of one operand
+  // are 32 rows (4096 bytes) apart with the same swizzle key.
+  const int lrow = lane & 31, lk = lane >> 5;
+  uint32_t aoff[KK][CPL], boff[KK][CPL];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c16 = kk * 2 * CPL + lk * CPL + j;
+      aoff[kk][j] = static_cast<uint32_t>(swz8(wm * 128 + lrow, c16));
+      boff[kk][j] = static_cast<uint32_t>(swz8(BM + wn * 128 + lrow, c16));
+    }
+  auto set_op = [](Op& o, int j, u32x4 v) {
+    if constexpr (FP8) {
+      o[4 * j + 0] = (int)v.x;
+      o[4 * j + 1] = (int)v.y;
+      o[4 * j + 2] = (int)v.z;
+      o[4 * j + 3] = (int)v.w;
+    } else {
+      o = __builtin_bit_cast(i32x4, v);
+    }
+  };
+  auto mma = [](const Op& a, const Op& b, Acc c) -> Acc {
+    if constexpr (FP8)
+      return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+    else
+      return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  };
+  // Operand registers: set 0 holds even kk, set 1 odd kk (KK is even).
+  Op af[2][FA], bf[2][FB];
+  constexpr int READS = (FA + FB) * CPL;  // 16-byte reads of one kk's operands
+  constexpr int NMF = FA * FB;            // MFMAs of one kk
+  auto read_one = [&](int set, const uint8_t* st, int kk, int r) {
+    const int f = r / CPL, j = r % CPL;
+    if (f < FA)
+      set_op(af[set][f], j, *reinterpret_cast<const u32x4*>(st + aoff[kk][j] + f * 4096));
+    else
+      set_op(bf[set][f - FA], j, *reinterpret_cast<const u32x4*>(st + boff[kk][j] + (f - FA) * 4096));
+  };
+
+  // The epilogue of a tile (m0, n0): lane l, register r of fragment (a, b) holds
+  // row m = m0 + 128 wm + 32 a + l % 32 and column n0 + 128 wn + 32 b + 8 (r / 4)
+  // + 4 (l / 32) + r % 4 (the weight is the MFMA's A operand).
+  auto epilogue = [&](int m0, int n0) {
+    float xs[FA];
+#pragma unroll
+    for (int a = 0; a < FA; ++a) xs[a] = x_scale[min(m0 + wm * 128 + a * 32 + lrow, M - 1)];
+#pragma unroll
+    for (int b = 0; b < FB; ++b) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int n = n0 + wn * 128 + b * 32 + 8 * q4 + 4 * lk;
+        const f32x4 ws = *reinterpret_cast<const f32x4*>(scale + n);
+#pragma unroll
+        for (int a = 0; a < FA; ++a) {
+          const int m = m0 + wm * 128 + a * 32 + lrow;
+          uint32_t o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = E::from_f32(static_cast<float>(acc[a][b][4 * q4 + i]) * xs[a] * ws[i]);
+          if (m < M)
+            *reinterpret_cast<u32x2*>(y + static_cast<size_t>(m) * N + n) = u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        }
+      }
+      // One column fragment at a time: the next tile's operands are live here.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // One kk of step g on stage `cur` (operand set kk & 1): NMF MFMA slots, the
+  // slots reading kk + 1's operands from `cur`, or, in the last kk, step g +
+  // 1's first operands from `nxt` and issuing step g + 2's loads (k-step ks2,
+  // `ld2` whether inside the stream) into `cur`, one a slot.
+  auto region = [&](int kk, auto first_tag, const uint8_t* cur, const uint8_t* nxt, bool ld2, int ks2) {
+    constexpr bool FIRST = decltype(first_tag)::value;  // a tile's first step
+    const int set = kk & 1;
+    const bool last = kk == KK - 1;
+#pragma unroll
+    for (int s = 0; s < NMF; ++s) {
+      const int a = s / FB, b = s % FB;
+      if (FIRST && kk == 0) acc[a][b] = mma(bf[set][b], af[set][a], Acc{});
+      else acc[a][b] = mma(bf[set][b], af[set][a], acc[a][b]);
+#pragma unroll
+      for (int r = s * READS / NMF; r < (s + 1) * READS / NMF; ++r) {
+        if (last) read_one(set ^ 1, nxt, 0, r);
+        else read_one(set ^ 1, cur, kk + 1, r);
+      }
+      if (last) {
+#pragma unroll
+        for (int i = s * LPW / NMF; i < (s + 1) * LPW / NMF; ++i) load_one(const_cast<uint8_t*>(cur), ld2, ks2, i);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Step g on stage `cur` (step g + 1 on `nxt`): regions kk = 0 .. KK - 2; this
+  // wave's loads of step g + 1 landed (nothing is issued after them before this
+  // point but the previous epilogue's stores) and its reads done; barrier; the
+  // last region.
+  auto step = [&](auto first_tag, const uint8_t* cur, const uint8_t* nxt, bool ld2, int ks2) {
+#pragma unroll
+    for (int kk = 0; kk + 1 < KK; ++kk) region(kk, first_tag, cur, nxt, false, 0);
+    wait_vm<0>();
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    region(KK - 1, first_tag, cur, nxt, ld2, ks2);
+  };
+
+  // Prologue: steps 0 and 1 (of tile 0: a tile has at least two steps)
+  // requested; step 0 landed (this wave's, then every wave's); its kk = 0
+  // operands read.
+  tile_offsets(0);
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) load_one(L0, true, 0, i);
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) load_one(L1, true, 1, i);
+  wait_vm<LPW>();
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int r = 0; r < READS; ++r) read_one(0, L0, 0, r);
+
+  // Pairs of steps (K % 256 == 0: a tile is whole pairs) g, g + 1 of tile r at
+  // k-step ks on stages L0, L1: they issue steps g + 2, g + 3, the next pair's
+  // (tile r, or r + 1 after a tile's last pair), with no branch inside the
+  // pair: the compiler would otherwise move the MFMAs across the blocks it
+  // split the pair into. A tile's first pair is its own copy (accumulators
+  // started at zero).
+  using T = std::integral_constant<bool, true>;
+  using F = std::integral_constant<bool, false>;
+  auto pair = [&](int g, int r, int ks, auto first_tag) {
+    const bool ends = ks + 2 == steps;
+    const int ks_n = ends ? 0 : ks + 2;
+    tile_offsets(r + (ends ? 1 : 0));
+    step(first_tag, L0, L1, g + 2 < nsteps, ks_n);
+    step(F{}, L1, L0, g + 3 < nsteps, ks_n + 1);
+  };
+  int g = 0;
+  for (int r = 0; r < mine; ++r) {
+    pair(g, r, 0, T{});
+    g += 2;
+    for (int ks = 2; ks < steps; ks += 2, g += 2) pair(g, r, ks, F{});
+    int tm, tn;
+    mm8_tile_of(b0 + r * G, tiles_m, tiles_n, tm, tn);
+    epilogue(tm * BM, tn * BN);
+  }
+  // Loads of the steps past the stream (0-byte reads) may be in flight.
+  wait_vm<0>();
+}
+
 }  // namespace lnq

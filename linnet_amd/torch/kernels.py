@@ -501,8 +501,8 @@ def int8_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype, fp8: bool,
          tile_n: int = 0) -> torch.Tensor:
     device = _on_gpu("mm8", q, weight, x_scale, scale)
-    if tile_n not in (0, 128, 256):
-        raise LinnetError(f"mm8: tile_n is 0 (automatic), 128 or 256, not {tile_n}")
+    if tile_n not in (0, MM8_PERSISTENT, 128, 256):
+        raise LinnetError(f"mm8: tile_n is 0 (automatic), 1 (persistent), 128 or 256, not {tile_n}")
     rows, depth = q.shape
     width = weight.shape[0]
     if weight.shape[1] != depth:
@@ -520,11 +520,15 @@ def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: to
     return y
 
 
-def mm8_plan(rows: int, out_features: int, in_features: int) -> int:
-    """The tile width (128 or 256 output columns) `int8_mm` / `fp8_mm` take for this
-    shape on the current device."""
+# `tile_n` naming the persistent 256 x 256 form of the 8-bit product.
+MM8_PERSISTENT = 1
+
+
+def mm8_plan(rows: int, out_features: int, in_features: int, fp8: bool = True) -> int:
+    """The kernel `fp8_mm` (fp8 True) or `int8_mm` takes for this shape on the
+    current device: the tile width (128 or 256 output columns) or MM8_PERSISTENT."""
     tile = ctypes.c_int32(0)
-    _lib.call("lnq_mm8_plan", rows, out_features, in_features, ctypes.byref(tile))
+    _lib.call("lnq_mm8_plan", rows, out_features, in_features, int(fp8), ctypes.byref(tile))
     return tile.value
 
 

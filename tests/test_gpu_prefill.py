@@ -123,10 +123,10 @@ def _fp8_weight(n: int, k: int, seed: int):
     return (w / s).to(torch.float8_e4m3fn), s
 
 
-def test_config4_fp8_at_4096_rows_runs_the_wide_tiles() -> None:
+def test_config4_fp8_at_4096_rows_runs_the_persistent_form() -> None:
     rows, k, n = 4096, 8192, 28672
     print(f"config 4 rows={rows} k={k} n={n}", flush=True)
-    assert kernels.mm8_plan(rows, n, k) == 256
+    assert kernels.mm8_plan(rows, n, k) == kernels.MM8_PERSISTENT
     q, s = _fp8_weight(n, k, seed=0)
     scale = s.expand(n).contiguous().to(torch.bfloat16)
     x = torch.randn(rows, k, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
@@ -138,11 +138,11 @@ def test_config4_fp8_at_4096_rows_runs_the_wide_tiles() -> None:
     qx_s = qx[pick].cpu().view(torch.uint8).numpy()
     ref = linear.rows8_product_f64(qx_s, xs[pick].cpu().numpy(), q.cpu().view(torch.uint8).numpy(),
                                    scale.float().cpu().numpy(), True)
-    err, top = _report("fp8 mm8<256> vs f64 product of the rounded operands", got[pick].float().cpu().numpy(), ref)
+    err, top = _report("fp8 mm8p vs f64 product of the rounded operands", got[pick].float().cpu().numpy(), ref)
     assert err <= 1e-2 * top
     unrounded = linear.product_f64(x[pick].float().numpy(),
                                    (q.float() * scale.float()[:, None]).cpu().numpy())
-    err, top = _report("fp8 mm8<256> vs f64 product of unrounded x", got[pick].float().cpu().numpy(), unrounded)
+    err, top = _report("fp8 mm8p vs f64 product of unrounded x", got[pick].float().cpu().numpy(), unrounded)
     assert err <= 0.06 * top
     narrow = kernels.fp8_mm(qx, q, xs, scale.float(), torch.bfloat16, tile_n=128)
     assert (narrow.float() - got.float()).abs().max().item() <= 1e-2 * top
@@ -153,7 +153,7 @@ def test_int8_w8a8_at_256_wide_tiles(dtype: torch.dtype) -> None:
     """int8 rows x int8 weights (sums exact in int32) at 2048 x 8192 x 4096: 256 tiles of 256 columns."""
     rows, k, n = 2048, 4096, 8192
     print(f"int8 W8A8 rows={rows} k={k} n={n} {dtype}", flush=True)
-    assert kernels.mm8_plan(rows, n, k) == 256
+    assert kernels.mm8_plan(rows, n, k, fp8=False) == 256
     g = torch.Generator(device=DEV).manual_seed(2)
     w = torch.randn(n, k, generator=g, device=DEV) * 0.02
     wq, ws = kernels.quantize_int8(w, k, "f32")
@@ -206,3 +206,45 @@ def test_fp8_rounded_quantize_matches_the_oracle_at_config4_width() -> None:
     wq, ws = quant.rows8(x.float().numpy(), True)
     np.testing.assert_array_equal(s.cpu().numpy(), ws)
     np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), wq.view(np.uint8))
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize(("rows", "k", "n"), [(333, 1024, 768), (1100, 512, 14336), (4096, 8192, 28672), (7, 256, 256)])
+def test_mm8_persistent_form(fp8: bool, rows: int, k: int, n: int) -> None:
+    """The persistent 256 x 256 form (one workgroup a CU walking its tiles; 1100
+    rows x 14336 columns: 280 tiles, some workgroups two) against the f64 product
+    of the rounded operands, and bit for bit against the 256-column tile kernel,
+    which sums the same MFMAs in the same k order."""
+    print(f"mm8 persistent fp8={fp8} rows={rows} k={k} n={n}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows + k)
+    x = torch.randn(rows, k, generator=g, device=DEV).to(torch.bfloat16)
+    if fp8:
+        wq = (torch.randn(n, k, generator=g, device=DEV) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+        ws = torch.rand(n, generator=g, device=DEV) * 0.01 + 0.001
+        qx, xs = kernels.fp8_rows(x)
+        run = lambda t: kernels.fp8_mm(qx, wq, xs, ws, torch.bfloat16, tile_n=t)  # noqa: E731
+    else:
+        wq = torch.randint(-127, 128, (n, k), generator=g, device=DEV, dtype=torch.int8)
+        ws = torch.rand(n, generator=g, device=DEV) * 0.01 + 0.001
+        qx, xs = kernels.int8_rows(x)
+        run = lambda t: kernels.int8_mm(qx, wq, xs, ws, torch.bfloat16, tile_n=t)  # noqa: E731
+    got = run(kernels.MM8_PERSISTENT)
+    assert torch.equal(got, run(256))
+    pick = _sample_rows(rows, seed=2) if rows > 64 else np.arange(rows)
+    wbytes = wq.cpu().view(torch.uint8).numpy() if fp8 else wq.cpu().numpy()
+    qxb = qx[pick].cpu().view(torch.uint8).numpy() if fp8 else qx[pick].cpu().numpy()
+    ref = linear.rows8_product_f64(qxb, xs[pick].cpu().numpy(), wbytes, ws.cpu().numpy(), fp8)
+    err, top = _report(f"mm8 persistent fp8={fp8}", got[pick].float().cpu().numpy(), ref)
+    assert err <= 1e-2 * top
+
+
+def test_mm8_persistent_form_refuses_other_shapes() -> None:
+    from linnet_amd.errors import LinnetError
+
+    qx = torch.zeros(8, 256, dtype=torch.int8, device=DEV)
+    xs = torch.ones(8, 1, device=DEV)
+    for n, k in ((200, 256), (256, 384)):
+        w = torch.zeros(n, k, dtype=torch.int8, device=DEV)
+        with pytest.raises(LinnetError, match="persistent form"):
+            kernels.int8_mm(qx[:, :k] if k <= 256 else torch.zeros(8, k, dtype=torch.int8, device=DEV), w, xs,
+                            torch.ones(n, device=DEV), torch.bfloat16, tile_n=kernels.MM8_PERSISTENT)
