@@ -44,7 +44,7 @@ typedef int32_t LnqStatus;
 #define LNQ_KERNEL_AUTO 0
 #define LNQ_KERNEL_SKINNY 1 /* dequant-GEMV/skinny GEMM on MFMA, rows <= 64 */
 #define LNQ_KERNEL_TILED 2  /* prefill dequant-GEMM, LDS-staged bf16 tiles on MFMA */
-#define LNQ_KERNEL_GEMV 3   /* few-token dequant-GEMV, one workgroup per CU (rows 1..16;
+#define LNQ_KERNEL_GEMV 3   /* few-token dequant-GEMV, one workgroup per CU (rows 1..32;
                                in % 256 == 0 and <= 4096, group 128 or a multiple of 256;
                                past 16384 outputs, more workgroups of 64 rows than CUs;
                                one row also in = 256 * S * waves for S = 2..4
@@ -52,6 +52,9 @@ typedef int32_t LnqStatus;
                                8192 (S = 2) or 4096 (S = 3, 4)) */
 #define LNQ_KERNEL_TILED_128 4 /* the tiled kernel with tiles of 128 output columns */
 #define LNQ_KERNEL_TILED_256 5 /* the tiled kernel with tiles of 256 output columns */
+#define LNQ_KERNEL_PERSISTENT 6 /* the persistent prefill dequant-GEMM: 256 x 256 tiles,
+                                   one workgroup a CU walking its tiles (out % 256 == 0,
+                                   in % 256 == 0, group a power of two >= 64) */
 
 /* The ABI version this library implements (LNQ_ABI_VERSION). */
 LNQ_API uint32_t lnq_abi_version(void);
@@ -129,8 +132,8 @@ LNQ_API LnqStatus lnq_int4_linear_prologue(const void* x, const void* u, const f
 
 /* The kernel lnq_int4_linear runs for these arguments on the current device, its
  * operands 16-byte aligned: *chosen = LNQ_KERNEL_GEMV, LNQ_KERNEL_SKINNY,
- * LNQ_KERNEL_TILED_128 or LNQ_KERNEL_TILED_256 (GEMV also for 17..64 rows run as
- * 16-row chunks). Fails as lnq_int4_linear would on arguments it refuses.
+ * LNQ_KERNEL_TILED_128, LNQ_KERNEL_TILED_256 or LNQ_KERNEL_PERSISTENT (GEMV also
+ * for 33..64 rows run as 32-row chunks). Fails as lnq_int4_linear would on arguments it refuses.
  * No counterpart in the reference (its dispatch is Python, torch_source.cpp:1553-1570):
  * lets a caller or a test see which kernel a shape takes. */
 LNQ_API LnqStatus lnq_int4_linear_plan(int64_t rows, int64_t in_features, int64_t out_features,

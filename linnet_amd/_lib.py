@@ -21,7 +21,7 @@ ABI_VERSION = 1
 
 LNQ_OK, LNQ_ERROR, LNQ_UNAVAILABLE = 0, 1, 2
 BF16, F16, F32 = 0, 1, 2
-KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV, KERNEL_TILED_128, KERNEL_TILED_256 = 0, 1, 2, 3, 4, 5
+KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV, KERNEL_TILED_128, KERNEL_TILED_256, KERNEL_PERSISTENT = range(7)
 PROLOGUE_RMSNORM, PROLOGUE_SILU_MUL = 1, 2
 PACKING_GPTQ, PACKING_AWQ = 0, 1
 

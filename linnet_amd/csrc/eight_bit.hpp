@@ -147,17 +147,20 @@ __global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
 
   // Load i of wave w writes stage rows 64 i + 8 w .. + 7 (1 KB; lane l at byte
   // 16 l: row 64 i + 8 w + l / 8, stored column l % 8 holding source column
-  // (l % 8) ^ key(row), key = (row >> 1) & 7, the same for every i).
+  // (l % 8) ^ key(row), key = (row >> 1) & 7, the same for every i). Each
+  // load's row offset is in its lane offset and only the step's k offset in
+  // the uniform one, so rows past M are out of range whether or not the
+  // uniform offset is range-checked.
   const int lrow8 = 8 * wave + (lane >> 3);
   const int lcol = (lane & 7) ^ ((lrow8 >> 1) & 7);
   const int aoff_g = (m0 + lrow8) * K + lcol * 16;
   const int boff_g = (n0 + lrow8) * K + lcol * 16;
   const int lds_w = wave * 1024;
   auto load_a = [&](uint8_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 64 * BK), 16, aoff_g, k0 + i * 64 * K, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 64 * BK), 16, aoff_g + i * 64 * K, k0, 0, 0);
   };
   auto load_b = [&](uint8_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 64 * BK), 16, boff_g, k0 + i * 64 * K, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 64 * BK), 16, boff_g + i * 64 * K, k0, 0, 0);
   };
 
   Acc acc[FA][FB];

@@ -617,6 +617,10 @@ LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* sc
                             int G, int dtype, int bn, hipStream_t stream);
 bool int4_tiled_supports(int M, int N, int K, int G, int dtype);
 int int4_tiled_width(int M, int N);
+LnqStatus launch_int4_persistent(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                 const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream);
+bool int4_persistent_supports(int M, int N, int K, int G, int dtype);
+bool int4_persistent_preferred(int M, int N, int K, int G, int dtype);
 
 // Defined in int4_gemv.hip: the one-token dequant-GEMV.
 bool int4_gemv_supports(int M, int N, int K, int G, const void* x, const void* packed, const void* scale,
@@ -656,16 +660,28 @@ static bool check_int4_linear(int64_t rows, int64_t in_features, int64_t out_fea
     set_error("%s: sizes exceed 2^31", who);
     return false;
   }
-  if (!(kernel >= LNQ_KERNEL_AUTO && kernel <= LNQ_KERNEL_TILED_256)) {
+  if (!(kernel >= LNQ_KERNEL_AUTO && kernel <= LNQ_KERNEL_PERSISTENT)) {
     set_error("%s: unknown kernel %d", who, kernel);
     return false;
   }
   return true;
 }
 
-// The kernel lnq_int4_linear runs (LNQ_KERNEL_GEMV, _SKINNY, _TILED_128 or
-// _TILED_256), or -1 with the message set when the one asked for does not take
-// the shape. GEMV at 33..64 rows means the few-token GEMV per 32-row chunk.
+// The prefill kernel for a shape the tiled kernel takes: where 256-column tiles
+// give (nearly) every CU a tile, the 256-column tiled kernel, or the persistent
+// 256 x 256 form where it takes the shape and there are more tiles than CUs
+// (config 3, (K, N) = (4096, 14336) at 2048 rows, 448 tiles: 1104-1114 against
+// 1043-1067 TFLOP/s for int4_tiled_kernel<256> in the same runs; at 1024 rows,
+// 224 tiles, one a workgroup: 1036 against 1064); otherwise 128-column tiles.
+static int prefill_kernel(int M, int N, int K, int G, int dtype) {
+  if (int4_tiled_width(M, N) != 256) return LNQ_KERNEL_TILED_128;
+  return int4_persistent_preferred(M, N, K, G, dtype) ? LNQ_KERNEL_PERSISTENT : LNQ_KERNEL_TILED_256;
+}
+
+// The kernel lnq_int4_linear runs (LNQ_KERNEL_GEMV, _SKINNY, _TILED_128,
+// _TILED_256 or _PERSISTENT), or -1 with the message set when the one asked for
+// does not take the shape. GEMV at 33..64 rows means the few-token GEMV per
+// 32-row chunk.
 static int choose_int4_kernel(int M, int N, int K, int G, int dtype, int kernel, const void* x,
                               const void* packed, const void* scale, const void* zero) {
   // The one-workgroup-per-CU GEMV takes 1..32 rows (1: one x row broadcast; 2..32:
@@ -695,17 +711,22 @@ static int choose_int4_kernel(int M, int N, int K, int G, int dtype, int kernel,
     const bool few = M <= 6;
     if (gemv_ok && (M == 1 || few || (M > 4 && wide))) return LNQ_KERNEL_GEMV;
     if (wide && M > 32 && M <= 64 && int4_gemv_supports(32, N, K, G, x, packed, scale, zero)) return LNQ_KERNEL_GEMV;
-    if (M > 64 && int4_tiled_supports(M, N, K, G, dtype))
-      return int4_tiled_width(M, N) == 256 ? LNQ_KERNEL_TILED_256 : LNQ_KERNEL_TILED_128;
+    if (M > 64 && int4_tiled_supports(M, N, K, G, dtype)) return prefill_kernel(M, N, K, G, dtype);
     return LNQ_KERNEL_SKINNY;
   }
   if (kernel == LNQ_KERNEL_SKINNY) return LNQ_KERNEL_SKINNY;
+  if (kernel == LNQ_KERNEL_PERSISTENT) {
+    if (!int4_persistent_supports(M, N, K, G, dtype)) {
+      set_error("lnq_int4_linear: the persistent kernel does not take M=%d N=%d K=%d group=%d", M, N, K, G);
+      return -1;
+    }
+    return LNQ_KERNEL_PERSISTENT;
+  }
   if (!int4_tiled_supports(M, N, K, G, dtype)) {
     set_error("lnq_int4_linear: the tiled kernel does not take M=%d N=%d K=%d group=%d", M, N, K, G);
     return -1;
   }
-  if (kernel == LNQ_KERNEL_TILED)
-    return int4_tiled_width(M, N) == 256 ? LNQ_KERNEL_TILED_256 : LNQ_KERNEL_TILED_128;
+  if (kernel == LNQ_KERNEL_TILED) return prefill_kernel(M, N, K, G, dtype);
   return kernel;
 }
 
@@ -745,6 +766,8 @@ LNQ_API LnqStatus lnq_int4_linear(const void* x, const uint8_t* packed, const vo
     }
     return LNQ_OK;
   }
+  if (code == LNQ_KERNEL_PERSISTENT)
+    return launch_int4_persistent(x, packed, scale, zero, bias, y, M, N, K, G, dtype, s);
   if (code == LNQ_KERNEL_TILED_128 || code == LNQ_KERNEL_TILED_256)
     return launch_int4_tiled(x, packed, scale, zero, bias, y, M, N, K, G, dtype,
                              code == LNQ_KERNEL_TILED_256 ? 256 : 128, s);

@@ -169,15 +169,18 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   // x: load i (0..3) of wave w writes LDS rows 64 i + 8 w .. + 7 (1 KB, lane l
   // at byte 16 l: row 64 i + 8 w + l / 8, stored column l % 8). The stored
   // column holds source column (l % 8) ^ key(row); key = (row >> 1) & 7 =
-  // (4 w + l / 16) & 7 does not depend on i, so the 4 loads differ only by a
-  // uniform offset.
+  // (4 w + l / 16) & 7 does not depend on i. Each load's row offset is in its
+  // lane offset and only the step's k offset in the uniform one, so rows past M
+  // are out of range whether or not the uniform offset is range-checked.
   const int xrow = 8 * wave + (lane >> 3);
   const int xcol = (lane & 7) ^ ((xrow >> 1) & 7);
-  const int xoff = (m0 + xrow) * K * 2 + xcol * 16;
+  int xoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xoff[i] = (m0 + xrow + 64 * i) * K * 2 + xcol * 16;
   const int xlds = wave * 512;  // elements
   auto load_x = [&](uint16_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + xlds + i * 64 * BK), 16, xoff, 2 * k0 + i * 128 * K, 0,
-                                              0);
+    const int v = xoff[i];  // through a local: an array element passed directly drops the host launch stub
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + xlds + i * 64 * BK), 16, v, 2 * k0, 0, 0);
   };
 
   // W: thread -> row n0 + tid / TPR, KPT weights (KPT / 2 packed bytes) at k
@@ -471,13 +474,16 @@ __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
 
   // x: DMA i (0..FA-1) of wave w writes rows 32 i + 8 w .. + 7 of a stage, in the
   // swizzled layout of int4_tiled_kernel (the key (row >> 1) & 7 = (4 w + l /
-  // 16) & 7 does not depend on i).
+  // 16) & 7 does not depend on i); the row offsets in the lane offsets.
   const int xrow = 8 * wave + (lane >> 3);
   const int xcol = (lane & 7) ^ ((xrow >> 1) & 7);
-  const int xoff = (m0 + xrow) * K * 2 + xcol * 16;
+  int xoff[FA];
+#pragma unroll
+  for (int i = 0; i < FA; ++i) xoff[i] = (m0 + xrow + 32 * i) * K * 2 + xcol * 16;
   auto load_x = [&](int stage, __amdgpu_buffer_rsrc_t r, int k0, int i) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(XS + stage * BM * BK + wave * 512 + i * 32 * BK), 16, xoff,
-                                              2 * k0 + i * 64 * K, 0, 0);
+    const int v = xoff[i];  // through a local: an array element passed directly drops the host launch stub
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(XS + stage * BM * BK + wave * 512 + i * 32 * BK), 16, v,
+                                              2 * k0, 0, 0);
   };
 
   // W: lane -> column n0 + 32 wave + lane % 32; half h = lane / 32 reads input
@@ -684,6 +690,334 @@ __global__ __launch_bounds__(narrow::THREADS, 1) void int4_narrow_kernel(
   }
 }
 
+// ------------------------------------------- persistent 256 x 256 form: int4_persistent_kernel
+// One workgroup per CU walks its 256 x 256 tiles (tile b, b + G, .. of the
+// XCD-grouped order of tile_of, G workgroups); the k-steps of all its tiles
+// form one stream, so the loads of the next tile's first steps are in flight
+// while a tile finishes.
+//
+// 4 waves, one per SIMD, each owning 128 x 128 outputs (4 x 4 MFMA 32x32x16
+// tiles, 256 accumulator registers): per MFMA a wave reads half the LDS bytes
+// of int4_tiled_kernel's 128 x 64 waves -- about 96 LDS bytes a clock per CU
+// with the weights' stores, against 128. 64 inputs a step, two stages of x
+// (256 rows) and of dequantized weights (256 rows of the 16-bit type), each a
+// 32 KB array of 128-byte rows with 16-byte columns XOR-swizzled by bits 1..3
+// of the row (x and weights in separate arrays: the compiler then waits for x's
+// loads only before reading x):
+//   * x moves HBM/L2 -> LDS by buffer_load ... lds, 8 rows x 128 bytes an
+//     instruction (whole lines), issued in step g's last kk for step g + 2;
+//   * thread t owns weight row t of the tile: its 32 packed bytes, scale and
+//     zero point of step g + 3 are requested in step g's first kk (four
+//     register sets, steps unrolled by four), and step g + 1's are dequantized
+//     ((q - z) * s in f32, exact, one rounding: every product is x * bf16(W) as
+//     in the reference's dequant + BLAS path) and stored over step g's first
+//     three kk;
+//   * one barrier a step, before the last kk: past it every wave's x and
+//     weights of step g + 1 are in LDS and no wave reads step g's stage again,
+//     so the last kk reads step g + 1's first operands and refills step g's x.
+// A tile's first step starts its accumulators from C = 0; after its last the
+// waves round their outputs (and add the bias) and store them.
+namespace gemmp {
+constexpr int BM = 256, BN = 256, BK = 64, NW = 4, THREADS = 64 * NW;
+constexpr int FA = 4, FB = 4;          // 32-row / 32-column fragments of a wave
+constexpr int PART = BM * BK * 2;      // bytes of a stage's x (or weight) array
+constexpr int XL = PART / 1024 / NW;   // x loads (1 KB) of a wave a step
+constexpr int WL = 4;                  // weight, scale and zero loads of a thread a step
+constexpr int U = 4;                   // steps a loop iteration (K % 256 == 0)
+static_assert(XL == 8 && BM == BN && BN == THREADS, "one weight row a thread");
+}  // namespace gemmp
+
+template <int DT>
+__global__ __launch_bounds__(gemmp::THREADS, 1) void int4_persistent_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+    const uint8_t* __restrict__ zero, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
+    int gshift) {
+  using namespace gemmp;
+  using E = Elem<DT>;
+  constexpr int KK = BK / 16;  // MFMA 32x32x16 sub-steps a step
+  __shared__ __attribute__((aligned(16))) uint8_t X0[PART];
+  __shared__ __attribute__((aligned(16))) uint8_t X1[PART];
+  __shared__ __attribute__((aligned(16))) uint8_t W0[PART];
+  __shared__ __attribute__((aligned(16))) uint8_t W1[PART];
+  LNQ_MFMA_IN_AGPRS();
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
+  const int total = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int b0 = blockIdx.x;
+  if (b0 >= total) return;
+  const int mine = (total - 1 - b0) / G + 1;  // tiles b0, b0 + G, ..
+  const int steps = K / BK;                   // a multiple of U
+  const int nsteps = mine * steps;
+  const int groups = K >> gshift;
+
+  // Rows past M read zeros through the range check (the row offset is in the
+  // lane offset, only the step's k offset in the uniform one); steps past the
+  // stream read through 0-byte descriptors (no traffic, the same count of loads).
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint32_t>(static_cast<size_t>(M) * K * 2));
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * (K >> 1)));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
+  const __amdgpu_buffer_rsrc_t rnull = buffer_rsrc(packed, 0);
+
+  // A tile's x lane offsets and weight row: x load i (0..7) of wave w fills x
+  // rows 32 i + 8 w + l / 8 (1 KB, lane l at byte 16 l, stored column l % 8
+  // holding source column (l % 8) ^ key(row), key = (row >> 1) & 7, the same
+  // for every i); thread t reads weight row n0 + t.
+  const int xr = 8 * wave + (lane >> 3);
+  const int x_lane = xr * K * 2 + 16 * ((lane & 7) ^ ((xr >> 1) & 7));
+  struct TileOff {
+    uint32_t x[XL];
+    int n;  // weight row of this thread
+  };
+  auto tile_off = [&](int r, TileOff& o) __attribute__((always_inline)) {
+    int tm, tn;
+    tile_of(b0 + r * G, tiles_m, tiles_n, tm, tn);
+#pragma unroll
+    for (int i = 0; i < XL; ++i) o.x[i] = static_cast<uint32_t>((tm * BM + 32 * i) * K * 2 + x_lane);
+    o.n = tn * BN + tid;
+  };
+  auto load_x = [&](uint8_t* st, bool in, const TileOff& o, int ks, int i) __attribute__((always_inline)) {
+    // The lane offset through a local: a structure member passed to the builtin
+    // directly makes the host pass drop the kernel's launch stub.
+    const __amdgpu_buffer_rsrc_t q = in ? rx : rnull;
+    const uint32_t v = o.x[i];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(q, (lds_ptr)(st + (4 * i + wave) * 1024), 16, v, in ? ks * BK * 2 : 0, 0,
+                                              0);
+  };
+  struct WRegs {
+    u32x4 w0, w1;  // 64 codes
+    uint32_t s, z;
+  };
+  auto load_w = [&](WRegs& r, bool in, const TileOff& o, int ks) __attribute__((always_inline)) {
+    const int g = (ks * BK) >> gshift;
+    const __amdgpu_buffer_rsrc_t qw = in ? rw : rnull, qs = in ? rs : rnull, qz = in ? rz : rnull;
+    const uint32_t wo = static_cast<uint32_t>(o.n * (K >> 1) + ks * (BK / 2));
+    r.w0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qw, wo, 0, 0));
+    r.w1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qw, wo + 16, 0, 0));
+    r.s = static_cast<uint16_t>(
+        __builtin_amdgcn_raw_buffer_load_b16(qs, static_cast<uint32_t>((o.n * groups + g) * 2), 0, 0));
+    r.z = __builtin_amdgcn_raw_buffer_load_b8(qz, static_cast<uint32_t>(o.n * groups + g), 0, 0);
+  };
+
+  // Dequantization of a step's 8 packed dwords into row tid of a weight stage,
+  // as 64 positions (8 a dword, 17 VALU instructions a dword): the codes become
+  // f16 halves without a conversion ((0x6400 | q) is 1024 + q, (0x6400 | 16 q)
+  // is 1024 + 16 q) and v_fma_mix_f32 gives (1024 + q) s - (1024 + z) s and
+  // (1024 + 16 q) (s / 16) - (64 + z) s, each exactly (q - z) s; one rounding a
+  // pair. Dword d holds codes 8 d .. 8 d + 7 of the step: 16-byte column d.
+  uint32_t mlo = 0x000f000fu, mhi = 0x00f000f0u, magic = 0x64006400u;
+  hide_in_vgpr(mlo);
+  hide_in_vgpr(mhi);
+  hide_in_vgpr(magic);
+  auto half_of = [](uint32_t m, int h) __attribute__((always_inline)) -> float { return static_cast<float>(__builtin_bit_cast(f16x2, m)[h]); };
+  struct Deq {
+    uint32_t m0, m1, m2, m3, t;
+    float v[8];
+    u32x4 o;
+    float sv, cv, sv16, cv16;
+  };
+  Deq q;
+  const int wkey = (tid >> 1) & 7;
+  auto deq_pos = [&](const WRegs& r, int pos, uint8_t* wst) __attribute__((always_inline)) {
+    const int d = pos >> 3;
+    const uint32_t w = d < 4 ? r.w0[d] : r.w1[d - 4];
+    switch (pos & 7) {
+      case 0:
+        if (d == 0) {
+          q.sv = E::to_f32(static_cast<uint16_t>(r.s));
+          const float z = static_cast<float>(r.z & 0xffu);
+          q.cv = -(1024.f + z) * q.sv;
+          q.sv16 = q.sv * 0.0625f;
+          q.cv16 = -(64.f + z) * q.sv;
+        }
+        q.m0 = and_or(w, mlo, magic);
+        q.t = w >> 8;
+        break;
+      case 1: q.m1 = and_or(w, mhi, magic); q.v[0] = fmaf(half_of(q.m0, 0), q.sv, q.cv); break;
+      case 2: q.v[4] = fmaf(half_of(q.m0, 1), q.sv, q.cv); q.v[1] = fmaf(half_of(q.m1, 0), q.sv16, q.cv16); break;
+      case 3: q.v[5] = fmaf(half_of(q.m1, 1), q.sv16, q.cv16); q.o.x = pack2<DT>(q.v[0], q.v[1]); break;
+      case 4: q.m2 = and_or(q.t, mlo, magic); q.m3 = and_or(q.t, mhi, magic); break;
+      case 5:
+        q.v[2] = fmaf(half_of(q.m2, 0), q.sv, q.cv);
+        q.v[3] = fmaf(half_of(q.m3, 0), q.sv16, q.cv16);
+        q.o.y = pack2<DT>(q.v[2], q.v[3]);
+        break;
+      case 6:
+        q.v[6] = fmaf(half_of(q.m2, 1), q.sv, q.cv);
+        q.v[7] = fmaf(half_of(q.m3, 1), q.sv16, q.cv16);
+        q.o.z = pack2<DT>(q.v[4], q.v[5]);
+        break;
+      default:
+        q.o.w = pack2<DT>(q.v[6], q.v[7]);
+        *reinterpret_cast<u32x4*>(wst + tid * 128 + ((d ^ wkey) << 4)) = q.o;
+        break;
+    }
+  };
+
+  f32x16 acc[FA][FB];
+  const int lrow = lane & 31, lk = lane >> 5;
+  // Operand offsets within a stage array per kk: fragments 32 rows (4096 bytes)
+  // apart with the same key.
+  uint32_t aoff[KK], boff[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    aoff[kk] = static_cast<uint32_t>((wm * 128 + lrow) * 128 + (((2 * kk + lk) ^ ((lrow >> 1) & 7)) << 4));
+    boff[kk] = static_cast<uint32_t>((wn * 128 + lrow) * 128 + (((2 * kk + lk) ^ ((lrow >> 1) & 7)) << 4));
+  }
+  u32x4 af[2][FA], bf[2][FB];
+  constexpr int NMF = FA * FB;
+  constexpr int READS = FA + FB;
+  auto read_one = [&](int set, const uint8_t* xs, const uint8_t* ws, int kk, int r) __attribute__((always_inline)) {
+    if (r < FA) af[set][r] = *reinterpret_cast<const u32x4*>(xs + aoff[kk] + r * 4096);
+    else bf[set][r - FA] = *reinterpret_cast<const u32x4*>(ws + boff[kk] + (r - FA) * 4096);
+  };
+
+  // The epilogue of tile (m0, n0): lane l, register r of fragment (a, b) holds
+  // row m0 + 128 wm + 32 a + l % 32 and column n0 + 128 wn + 32 b + 8 (r / 4) + 4
+  // (l / 32) + r % 4 (the weights are the MFMA's A operand).
+  auto epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < FB; ++b) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int n = n0 + wn * 128 + b * 32 + 8 * q4 + 4 * lk;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (bias != nullptr) {
+          const u32x2 bb = *reinterpret_cast<const u32x2*>(bias + n);
+          bv[0] = E::to_f32(static_cast<uint16_t>(bb.x & 0xffffu));
+          bv[1] = E::to_f32(static_cast<uint16_t>(bb.x >> 16));
+          bv[2] = E::to_f32(static_cast<uint16_t>(bb.y & 0xffffu));
+          bv[3] = E::to_f32(static_cast<uint16_t>(bb.y >> 16));
+        }
+#pragma unroll
+        for (int a = 0; a < FA; ++a) {
+          const int m = m0 + wm * 128 + a * 32 + lrow;
+          uint32_t o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            uint16_t v = E::from_f32(acc[a][b][4 * q4 + i]);
+            if (bias != nullptr) v = E::from_f32(E::to_f32(v) + bv[i]);
+            o[i] = v;
+          }
+          if (m < M)
+            *reinterpret_cast<u32x2*>(y + static_cast<size_t>(m) * N + n) =
+                u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        }
+      }
+      // One column fragment at a time: the next tile's operands are live here.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Step g on stages (xc, wc), step g + 1's on (xn, wn_): kk 0..2 run MFMAs on kk
+  // while kk + 1's operands are read, dequantize step g + 1's weights (dq) into
+  // wn_ (64 positions over their 48 slots) and, in kk 0, request step g + 3's
+  // weights (into req); then this wave's x loads of step g + 1 have landed (only
+  // this step's WL weight loads were issued after them) and its LDS stores and
+  // reads are done, the barrier, and kk 3 reads step g + 1's first operands
+  // and issues step g + 2's x loads into xc, one every other slot.
+  auto step = [&](auto first_tag, uint8_t* xc, uint8_t* wc, uint8_t* xn, uint8_t* wn_, const WRegs& dq, WRegs& req,
+                  bool w_in, const TileOff& wo, int w_ks, bool x_in, const TileOff& xo, int x_ks) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(first_tag)::value;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const int set = kk & 1;
+      const bool last = kk == KK - 1;
+      if (last) {
+        wait_vm<WL>();
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int sl = 0; sl < NMF; ++sl) {
+        const int a = sl / FB, b = sl % FB;
+        if (FIRST && kk == 0) acc[a][b] = mfma32x32x16<DT>(bf[set][b], af[set][a], f32x16{});
+        else acc[a][b] = mfma32x32x16<DT>(bf[set][b], af[set][a], acc[a][b]);
+        static_assert(2 * READS == NMF, "one operand read every other slot");
+        if ((sl & 1) == 0) {
+          if (last) read_one(set ^ 1, xn, wn_, 0, sl >> 1);
+          else read_one(set ^ 1, xc, wc, kk + 1, sl >> 1);
+        }
+        if (!last) {
+          const int p0 = (kk * 64) / 3, p1 = ((kk + 1) * 64) / 3;
+#pragma unroll
+          for (int p = p0 + (sl * (p1 - p0)) / NMF; p < p0 + ((sl + 1) * (p1 - p0)) / NMF; ++p) deq_pos(dq, p, wn_);
+        }
+        if (kk == 0 && sl == 0) load_w(req, w_in, wo, w_ks);
+        if (last && (sl & 1)) load_x(xc, x_in, xo, x_ks, sl >> 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  // Prologue (tile 0; a tile has at least U steps): x of steps 0 and 1 and the
+  // weights of steps 0..2 requested; step 0's weights dequantized into W0;
+  // barrier; step 0's first operands read.
+  TileOff oc, on;
+  tile_off(0, oc);
+  WRegs wr[4];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) load_x(X0, true, oc, 0, i);
+#pragma unroll
+  for (int i = 0; i < XL; ++i) load_x(X1, true, oc, 1, i);
+  load_w(wr[0], true, oc, 0);
+  load_w(wr[1], true, oc, 1);
+  load_w(wr[2], true, oc, 2);
+  wait_vm<2 * WL>();
+#pragma unroll
+  for (int pos = 0; pos < 64; ++pos) deq_pos(wr[0], pos, W0);
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int r = 0; r < READS; ++r) read_one(0, X0, W0, 0, r);
+
+  // Groups of U = 4 steps (a tile is whole groups): step g + s of tile r at
+  // k-step ks + s, on stage (g + s) % 2, weight registers (g + s) % 4. Step g + s
+  // requests the weights of step g + s + 3 and the x of step g + s + 2: of tile r
+  // while they lie in this group, else of the next group's tile (r, or r + 1
+  // after a tile's last group). No branch inside a group: the compiler would
+  // otherwise move the MFMAs across the blocks it split the group into. A tile's
+  // first group is its own copy (accumulators started at zero).
+  using T = std::integral_constant<bool, true>;
+  using F = std::integral_constant<bool, false>;
+  int r = 0;
+  auto group = [&](int g, int ks, auto first_tag) __attribute__((always_inline)) {
+    const bool ends = ks + U == steps;
+    const int kn = ends ? 0 : ks + U;
+    tile_off(r + (ends ? 1 : 0), on);
+    step(first_tag, X0, W0, X1, W1, wr[1], wr[3], g + 3 < nsteps, oc, ks + 3, g + 2 < nsteps, oc, ks + 2);
+    step(F{}, X1, W1, X0, W0, wr[2], wr[0], g + 4 < nsteps, on, kn, g + 3 < nsteps, oc, ks + 3);
+    step(F{}, X0, W0, X1, W1, wr[3], wr[1], g + 5 < nsteps, on, kn + 1, g + 4 < nsteps, on, kn);
+    step(F{}, X1, W1, X0, W0, wr[0], wr[2], g + 6 < nsteps, on, kn + 2, g + 5 < nsteps, on, kn + 1);
+    oc = on;
+  };
+  int g = 0;
+  for (; r < mine; ++r) {
+    group(g, 0, T{});
+    g += U;
+    for (int ks = U; ks < steps; ks += U, g += U) group(g, ks, F{});
+    int tm, tn;
+    tile_of(b0 + r * G, tiles_m, tiles_n, tm, tn);
+    epilogue(tm * BM, tn * BN);
+  }
+  // Loads of the steps past the stream (0-byte reads) may be in flight.
+  wait_vm<0>();
+}
+
+bool int4_persistent_supports(int M, int N, int K, int G, int dtype) {
+  // 256-column tiles (N % 256), groups of 4 steps of 64 inputs (K % 256), a step
+  // within one group (G a multiple of 64), 32-bit buffer offsets.
+  return (dtype == LNQ_BF16 || dtype == LNQ_F16) && M > 0 && N > 0 && N % gemmp::BN == 0 && K > 0 && K % 256 == 0 &&
+         G >= 64 && G % 64 == 0 && (G & (G - 1)) == 0 && K % G == 0 && static_cast<size_t>(M) * K * 2 < (1ull << 31) &&
+         static_cast<size_t>(N) * (K >> 1) < (1ull << 31);
+}
+
 bool int4_tiled_supports(int M, int N, int K, int G, int dtype) {
   // Buffer offsets are 32-bit: x and the packed weight stay under 2 GiB. A
   // thread's 16 or 32 weights of a step lie in one group: G is a power of two
@@ -728,6 +1062,14 @@ static void launch_tiled(const void* x, const uint8_t* packed, const void* scale
                        bs, ys, M, N, K, gshift);
 }
 
+// Whether the persistent form takes the shape and has more 256 x 256 tiles than
+// there are CUs (with one tile a workgroup it has no next tile to prefetch and
+// the 8-wave tiled kernel is ahead).
+bool int4_persistent_preferred(int M, int N, int K, int G, int dtype) {
+  const long tiles = static_cast<long>((M + gemmp::BM - 1) / gemmp::BM) * ((N + gemmp::BN - 1) / gemmp::BN);
+  return tiles > compute_units() && int4_persistent_supports(M, N, K, G, dtype);
+}
+
 // 256-column tiles read half the x bytes per FLOP of 128-column ones, but only
 // pay while they still give nearly every compute unit a tile.
 int int4_tiled_width(int M, int N) {
@@ -737,6 +1079,24 @@ int int4_tiled_width(int M, int N) {
   // against 97 us).
   const long tiles256 = static_cast<long>((M + gemm::BM - 1) / gemm::BM) * ((N + 255) / 256);
   return 8 * tiles256 >= 7L * compute_units() ? 256 : 128;
+}
+
+LnqStatus launch_int4_persistent(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                 const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream) {
+  const int gshift = __builtin_ctz(static_cast<unsigned>(G));
+  const int tiles = ((M + gemmp::BM - 1) / gemmp::BM) * (N / gemmp::BN);
+  const dim3 grid(tiles < compute_units() ? tiles : compute_units());
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* ys = static_cast<uint16_t*>(y);
+  if (dtype == LNQ_BF16)
+    hipLaunchKernelGGL((int4_persistent_kernel<LNQ_BF16>), grid, dim3(gemmp::THREADS), 0, stream, xs, packed, ss, zero,
+                       bs, ys, M, N, K, gshift);
+  else
+    hipLaunchKernelGGL((int4_persistent_kernel<LNQ_F16>), grid, dim3(gemmp::THREADS), 0, stream, xs, packed, ss, zero,
+                       bs, ys, M, N, K, gshift);
+  return launched("int4_persistent");
 }
 
 LnqStatus launch_int4_tiled(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,

@@ -26,6 +26,7 @@ KERNELS = {
     "gemv": _lib.KERNEL_GEMV,
     "tiled128": _lib.KERNEL_TILED_128,
     "tiled256": _lib.KERNEL_TILED_256,
+    "persistent": _lib.KERNEL_PERSISTENT,
 }
 _KERNEL_NAMES = {code: name for name, code in KERNELS.items()}
 
@@ -218,8 +219,8 @@ def take_inputs(x: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
 def int4_linear_plan(rows: int, in_features: int, out_features: int, group: int,
                      dtype: torch.dtype = torch.bfloat16, kernel: str = "auto") -> str:
     """The kernel `int4_linear` runs for this shape on the current device: "gemv"
-    (17..64 rows: the few-token GEMV per 16-row chunk), "skinny", "tiled128" or
-    "tiled256". Raises as `int4_linear` would for a shape it refuses."""
+    (33..64 rows: the few-token GEMV per 32-row chunk), "skinny", "tiled128",
+    "tiled256" or "persistent". Raises as `int4_linear` would for a shape it refuses."""
     if kernel not in KERNELS:
         raise LinnetError(f"int4_linear_plan: kernel is one of {', '.join(KERNELS)}")
     chosen = ctypes.c_int32(-1)

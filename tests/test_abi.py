@@ -213,7 +213,9 @@ def test_plan_queries_name_the_kernel_without_a_device() -> None:
     8-bit tiles; a forced kernel that does not take the shape is refused."""
     assert kernels.int4_linear_plan(1, 4096, 14336, 128) == "gemv"
     assert kernels.int4_linear_plan(16, 4096, 14336, 128) == "gemv"
-    assert kernels.int4_linear_plan(2048, 4096, 14336, 128) == "tiled256"
+    assert kernels.int4_linear_plan(2048, 4096, 14336, 128) == "persistent"
+    assert kernels.int4_linear_plan(2048, 4096, 14336, 128, kernel="tiled") == "persistent"
+    assert kernels.int4_linear_plan(2048, 4096, 14336, 32) == "tiled256"
     assert kernels.int4_linear_plan(2048, 4096, 4096, 128) == "tiled128"
     assert kernels.int4_linear_plan(2048, 14336, 4096, 128) == "tiled128"
     assert kernels.int4_linear_plan(8, 512, 64, 128) == "skinny"

@@ -62,9 +62,9 @@ def _sample_rows(rows: int, seed: int) -> np.ndarray:
 # At 1024 rows the 128-column kernel runs 128-row tiles (256-row tiles would
 # leave more than half the compute units idle); at 2048 rows, 256-row tiles.
 # 224 tiles of 256 x 256 (1024 rows, N = 14336) fill 7/8 of the CUs: the
-# 256-column kernel.
+# 256-column kernel; at 2048 rows, 448 tiles, the persistent 256 x 256 form.
 @pytest.mark.parametrize(("rows", "k", "n", "want_kernel"), [
-    (2048, 4096, 14336, "tiled256"), (2048, 4096, 4096, "tiled128"), (2048, 14336, 4096, "tiled128"),
+    (2048, 4096, 14336, "persistent"), (2048, 4096, 4096, "tiled128"), (2048, 14336, 4096, "tiled128"),
     (1024, 14336, 4096, "tiled128"), (1024, 4096, 14336, "tiled256"),
 ])
 def test_config3_prefill_matches_the_oracle(rows: int, k: int, n: int, want_kernel: str) -> None:
@@ -85,8 +85,8 @@ def test_config3_prefill_matches_the_oracle(rows: int, k: int, n: int, want_kern
     full = (xd.float() @ w.float().T)
     err, top = _report(f"int4 {want_kernel} vs dequantize + GEMM (all rows)", y.float().cpu().numpy(), full.cpu().numpy())
     assert err <= 1e-2 * top
-    # The other tile width agrees within bf16 rounding.
-    other = "tiled128" if want_kernel == "tiled256" else "tiled256"
+    # Another prefill kernel agrees within bf16 rounding.
+    other = "tiled256" if want_kernel == "tiled128" else "tiled128"
     y2 = kernels.int4_linear(xd, packed, scale, zero, kernel=other).float()
     assert (y2 - y.float()).abs().max().item() <= 1e-2 * top
 
@@ -248,3 +248,44 @@ def test_mm8_persistent_form_refuses_other_shapes() -> None:
         with pytest.raises(LinnetError, match="persistent form"):
             kernels.int8_mm(qx[:, :k] if k <= 256 else torch.zeros(8, k, dtype=torch.int8, device=DEV), w, xs,
                             torch.ones(n, device=DEV), torch.bfloat16, tile_n=kernels.MM8_PERSISTENT)
+
+
+@pytest.mark.parametrize(("rows", "k", "n", "group", "dtype"), [
+    (333, 1024, 768, 128, torch.bfloat16),   # a partial row tile
+    (1100, 512, 14336, 128, torch.bfloat16),  # 280 tiles: some workgroups two
+    (2048, 4096, 14336, 128, torch.bfloat16),  # config 3
+    (96, 2048, 512, 256, torch.float16),
+    (7, 256, 256, 64, torch.bfloat16),        # one tile of one group of steps
+])
+def test_int4_persistent_form(rows: int, k: int, n: int, group: int, dtype: torch.dtype) -> None:
+    """The persistent 256 x 256 dequant-GEMM against the f64 product of the
+    dequantized weight (sampled rows), and against the 256-column tiled kernel."""
+    print(f"int4 persistent rows={rows} k={k} n={n} group={group} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows + k)
+    w = torch.randn(n, k, generator=g, device=DEV) * 0.02
+    packed, scale, zero = kernels.quantize_int4(w, group)
+    scale = scale.to(dtype)
+    x = torch.randn(rows, k, generator=g, device=DEV).to(dtype)
+    bias = torch.randn(n, generator=g, device=DEV).to(dtype)
+    got = kernels.int4_linear(x, packed, scale, zero, kernel="persistent")
+    pick = _sample_rows(rows, seed=5) if rows > 64 else np.arange(rows)
+    wdq = kernels.int4_weight(packed, scale, zero).float().cpu().numpy().astype(np.float64)
+    ref = x[pick].float().cpu().numpy().astype(np.float64) @ wdq.T
+    err, top = _report("int4 persistent", got[pick].float().cpu().numpy(), ref)
+    assert err <= 1e-2 * top
+    tiled = kernels.int4_linear(x, packed, scale, zero, kernel="tiled256").float()
+    assert (got.float() - tiled).abs().max().item() <= 1e-2 * top
+    with_bias = kernels.int4_linear(x, packed, scale, zero, bias, kernel="persistent")
+    assert torch.equal(with_bias, (got.float() + bias.float()).to(dtype))
+
+
+def test_int4_persistent_form_refuses_other_shapes() -> None:
+    from linnet_amd.errors import LinnetError
+
+    for n, k, group in ((200, 256, 128), (256, 384, 128), (256, 256, 32)):
+        packed = torch.zeros(n, k // group, group // 2, dtype=torch.uint8, device=DEV)
+        scale = torch.ones(n, k // group, dtype=torch.bfloat16, device=DEV)
+        zero = torch.zeros(n, k // group, dtype=torch.uint8, device=DEV)
+        x = torch.zeros(300, k, dtype=torch.bfloat16, device=DEV)
+        with pytest.raises(LinnetError, match="persistent kernel"):
+            kernels.int4_linear(x, packed, scale, zero, kernel="persistent")
