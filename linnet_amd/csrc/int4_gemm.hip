@@ -174,9 +174,10 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   // are out of range whether or not the uniform offset is range-checked.
   const int xrow = 8 * wave + (lane >> 3);
   const int xcol = (lane & 7) ^ ((xrow >> 1) & 7);
-  int xoff[4];
+  constexpr int X_LOADS = 4;  // x loads (one buffer_load ... lds each) of a wave a step
+  int xoff[X_LOADS];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) xoff[i] = (m0 + xrow + 64 * i) * K * 2 + xcol * 16;
+  for (int i = 0; i < X_LOADS; ++i) xoff[i] = (m0 + xrow + 64 * i) * K * 2 + xcol * 16;
   const int xlds = wave * 512;  // elements
   auto load_x = [&](uint16_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) {
     const int v = xoff[i];  // through a local: an array element passed directly drops the host launch stub
@@ -195,6 +196,9 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
     uint32_t w[DW];
     uint32_t s, z;
   };
+  // Vector-memory instructions of one load_w (scale, zero, the packed words as
+  // one b128 or b64): the step's wait counts them with the X_LOADS x loads.
+  constexpr int W_LOADS = 3;
   auto load_w = [&](WRegs& r, int ks) {
     const bool in = ks < steps;
     const int k0 = in ? ks * BK : 0;
@@ -323,20 +327,22 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
     const bool xin = ks + 2 < steps;
     const __amdgpu_buffer_rsrc_t xr = xin ? rx : rnull;
     const int xk0 = xin ? (ks + 2) * BK : 0;
-    constexpr int XGAP = NMF / 4 + 1;  // slots between the 4 x loads
+    constexpr int XGAP = NMF / X_LOADS + 1;  // slots between the x loads
     auto vm = [&](int r, int s) {
       const int p = r * NMF + s;
       if (p == 1) load_w(req, ks + 3);
-      if (p >= 3 && (p - 3) % XGAP == 0 && (p - 3) / XGAP < 4) load_x(xn2, xr, xk0, (p - 3) / XGAP);
+      if (p >= 3 && (p - 3) % XGAP == 0 && (p - 3) / XGAP < X_LOADS) load_x(xn2, xr, xk0, (p - 3) / XGAP);
     };
     region(af0, bf0, af1, bf1, xc, wc, 1, d1, wn, NMF, [&](int s) { vm(0, s); });
     region(af1, bf1, af0, bf0, xc, wc, 2, d1, wn, 2 * NMF, [&](int s) { vm(1, s); });
     region(af0, bf0, af1, bf1, xc, wc, 3, d1, wn, 3 * NMF, [&](int s) { vm(2, s); });
-    // This wave's x of step ks + 1 has arrived once at most the 7 loads issued
-    // after it (this step's 3 weight loads and 4 x loads) remain; its W stores
-    // are done at lgkmcnt(0). Past the barrier every wave's are, and no wave
-    // reads step ks's stages again.
-    __asm__ volatile("s_waitcnt vmcnt(7)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+    // This wave's x of step ks + 1 has arrived once at most the loads issued
+    // after it -- this step's load_w (W_LOADS instructions) and load_x calls
+    // (X_LOADS, one instruction each) -- remain; its W stores are done at
+    // lgkmcnt(0). Past the barrier every wave's are, and no wave reads step ks's
+    // stages again.
+    wait_vm<W_LOADS + X_LOADS>();
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     set_scale(d2);
     region(af1, bf1, af0, bf0, xn1, wn, 0, d2, wc, 0, [&](int) {});
@@ -348,10 +354,10 @@ __global__ __launch_bounds__(gemm::THREADS, 1) void int4_tiled_kernel(
   WRegs ra, rb, rc;
   load_w(ra, 0);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) load_x(X0, rx, 0, i);
+  for (int i = 0; i < X_LOADS; ++i) load_x(X0, rx, 0, i);
   load_w(rb, 1);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) load_x(X1, steps > 1 ? rx : rnull, steps > 1 ? BK : 0, i);
+  for (int i = 0; i < X_LOADS; ++i) load_x(X1, steps > 1 ? rx : rnull, steps > 1 ? BK : 0, i);
   load_w(rc, 2);
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   set_scale(ra);

@@ -59,6 +59,7 @@ class Int4Llama:
         # Position ctx is written by the step; `spare` more positions stay free for
         # steps past it.
         cap = (ctx + 1 + spare + 3) // 4 * 4
+        self.cap = cap
         self.kt = [torch.randn(batch, kv_heads, self.hd, cap, generator=g, device=dev).to(torch.bfloat16)
                    for _ in range(layers)]
         self.vc = [torch.randn(batch, kv_heads, cap, self.hd, generator=g, device=dev).to(torch.bfloat16)
@@ -72,6 +73,9 @@ class Int4Llama:
         from linnet_amd.torch import decode
 
         self.pos_t = torch.tensor([ctx], dtype=torch.int32, device=dev)
+        # Host mirror of pos_t: advanced by every step_at that runs (eagerly or
+        # through `replay`), so that no step runs past the cache.
+        self.device_pos = ctx
         self.cos_tab, self.sin_tab = decode.rope_tables(self.hd, cap, 500000.0, dev)
         self.linear = lambda x, w: kernels.int4_linear(x, *w)
         # One-token steps fold the glue into the linear layers (`layer_folded`).
@@ -86,6 +90,22 @@ class Int4Llama:
         ang = pos * inv
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)
         self.pos_t.fill_(pos)
+        self.device_pos = pos
+
+    def _check_room(self):
+        if self.device_pos >= self.cap:
+            from linnet_amd.errors import LinnetError
+
+            raise LinnetError(f"decode step at cache position {self.device_pos}: the cache holds {self.cap} positions")
+
+    def replay(self, graph):
+        """Replays a graph that recorded one `step_at` (which moves the device
+        position by one), refusing to run past the cache. A graph replayed
+        directly (`graph.replay()`) bypasses this check: the attention kernel then
+        reads and writes nothing past the cache, and the logits are wrong."""
+        self._check_room()
+        graph.replay()
+        self.device_pos += 1
 
     def _rms(self, x, w):
         torch = self.torch
@@ -247,7 +267,13 @@ class Int4Llama:
     def step_at(self, x):
         """One fused decode step at the position held in `pos_t` on the device,
         which it then advances by one (a graph recording this step moves along the
-        cache on each replay). Returns the logits."""
+        cache on each replay: replay it with `replay`). Returns the logits.
+        Refuses a step past the cache; `pos` (the host-side position of `step`)
+        is not moved."""
+        torch = self.torch
+        capturing = torch.cuda.is_current_stream_capturing()
+        if not capturing:
+            self._check_room()
         if self._folds(x):
             for i in range(len(self.layers)):
                 x = self.layer_folded(i, x, device_pos=True)
@@ -259,6 +285,8 @@ class Int4Llama:
                 delta = self.layer_fused(i, x, delta, device_pos=True)
             logits = self.head_fused(x, delta)
         self.pos_t.add_(1)
+        if not capturing:
+            self.device_pos += 1
         return logits
 
     def step(self, x):

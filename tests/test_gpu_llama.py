@@ -191,7 +191,7 @@ def test_captured_step_advances_the_position(batch: int) -> None:
     torch.cuda.synchronize()
     assert int(live.pos_t.item()) == 64, "recording a step does not run it"
     for k in range(3):
-        graph.replay()
+        live.replay(graph)
         torch.cuda.synchronize()
         twin.set_position(64 + k)
         want = twin.step(x)
@@ -201,6 +201,30 @@ def test_captured_step_advances_the_position(batch: int) -> None:
         for i in range(SMALL["layers"]):
             assert torch.equal(live.kt[i][..., 64 + k], twin.kt[i][..., 64 + k])
             assert torch.equal(live.vc[i][:, :, 64 + k], twin.vc[i][:, :, 64 + k])
+
+
+def test_steps_past_the_cache_are_refused() -> None:
+    """`step_at` and `replay` keep a host mirror of the device position and
+    refuse a step at a position the cache does not hold."""
+    from linnet_amd.errors import LinnetError
+
+    x = (torch.randn(1, SMALL["hidden"], generator=torch.Generator().manual_seed(4)) * 0.5).to(torch.bfloat16).to(DEV)
+    model = Int4Llama(torch, kernels, DEV, batch=1, seed=3, spare=0, **SMALL)
+    model.set_position(model.cap - 2)
+    model.step_at(x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model.step_at(x)
+    assert model.device_pos == model.cap - 1, "recording a step does not move the mirror"
+    model.replay(graph)
+    torch.cuda.synchronize()
+    assert model.device_pos == model.cap and int(model.pos_t.item()) == model.cap
+    with pytest.raises(LinnetError, match="cache holds"):
+        model.replay(graph)
+    with pytest.raises(LinnetError, match="cache holds"):
+        model.step_at(x)
+    del model, graph
 
 
 def test_device_position_outside_the_cache_writes_nothing() -> None:

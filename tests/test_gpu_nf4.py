@@ -89,6 +89,33 @@ def test_gemv_against_f64(dtype: torch.dtype, rows: int, out_features: int, in_f
     _check(got, want)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("rows", "out_features", "in_features", "block"), [
+    (1, 64, 16, 16), (4, 40, 48, 16), (16, 72, 4096, 64), (3, 1000, 14336, 128)])
+def test_gemv_uses_the_rounded_nf4_values(dtype: torch.dtype, rows: int, out_features: int, in_features: int,
+                                          block: int) -> None:
+    """The GEMV's arithmetic, pinned tightly: each code's value rounded to x's
+    type, products summed in f32, each block's sum scaled by its absmax, the
+    output rounded once. Against the f64 sum over the rounded values: half a unit
+    in the last place of the output's type plus 16 f32 units of the row's
+    absolute sum, so one wrong entry of the lookup table (or a bf16 / f16 bit
+    pattern off by one) fails, where the 1e-2 tolerance above would not."""
+    print(f"nf4 gemv table rows {rows} {out_features}x{in_features} block {block} {dtype}", flush=True)
+    codes, absmax = _layer(out_features, in_features, block, rows + in_features + 3)
+    x = torch.randn(rows, in_features, generator=torch.Generator().manual_seed(rows)).to(dtype)
+    got = kernels.nf4_gemv(x.to(DEV), torch.from_numpy(codes).to(DEV), torch.from_numpy(absmax).to(DEV), block)
+    values = torch.from_numpy(quant.NF4_VALUES.copy()).to(dtype).double().numpy()
+    q = np.stack([codes & 15, codes >> 4], axis=-1).reshape(out_features, in_features)  # low nibble first
+    w = values[q] * np.repeat(absmax.astype(np.float64), block, axis=1)
+    terms = x.double().numpy()[:, None, :] * w[None, :, :]
+    ref, mag = terms.sum(axis=-1), np.abs(terms).sum(axis=-1)
+    half_ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    err = np.abs(got.double().cpu().numpy() - ref)
+    bound = half_ulp * np.abs(ref) + 2.0 ** -20 * mag + 2.0 ** -24
+    print(f"max err / bound {float((err / bound).max()):.3f}", flush=True)
+    assert np.all(err <= bound)
+
+
 def test_gemv_takes_strided_rows_and_leading_axes() -> None:
     codes, absmax = _layer(96, 512, 64, 11)
     x = torch.randn(2, 3, 1024, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
