@@ -55,6 +55,11 @@ typedef int32_t LnqStatus;
 #define LNQ_KERNEL_PERSISTENT 6 /* the persistent prefill dequant-GEMM: 256 x 256 tiles,
                                    one workgroup a CU walking its tiles (out % 256 == 0,
                                    in % 256 == 0, group a power of two >= 64) */
+#define LNQ_KERNEL_SPLIT 7 /* the 32-row GEMV with `in` split over workgroups, the chunks'
+                              f32 sums in a caller workspace (lnq_int4_linear_ws only):
+                              rows 1..64 (33..64 as two chunks), out % 4 == 0, in = 4096
+                              or a multiple of 256 above it whose slices of 256 split into
+                              chunks of 8..16 (e.g. 6144, 8192, 12288, 14336) */
 
 /* The ABI version this library implements (LNQ_ABI_VERSION). */
 LNQ_API uint32_t lnq_abi_version(void);
@@ -139,6 +144,32 @@ LNQ_API LnqStatus lnq_int4_linear_prologue(const void* x, const void* u, const f
 LNQ_API LnqStatus lnq_int4_linear_plan(int64_t rows, int64_t in_features, int64_t out_features,
                                        int64_t group, int32_t dtype, int32_t kernel,
                                        int32_t* chosen);
+
+/* lnq_int4_linear with scratch memory of the caller's: `workspace` (16-byte aligned,
+ * workspace_bytes long; NULL with 0 is allowed) lets the automatic choice take
+ * LNQ_KERNEL_SPLIT where it is faster (16..64 rows with in > 4096 -- the down
+ * projection of a decode batch -- and 17..64 rows over out >= 65536 at in = 4096),
+ * the K chunks' partial sums written there and added in chunk order (deterministic).
+ * Without enough workspace it chooses as lnq_int4_linear does; kernel
+ * LNQ_KERNEL_SPLIT runs the split GEMV or fails. Calls that overlap on one
+ * workspace race. Other kernels as lnq_int4_linear.
+ * Replaces: the same reference calls as lnq_int4_linear (torch_source.cpp:1553-1570,
+ * Triton's `int4_linear` at 16..64 rows); the workspace is the caller allocator's
+ * memory a generated module hands over, as it does for the reference's BLAS calls. */
+LNQ_API LnqStatus lnq_int4_linear_ws(const void* x, const uint8_t* packed, const void* scale,
+                                     const uint8_t* zero, const void* bias, void* y, int64_t rows,
+                                     int64_t in_features, int64_t out_features, int64_t group,
+                                     int32_t dtype, int32_t kernel, void* workspace,
+                                     int64_t workspace_bytes, void* stream);
+
+/* The kernel lnq_int4_linear_ws runs for these arguments given enough workspace
+ * (*chosen as lnq_int4_linear_plan's, or LNQ_KERNEL_SPLIT) and the workspace bytes
+ * it needs (*workspace_bytes: 0 unless LNQ_KERNEL_SPLIT, then K chunks * min(rows, 32)
+ * * out * 4). No counterpart in the reference (its dispatch is Python,
+ * torch_source.cpp:1553-1570): lets a caller size the workspace. */
+LNQ_API LnqStatus lnq_int4_linear_workspace(int64_t rows, int64_t in_features, int64_t out_features,
+                                            int64_t group, int32_t dtype, int32_t kernel,
+                                            int32_t* chosen, int64_t* workspace_bytes);
 
 /* out[out, in] = (q - zero) * scale computed in f32 and rounded once to `dtype`
  * (the scale's dtype: bf16, f16 or f32). Any even group dividing `in`.

@@ -21,7 +21,8 @@ ABI_VERSION = 1
 
 LNQ_OK, LNQ_ERROR, LNQ_UNAVAILABLE = 0, 1, 2
 BF16, F16, F32 = 0, 1, 2
-KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV, KERNEL_TILED_128, KERNEL_TILED_256, KERNEL_PERSISTENT = range(7)
+(KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILED, KERNEL_GEMV, KERNEL_TILED_128, KERNEL_TILED_256, KERNEL_PERSISTENT,
+ KERNEL_SPLIT) = range(8)
 PROLOGUE_RMSNORM, PROLOGUE_SILU_MUL = 1, 2
 PACKING_GPTQ, PACKING_AWQ = 0, 1
 
@@ -35,6 +36,8 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_device_probe": [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "lnq_int4_linear": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p],
     "lnq_int4_linear_plan": [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i32)],
+    "lnq_int4_linear_ws": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p],
+    "lnq_int4_linear_workspace": [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
     "lnq_int4_linear_executable": [_i64, _i64, _i64, _i32, _p],
     "lnq_int4_dequantize": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_int4_quantize": [_p, _p, _p, _p, _i64, _i64, _i64, _p],

@@ -634,6 +634,52 @@ bool int4_gemv_takes_order(int M, int N, int K, int G, const void* x, const void
 bool int4_gemv_takes_prologue(int M, int N, int K, int G, int dtype, const void* x, const void* packed,
                               const void* scale, const void* zero, int prologue, const void* operand);
 
+// Defined in int4_gemv.hip: the 32-row GEMV with K split over workgroups.
+bool int4_gemv_split_supports(int M, int N, int K, int G, int u8, int S, const void* x, const void* packed,
+                              const void* scale, const void* zero, const void* part);
+LnqStatus launch_int4_gemv_split(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                 const void* bias, void* y, int M, int N, int K, int G, int dtype, int u8, int S,
+                                 float* part, hipStream_t stream);
+
+// The split GEMV's workgroup shape for K: past K = 4096 (where the few-row
+// GEMV stops), 64-row blocks and the fewest K chunks of at most 16 slices of
+// 256 inputs, if that leaves a chunk 8 or more (K = 14336: 4 chunks of 14;
+// 8192: 2 of 16); at K = 4096, 128-row blocks in 2 chunks of 8 slices.
+static bool split_shape(int K, int& u8, int& S) {
+  if (K % 256 != 0) return false;
+  const int slices = K / 256;
+  if (K == 4096) {
+    u8 = 16;
+    S = 2;
+    return true;
+  }
+  if (K <= 4096) return false;
+  for (int s = 2; s <= slices; ++s)
+    if (slices % s == 0 && slices / s <= 16) {
+      u8 = 8;
+      S = s;
+      return slices / s >= 8;
+    }
+  return false;
+}
+
+// Whether the automatic choice with a workspace takes the split GEMV (rows run
+// in 32-row chunks). Measured (bf16, group 128, graphs over rotating weight
+// copies): K = 14336, N = 4096 at 32 rows 18.7-19.2 us against 32.3 for the
+// skinny kernel, 16 rows 16.7 against 19.7, 8 rows 17.3 against 15.9; K = 4096
+// only over the widest outputs (N = 128256 at 32 rows 109.9 against 117.5 for
+// the unsplit 32-row GEMV; N = 28672: 31.5 against 30.6, N = 4096: 11.7 against
+// 11.5, so the rest keep their kernels).
+static bool split_preferred(int M, int N, int K) {
+  if (M < 16 || M > 64 || N % 4 != 0) return false;
+  if (K > 4096) return true;
+  return K == 4096 && M > 16 && N >= 65536;
+}
+
+static int64_t split_workspace_bytes(int M, int N, int S) {
+  return static_cast<int64_t>(S) * (M < 32 ? M : 32) * N * 4;
+}
+
 // The argument checks of lnq_int4_linear that do not look at the operands;
 // false (with the message set) when one fails.
 static bool check_int4_linear(int64_t rows, int64_t in_features, int64_t out_features, int64_t group,
@@ -795,6 +841,72 @@ LNQ_API LnqStatus lnq_int4_linear_plan(int64_t rows, int64_t in_features, int64_
   if (code < 0) return LNQ_ERROR;
   *chosen = code;
   clear_error();
+  return LNQ_OK;
+}
+
+LNQ_API LnqStatus lnq_int4_linear_workspace(int64_t rows, int64_t in_features, int64_t out_features, int64_t group,
+                                            int32_t dtype, int32_t kernel, int32_t* chosen,
+                                            int64_t* workspace_bytes) {
+  LNQ_REQUIRE(chosen != nullptr && workspace_bytes != nullptr, "lnq_int4_linear_workspace: null pointer");
+  const int32_t base = kernel == LNQ_KERNEL_SPLIT ? LNQ_KERNEL_AUTO : kernel;
+  if (!check_int4_linear(rows, in_features, out_features, group, dtype, base, "lnq_int4_linear_workspace"))
+    return LNQ_ERROR;
+  *workspace_bytes = 0;
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features), K = static_cast<int>(in_features);
+  int u8 = 0, S = 0;
+  const bool shaped = rows > 0 && split_shape(K, u8, S);
+  if (kernel == LNQ_KERNEL_SPLIT || (kernel == LNQ_KERNEL_AUTO && shaped && split_preferred(M, N, K))) {
+    static const uint8_t* const kAligned = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(256));
+    LNQ_REQUIRE(rows == 0 || (shaped && rows <= 64 &&
+                              int4_gemv_split_supports(M < 32 ? M : 32, N, K, static_cast<int>(group), u8, S,
+                                                       kAligned, kAligned, kAligned, kAligned, kAligned) &&
+                              (M <= 32 || int4_gemv_split_supports(M - 32, N, K, static_cast<int>(group), u8, S,
+                                                                   kAligned, kAligned, kAligned, kAligned,
+                                                                   kAligned))),
+                "lnq_int4_linear_workspace: the split GEMV does not take rows=%lld in=%lld out=%lld group=%lld",
+                (long long)rows, (long long)in_features, (long long)out_features, (long long)group);
+    *chosen = LNQ_KERNEL_SPLIT;
+    *workspace_bytes = rows == 0 ? 0 : split_workspace_bytes(M, N, S);
+    clear_error();
+    return LNQ_OK;
+  }
+  return lnq_int4_linear_plan(rows, in_features, out_features, group, dtype, kernel, chosen);
+}
+
+LNQ_API LnqStatus lnq_int4_linear_ws(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                     const void* bias, void* y, int64_t rows, int64_t in_features,
+                                     int64_t out_features, int64_t group, int32_t dtype, int32_t kernel,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  int32_t chosen = -1;
+  int64_t need = 0;
+  if (lnq_int4_linear_workspace(rows, in_features, out_features, group, dtype, kernel, &chosen, &need) != LNQ_OK)
+    return LNQ_ERROR;
+  const bool fits = workspace != nullptr && aligned(workspace, 16) && workspace_bytes >= need;
+  if (chosen != LNQ_KERNEL_SPLIT || rows == 0 || (kernel == LNQ_KERNEL_AUTO && !fits))
+    return lnq_int4_linear(x, packed, scale, zero, bias, y, rows, in_features, out_features, group, dtype,
+                           kernel == LNQ_KERNEL_SPLIT ? LNQ_KERNEL_AUTO : kernel, stream);
+  LNQ_REQUIRE(fits, "lnq_int4_linear_ws: the split GEMV needs %lld workspace bytes, 16-byte aligned (got %lld)",
+              (long long)need, (long long)workspace_bytes);
+  LNQ_REQUIRE(x && packed && scale && zero && y, "lnq_int4_linear_ws: null pointer");
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  int u8 = 0, S = 0;
+  split_shape(K, u8, S);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  const size_t xrow = static_cast<size_t>(K) * 2, yrow = static_cast<size_t>(N) * 2;
+  // 33..64 rows: one 32-row chunk after another on the stream, sharing the workspace.
+  for (int c = 0; c < M; c += 32) {
+    const int rc = M - c < 32 ? M - c : 32;
+    const void* xc = static_cast<const uint8_t*>(x) + c * xrow;
+    LNQ_REQUIRE(int4_gemv_split_supports(rc, N, K, G, u8, S, xc, packed, scale, zero, part),
+                "lnq_int4_linear_ws: the split GEMV does not take these operands (rows=%d in=%d out=%d group=%d; x, "
+                "packed and the workspace 16-byte aligned, group 128 scales 4- and zeros 2-byte aligned)",
+                rc, K, N, G);
+    const LnqStatus st = launch_int4_gemv_split(xc, packed, scale, zero, bias, static_cast<uint8_t*>(y) + c * yrow,
+                                                rc, N, K, G, dtype, u8, S, part, s);
+    if (st != LNQ_OK) return st;
+  }
   return LNQ_OK;
 }
 

@@ -68,6 +68,20 @@ constexpr int MAX_ROWS = 32;   // tokens of one few-token launch
 // T, and the array's bytes (a 16-byte placeholder past the last tile):
 constexpr int tile_wave_bytes(int u8, int t) { return 2 * t + 1 < u8 ? 2048 : 1024; }
 constexpr int tile_bytes(int u8, int t) { return 2 * t < u8 ? tile_wave_bytes(u8, t) * MAX_WAVES : 16; }
+
+// The 32-row kernel also takes 128 and 256 rows a workgroup (U8 = 16, 32; split
+// K only), with at most wmax(U8) waves: 128 KB of weight tiles in all. Its
+// tiles sit in four LDS arrays, tiles_per_array(U8) consecutive tiles each
+// (one tile an array up to U8 = 8, the layout above).
+constexpr int wmax(int u8) { return u8 <= 8 ? MAX_WAVES : 128 / u8; }
+constexpr int tiles_per_array(int u8) { return ((u8 + 1) / 2 + 3) / 4; }
+constexpr int array_wave_bytes(int u8, int a) {
+  int bytes = 0;
+  for (int t = a * tiles_per_array(u8); t < (a + 1) * tiles_per_array(u8) && 2 * t < u8; ++t)
+    bytes += tile_wave_bytes(u8, t);
+  return bytes;
+}
+constexpr int array_bytes(int u8, int a) { return array_wave_bytes(u8, a) > 0 ? array_wave_bytes(u8, a) * wmax(u8) : 16; }
 }  // namespace gemv
 
 // The prologue's operands (PRO_NORM: w, eps; PRO_SILU: u), by value.
@@ -88,6 +102,23 @@ struct GemvPrologue {
   auto tile_lds = [&](int T, int w) -> uint8_t* {                                            \
     uint8_t* base = T == 0 ? L0 : T == 1 ? L1 : T == 2 ? L2 : L3;                            \
     return base + w * gemv::tile_wave_bytes(U8, T);                                          \
+  }
+
+// The tile arrays of the 32-row kernel (four arrays of tiles_per_array(U8)
+// tiles), and tile_lds(T, wave) as above.
+#define LNQ_GEMV_TILE_GROUPS(U8)                                                                  \
+  __shared__ __attribute__((aligned(16))) uint8_t L0[gemv::array_bytes(U8, 0)];                  \
+  __shared__ __attribute__((aligned(16))) uint8_t L1[gemv::array_bytes(U8, 1)];                  \
+  __shared__ __attribute__((aligned(16))) uint8_t L2[gemv::array_bytes(U8, 2)];                  \
+  __shared__ __attribute__((aligned(16))) uint8_t L3[gemv::array_bytes(U8, 3)];                  \
+  static_assert(U8 <= 8 || U8 % 8 == 0, "whole arrays past U8 = 8");                               \
+  auto tile_lds = [&](int T, int w) -> uint8_t* {                                                 \
+    constexpr int P = gemv::tiles_per_array(U8);                                                  \
+    const int g = T / P;                                                                          \
+    uint8_t* base = g == 0 ? L0 : g == 1 ? L1 : g == 2 ? L2 : L3;                                 \
+    const int wb = g == 0 ? gemv::array_wave_bytes(U8, 0) : g == 1 ? gemv::array_wave_bytes(U8, 1) \
+                 : g == 2 ? gemv::array_wave_bytes(U8, 2) : gemv::array_wave_bytes(U8, 3);        \
+    return base + w * wb + (T % P) * 2048;                                                        \
   }
 
 // The widened B operands of two packed dwords (16 codes): (MAGIC | q) pairs in
@@ -915,17 +946,27 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
 // wave's own part of the tile array (2 KB: 16 outputs x 32 rows, output-minor;
 // the 8-row last tile of an odd U8 1 KB: its 8 outputs x 32 rows). The 16
 // waves' sums are then added as in int4_gemv_rows_kernel.
-template <int DT, int U8, bool G128>
+//
+// SPLIT: the K range is cut into gridDim.y chunks of nw slices, workgroup
+// (bx, c) taking chunk c of rows bx * R ..; its sums over the chunk go unrounded
+// to part[c][m][n] (f32) and int4_split_reduce_kernel adds the chunks in order.
+// Every workgroup reads x only over its own chunk, so a 64-row block with a
+// quarter of K reads a quarter of x where the unsplit kernel's 16-row blocks
+// read all of it (the down projection at 32 rows: 229 KB of x against 115 KB of
+// weights a workgroup, in place of 917 KB against 115 KB).
+template <int DT, int U8, bool G128, bool SPLIT = false>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G) {
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int G,
+    float* __restrict__ part = nullptr) {
   using E = Elem<DT>;
-  constexpr int MX = 32;
   constexpr int R = 8 * U8;
   constexpr int NT = (U8 + 1) / 2;
   constexpr bool HALF = (U8 & 1) != 0;
-  LNQ_GEMV_TILE_ARRAYS(U8);
+  constexpr int SR = (R + 63) / 64;  // scale (and zero) registers: rows 64 i + lane
+  static_assert(SPLIT || U8 <= 8, "more than 64 rows only with split K");
+  LNQ_GEMV_TILE_GROUPS(U8);
   // Outputs of tile T a wave part holds (its floats: 32 times as many).
   auto outs = [](int T) { return HALF && T == NT - 1 ? 8 : 16; };
   static_assert(gemv::tile_wave_bytes(U8, NT - 1) == (HALF ? 1024 : 2048), "tile parts hold the partial sums");
@@ -937,7 +978,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
   const int nw = blockDim.x >> 6;
   const int col = lane & 15, j = lane >> 4;
   const int n0 = blockIdx.x * R;
-  const int k0 = wave * 256;
+  const int k0 = ((SPLIT ? blockIdx.y * nw : 0) + wave) * 256;
   const int rowb = K >> 1;
   const int groups = K / G;
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * rowb));
@@ -946,16 +987,19 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
 
   // ---- loads: scales and zeros, x (16 per lane), weights.
-  const int srow = n0 + (lane < R ? lane : R - 1);
   const int g0 = k0 / G;
-  uint32_t sv;
-  uint16_t zv16;
-  if constexpr (G128) {
-    sv = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);
-    zv16 = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);
-  } else {
-    sv = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
-    zv16 = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
+  uint32_t sv[SR];
+  uint16_t zv16[SR];
+#pragma unroll
+  for (int i = 0; i < SR; ++i) {
+    const int srow = n0 + 64 * i + (lane < R - 64 * i ? lane : R - 64 * i - 1);
+    if constexpr (G128) {
+      sv[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (srow * groups + g0) * 2, 0, 0);
+      zv16[i] = __builtin_amdgcn_raw_buffer_load_b16(rz, srow * groups + g0, 0, 0);
+    } else {
+      sv[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, (srow * groups + g0) * 2, 0, 0);
+      zv16[i] = __builtin_amdgcn_raw_buffer_load_b8(rz, srow * groups + g0, 0, 0);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   u32x4 xa[2][2][4];
@@ -1003,11 +1047,15 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
     }
   __builtin_amdgcn_sched_barrier(0);
 
-  __asm__ volatile("" : "+v"(sv), "+v"(zv16));
-  uint32_t zv = zv16;
-  if constexpr (!G128) {
-    sv = (sv & 0xffffu) | (sv << 16);
-    zv = (zv & 0xffu) | (zv << 8);
+  uint32_t zv[SR];
+#pragma unroll
+  for (int r = 0; r < SR; ++r) {
+    __asm__ volatile("" : "+v"(sv[r]), "+v"(zv16[r]));
+    zv[r] = zv16[r];
+    if constexpr (!G128) {
+      sv[r] = (sv[r] & 0xffffu) | (sv[r] << 16);
+      zv[r] = (zv[r] & 0xffu) | (zv[r] << 8);
+    }
   }
   uint32_t nib_mask = 0x000f000fu, nib_magic = E::MAGIC2;
   hide_in_vgpr(nib_mask);
@@ -1055,9 +1103,9 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
     }
     // Fold: output row 16 T + col, x rows 16 b + 4 j + i.
     const int n = 16 * T + col;
-    const int src = n < R ? n : R - 1;
-    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(sv)));
-    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(zv)));
+    const int src = (n < R ? n : R - 1) & 63;  // rows 16 T .. 16 T + 15 lie in register T / 4
+    const uint32_t sp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(sv[T / 4])));
+    const uint32_t zp = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(zv[T / 4])));
     const float s0 = E::to_f32(static_cast<uint16_t>(sp & 0xffffu)), s1 = E::to_f32(static_cast<uint16_t>(sp >> 16));
     const float z0 = E::MAGIC_VALUE + static_cast<float>(zp & 0xffu);
     const float z1 = E::MAGIC_VALUE + static_cast<float>((zp >> 8) & 0xffu);
@@ -1075,49 +1123,83 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
     }
   }
   __syncthreads();
-  // Output (T, m, c): lanes 16 q + c of a wave add waves 4 q .. 4 q + 3, two
-  // exchanges finish the sum; wave w takes passes w, w + nw, .. .
-  constexpr int PASSES = NT * MX;
-  constexpr int PW = (PASSES + gemv::MAX_WAVES - 1) / gemv::MAX_WAVES;
-  const int q = j;
-  auto pass = [&](const int o, float (&r)[4]) {
-    const int T = min(o / MX, NT - 1), m = o % MX;
+  // The waves' partial sums added four outputs at a time: thread t takes quads
+  // t, t + 64 nw, .. of the workgroup (tile T: 32 row slots x CW / 4 column
+  // quads, slot s = 16 b + 4 i + j holding x row 16 b + 4 j + i), reads the quad
+  // of every wave (16 contiguous bytes at the rotated place it was written to)
+  // and adds them in wave order. No lane exchange: one LDS read a wave a quad.
+  constexpr int TQ = 32 * 16 / 4;  // quads of a full tile
+  constexpr int QUADS = HALF ? (NT - 1) * TQ + TQ / 2 : NT * TQ;
+  for (int qd = threadIdx.x; qd < QUADS; qd += blockDim.x) {
+    const int T = qd / TQ, r = qd % TQ;
     const int cw = outs(T);
-    const int b = m >> 4, i = m & 3, jj = (m >> 2) & 3;
-    const int e = ((b * 4 + i) * 4 + jj) * cw + min(col, cw - 1);
-#pragma unroll
-    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
-      const int wv = 4 * q + w;
-      r[w] = reinterpret_cast<const float*>(tile_lds(T, wv))[(e + 4 * wv) & (32 * cw - 1)];
+    const int cq = cw / 4;  // column quads of the tile
+    const int slot = r / cq, c4 = 4 * (r % cq);
+    const int e = slot * cw + c4;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < nw; ++w) {
+      const f32x4 p = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(tile_lds(T, w)) +
+                                                       ((e + 4 * w) & (32 * cw - 1)));
+      v = f32x4{v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
     }
-  };
-  auto finish = [&](const int o, const float (&r)[4]) {
-    const int T = o / MX, m = o % MX;
-    float v = 0.f;
+    const int m = (slot & 16) | ((slot & 3) << 2) | ((slot >> 2) & 3);
+    const int n = n0 + 16 * T + c4;
+    if (m >= M || 16 * T + c4 >= R) continue;
+    if constexpr (SPLIT) {
+      float* dst = part + (static_cast<size_t>(blockIdx.y) * M + m) * N + n;
+      if (n + 3 < N && (N & 3) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = v;
+      } else {
 #pragma unroll
-    for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) v += 4 * q + w < nw ? r[w] : 0.f;
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    const int n = n0 + 16 * T + col;
-    if (q == 0 && o < PASSES && m < M && 16 * T + col < R && n < N) {
-      uint16_t out = E::from_f32(v);
-      if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n]));
-      y[static_cast<size_t>(m) * N + n] = out;
-    }
-  };
-  if (nw == gemv::MAX_WAVES) {
-    float r[PW][4];
+        for (int i = 0; i < 4; ++i)
+          if (n + i < N) dst[i] = v[i];
+      }
+    } else {
+      uint16_t o[4];
 #pragma unroll
-    for (int p = 0; p < PW; ++p) pass(wave + gemv::MAX_WAVES * p, r[p]);
+      for (int i = 0; i < 4; ++i) {
+        o[i] = E::from_f32(v[i]);
+        if (bias != nullptr && n + i < N) o[i] = E::from_f32(E::to_f32(o[i]) + E::to_f32(bias[n + i]));
+      }
+      uint16_t* dst = y + static_cast<size_t>(m) * N + n;
+      if (n + 3 < N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                               o[2] | (static_cast<uint32_t>(o[3]) << 16)};
+      } else {
 #pragma unroll
-    for (int p = 0; p < PW; ++p) finish(wave + gemv::MAX_WAVES * p, r[p]);
-  } else {
-    for (int o = wave; o < PASSES; o += nw) {
-      float r[4];
-      pass(o, r);
-      finish(o, r);
+        for (int i = 0; i < 4; ++i)
+          if (n + i < N) dst[i] = o[i];
+      }
     }
   }
+}
+
+// The chunks of a split product added in chunk order (deterministic), rounded
+// once to the output type, the bias added as the unsplit kernels add it
+// (y = round(round(sum) + bias)). Thread t owns four consecutive outputs of one
+// row (N % 4 == 0).
+template <int DT>
+__global__ __launch_bounds__(256) void int4_split_reduce_kernel(const float* __restrict__ part,
+                                                                const uint16_t* __restrict__ bias,
+                                                                uint16_t* __restrict__ y, int M, int N, int S) {
+  using E = Elem<DT>;
+  const size_t e = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  const size_t total = static_cast<size_t>(M) * N;
+  if (e >= total) return;
+  f32x4 v = *reinterpret_cast<const f32x4*>(part + e);
+  for (int c = 1; c < S; ++c) {
+    const f32x4 p = *reinterpret_cast<const f32x4*>(part + static_cast<size_t>(c) * total + e);
+    v = f32x4{v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
+  }
+  const int n = static_cast<int>(e % N);
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint16_t out = E::from_f32(v[i]);
+    if (bias != nullptr) out = E::from_f32(E::to_f32(out) + E::to_f32(bias[n + i]));
+    o[i] = out;
+  }
+  *reinterpret_cast<u32x2*>(y + e) = u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
 }
 
 // Whether the one-token kernel takes this shape (else the caller uses the
@@ -1274,6 +1356,35 @@ static void launch_rows32_dt(const void* x, const uint8_t* packed, const void* s
   }
 }
 
+template <int DT, int U8>
+static void launch_split_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero, int M,
+                            int N, int K, int G, int S, float* part, hipStream_t stream) {
+  const dim3 grid((N + 8 * U8 - 1) / (8 * U8), S), block(64 * (K / (256 * S)));
+  const auto* xs = static_cast<const uint16_t*>(x);
+  const auto* ss = static_cast<const uint16_t*>(scale);
+  if (G == 128)
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, true, true>), grid, block, 0, stream, xs, packed, ss, zero,
+                       nullptr, nullptr, M, N, K, G, part);
+  else
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, false, true>), grid, block, 0, stream, xs, packed, ss, zero,
+                       nullptr, nullptr, M, N, K, G, part);
+}
+
+template <int DT>
+static void launch_split_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                            const void* bias, void* y, int M, int N, int K, int G, int u8, int S, float* part,
+                            hipStream_t stream) {
+  switch (u8) {
+    case 4: launch_split_u8<DT, 4>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
+    case 8: launch_split_u8<DT, 8>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
+    case 16: launch_split_u8<DT, 16>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
+    default: launch_split_u8<DT, 32>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
+  }
+  const size_t quads = static_cast<size_t>(M) * N / 4;
+  hipLaunchKernelGGL((int4_split_reduce_kernel<DT>), dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                     stream, part, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, S);
+}
+
 template <int DT, int U8, int S>
 static void launch_slices_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                              const void* bias, void* y, int N, int K, int G, const int32_t* order, int kind,
@@ -1329,6 +1440,34 @@ bool int4_gemv_takes_prologue(int M, int N, int K, int G, int dtype, const void*
                               const void* scale, const void* zero, int prologue, const void* operand) {
   return M == 1 && dtype == LNQ_BF16 && G == 128 && (prologue == gemv::PRO_NORM || prologue == gemv::PRO_SILU) &&
          N <= 32768 && aligned(operand, 16) && int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
+}
+
+// The split 32-row GEMV (1..32 rows): R = 8 * u8 rows a workgroup (u8 4, 8, 16
+// or 32), K in S chunks of at most wmax(u8) slices of 256 inputs (16, 8, 4),
+// the chunks' f32 sums in part (S * M * N floats, 16-byte aligned), then added
+// in order.
+bool int4_gemv_split_supports(int M, int N, int K, int G, int u8, int S, const void* x, const void* packed,
+                              const void* scale, const void* zero, const void* part) {
+  if (M < 1 || M > gemv::MAX_ROWS || N <= 0 || N % 4 != 0 || S < 1) return false;
+  if (!(u8 == 4 || u8 == 8 || u8 == 16 || u8 == 32)) return false;
+  if (K <= 0 || K % (256 * S) != 0 || K / (256 * S) > gemv::wmax(u8)) return false;
+  if (!(G == 128 || G % 256 == 0) || K % G != 0) return false;
+  if (static_cast<size_t>(N) * (K / 2) >= (1ull << 31) || static_cast<size_t>(M) * K * 2 >= (1ull << 31)) return false;
+  return aligned(x, 16) && aligned(packed, 16) && aligned(part, 16) && (G != 128 || aligned(scale, 4)) &&
+         (G != 128 || aligned(zero, 2));
+}
+
+LnqStatus launch_int4_gemv_split(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                 const void* bias, void* y, int M, int N, int K, int G, int dtype, int u8, int S,
+                                 float* part, hipStream_t stream) {
+  if (!int4_gemv_split_supports(M, N, K, G, u8, S, x, packed, scale, zero, part)) {
+    set_error("launch_int4_gemv_split: the split GEMV does not take rows=%d N=%d K=%d group=%d u8=%d splits=%d", M,
+              N, K, G, u8, S);
+    return LNQ_ERROR;
+  }
+  if (dtype == LNQ_BF16) launch_split_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
+  else launch_split_dt<LNQ_F16>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
+  return launched("int4_gemv_split");
 }
 
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,

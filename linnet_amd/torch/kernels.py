@@ -11,6 +11,7 @@ captured into a HIP graph. CPU tensors, or a missing library, raise
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 
@@ -27,6 +28,7 @@ KERNELS = {
     "tiled128": _lib.KERNEL_TILED_128,
     "tiled256": _lib.KERNEL_TILED_256,
     "persistent": _lib.KERNEL_PERSISTENT,
+    "split": _lib.KERNEL_SPLIT,
 }
 _KERNEL_NAMES = {code: name for name, code in KERNELS.items()}
 
@@ -130,11 +132,30 @@ def int4_linear(
             )
         return y
     with torch.cuda.device(device):
-        _lib.call(
-            "lnq_int4_linear", _ptr(x), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),
-            rows, depth, width, group, code, KERNELS[kernel], _stream(device),
-        )
+        _, need = _workspace(rows, depth, width, group, code, KERNELS[kernel])
+        if need:
+            # The split GEMV's partial sums: memory of torch's caching allocator
+            # (the graph pool under capture), freed when the call is enqueued.
+            ws = torch.empty(need // 4, dtype=torch.float32, device=device)
+            _lib.call(
+                "lnq_int4_linear_ws", _ptr(x), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),
+                rows, depth, width, group, code, KERNELS[kernel], _ptr(ws), need, _stream(device),
+            )
+        else:
+            _lib.call(
+                "lnq_int4_linear", _ptr(x), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),
+                rows, depth, width, group, code, KERNELS[kernel], _stream(device),
+            )
     return y
+
+
+@functools.lru_cache(maxsize=4096)
+def _workspace(rows: int, depth: int, width: int, group: int, code: int, kernel: int) -> tuple[int, int]:
+    """(kernel code, workspace bytes) `lnq_int4_linear_ws` takes for the shape."""
+    chosen, need = ctypes.c_int32(-1), ctypes.c_int64(0)
+    _lib.call("lnq_int4_linear_workspace", rows, depth, width, group, code, kernel, ctypes.byref(chosen),
+              ctypes.byref(need))
+    return chosen.value, need.value
 
 
 def _prologue_linear(what: str, prologue: int, x: torch.Tensor, operand: torch.Tensor, eps: float,
@@ -219,14 +240,13 @@ def take_inputs(x: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
 def int4_linear_plan(rows: int, in_features: int, out_features: int, group: int,
                      dtype: torch.dtype = torch.bfloat16, kernel: str = "auto") -> str:
     """The kernel `int4_linear` runs for this shape on the current device: "gemv"
-    (33..64 rows: the few-token GEMV per 32-row chunk), "skinny", "tiled128",
+    (33..64 rows: the few-token GEMV per 32-row chunk), "skinny", "split" (the
+    32-row GEMV with K split over workgroups, a workspace of torch's), "tiled128",
     "tiled256" or "persistent". Raises as `int4_linear` would for a shape it refuses."""
     if kernel not in KERNELS:
         raise LinnetError(f"int4_linear_plan: kernel is one of {', '.join(KERNELS)}")
-    chosen = ctypes.c_int32(-1)
-    _lib.call("lnq_int4_linear_plan", rows, in_features, out_features, group, _code(dtype, "int4_linear_plan"),
-              KERNELS[kernel], ctypes.byref(chosen))
-    return _KERNEL_NAMES[chosen.value]
+    chosen, _ = _workspace(rows, in_features, out_features, group, _code(dtype, "int4_linear_plan"), KERNELS[kernel])
+    return _KERNEL_NAMES[chosen]
 
 
 def int4_weight(raw: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor) -> torch.Tensor:

@@ -224,6 +224,31 @@ def test_plan_queries_name_the_kernel_without_a_device() -> None:
         kernels.int4_linear_plan(1, 512, 64, 32, kernel="gemv")
     with pytest.raises(LinnetError, match="unknown kernel"):
         _lib.call("lnq_int4_linear_plan", 1, 512, 64, 128, _lib.BF16, 9, ctypes.byref(ctypes.c_int32()))
+    # The split GEMV (a workspace of the caller's): the decode batch's down
+    # projection and 17..64 rows over the widest outputs; without a workspace
+    # (lnq_int4_linear and its plan) it is never chosen and refused when asked for.
+    assert kernels.int4_linear_plan(32, 14336, 4096, 128) == "split"
+    assert kernels.int4_linear_plan(16, 14336, 4096, 128) == "split"
+    assert kernels.int4_linear_plan(64, 14336, 4096, 128) == "split"
+    assert kernels.int4_linear_plan(8, 14336, 4096, 128) == "skinny"
+    assert kernels.int4_linear_plan(32, 4096, 128256, 128) == "split"
+    assert kernels.int4_linear_plan(32, 4096, 28672, 128) == "gemv"
+    assert kernels.int4_linear_plan(4, 4096, 4096, 128, kernel="split") == "split"
+    chosen, need = ctypes.c_int32(-1), ctypes.c_int64(-1)
+    _lib.call("lnq_int4_linear_workspace", 32, 14336, 4096, 128, _lib.BF16, 0, ctypes.byref(chosen), ctypes.byref(need))
+    assert (chosen.value, need.value) == (_lib.KERNEL_SPLIT, 4 * 32 * 4096 * 4)
+    _lib.call("lnq_int4_linear_workspace", 48, 14336, 4096, 128, _lib.BF16, 0, ctypes.byref(chosen), ctypes.byref(need))
+    assert (chosen.value, need.value) == (_lib.KERNEL_SPLIT, 4 * 32 * 4096 * 4)
+    _lib.call("lnq_int4_linear_workspace", 1, 4096, 14336, 128, _lib.BF16, 0, ctypes.byref(chosen), ctypes.byref(need))
+    assert (chosen.value, need.value) == (_lib.KERNEL_GEMV, 0)
+    with pytest.raises(LinnetError, match="unknown kernel"):
+        _lib.call("lnq_int4_linear_plan", 32, 14336, 4096, 128, _lib.BF16, _lib.KERNEL_SPLIT, ctypes.byref(chosen))
+    with pytest.raises(LinnetError, match="split GEMV does not take"):
+        kernels.int4_linear_plan(32, 4352, 4096, 128, kernel="split")  # 17 slices: no chunk of 8..16
+    with pytest.raises(LinnetError, match="split GEMV does not take"):
+        kernels.int4_linear_plan(65, 14336, 4096, 128, kernel="split")
+    with pytest.raises(LinnetError, match="split GEMV does not take"):
+        kernels.int4_linear_plan(32, 14336, 4094, 128, kernel="split")
     assert kernels.mm8_plan(4096, 28672, 8192) == kernels.MM8_PERSISTENT
     assert kernels.mm8_plan(4096, 28672, 8192, fp8=False) == 256
     assert kernels.mm8_plan(256, 28672, 8192) == 128
