@@ -1136,12 +1136,17 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
     const int cq = cw / 4;  // column quads of the tile
     const int slot = r / cq, c4 = 4 * (r % cq);
     const int e = slot * cw + c4;
-    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < nw; ++w) {
-      const f32x4 p = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(tile_lds(T, w)) +
-                                                       ((e + 4 * w) & (32 * cw - 1)));
-      v = f32x4{v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
-    }
+    // Every wave's quad requested before the first add (one LDS round trip).
+    f32x4 p[gemv::MAX_WAVES];
+#pragma unroll
+    for (int w = 0; w < gemv::MAX_WAVES; ++w)
+      if (w < nw)
+        p[w] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(tile_lds(T, w)) +
+                                               ((e + 4 * w) & (32 * cw - 1)));
+    f32x4 v = p[0];
+#pragma unroll
+    for (int w = 1; w < gemv::MAX_WAVES; ++w)
+      if (w < nw) v = f32x4{v[0] + p[w][0], v[1] + p[w][1], v[2] + p[w][2], v[3] + p[w][3]};
     const int m = (slot & 16) | ((slot & 3) << 2) | ((slot >> 2) & 3);
     const int n = n0 + 16 * T + c4;
     if (m >= M || 16 * T + c4 >= R) continue;
