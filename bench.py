@@ -386,11 +386,13 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
     decode step of the int4 Llama-3.1-8B-shaped stack at a
     1024-token context, captured as one HIP graph and replayed; tokens/s =
     batch / step time. Batch 1 runs every linear on the one-token GEMV
-    kernels, batch 32 on the few-token GEMV (gate, up) and the skinny kernel;
-    q|k|v and gate|up run as joined projections; between the linears, the
-    decode kernels of `torch/decode.py` (4 a layer). `linears_ms` replays the
-    step's 161 int4 linear calls alone; `torch_glue_ms` is the same step with the
-    glue as torch ops (~40 small kernels a layer) and the projections apart."""
+    kernels; batch 32 runs q|k|v, gate|up and the head on the 32-row GEMV (the
+    head split over K), down on the split GEMV -- their inputs written as x tiles
+    by the glue -- and o on the skinny kernel; q|k|v and gate|up run as joined
+    projections; between the linears, the decode kernels of `torch/decode.py` (4
+    a layer). `linears_ms` replays the step's 161 int4 linear calls alone (on x
+    tiles where the step's are); `torch_glue_ms` is the same step with the glue as
+    torch ops (~40 small kernels a layer) and the projections apart."""
     out: dict[str, object] = {"layers": 32, "hidden": 4096, "heads": "32/8", "ffn": 14336, "vocab": 128256,
                               "context": 1024, "weights": "int4 g128, bf16 scales, u8 zeros; random-init"}
     from linnet_amd.llama import Int4Llama
@@ -438,19 +440,28 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         end.record()
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / reps
-        # The same step's 161 int4 linear calls alone (inputs and outputs preallocated).
+        # The same step's 161 int4 linear calls alone (inputs and outputs preallocated),
+        # on x tiles where the step's glue hands its projections tiles (17..64 rows:
+        # all but o).
         calls = []
+
+        def x_in(k, tiles):
+            xin = (torch.randn(batch, k, device=dev) * 0.5).to(torch.bfloat16)
+            return kernels.x_tiles(xin) if tiles else xin
+
+        tiles = model._tiles(x)
         for p in model.layers:
             for name, k in (("qkv", 4096), ("o", 4096), ("gate_up", 4096), ("down", 14336)):
-                xin = (torch.randn(batch, k, device=dev) * 0.5).to(torch.bfloat16)
                 yout = torch.empty(batch, p[name][0].shape[0], dtype=torch.bfloat16, device=dev)
-                calls.append((xin, p[name], yout))
-        calls.append(((torch.randn(batch, 4096, device=dev) * 0.5).to(torch.bfloat16), model.head,
-                      torch.empty(batch, 128256, dtype=torch.bfloat16, device=dev)))
+                calls.append((x_in(k, tiles and name != "o"), p[name], yout))
+        calls.append((x_in(4096, tiles), model.head, torch.empty(batch, 128256, dtype=torch.bfloat16, device=dev)))
         lin_graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(lin_graph):
             for xin, w, yout in calls:
-                kernels.int4_linear(xin, *w, out=yout)
+                if isinstance(xin, kernels.XTiles):
+                    kernels.int4_linear_tiles(xin, *w, out=yout)
+                else:
+                    kernels.int4_linear(xin, *w, out=yout)
         lin_graph.replay()
         torch.cuda.synchronize()
         start.record()

@@ -171,6 +171,30 @@ LNQ_API LnqStatus lnq_int4_linear_workspace(int64_t rows, int64_t in_features, i
                                             int64_t group, int32_t dtype, int32_t kernel,
                                             int32_t* chosen, int64_t* workspace_bytes);
 
+/* x tiles: activations laid out for the few-row GEMVs' matrix-core operands, so
+ * that each 1 KB operand they load is contiguous (row-major x makes every load
+ * instruction read 16 rows x 64 bytes, a third of the rate of whole lines). For rows
+ * x in values (in % 256 == 0), chunks of 32 rows of in * 32 values; within a chunk,
+ * value (m, k) sits at ((k / 256 * 16 + 8 (m / 16 % 2) + 4 (k / 128 % 2) + k / 32 % 4)
+ * * 64 + 16 (k / 8 % 4) + m % 16) * 8 + k % 8. lnq_x_tiles writes them from row-major
+ * x (2-byte values; rows of the last chunk past `rows` zero; x, xt 16-byte aligned).
+ * No counterpart in the reference (a layout of this library's decode kernels). */
+LNQ_API LnqStatus lnq_x_tiles(const void* x, void* xt, int64_t rows, int64_t in_features, void* stream);
+
+/* lnq_int4_linear_ws on x given as x tiles (rows 1..64, in % 256 == 0): the 32-row
+ * GEMV (in <= 4096; kernel AUTO or GEMV) or the split GEMV (kernel SPLIT, where the
+ * automatic choice of lnq_int4_linear_ws takes it with this workspace, and always
+ * past in = 4096, which then needs the workspace lnq_int4_linear_workspace names).
+ * The products are those of the same kernels on row-major x, bit for bit.
+ * Replaces: the same reference calls as lnq_int4_linear (torch_source.cpp:1553-1570),
+ * for a caller whose previous kernel wrote x tiles (lnq_rmsnorm_tiles,
+ * lnq_silu_mul_tiles). */
+LNQ_API LnqStatus lnq_int4_linear_tiles(const void* xt, const uint8_t* packed, const void* scale,
+                                        const uint8_t* zero, const void* bias, void* y, int64_t rows,
+                                        int64_t in_features, int64_t out_features, int64_t group,
+                                        int32_t dtype, int32_t kernel, void* workspace,
+                                        int64_t workspace_bytes, void* stream);
+
 /* out[out, in] = (q - zero) * scale computed in f32 and rounded once to `dtype`
  * (the scale's dtype: bf16, f16 or f32). Any even group dividing `in`.
  * Replaces: `_int4_unpack`/`_int4_weight` (torch_source.cpp:1518-1550) and the
@@ -465,6 +489,11 @@ LNQ_API LnqStatus lnq_nf4_repack(const uint8_t* packed, const void* absmax_in, c
 LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, void* h, int64_t rows,
                               int64_t hidden, float eps, void* stream);
 
+/* lnq_rmsnorm with h written as x tiles (lnq_x_tiles; hidden % 256 == 0 and <=
+ * 16384, operands 16-byte aligned): the same bits, for lnq_int4_linear_tiles. */
+LNQ_API LnqStatus lnq_rmsnorm_tiles(void* x, const void* delta, const float* weight, void* xt, int64_t rows,
+                                    int64_t hidden, float eps, void* stream);
+
 /* One decode step of grouped-query attention: q [rows, heads*head_dim], k and v
  * [rows, kv_heads*head_dim] (bf16); rotary embedding of q and k with cos/sin f32
  * [head_dim/2] (pairs i, i + head_dim/2); k and v stored (rounded to bf16) at `pos`
@@ -550,6 +579,11 @@ LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n,
  * gate|up projection's output [rows, 2*width]: u = g + width, both strides 2*width). */
 LNQ_API LnqStatus lnq_silu_mul_rows(const void* g, const void* u, void* a, int64_t rows, int64_t width,
                                     int64_t g_stride, int64_t u_stride, void* stream);
+
+/* lnq_silu_mul_rows with a written as x tiles (lnq_x_tiles; width % 256 == 0): the
+ * same bits, for lnq_int4_linear_tiles. */
+LNQ_API LnqStatus lnq_silu_mul_tiles(const void* g, const void* u, void* xt, int64_t rows, int64_t width,
+                                     int64_t g_stride, int64_t u_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -69,6 +69,20 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // f32 -> bf16 bits, round to nearest even: gfx950's v_cvt_pk_bf16_f32.
+// "x tiles": rows x K activations in the MFMA A-operand order of the 32-row
+// GEMVs, so that each operand they load is 1 KB of contiguous memory (a wave
+// instruction reading 16 rows x 64 bytes of row-major x runs at a third of the
+// rate of one reading whole 128-byte lines). Rows come in chunks of 32 (K * 32
+// values each); a chunk holds K / 256 slices of 16 operands 8 b + 4 H + t, and
+// lane 16 j + c of an operand holds row 16 b + c, inputs 256 s + 128 H + 32 t +
+// 8 j .. + 7. The index of value (m, k) (K % 256 == 0):
+__host__ __device__ inline size_t x_tile_index(int m, int k, int K) {
+  const int chunk = m >> 5, b = (m >> 4) & 1, c = m & 15;
+  const int s = k >> 8, H = (k >> 7) & 1, t = (k >> 5) & 3, j = (k >> 3) & 3, e = k & 7;
+  return static_cast<size_t>(chunk) * K * 32 +
+         ((static_cast<size_t>(s) * 16 + 8 * b + 4 * H + t) * 64 + 16 * j + c) * 8 + e;
+}
+
 __device__ inline uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }

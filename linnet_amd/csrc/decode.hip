@@ -110,7 +110,8 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_kernel(uint16_t* __re
 // t + 256, ... (CH of them, up to 8: hidden <= 2048 CH, hidden % 8 == 0), every load of x,
 // delta and the weight issued before any is used (the scalar loop above waits on
 // each of its 16 loads a thread in turn: 14 us for one 4096-wide row).
-template <int CH>
+// TILES: h is written as x tiles (x_tile_index) for the 32-row GEMVs.
+template <int CH, bool TILES = false>
 __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* __restrict__ x,
                                                                       const uint16_t* __restrict__ delta,
                                                                       const float* __restrict__ w,
@@ -171,7 +172,8 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
   for (int c = 0; c < CH; ++c) {
     const int i = threadIdx.x + c * decode::THREADS;
     if (i >= chunks) continue;
-    *reinterpret_cast<u32x4*>(hr + 8 * i) = norm_bf16x8(v[c], scale, wv[c][0], wv[c][1]);
+    uint16_t* dst = TILES ? h + x_tile_index(blockIdx.x, 8 * i, hidden) : hr + 8 * i;
+    *reinterpret_cast<u32x4*>(dst) = norm_bf16x8(v[c], scale, wv[c][0], wv[c][1]);
   }
 }
 
@@ -553,14 +555,16 @@ __global__ __launch_bounds__(decode::THREADS) void prefill_rope_kernel(
 __global__ __launch_bounds__(decode::THREADS) void silu_mul_kernel(const uint16_t* __restrict__ g,
                                                                    const uint16_t* __restrict__ u,
                                                                    uint16_t* __restrict__ a, int64_t n, int64_t width,
-                                                                   int64_t g_stride, int64_t u_stride) {
+                                                                   int64_t g_stride, int64_t u_stride, bool tiles) {
   // Element i of a [rows, width]: row i / width of g and u, whose rows are
   // g_stride and u_stride elements apart (the two halves of a joined gate|up
-  // projection's output, say).
+  // projection's output, say); with `tiles`, a is written as x tiles.
   for (int64_t i = blockIdx.x * static_cast<int64_t>(decode::THREADS) + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * decode::THREADS) {
     const int64_t r = i / width, c = i - r * width;
-    a[i] = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g[r * g_stride + c]), bf16_bits_to_f32(u[r * u_stride + c])));
+    const size_t o = tiles ? x_tile_index(static_cast<int>(r), static_cast<int>(c), static_cast<int>(width))
+                           : static_cast<size_t>(i);
+    a[o] = f32_to_bf16_bits(silu_times(bf16_bits_to_f32(g[r * g_stride + c]), bf16_bits_to_f32(u[r * u_stride + c])));
   }
 }
 
@@ -595,6 +599,32 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
   else if (vec) hipLaunchKernelGGL(rmsnorm_vec_kernel<8>, grid, block, 0, s, xs, ds, weight, hs, H, eps);
   else hipLaunchKernelGGL(rmsnorm_kernel, grid, block, 0, s, xs, ds, weight, hs, H, eps);
   return launched("rmsnorm");
+}
+
+LNQ_API LnqStatus lnq_rmsnorm_tiles(void* x, const void* delta, const float* weight, void* xt, int64_t rows,
+                                    int64_t hidden, float eps, void* stream) {
+  LNQ_REQUIRE(rows >= 0 && rows <= INT32_MAX && hidden > 0 && hidden % 256 == 0 && hidden <= 64 * decode::THREADS,
+              "lnq_rmsnorm_tiles: bad shape rows=%lld hidden=%lld (hidden %% 256 == 0, <= %d)", (long long)rows,
+              (long long)hidden, 64 * decode::THREADS);
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(x && weight && xt, "lnq_rmsnorm_tiles: null pointer");
+  LNQ_REQUIRE(aligned(x, 16) && aligned(xt, 16) && aligned(weight, 16) && (delta == nullptr || aligned(delta, 16)),
+              "lnq_rmsnorm_tiles: operands must be 16-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto* xs = static_cast<uint16_t*>(x);
+  const auto* ds = static_cast<const uint16_t*>(delta);
+  auto* hs = static_cast<uint16_t*>(xt);
+  const int H = static_cast<int>(hidden);
+  const int ch = (H + 8 * decode::THREADS - 1) / (8 * decode::THREADS);
+  const dim3 grid(static_cast<unsigned>(rows)), block(decode::THREADS);
+  if (ch == 1) hipLaunchKernelGGL((rmsnorm_vec_kernel<1, true>), grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else if (ch == 2) hipLaunchKernelGGL((rmsnorm_vec_kernel<2, true>), grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else if (ch <= 4) hipLaunchKernelGGL((rmsnorm_vec_kernel<4, true>), grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  else hipLaunchKernelGGL((rmsnorm_vec_kernel<8, true>), grid, block, 0, s, xs, ds, weight, hs, H, eps);
+  return launched("rmsnorm_tiles");
 }
 
 // pos_dev: nullptr (the position is `pos`) or the device address of the int32
@@ -769,7 +799,7 @@ LNQ_API LnqStatus lnq_silu_mul(const void* g, const void* u, void* a, int64_t n,
   const int64_t blocks = (n + decode::THREADS - 1) / decode::THREADS;
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
                      dim3(decode::THREADS), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(g),
-                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n, n, int64_t{0}, int64_t{0});
+                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n, n, int64_t{0}, int64_t{0}, false);
   return launched("silu_mul");
 }
 
@@ -785,8 +815,26 @@ LNQ_API LnqStatus lnq_silu_mul_rows(const void* g, const void* u, void* a, int64
   const int64_t blocks = (n + decode::THREADS - 1) / decode::THREADS;
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
                      dim3(decode::THREADS), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(g),
-                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n, width, g_stride, u_stride);
+                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(a), n, width, g_stride, u_stride, false);
   return launched("silu_mul_rows");
+}
+
+LNQ_API LnqStatus lnq_silu_mul_tiles(const void* g, const void* u, void* xt, int64_t rows, int64_t width,
+                                     int64_t g_stride, int64_t u_stride, void* stream) {
+  LNQ_REQUIRE(rows >= 0 && rows <= INT32_MAX && width > 0 && width % 256 == 0 && width <= INT32_MAX &&
+                  g_stride >= width && u_stride >= width,
+              "lnq_silu_mul_tiles: bad shape (width %% 256 == 0)");
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(g && u && xt, "lnq_silu_mul_tiles: null pointer");
+  const int64_t n = rows * width;
+  const int64_t blocks = (n + decode::THREADS - 1) / decode::THREADS;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
+                     dim3(decode::THREADS), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(g),
+                     static_cast<const uint16_t*>(u), static_cast<uint16_t*>(xt), n, width, g_stride, u_stride, true);
+  return launched("silu_mul_tiles");
 }
 
 }  // extern "C"

@@ -639,7 +639,10 @@ bool int4_gemv_split_supports(int M, int N, int K, int G, int u8, int S, const v
                               const void* scale, const void* zero, const void* part);
 LnqStatus launch_int4_gemv_split(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                                  const void* bias, void* y, int M, int N, int K, int G, int dtype, int u8, int S,
-                                 float* part, hipStream_t stream);
+                                 float* part, hipStream_t stream, bool tiles = false);
+LnqStatus launch_int4_gemv_tiles(const void* xt, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                 const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream);
+LnqStatus launch_x_tiles(const void* x, void* xt, int rows, int K, hipStream_t stream);
 
 // The split GEMV's workgroup shape for K: past K = 4096 (where the few-row
 // GEMV stops), 64-row blocks and the fewest K chunks of at most 16 slices of
@@ -906,6 +909,70 @@ LNQ_API LnqStatus lnq_int4_linear_ws(const void* x, const uint8_t* packed, const
     const LnqStatus st = launch_int4_gemv_split(xc, packed, scale, zero, bias, static_cast<uint8_t*>(y) + c * yrow,
                                                 rc, N, K, G, dtype, u8, S, part, s);
     if (st != LNQ_OK) return st;
+  }
+  return LNQ_OK;
+}
+
+LNQ_API LnqStatus lnq_x_tiles(const void* x, void* xt, int64_t rows, int64_t in_features, void* stream) {
+  LNQ_REQUIRE(rows >= 0 && rows <= INT32_MAX && in_features > 0 && in_features % 256 == 0 &&
+                  in_features * 64 <= INT32_MAX,
+              "lnq_x_tiles: bad shape rows=%lld in=%lld (in %% 256 == 0)", (long long)rows, (long long)in_features);
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(x && xt, "lnq_x_tiles: null pointer");
+  LNQ_REQUIRE(aligned(x, 16) && aligned(xt, 16), "lnq_x_tiles: x and xt must be 16-byte aligned");
+  return launch_x_tiles(x, xt, static_cast<int>(rows), static_cast<int>(in_features), static_cast<hipStream_t>(stream));
+}
+
+LNQ_API LnqStatus lnq_int4_linear_tiles(const void* xt, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                        const void* bias, void* y, int64_t rows, int64_t in_features,
+                                        int64_t out_features, int64_t group, int32_t dtype, int32_t kernel,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!check_int4_linear(rows, in_features, out_features, group, dtype, LNQ_KERNEL_AUTO, "lnq_int4_linear_tiles"))
+    return LNQ_ERROR;
+  LNQ_REQUIRE(kernel == LNQ_KERNEL_AUTO || kernel == LNQ_KERNEL_GEMV || kernel == LNQ_KERNEL_SPLIT,
+              "lnq_int4_linear_tiles: kernel is AUTO, GEMV or SPLIT, not %d", kernel);
+  LNQ_REQUIRE(rows <= 64 && in_features % 256 == 0,
+              "lnq_int4_linear_tiles: x tiles of up to 64 rows with in %% 256 == 0, got rows=%lld in=%lld",
+              (long long)rows, (long long)in_features);
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(xt && packed && scale && zero && y, "lnq_int4_linear_tiles: null pointer");
+  LNQ_REQUIRE(kernel != LNQ_KERNEL_GEMV || in_features <= 4096,
+              "lnq_int4_linear_tiles: the 32-row GEMV takes in <= 4096, got %lld", (long long)in_features);
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  int u8 = 0, S = 0;
+  const bool shaped = split_shape(K, u8, S);
+  const int64_t need = shaped ? split_workspace_bytes(M, N, S) : 0;
+  const bool fits = workspace != nullptr && aligned(workspace, 16) && workspace_bytes >= need;
+  // The split GEMV where the row-major path would take it (and always past K =
+  // 4096, where the 32-row GEMV stops), else the 32-row GEMV.
+  const bool split = kernel == LNQ_KERNEL_SPLIT || K > 4096 ||
+                     (kernel == LNQ_KERNEL_AUTO && shaped && fits && split_preferred(M < 16 ? 16 : M, N, K));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t tile_chunk = static_cast<size_t>(K) * 64, yrow = static_cast<size_t>(N) * 2;
+  for (int c = 0; c < M; c += 32) {
+    const int rc = M - c < 32 ? M - c : 32;
+    const void* xc = static_cast<const uint8_t*>(xt) + (c / 32) * tile_chunk;
+    void* yc = static_cast<uint8_t*>(y) + c * yrow;
+    if (split) {
+      LNQ_REQUIRE(shaped, "lnq_int4_linear_tiles: the split GEMV does not take in=%d", K);
+      LNQ_REQUIRE(fits, "lnq_int4_linear_tiles: the split GEMV needs %lld workspace bytes, 16-byte aligned (got %lld)",
+                  (long long)need, (long long)workspace_bytes);
+      LNQ_REQUIRE(int4_gemv_split_supports(rc, N, K, G, u8, S, xc, packed, scale, zero, workspace),
+                  "lnq_int4_linear_tiles: the split GEMV does not take rows=%d in=%d out=%d group=%d", rc, K, N, G);
+      const LnqStatus st = launch_int4_gemv_split(xc, packed, scale, zero, bias, yc, rc, N, K, G, dtype, u8, S,
+                                                  static_cast<float*>(workspace), s, true);
+      if (st != LNQ_OK) return st;
+    } else {
+      const LnqStatus st = launch_int4_gemv_tiles(xc, packed, scale, zero, bias, yc, rc, N, K, G, dtype, s);
+      if (st != LNQ_OK) return st;
+    }
   }
   return LNQ_OK;
 }

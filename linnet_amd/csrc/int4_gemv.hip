@@ -947,6 +947,9 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
 // the 8-row last tile of an odd U8 1 KB: its 8 outputs x 32 rows). The 16
 // waves' sums are then added as in int4_gemv_rows_kernel.
 //
+// XT: x is given as x tiles (one 32-row chunk, x_tile_index): operand (b, H,
+// t) of the wave's slice is one contiguous 1 KB load.
+//
 // SPLIT: the K range is cut into gridDim.y chunks of nw slices, workgroup
 // (bx, c) taking chunk c of rows bx * R ..; its sums over the chunk go unrounded
 // to part[c][m][n] (f32) and int4_split_reduce_kernel adds the chunks in order.
@@ -954,7 +957,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
 // quarter of K reads a quarter of x where the unsplit kernel's 16-row blocks
 // read all of it (the down projection at 32 rows: 229 KB of x against 115 KB of
 // weights a workgroup, in place of 917 KB against 115 KB).
-template <int DT, int U8, bool G128, bool SPLIT = false>
+template <int DT, int U8, bool G128, bool SPLIT = false, bool XT = false>
 __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zero,
@@ -982,7 +985,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
   const int rowb = K >> 1;
   const int groups = K / G;
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(packed, static_cast<uint32_t>(static_cast<size_t>(N) * rowb));
-  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint32_t>(static_cast<size_t>(M) * K * 2));
+  const __amdgpu_buffer_rsrc_t rx =
+      buffer_rsrc(x, static_cast<uint32_t>(static_cast<size_t>(XT ? 32 : M) * K * 2));
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scale, static_cast<uint32_t>(N * groups * 2));
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(zero, static_cast<uint32_t>(N * groups));
 
@@ -1011,7 +1015,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
       for (int t = 0; t < 4; ++t)
         xa[b][H][t] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rx, ((16 * b + col) * K + k0 + 128 * H + 32 * t + 8 * j) * 2, 0, 0));
+                       rx, XT ? (((k0 >> 8) * 16 + 8 * b + 4 * H + t) * 64 + lane) * 16
+                              : ((16 * b + col) * K + k0 + 128 * H + 32 * t + 8 * j) * 2, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
   {
     const int a = lane >> 4, bb = lane & 15;
@@ -1330,7 +1335,7 @@ static void launch_rows_dt(const void* x, const uint8_t* packed, const void* sca
   }
 }
 
-template <int DT, int U8>
+template <int DT, int U8, bool XT>
 static void launch_rows32_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                              const void* bias, void* y, int M, int N, int K, int G, hipStream_t stream) {
   const dim3 grid((N + 8 * U8 - 1) / (8 * U8)), block(64 * (K / 256));
@@ -1339,55 +1344,78 @@ static void launch_rows32_u8(const void* x, const uint8_t* packed, const void* s
   const auto* bs = static_cast<const uint16_t*>(bias);
   auto* ys = static_cast<uint16_t*>(y);
   if (G == 128)
-    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, true>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
-                       M, N, K, G);
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, true, false, XT>), grid, block, 0, stream, xs, packed, ss, zero,
+                       bs, ys, M, N, K, G, nullptr);
   else
-    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, false>), grid, block, 0, stream, xs, packed, ss, zero, bs, ys,
-                       M, N, K, G);
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, false, false, XT>), grid, block, 0, stream, xs, packed, ss,
+                       zero, bs, ys, M, N, K, G, nullptr);
 }
 
-template <int DT>
+template <int DT, bool XT>
 static void launch_rows32_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                              const void* bias, void* y, int M, int N, int K, int G, hipStream_t stream) {
   switch ((N + 2047) / 2048) {
-    case 1: launch_rows32_u8<DT, 1>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
-    case 2: launch_rows32_u8<DT, 2>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
-    case 3: launch_rows32_u8<DT, 3>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
-    case 4: launch_rows32_u8<DT, 4>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
-    case 5: launch_rows32_u8<DT, 5>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
-    case 6: launch_rows32_u8<DT, 6>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
-    case 7: launch_rows32_u8<DT, 7>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
-    default: launch_rows32_u8<DT, 8>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 1: launch_rows32_u8<DT, 1, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 2: launch_rows32_u8<DT, 2, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 3: launch_rows32_u8<DT, 3, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 4: launch_rows32_u8<DT, 4, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 5: launch_rows32_u8<DT, 5, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 6: launch_rows32_u8<DT, 6, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    case 7: launch_rows32_u8<DT, 7, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
+    default: launch_rows32_u8<DT, 8, XT>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
   }
 }
 
-template <int DT, int U8>
+template <int DT, int U8, bool XT>
 static void launch_split_u8(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero, int M,
                             int N, int K, int G, int S, float* part, hipStream_t stream) {
   const dim3 grid((N + 8 * U8 - 1) / (8 * U8), S), block(64 * (K / (256 * S)));
   const auto* xs = static_cast<const uint16_t*>(x);
   const auto* ss = static_cast<const uint16_t*>(scale);
   if (G == 128)
-    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, true, true>), grid, block, 0, stream, xs, packed, ss, zero,
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, true, true, XT>), grid, block, 0, stream, xs, packed, ss, zero,
                        nullptr, nullptr, M, N, K, G, part);
   else
-    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, false, true>), grid, block, 0, stream, xs, packed, ss, zero,
-                       nullptr, nullptr, M, N, K, G, part);
+    hipLaunchKernelGGL((int4_gemv_rows32_kernel<DT, U8, false, true, XT>), grid, block, 0, stream, xs, packed, ss,
+                       zero, nullptr, nullptr, M, N, K, G, part);
 }
 
-template <int DT>
+template <int DT, bool XT>
 static void launch_split_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                             const void* bias, void* y, int M, int N, int K, int G, int u8, int S, float* part,
                             hipStream_t stream) {
-  switch (u8) {
-    case 4: launch_split_u8<DT, 4>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
-    case 8: launch_split_u8<DT, 8>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
-    case 16: launch_split_u8<DT, 16>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
-    default: launch_split_u8<DT, 32>(x, packed, scale, zero, M, N, K, G, S, part, stream); break;
-  }
+  if (u8 == 8) launch_split_u8<DT, 8, XT>(x, packed, scale, zero, M, N, K, G, S, part, stream);
+  else launch_split_u8<DT, 16, XT>(x, packed, scale, zero, M, N, K, G, S, part, stream);
   const size_t quads = static_cast<size_t>(M) * N / 4;
   hipLaunchKernelGGL((int4_split_reduce_kernel<DT>), dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
                      stream, part, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), M, N, S);
+}
+
+// rows x K values, row-major, to x tiles (x_tile_index; chunks of 32 rows, rows
+// past `rows` of the last chunk zero): thread t of workgroup (chunk, slice)
+// moves the 16-byte pieces t, t + 256, t + 512, t + 768 of the slice's 16 KB.
+__global__ __launch_bounds__(256) void x_tiles_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xt,
+                                                      int rows, int K) {
+  const int chunk = blockIdx.y, s = blockIdx.x;
+  uint16_t* out = xt + static_cast<size_t>(chunk) * K * 32 + static_cast<size_t>(s) * 16 * 64 * 8;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int piece = threadIdx.x + 256 * r;  // operand piece / 64, lane piece % 64
+    const int op = piece >> 6, lane = piece & 63;
+    const int m = 32 * chunk + 16 * (op >> 3) + (lane & 15);
+    const int k = 256 * s + 128 * ((op >> 2) & 1) + 32 * (op & 3) + 8 * (lane >> 4);
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (m < rows) v = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m) * K + k);
+    *reinterpret_cast<u32x4*>(out + static_cast<size_t>(piece) * 8) = v;
+  }
+}
+
+LnqStatus launch_x_tiles(const void* x, void* xt, int rows, int K, hipStream_t stream) {
+  if (rows <= 0) return LNQ_OK;
+  const dim3 grid(K / 256, (rows + 31) / 32);
+  hipLaunchKernelGGL(x_tiles_kernel, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
+                     static_cast<uint16_t*>(xt), rows, K);
+  return launched("x_tiles");
 }
 
 template <int DT, int U8, int S>
@@ -1447,14 +1475,14 @@ bool int4_gemv_takes_prologue(int M, int N, int K, int G, int dtype, const void*
          N <= 32768 && aligned(operand, 16) && int4_gemv_supports(M, N, K, G, x, packed, scale, zero);
 }
 
-// The split 32-row GEMV (1..32 rows): R = 8 * u8 rows a workgroup (u8 4, 8, 16
-// or 32), K in S chunks of at most wmax(u8) slices of 256 inputs (16, 8, 4),
+// The split 32-row GEMV (1..32 rows): R = 8 * u8 rows a workgroup (u8 8 or 16),
+// K in S chunks of at most wmax(u8) slices of 256 inputs (16 or 8),
 // the chunks' f32 sums in part (S * M * N floats, 16-byte aligned), then added
 // in order.
 bool int4_gemv_split_supports(int M, int N, int K, int G, int u8, int S, const void* x, const void* packed,
                               const void* scale, const void* zero, const void* part) {
   if (M < 1 || M > gemv::MAX_ROWS || N <= 0 || N % 4 != 0 || S < 1) return false;
-  if (!(u8 == 4 || u8 == 8 || u8 == 16 || u8 == 32)) return false;
+  if (!(u8 == 8 || u8 == 16)) return false;
   if (K <= 0 || K % (256 * S) != 0 || K / (256 * S) > gemv::wmax(u8)) return false;
   if (!(G == 128 || G % 256 == 0) || K % G != 0) return false;
   if (static_cast<size_t>(N) * (K / 2) >= (1ull << 31) || static_cast<size_t>(M) * K * 2 >= (1ull << 31)) return false;
@@ -1464,15 +1492,33 @@ bool int4_gemv_split_supports(int M, int N, int K, int G, int u8, int S, const v
 
 LnqStatus launch_int4_gemv_split(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                                  const void* bias, void* y, int M, int N, int K, int G, int dtype, int u8, int S,
-                                 float* part, hipStream_t stream) {
+                                 float* part, hipStream_t stream, bool tiles) {
   if (!int4_gemv_split_supports(M, N, K, G, u8, S, x, packed, scale, zero, part)) {
     set_error("launch_int4_gemv_split: the split GEMV does not take rows=%d N=%d K=%d group=%d u8=%d splits=%d", M,
               N, K, G, u8, S);
     return LNQ_ERROR;
   }
-  if (dtype == LNQ_BF16) launch_split_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
-  else launch_split_dt<LNQ_F16>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
+  if (dtype == LNQ_BF16) {
+    if (tiles) launch_split_dt<LNQ_BF16, true>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
+    else launch_split_dt<LNQ_BF16, false>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
+  } else {
+    if (tiles) launch_split_dt<LNQ_F16, true>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
+    else launch_split_dt<LNQ_F16, false>(x, packed, scale, zero, bias, y, M, N, K, G, u8, S, part, stream);
+  }
   return launched("int4_gemv_split");
+}
+
+// The 32-row GEMV (1..32 rows, K <= 4096) on x tiles of one 32-row chunk; the
+// shape limits of int4_gemv_supports at 17..32 rows.
+LnqStatus launch_int4_gemv_tiles(const void* xt, const uint8_t* packed, const void* scale, const uint8_t* zero,
+                                 const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream) {
+  if (M < 1 || M > 32 || !int4_gemv_supports(32, N, K, G, xt, packed, scale, zero)) {
+    set_error("launch_int4_gemv_tiles: the 32-row GEMV does not take rows=%d N=%d K=%d group=%d", M, N, K, G);
+    return LNQ_ERROR;
+  }
+  if (dtype == LNQ_BF16) launch_rows32_dt<LNQ_BF16, true>(xt, packed, scale, zero, bias, y, M, N, K, G, stream);
+  else launch_rows32_dt<LNQ_F16, true>(xt, packed, scale, zero, bias, y, M, N, K, G, stream);
+  return launched("int4_gemv_tiles");
 }
 
 LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
@@ -1505,8 +1551,8 @@ LnqStatus launch_int4_gemv(const void* x, const uint8_t* packed, const void* sca
     if (dtype == LNQ_BF16) launch_rows_dt<LNQ_BF16, 16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
     else launch_rows_dt<LNQ_F16, 16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
   } else {
-    if (dtype == LNQ_BF16) launch_rows32_dt<LNQ_BF16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
-    else launch_rows32_dt<LNQ_F16>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+    if (dtype == LNQ_BF16) launch_rows32_dt<LNQ_BF16, false>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
+    else launch_rows32_dt<LNQ_F16, false>(x, packed, scale, zero, bias, y, M, N, K, G, stream);
   }
   return launched("int4_gemv");
 }

@@ -29,8 +29,8 @@ class Int4Llama:
     linear layers' own kernels (`layer_folded`)."""
 
     def __init__(self, torch, kernels, dev, layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336,
-                 vocab=128256, ctx=1024, batch=1, seed=0, fused=True, spare=0):
-        self.torch, self.kernels, self.fused = torch, kernels, fused
+                 vocab=128256, ctx=1024, batch=1, seed=0, fused=True, spare=0, tiles=True):
+        self.torch, self.kernels, self.fused, self.tiles = torch, kernels, fused, tiles
         self.hidden, self.heads, self.kv_heads, self.hd = hidden, heads, kv_heads, hidden // heads
         g = torch.Generator(device=dev).manual_seed(seed)
 
@@ -77,7 +77,9 @@ class Int4Llama:
         # through `replay`), so that no step runs past the cache.
         self.device_pos = ctx
         self.cos_tab, self.sin_tab = decode.rope_tables(self.hd, cap, 500000.0, dev)
-        self.linear = lambda x, w: kernels.int4_linear(x, *w)
+        # x tiles (the glue writes the few-row GEMVs' operand order) for 17..64 rows.
+        self.linear = lambda x, w: (kernels.int4_linear_tiles(x, *w) if isinstance(x, kernels.XTiles)
+                                    else kernels.int4_linear(x, *w))
         # One-token steps fold the glue into the linear layers (`layer_folded`).
         self.fold = True
         self._flash = None  # whether PyTorch's fused attention ran (None: not tried)
@@ -158,7 +160,8 @@ class Int4Llama:
         from linnet_amd.torch import decode, generated
 
         p = self.layers[i]
-        h = decode.rmsnorm(x, p["n1"], 1e-5, delta)
+        tiles = self._tiles(x)
+        h = decode.rmsnorm(x, p["n1"], 1e-5, delta, tiles=tiles)
         q, k, v = generated._int4_split(self.linear(h, p["qkv"]), p["qkv_rows"])
         if device_pos:
             att = decode.decode_attention(q, k, v, self.cos_tab, self.sin_tab, self.kt[i], self.vc[i], self.pos_t)
@@ -167,9 +170,14 @@ class Int4Llama:
         o = self.linear(att, p["o"])
         if parts is not None:
             parts["attn"] = o
-        h = decode.rmsnorm(x, p["n2"], 1e-5, o)
+        h = decode.rmsnorm(x, p["n2"], 1e-5, o, tiles=tiles)
         g, u = generated._int4_split(self.linear(h, p["gate_up"]), p["gate_up_rows"])
-        return self.linear(decode.silu_mul(g, u), p["down"])
+        return self.linear(decode.silu_mul(g, u, tiles=tiles), p["down"])
+
+    def _tiles(self, x):
+        """Whether the glue hands the projections x tiles: 17..64 rows, where the
+        32-row and split GEMVs take them."""
+        return self.tiles and 17 <= x.shape[0] <= 64
 
     def layer_folded(self, i, x, parts=None, device_pos=False):
         """Layer i of a one-token step with the glue folded into the linear layers:
@@ -202,7 +210,7 @@ class Int4Llama:
     def head_fused(self, x, delta):
         from linnet_amd.torch import decode
 
-        return self.linear(decode.rmsnorm(x, self.norm, 1e-5, delta), self.head)
+        return self.linear(decode.rmsnorm(x, self.norm, 1e-5, delta, tiles=self._tiles(x)), self.head)
 
     def _attend_prompt(self, qh, kh, vh):
         """Causal grouped-query attention of a prompt, q [1, heads, P, hd], k and v
@@ -239,7 +247,8 @@ class Int4Llama:
         from linnet_amd.torch import decode, generated
 
         p = self.layers[i]
-        h = decode.rmsnorm(x, p["n1"], 1e-5, delta)
+        tiles = self._tiles(x)
+        h = decode.rmsnorm(x, p["n1"], 1e-5, delta, tiles=tiles)
         q, k, v = generated._int4_split(self.linear(h, p["qkv"]), p["qkv_rows"])
         qh, kh, vh = decode.prefill_rope(q, k, v, self.cos_tab, self.sin_tab, self.kt[i][0], self.vc[i][0])
         o = self.linear(self._attend_prompt(qh, kh, vh), p["o"])

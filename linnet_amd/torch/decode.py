@@ -11,7 +11,7 @@ import torch
 
 from .. import _lib
 from ..errors import LinnetError
-from .kernels import _on_gpu, _ptr, _stream
+from .kernels import XTiles, _on_gpu, _ptr, _stream
 
 
 def _bf16(what: str, *tensors: torch.Tensor) -> None:
@@ -20,10 +20,12 @@ def _bf16(what: str, *tensors: torch.Tensor) -> None:
             raise LinnetError(f"{what}: takes contiguous bf16 tensors, got {t.dtype}")
 
 
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: torch.Tensor | None = None) -> torch.Tensor:
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: torch.Tensor | None = None,
+            tiles: bool = False) -> torch.Tensor | XTiles:
     """`h = x * rsqrt(mean(x^2) + eps) * weight` per row of x [rows, hidden]; with
     `delta`, first `x += delta` in place (rounded to bf16), as the residual add
-    before a norm. weight: f32 [hidden]."""
+    before a norm. weight: f32 [hidden]. `tiles`: h is returned as x tiles (for
+    `int4_linear_tiles`; hidden % 256 == 0), the same bits."""
     device = _on_gpu("rmsnorm", x, weight, delta)
     _bf16("rmsnorm", x, *(() if delta is None else (delta,)))
     if weight.dtype != torch.float32 or weight.numel() != x.shape[-1]:
@@ -31,9 +33,16 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: tor
     weight = weight.contiguous()  # a strided view (a column of stacked weights) is read packed
     if delta is not None and delta.shape != x.shape:
         raise LinnetError("rmsnorm: delta has x's shape")
+    rows = x.numel() // x.shape[-1]
+    if tiles:
+        xt = XTiles.empty(rows, x.shape[-1], x.dtype, device)
+        with torch.cuda.device(device):
+            _lib.call("lnq_rmsnorm_tiles", _ptr(x), _ptr(delta), _ptr(weight), _ptr(xt.data), rows, x.shape[-1],
+                      float(eps), _stream(device))
+        return xt
     h = torch.empty_like(x)
     with torch.cuda.device(device):
-        _lib.call("lnq_rmsnorm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(h), x.numel() // x.shape[-1], x.shape[-1],
+        _lib.call("lnq_rmsnorm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(h), rows, x.shape[-1],
                   float(eps), _stream(device))
     return h
 
@@ -138,15 +147,24 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
     return out
 
 
-def silu_mul(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+def silu_mul(g: torch.Tensor, u: torch.Tensor, tiles: bool = False) -> torch.Tensor | XTiles:
     """`silu(g) * u` elementwise in f32, rounded once to bf16. g and u may be 2-D
     column slices (rows strided, each row contiguous), e.g. the two halves of a
-    joined gate|up projection's output; the result is contiguous."""
+    joined gate|up projection's output; the result is contiguous. `tiles`: the
+    result as x tiles (2-D, width % 256 == 0), the same bits."""
     device = _on_gpu("silu_mul", g, u)
     if g.dtype != torch.bfloat16 or u.dtype != torch.bfloat16:
         raise LinnetError("silu_mul: g and u are bf16")
     if g.shape != u.shape:
         raise LinnetError("silu_mul: g and u have one shape")
+    if tiles:
+        if g.dim() != 2 or g.stride(1) != 1 or u.stride(1) != 1:
+            g, u = g.contiguous(), u.contiguous()
+        xt = XTiles.empty(g.shape[0], g.shape[1], g.dtype, device)
+        with torch.cuda.device(device):
+            _lib.call("lnq_silu_mul_tiles", _ptr(g), _ptr(u), _ptr(xt.data), g.shape[0], g.shape[1], g.stride(0),
+                      u.stride(0), _stream(device))
+        return xt
     if g.is_contiguous() and u.is_contiguous():
         a = torch.empty_like(g)
         with torch.cuda.device(device):

@@ -11,6 +11,7 @@ captured into a HIP graph. CPU tensors, or a missing library, raise
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import functools
 
 import torch
@@ -146,6 +147,89 @@ def int4_linear(
                 "lnq_int4_linear", _ptr(x), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),
                 rows, depth, width, group, code, KERNELS[kernel], _stream(device),
             )
+    return y
+
+
+@dataclasses.dataclass
+class XTiles:
+    """Activations [rows, width] as x tiles (`lnq_x_tiles`): the matrix-core operand
+    order of the few-row GEMVs, chunks of 32 rows, held flat in `data`."""
+
+    data: torch.Tensor
+    rows: int
+    width: int
+
+    @staticmethod
+    def empty(rows: int, width: int, dtype: torch.dtype, device: torch.device) -> "XTiles":
+        if width % 256:
+            raise LinnetError(f"x tiles: the width {width} is not a multiple of 256")
+        return XTiles(torch.empty(-(-rows // 32) * 32 * width, dtype=dtype, device=device), rows, width)
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.data.dtype
+
+    @property
+    def device(self) -> torch.device:
+        return self.data.device
+
+    def rows_major(self) -> torch.Tensor:
+        """The [rows, width] tensor the tiles hold (a torch reordering, for tests)."""
+        chunks = self.data.numel() // (32 * self.width)
+        t = self.data.view(chunks, self.width // 256, 2, 2, 4, 4, 16, 8)  # chunk, s, b, H, t, j, c, e
+        t = t.permute(0, 2, 6, 1, 3, 4, 5, 7).reshape(chunks * 32, self.width)
+        return t[: self.rows]
+
+
+def x_tiles(x: torch.Tensor) -> XTiles:
+    """x [rows, width] (16-bit, width % 256 == 0) as x tiles."""
+    device = _on_gpu("x_tiles", x)
+    if x.dim() != 2 or x.element_size() != 2:
+        raise LinnetError("x_tiles: x is a [rows, width] tensor of a 16-bit type")
+    x = x.contiguous()
+    xt = XTiles.empty(x.shape[0], x.shape[1], x.dtype, device)
+    with torch.cuda.device(device):
+        _lib.call("lnq_x_tiles", _ptr(x), _ptr(xt.data), x.shape[0], x.shape[1], _stream(device))
+    return xt
+
+
+def int4_linear_tiles(xt: XTiles, packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor,
+                      bias: torch.Tensor | None = None, kernel: str = "auto",
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """`int4_linear` of the activations held as x tiles (`lnq_int4_linear_tiles`):
+    rows 1..64, the 32-row GEMV or, past In = 4096 and where `int4_linear` would
+    take it, the split GEMV (a workspace of torch's). The bits of the same kernel
+    on row-major x."""
+    device = _on_gpu("int4_linear_tiles", xt.data, packed, scale, zero, bias)
+    rows, depth = xt.rows, xt.width
+    width, groups, half = packed.shape
+    group = 2 * half
+    if groups * group != depth:
+        raise LinnetError(f"int4_linear_tiles: packed {tuple(packed.shape)} does not hold In={depth}")
+    code = _code(xt.dtype, "int4_linear_tiles")
+    if scale.dtype != xt.dtype or (bias is not None and bias.dtype != xt.dtype):
+        raise LinnetError("int4_linear_tiles: scale and bias have x's dtype")
+    if kernel not in ("auto", "gemv", "split"):
+        raise LinnetError("int4_linear_tiles: kernel is auto, gemv or split")
+    packed, scale, zero = packed.contiguous(), scale.contiguous(), zero.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    if out is None:
+        y = torch.empty(rows, width, dtype=xt.dtype, device=device)
+    else:
+        if tuple(out.shape) != (rows, width) or out.dtype != xt.dtype or out.device != device or not out.is_contiguous():
+            raise LinnetError(f"int4_linear_tiles: out is a contiguous [{rows}, {width}] {xt.dtype} tensor on {device}")
+        y = out
+    with torch.cuda.device(device):
+        need = 0
+        if kernel == "split" or depth > 4096:
+            _, need = _workspace(rows, depth, width, group, code, _lib.KERNEL_SPLIT)
+        elif kernel == "auto":
+            _, need = _workspace(rows, depth, width, group, code, _lib.KERNEL_AUTO)
+        ws = torch.empty(max(need, 16) // 4, dtype=torch.float32, device=device) if need else None
+        _lib.call(
+            "lnq_int4_linear_tiles", _ptr(xt.data), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),
+            rows, depth, width, group, code, KERNELS[kernel], _ptr(ws), need, _stream(device),
+        )
     return y
 
 
