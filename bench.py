@@ -386,9 +386,9 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
     decode step of the int4 Llama-3.1-8B-shaped stack at a
     1024-token context, captured as one HIP graph and replayed; tokens/s =
     batch / step time. Batch 1 runs every linear on the one-token GEMV
-    kernels; batch 32 runs q|k|v, gate|up and the head on the 32-row GEMV (the
-    head split over K), down on the split GEMV -- their inputs written as x tiles
-    by the glue -- and o on the skinny kernel; q|k|v and gate|up run as joined
+    kernels; batch 32 runs q|k|v, o, gate|up and the head on the 32-row GEMV
+    and down on the split GEMV, their inputs written as x tiles by the glue;
+    q|k|v and gate|up run as joined
     projections; between the linears, the decode kernels of `torch/decode.py` (4
     a layer). `linears_ms` replays the step's 161 int4 linear calls alone (on x
     tiles where the step's are); `torch_glue_ms` is the same step with the glue as
@@ -441,8 +441,7 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / reps
         # The same step's 161 int4 linear calls alone (inputs and outputs preallocated),
-        # on x tiles where the step's glue hands its projections tiles (17..64 rows:
-        # all but o).
+        # on x tiles where the step's glue hands its projections tiles (17..64 rows).
         calls = []
 
         def x_in(k, tiles):
@@ -453,7 +452,7 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
         for p in model.layers:
             for name, k in (("qkv", 4096), ("o", 4096), ("gate_up", 4096), ("down", 14336)):
                 yout = torch.empty(batch, p[name][0].shape[0], dtype=torch.bfloat16, device=dev)
-                calls.append((x_in(k, tiles and name != "o"), p[name], yout))
+                calls.append((x_in(k, tiles), p[name], yout))
         calls.append((x_in(4096, tiles), model.head, torch.empty(batch, 128256, dtype=torch.bfloat16, device=dev)))
         lin_graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(lin_graph):

@@ -529,6 +529,18 @@ LNQ_API LnqStatus lnq_decode_attention_at(const void* q, const void* k, const vo
                                           int64_t kv_heads, int64_t head_dim, int64_t cap, const int32_t* pos,
                                           int64_t q_stride, int64_t kv_stride, void* stream);
 
+/* lnq_decode_attention (pos_dev NULL: position pos, cos / sin at it) or
+ * lnq_decode_attention_at (pos_dev the device position, cos / sin the tables over
+ * the cache, pos ignored), the output written as x tiles (lnq_x_tiles; heads *
+ * head_dim % 256 == 0, out_tiles 16-byte aligned): the same bits, for the o
+ * projection's lnq_int4_linear_tiles. */
+LNQ_API LnqStatus lnq_decode_attention_tiles(const void* q, const void* k, const void* v, const float* cos,
+                                             const float* sin, void* kt_cache, void* v_cache, void* out_tiles,
+                                             float* workspace, int64_t workspace_floats, int64_t rows, int64_t heads,
+                                             int64_t kv_heads, int64_t head_dim, int64_t cap, int64_t pos,
+                                             const int32_t* pos_dev, int64_t q_stride, int64_t kv_stride,
+                                             void* stream);
+
 /* Floats of lnq_decode_attention's workspace: rows * kv_heads * ceil((pos + 1) / 64)
  * * 8 * (head_dim + 2). */
 LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim,

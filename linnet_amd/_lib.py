@@ -67,6 +67,8 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_rmsnorm_tiles": [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p],
     "lnq_decode_attention": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "lnq_decode_attention_at": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p],
+    "lnq_decode_attention_tiles": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,
+                                   _i64, _i64, _p],
     "lnq_decode_attention_noalloc": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "lnq_prefill_rope": [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "lnq_silu_mul": [_p, _p, _p, _i64, _p],

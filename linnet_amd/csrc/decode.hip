@@ -410,11 +410,12 @@ __global__ __launch_bounds__(decode::THREADS) void decode_attention_kernel(
   }
 }
 
-// out[row, head] = sum_c acc_c exp(m_c - M) / sum_c s_c exp(m_c - M), chunks in order.
+// out[row, head] = sum_c acc_c exp(m_c - M) / sum_c s_c exp(m_c - M), chunks in order;
+// with `tiles`, out is written as x tiles of the [rows, heads * HD] output.
 template <int HD>
 __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restrict__ work, uint16_t* __restrict__ out,
                                                             int heads, int kv_heads, int chunks,
-                                                            const int32_t* __restrict__ pos_dev, int cap) {
+                                                            const int32_t* __restrict__ pos_dev, int cap, bool tiles) {
   // One round trip to memory: every load is issued as the kernel starts -- the
   // chunks' (m, s) (thread t: chunks t, t + HD, ...) and thread d's dimension
   // of the first PRE chunks' sums -- then the max and the sum of the weights
@@ -428,6 +429,8 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
   const int row = blockIdx.x / heads, head = blockIdx.x % heads;
   const int kvh = head / G, g = head % G;
   const int d = threadIdx.x;
+  const size_t o_at = tiles ? x_tile_index(row, head * HD + d, heads * HD)
+                            : (static_cast<size_t>(row) * heads + head) * HD + d;
   const float* base = work + (static_cast<size_t>(row) * kv_heads + kvh) * chunks * decode::MAX_GROUP * (HD + 2) +
                       g * (HD + 2);
   const size_t stride = static_cast<size_t>(decode::MAX_GROUP) * (HD + 2);
@@ -438,7 +441,7 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
     const int p = *pos_dev;
     live = p >= 0 && p < cap ? p / decode::CHUNK + 1 : 0;
     if (live == 0) {
-      out[(static_cast<size_t>(row) * heads + head) * HD + d] = 0;
+      out[o_at] = 0;
       return;
     }
   }
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(const float* __restr
   for (int i = 0; i < PRE; ++i)
     if (i < live) o = fmaf(a_pre[i], wts[i], o);
   for (int c = PRE; c < live; ++c) o = fmaf(base[c * stride + 2 + d], wts[c], o);
-  out[(static_cast<size_t>(row) * heads + head) * HD + d] = f32_to_bf16_bits(o / S);
+  out[o_at] = f32_to_bf16_bits(o / S);
 }
 
 // A prompt's rotary embedding and cache writes, one kernel for what the torch
@@ -633,7 +636,7 @@ static LnqStatus decode_attention(const void* q, const void* k, const void* v, c
                                   void* kt_cache, void* v_cache, void* out, float* workspace,
                                   int64_t workspace_floats, int64_t rows, int64_t heads, int64_t kv_heads,
                                   int64_t head_dim, int64_t cap, int64_t pos, int64_t q_stride, int64_t kv_stride,
-                                  const int32_t* pos_dev, void* stream) {
+                                  const int32_t* pos_dev, void* stream, bool tiles = false) {
   LNQ_REQUIRE(head_dim == 64 || head_dim == 128, "lnq_decode_attention: head_dim is 64 or 128, not %lld",
               static_cast<long long>(head_dim));
   LNQ_REQUIRE(rows >= 0 && kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= decode::MAX_GROUP,
@@ -666,7 +669,7 @@ static LnqStatus decode_attention(const void* q, const void* k, const void* v, c
                      static_cast<int>(chunks), qs_, kvs_, pos_dev);                                                 \
   hipLaunchKernelGGL(decode_combine_kernel<HD_>, grid2, dim3(HD_), 0, s, workspace, static_cast<uint16_t*>(out),   \
                      static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(chunks), pos_dev,         \
-                     static_cast<int>(cap))
+                     static_cast<int>(cap), tiles)
 #define LNQ_ATT(HD_)                                      \
   switch (group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8) { \
     case 1: LNQ_ATT_G(HD_, 1); break;                     \
@@ -682,6 +685,8 @@ static LnqStatus decode_attention(const void* q, const void* k, const void* v, c
   LNQ_REQUIRE(rows == 1 || (q_stride >= heads * head_dim && kv_stride >= kv_heads * head_dim),
               "lnq_decode_attention: row strides %lld / %lld shorter than a row", static_cast<long long>(q_stride),
               static_cast<long long>(kv_stride));
+  LNQ_REQUIRE(!tiles || ((heads * head_dim) % 256 == 0 && aligned(out, 16)),
+              "lnq_decode_attention_tiles: x tiles take heads * head_dim %% 256 == 0 and a 16-byte aligned output");
   const int64_t qs_ = rows == 1 ? heads * head_dim : q_stride;
   const int64_t kvs_ = rows == 1 ? kv_heads * head_dim : kv_stride;
   if (head_dim == 64) {
@@ -712,6 +717,20 @@ LNQ_API LnqStatus lnq_decode_attention_at(const void* q, const void* k, const vo
   LNQ_REQUIRE(cap > 0, "lnq_decode_attention_at: empty cache");
   return decode_attention(q, k, v, cos_table, sin_table, kt_cache, v_cache, out, workspace, workspace_floats, rows,
                           heads, kv_heads, head_dim, cap, cap - 1, q_stride, kv_stride, pos, stream);
+}
+
+LNQ_API LnqStatus lnq_decode_attention_tiles(const void* q, const void* k, const void* v, const float* cos,
+                                             const float* sin, void* kt_cache, void* v_cache, void* out_tiles,
+                                             float* workspace, int64_t workspace_floats, int64_t rows, int64_t heads,
+                                             int64_t kv_heads, int64_t head_dim, int64_t cap, int64_t pos,
+                                             const int32_t* pos_dev, int64_t q_stride, int64_t kv_stride,
+                                             void* stream) {
+  if (pos_dev != nullptr) {
+    LNQ_REQUIRE(cap > 0, "lnq_decode_attention_tiles: empty cache");
+    pos = cap - 1;
+  }
+  return decode_attention(q, k, v, cos, sin, kt_cache, v_cache, out_tiles, workspace, workspace_floats, rows, heads,
+                          kv_heads, head_dim, cap, pos, q_stride, kv_stride, pos_dev, stream, true);
 }
 
 LNQ_API int64_t lnq_decode_attention_workspace(int64_t rows, int64_t kv_heads, int64_t head_dim, int64_t pos) {

@@ -164,9 +164,10 @@ class Int4Llama:
         h = decode.rmsnorm(x, p["n1"], 1e-5, delta, tiles=tiles)
         q, k, v = generated._int4_split(self.linear(h, p["qkv"]), p["qkv_rows"])
         if device_pos:
-            att = decode.decode_attention(q, k, v, self.cos_tab, self.sin_tab, self.kt[i], self.vc[i], self.pos_t)
+            att = decode.decode_attention(q, k, v, self.cos_tab, self.sin_tab, self.kt[i], self.vc[i], self.pos_t,
+                                          tiles=tiles)
         else:
-            att = decode.decode_attention(q, k, v, self.cos, self.sin, self.kt[i], self.vc[i], self.pos)
+            att = decode.decode_attention(q, k, v, self.cos, self.sin, self.kt[i], self.vc[i], self.pos, tiles=tiles)
         o = self.linear(att, p["o"])
         if parts is not None:
             parts["attn"] = o

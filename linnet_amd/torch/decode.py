@@ -94,7 +94,8 @@ def rope_tables(head_dim: int, positions: int, theta: float = 500000.0,
 
 
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                     kt_cache: torch.Tensor, v_cache: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
+                     kt_cache: torch.Tensor, v_cache: torch.Tensor, pos: int | torch.Tensor,
+                     tiles: bool = False) -> torch.Tensor | XTiles:
     """One decode step of grouped-query attention for q [rows, heads*hd], k, v
     [rows, kv_heads*hd] (bf16): rotary embedding (cos, sin f32 [hd/2] at `pos`) of
     q and k, k and v written (rounded) into the bf16 caches at `pos` (K transposed:
@@ -103,7 +104,8 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
 
     `pos` may be a one-element int32 tensor on the device instead: the kernels then
     read it there (a graph replaying the step follows the position as the device
-    advances it), and cos / sin are the whole tables [cap, hd/2] of `rope_tables`."""
+    advances it), and cos / sin are the whole tables [cap, hd/2] of `rope_tables`.
+    `tiles`: the output as x tiles (heads*hd % 256 == 0), the same bits."""
     device = _on_gpu("decode_attention", q, k, v, cos, sin, kt_cache, v_cache)
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise LinnetError("decode_attention: q, k and v are bf16")
@@ -127,9 +129,16 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
         if tuple(cos.shape) != (cap, hd // 2) or tuple(sin.shape) != (cap, hd // 2) or cos.dtype != torch.float32 \
                 or sin.dtype != torch.float32:
             raise LinnetError(f"decode_attention: with a device position cos and sin are f32 [{cap}, {hd // 2}]")
-        out = torch.empty_like(q)
         floats = _lib.load().lnq_decode_attention_workspace(rows, kvh, hd, cap - 1)
         work = torch.empty(max(floats, 1), dtype=torch.float32, device=device)
+        if tiles:
+            xt = XTiles.empty(rows, heads * hd, q.dtype, device)
+            with torch.cuda.device(device):
+                _lib.call("lnq_decode_attention_tiles", _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin),
+                          _ptr(kt_cache), _ptr(v_cache), _ptr(xt.data), _ptr(work), work.numel(), rows, heads, kvh,
+                          hd, cap, 0, _ptr(pos), q.stride(0), k.stride(0), _stream(device))
+            return xt
+        out = torch.empty_like(q)
         with torch.cuda.device(device):
             _lib.call("lnq_decode_attention_at", _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(kt_cache),
                       _ptr(v_cache), _ptr(out), _ptr(work), work.numel(), rows, heads, kvh, hd, cap, _ptr(pos),
@@ -137,9 +146,16 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: tor
         return out
     if cos.numel() != hd // 2 or sin.numel() != hd // 2 or cos.dtype != torch.float32 or sin.dtype != torch.float32:
         raise LinnetError("decode_attention: cos and sin are f32 [hd/2]")
-    out = torch.empty_like(q)
     floats = _lib.load().lnq_decode_attention_workspace(rows, kvh, hd, pos)
     work = torch.empty(max(floats, 1), dtype=torch.float32, device=device)
+    if tiles:
+        xt = XTiles.empty(rows, heads * hd, q.dtype, device)
+        with torch.cuda.device(device):
+            _lib.call("lnq_decode_attention_tiles", _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(kt_cache),
+                      _ptr(v_cache), _ptr(xt.data), _ptr(work), work.numel(), rows, heads, kvh, hd, cap, pos, None,
+                      q.stride(0), k.stride(0), _stream(device))
+        return xt
+    out = torch.empty_like(q)
     with torch.cuda.device(device):
         _lib.call("lnq_decode_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), _ptr(kt_cache),
                   _ptr(v_cache), _ptr(out), _ptr(work), work.numel(), rows, heads, kvh, hd, cap, pos, q.stride(0),

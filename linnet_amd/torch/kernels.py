@@ -197,9 +197,9 @@ def int4_linear_tiles(xt: XTiles, packed: torch.Tensor, scale: torch.Tensor, zer
                       bias: torch.Tensor | None = None, kernel: str = "auto",
                       out: torch.Tensor | None = None) -> torch.Tensor:
     """`int4_linear` of the activations held as x tiles (`lnq_int4_linear_tiles`):
-    rows 1..64, the 32-row GEMV or, past In = 4096 and where `int4_linear` would
-    take it, the split GEMV (a workspace of torch's). The bits of the same kernel
-    on row-major x."""
+    rows 1..64, the 32-row GEMV up to In = 4096, the split GEMV past it (a
+    workspace of torch's) or when asked for. The bits of the same kernel on
+    row-major x."""
     device = _on_gpu("int4_linear_tiles", xt.data, packed, scale, zero, bias)
     rows, depth = xt.rows, xt.width
     width, groups, half = packed.shape
@@ -223,8 +223,6 @@ def int4_linear_tiles(xt: XTiles, packed: torch.Tensor, scale: torch.Tensor, zer
         need = 0
         if kernel == "split" or depth > 4096:
             _, need = _workspace(rows, depth, width, group, code, _lib.KERNEL_SPLIT)
-        elif kernel == "auto":
-            _, need = _workspace(rows, depth, width, group, code, _lib.KERNEL_AUTO)
         ws = torch.empty(max(need, 16) // 4, dtype=torch.float32, device=device) if need else None
         _lib.call(
             "lnq_int4_linear_tiles", _ptr(xt.data), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(bias), _ptr(y),

@@ -36,7 +36,7 @@ def test_int4_decode_step_matches_the_dequantized_reference(batch: int, fused: b
     x = (torch.randn(batch, SMALL["hidden"], generator=torch.Generator().manual_seed(7)) * 0.5).to(torch.bfloat16).to(DEV)
     calls = []
     attention = decode.decode_attention
-    decode.decode_attention = lambda *a: calls.append(1) or attention(*a)
+    decode.decode_attention = lambda *a, **kw: calls.append(1) or attention(*a, **kw)
     try:
         got = model.step(x).float()
     finally:

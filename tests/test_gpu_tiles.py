@@ -59,7 +59,7 @@ def test_products_on_tiles_are_the_row_major_bits(rows, width, out, kernel, dtyp
     assert torch.equal(got, want)
     auto = kernels.int4_linear_tiles(kernels.x_tiles(x), packed, scale, zero, bias)
     assert torch.equal(auto, torch.cat([kernels.int4_linear(x[c:c + 32], packed, scale, zero, bias,
-                                                            kernel="split" if width > 4096 or out >= 65536 else "gemv")
+                                                            kernel="split" if width > 4096 else "gemv")
                                         for c in range(0, rows, 32)]))
 
 
@@ -91,6 +91,25 @@ def test_glue_writes_the_tiles_of_its_row_major_output() -> None:
     assert torch.equal(decode.silu_mul(g, u, tiles=True).rows_major(), decode.silu_mul(g, u))
 
 
+@pytest.mark.parametrize("device_pos", [False, True])
+def test_decode_attention_writes_the_tiles_of_its_output(device_pos: bool) -> None:
+    rows, heads, kvh, hd, cap, pos = 32, 32, 8, 128, 260, 200
+    g = torch.Generator(device=DEV).manual_seed(7)
+    qkv = torch.randn(rows, (heads + 2 * kvh) * hd, generator=g, device=DEV).to(torch.bfloat16)
+    q, k, v = qkv[:, :heads * hd], qkv[:, heads * hd:(heads + kvh) * hd], qkv[:, (heads + kvh) * hd:]
+    kt = torch.randn(rows, kvh, hd, cap, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(rows, kvh, cap, hd, generator=g, device=DEV).to(torch.bfloat16)
+    if device_pos:
+        cos, sin = decode.rope_tables(hd, cap, 500000.0, DEV)
+        p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    else:
+        inv = 1.0 / (500000.0 ** (torch.arange(0, hd, 2, device=DEV, dtype=torch.float32) / hd))
+        cos, sin, p = torch.cos(pos * inv), torch.sin(pos * inv), pos
+    want = decode.decode_attention(q, k, v, cos, sin, kt.clone(), vc.clone(), p)
+    got = decode.decode_attention(q, k, v, cos, sin, kt.clone(), vc.clone(), p, tiles=True)
+    assert torch.equal(got.rows_major(), want)
+
+
 def test_batch32_step_on_tiles_gives_the_row_major_logits() -> None:
     """A two-layer config-5-shaped model at 32 rows: the step with the glue writing
     x tiles against the same step on row-major x (every projection the same
@@ -103,9 +122,7 @@ def test_batch32_step_on_tiles_gives_the_row_major_logits() -> None:
     # Row-major x through the kernels the tiles path takes (the automatic choice on
     # row-major x picks the skinny kernel for some of these shapes).
     def row_major(h, w):
-        if h.shape[1] == 4096 and w[0].shape[0] == 4096:  # o: row-major on both paths
-            return kernels.int4_linear(h, *w)
-        kernel = "split" if h.shape[1] > 4096 or w[0].shape[0] >= 65536 else "gemv"
+        kernel = "split" if h.shape[1] > 4096 else "gemv"
         return torch.cat([kernels.int4_linear(h[c:c + 32], *w, kernel=kernel) for c in range(0, h.shape[0], 32)])
 
     model.linear = row_major
