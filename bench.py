@@ -387,12 +387,14 @@ def llama_decode(torch, kernels, dev) -> dict[str, object]:
     1024-token context, captured as one HIP graph and replayed; tokens/s =
     batch / step time. Batch 1 runs every linear on the one-token GEMV
     kernels; batch 32 runs q|k|v, o, gate|up and the head on the 32-row GEMV
-    and down on the split GEMV, their inputs written as x tiles by the glue;
-    q|k|v and gate|up run as joined
-    projections; between the linears, the decode kernels of `torch/decode.py` (4
-    a layer). `linears_ms` replays the step's 161 int4 linear calls alone (on x
-    tiles where the step's are); `torch_glue_ms` is the same step with the glue as
-    torch ops (~40 small kernels a layer) and the projections apart."""
+    and down on the split GEMV, their inputs written as x tiles by the glue, and
+    down's K-chunk partial sums added by the next layer's RMSNorm (which reads
+    them as its residual delta) instead of a reduction kernel of their own; q|k|v
+    and gate|up run as joined projections; between the linears, the decode
+    kernels of `torch/decode.py` (4 a layer). `linears_ms` replays the step's 161
+    int4 linear calls alone as the step makes them (x tiles, down's partial sums);
+    `torch_glue_ms` is the same step with the glue as torch ops (~40 small kernels
+    a layer) and the projections apart."""
     out: dict[str, object] = {"layers": 32, "hidden": 4096, "heads": "32/8", "ffn": 14336, "vocab": 128256,
                               "context": 1024, "weights": "int4 g128, bf16 scales, u8 zeros; random-init"}
     from linnet_amd.llama import Int4Llama

@@ -195,6 +195,16 @@ LNQ_API LnqStatus lnq_int4_linear_tiles(const void* xt, const uint8_t* packed, c
                                         int32_t dtype, int32_t kernel, void* workspace,
                                         int64_t workspace_bytes, void* stream);
 
+/* The split GEMV of lnq_int4_linear_tiles (1..32 rows, in > 4096) without its
+ * last step: the K chunks' f32 partial sums are left in parts [*splits, rows, out]
+ * (16-byte aligned, lnq_int4_linear_workspace's bytes) for a consumer that adds
+ * them in chunk order and rounds once, giving the bits of lnq_int4_linear_tiles
+ * with no bias (lnq_rmsnorm_parts takes them as its residual delta). */
+LNQ_API LnqStatus lnq_int4_linear_tiles_parts(const void* xt, const uint8_t* packed, const void* scale,
+                                              const uint8_t* zero, float* parts, int64_t parts_bytes, int64_t rows,
+                                              int64_t in_features, int64_t out_features, int64_t group,
+                                              int32_t dtype, int32_t* splits, void* stream);
+
 /* out[out, in] = (q - zero) * scale computed in f32 and rounded once to `dtype`
  * (the scale's dtype: bf16, f16 or f32). Any even group dividing `in`.
  * Replaces: `_int4_unpack`/`_int4_weight` (torch_source.cpp:1518-1550) and the
@@ -493,6 +503,13 @@ LNQ_API LnqStatus lnq_rmsnorm(void* x, const void* delta, const float* weight, v
  * 16384, operands 16-byte aligned): the same bits, for lnq_int4_linear_tiles. */
 LNQ_API LnqStatus lnq_rmsnorm_tiles(void* x, const void* delta, const float* weight, void* xt, int64_t rows,
                                     int64_t hidden, float eps, void* stream);
+
+/* lnq_rmsnorm (h_tiles 0) or lnq_rmsnorm_tiles (1) whose delta is the sum of `splits`
+ * f32 partial sums parts [splits, rows, hidden] added in order and rounded once to
+ * bf16 -- the output lnq_int4_linear_tiles_parts leaves in parts -- read in place
+ * of a bf16 delta (hidden % 256 == 0 and <= 16384; operands 16-byte aligned). */
+LNQ_API LnqStatus lnq_rmsnorm_parts(void* x, const float* parts, int32_t splits, const float* weight, void* h,
+                                    int32_t h_tiles, int64_t rows, int64_t hidden, float eps, void* stream);
 
 /* One decode step of grouped-query attention: q [rows, heads*head_dim], k and v
  * [rows, kv_heads*head_dim] (bf16); rotary embedding of q and k with cos/sin f32

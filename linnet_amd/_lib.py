@@ -40,6 +40,7 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_int4_linear_workspace": [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
     "lnq_x_tiles": [_p, _p, _i64, _i64, _p],
     "lnq_int4_linear_tiles": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p],
+    "lnq_int4_linear_tiles_parts": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_i32), _p],
     "lnq_int4_linear_executable": [_i64, _i64, _i64, _i32, _p],
     "lnq_int4_dequantize": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "lnq_int4_quantize": [_p, _p, _p, _p, _i64, _i64, _i64, _p],
@@ -65,6 +66,7 @@ SIGNATURES: dict[str, list[object]] = {
     "lnq_nf4_repack": [_p, _p, _p, _p, _i64, _f32, _p, _p, _i64, _i64, _i64, _p],
     "lnq_rmsnorm": [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p],
     "lnq_rmsnorm_tiles": [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p],
+    "lnq_rmsnorm_parts": [_p, _p, _i32, _p, _p, _i32, _i64, _i64, ctypes.c_float, _p],
     "lnq_decode_attention": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "lnq_decode_attention_at": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p],
     "lnq_decode_attention_tiles": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,

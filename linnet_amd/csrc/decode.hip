@@ -111,15 +111,23 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_kernel(uint16_t* __re
 // delta and the weight issued before any is used (the scalar loop above waits on
 // each of its 16 loads a thread in turn: 14 us for one 4096-wide row).
 // TILES: h is written as x tiles (x_tile_index) for the 32-row GEMVs.
+// parts (else nullptr): the delta is the sum of `splits` f32 partial sums
+// parts[s][row][k] added in order and rounded once to bf16 -- what the split
+// GEMV's reduction writes as its output with no bias -- read in place of delta.
 template <int CH, bool TILES = false>
 __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* __restrict__ x,
                                                                       const uint16_t* __restrict__ delta,
                                                                       const float* __restrict__ w,
-                                                                      uint16_t* __restrict__ h, int hidden, float eps) {
+                                                                      uint16_t* __restrict__ h, int hidden, float eps,
+                                                                      const float* __restrict__ parts = nullptr,
+                                                                      int splits = 0) {
   __shared__ float group_ss[CH * decode::THREADS / 32];
   uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * hidden;
   uint16_t* hr = h + static_cast<size_t>(blockIdx.x) * hidden;
   const uint16_t* dr = delta ? delta + static_cast<size_t>(blockIdx.x) * hidden : nullptr;
+  const bool has_delta = dr != nullptr || parts != nullptr;
+  const size_t part_stride = static_cast<size_t>(gridDim.x) * hidden;  // one chunk's [rows, hidden]
+  const float* pr = parts ? parts + static_cast<size_t>(blockIdx.x) * hidden : nullptr;
   const int chunks = hidden >> 3;
   u32x4 xv[CH], dv[CH];
   f32x4 wv[CH][2];
@@ -131,6 +139,21 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
       dv[c] = dr ? *reinterpret_cast<const u32x4*>(dr + 8 * i) : u32x4{0u, 0u, 0u, 0u};
       wv[c][0] = *reinterpret_cast<const f32x4*>(w + 8 * i);
       wv[c][1] = *reinterpret_cast<const f32x4*>(w + 8 * i + 4);
+    }
+  }
+  if (pr != nullptr) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int i = threadIdx.x + c * decode::THREADS;
+      if (i >= chunks) continue;
+      f32x4 a = *reinterpret_cast<const f32x4*>(pr + 8 * i), b = *reinterpret_cast<const f32x4*>(pr + 8 * i + 4);
+      for (int sp = 1; sp < splits; ++sp) {
+        const float* q = pr + sp * part_stride + 8 * i;
+        const f32x4 qa = *reinterpret_cast<const f32x4*>(q), qb = *reinterpret_cast<const f32x4*>(q + 4);
+        a = f32x4{a[0] + qa[0], a[1] + qa[1], a[2] + qa[2], a[3] + qa[3]};
+        b = f32x4{b[0] + qb[0], b[1] + qb[1], b[2] + qb[2], b[3] + qb[3]};
+      }
+      dv[c] = u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])};
     }
   }
   float v[CH][8];
@@ -145,7 +168,7 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
     for (int e = 0; e < 4; ++e) {
       float lo = bf16_bits_to_f32(static_cast<uint16_t>(xv[c][e] & 0xffffu));
       float hi = bf16_bits_to_f32(static_cast<uint16_t>(xv[c][e] >> 16));
-      if (dr) {
+      if (has_delta) {
         lo = bf16_bits_to_f32(f32_to_bf16_bits(lo + bf16_bits_to_f32(static_cast<uint16_t>(dv[c][e] & 0xffffu))));
         hi = bf16_bits_to_f32(f32_to_bf16_bits(hi + bf16_bits_to_f32(static_cast<uint16_t>(dv[c][e] >> 16))));
       }
@@ -153,7 +176,7 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
       v[c][2 * e + 1] = hi;
       out[e] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
     }
-    if (dr) *reinterpret_cast<u32x4*>(xr + 8 * i) = out;
+    if (has_delta) *reinterpret_cast<u32x4*>(xr + 8 * i) = out;
     ss[c] = chunk_squares(v[c]);
   }
   // The sum of squares in the order the one-token GEMV's norm prologue uses (so
@@ -628,6 +651,38 @@ LNQ_API LnqStatus lnq_rmsnorm_tiles(void* x, const void* delta, const float* wei
   else if (ch <= 4) hipLaunchKernelGGL((rmsnorm_vec_kernel<4, true>), grid, block, 0, s, xs, ds, weight, hs, H, eps);
   else hipLaunchKernelGGL((rmsnorm_vec_kernel<8, true>), grid, block, 0, s, xs, ds, weight, hs, H, eps);
   return launched("rmsnorm_tiles");
+}
+
+LNQ_API LnqStatus lnq_rmsnorm_parts(void* x, const float* parts, int32_t splits, const float* weight, void* h,
+                                    int32_t h_tiles, int64_t rows, int64_t hidden, float eps, void* stream) {
+  LNQ_REQUIRE(rows >= 0 && rows <= INT32_MAX && hidden > 0 && hidden % 256 == 0 && hidden <= 64 * decode::THREADS &&
+                  splits >= 1,
+              "lnq_rmsnorm_parts: bad shape rows=%lld hidden=%lld splits=%d (hidden %% 256 == 0, <= %d)",
+              (long long)rows, (long long)hidden, splits, 64 * decode::THREADS);
+  if (rows == 0) {
+    clear_error();
+    return LNQ_OK;
+  }
+  LNQ_REQUIRE(x && parts && weight && h, "lnq_rmsnorm_parts: null pointer");
+  LNQ_REQUIRE(aligned(x, 16) && aligned(h, 16) && aligned(weight, 16) && aligned(parts, 16),
+              "lnq_rmsnorm_parts: operands must be 16-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto* xs = static_cast<uint16_t*>(x);
+  auto* hs = static_cast<uint16_t*>(h);
+  const int H = static_cast<int>(hidden);
+  const int ch = (H + 8 * decode::THREADS - 1) / (8 * decode::THREADS);
+  const dim3 grid(static_cast<unsigned>(rows)), block(decode::THREADS);
+#define LNQ_RMS_PARTS(C_)                                                                                             \
+  if (h_tiles) hipLaunchKernelGGL((rmsnorm_vec_kernel<C_, true>), grid, block, 0, s, xs, nullptr, weight, hs, H, eps,  \
+                                  parts, splits);                                                                      \
+  else hipLaunchKernelGGL((rmsnorm_vec_kernel<C_, false>), grid, block, 0, s, xs, nullptr, weight, hs, H, eps, parts,  \
+                          splits)
+  if (ch == 1) { LNQ_RMS_PARTS(1); }
+  else if (ch == 2) { LNQ_RMS_PARTS(2); }
+  else if (ch <= 4) { LNQ_RMS_PARTS(4); }
+  else { LNQ_RMS_PARTS(8); }
+#undef LNQ_RMS_PARTS
+  return launched("rmsnorm_parts");
 }
 
 // pos_dev: nullptr (the position is `pos`) or the device address of the int32

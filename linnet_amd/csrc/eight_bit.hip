@@ -699,14 +699,6 @@ LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t r
   return launched("rows8");
 }
 
-static int compute_units_of_device() {
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-  }
-  return cus;
-}
 
 // The kernel of an 8-bit product: 256-column tiles read half the bytes per
 // FLOP of 128-column ones, but only pay while they still give every compute
@@ -715,7 +707,7 @@ static int compute_units_of_device() {
 // on the tiles: 2231 against 2177).
 static int mm8_kernel_for(int M, int N, int K, bool fp8) {
   const long tiles256 = static_cast<long>((M + mm8::BM - 1) / mm8::BM) * ((N + 255) / 256);
-  if (tiles256 < compute_units_of_device()) return 128;
+  if (tiles256 < compute_units()) return 128;
   return fp8 && N % 256 == 0 && K % 256 == 0 ? LNQ_MM8_PERSISTENT : 256;
 }
 
@@ -748,7 +740,7 @@ LNQ_API LnqStatus lnq_mm8_tiles(const uint8_t* qx, const uint8_t* weight, const 
   const int bn = tile_n == 0 ? mm8_kernel_for(M, N, K, fp8 != 0) : tile_n;
   if (bn == LNQ_MM8_PERSISTENT) {
     const int tiles = ((M + mm8p::BM - 1) / mm8p::BM) * (N / mm8p::BN);
-    const dim3 grid(tiles < compute_units_of_device() ? tiles : compute_units_of_device());
+    const dim3 grid(tiles < compute_units() ? tiles : compute_units());
 #define LNQ_MM8P(DT, F) \
   hipLaunchKernelGGL((mm8p_kernel<DT, F>), grid, dim3(mm8p::THREADS), 0, s, qx, weight, x_scale, scale, ys, M, N, K)
     if (dtype == LNQ_BF16) { if (fp8) { LNQ_MM8P(LNQ_BF16, 1); } else { LNQ_MM8P(LNQ_BF16, 0); } }

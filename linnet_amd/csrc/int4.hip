@@ -639,7 +639,7 @@ bool int4_gemv_split_supports(int M, int N, int K, int G, int u8, int S, const v
                               const void* scale, const void* zero, const void* part);
 LnqStatus launch_int4_gemv_split(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                                  const void* bias, void* y, int M, int N, int K, int G, int dtype, int u8, int S,
-                                 float* part, hipStream_t stream, bool tiles = false);
+                                 float* part, hipStream_t stream, bool tiles = false, bool reduce = true);
 LnqStatus launch_int4_gemv_tiles(const void* xt, const uint8_t* packed, const void* scale, const uint8_t* zero,
                                  const void* bias, void* y, int M, int N, int K, int G, int dtype, hipStream_t stream);
 LnqStatus launch_x_tiles(const void* x, void* xt, int rows, int K, hipStream_t stream);
@@ -976,6 +976,32 @@ LNQ_API LnqStatus lnq_int4_linear_tiles(const void* xt, const uint8_t* packed, c
     }
   }
   return LNQ_OK;
+}
+
+LNQ_API LnqStatus lnq_int4_linear_tiles_parts(const void* xt, const uint8_t* packed, const void* scale,
+                                              const uint8_t* zero, float* parts, int64_t parts_bytes, int64_t rows,
+                                              int64_t in_features, int64_t out_features, int64_t group,
+                                              int32_t dtype, int32_t* splits, void* stream) {
+  if (!check_int4_linear(rows, in_features, out_features, group, dtype, LNQ_KERNEL_AUTO,
+                         "lnq_int4_linear_tiles_parts"))
+    return LNQ_ERROR;
+  LNQ_REQUIRE(splits != nullptr, "lnq_int4_linear_tiles_parts: null pointer");
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features);
+  const int K = static_cast<int>(in_features), G = static_cast<int>(group);
+  int u8 = 0, S = 0;
+  LNQ_REQUIRE(K > 4096 && split_shape(K, u8, S) && rows >= 1 && rows <= 32,
+              "lnq_int4_linear_tiles_parts: the split GEMV's parts take 1..32 rows and in > 4096 split into chunks "
+              "of 8..16 slices, got rows=%lld in=%lld", (long long)rows, (long long)in_features);
+  const int64_t need = split_workspace_bytes(M, N, S);
+  LNQ_REQUIRE(xt && packed && scale && zero && parts, "lnq_int4_linear_tiles_parts: null pointer");
+  LNQ_REQUIRE(aligned(parts, 16) && parts_bytes >= need,
+              "lnq_int4_linear_tiles_parts: the parts take %lld bytes, 16-byte aligned (got %lld)", (long long)need,
+              (long long)parts_bytes);
+  LNQ_REQUIRE(int4_gemv_split_supports(M, N, K, G, u8, S, xt, packed, scale, zero, parts),
+              "lnq_int4_linear_tiles_parts: the split GEMV does not take rows=%d in=%d out=%d group=%d", M, K, N, G);
+  *splits = S;
+  return launch_int4_gemv_split(xt, packed, scale, zero, nullptr, nullptr, M, N, K, G, dtype, u8, S, parts,
+                                static_cast<hipStream_t>(stream), true, false);
 }
 
 LNQ_API LnqStatus lnq_int4_dequantize(const uint8_t* packed, const void* scale,

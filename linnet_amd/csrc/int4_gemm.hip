@@ -1033,18 +1033,6 @@ bool int4_tiled_supports(int M, int N, int K, int G, int dtype) {
          static_cast<size_t>(N) * (K >> 1) < (1ull << 31);
 }
 
-// Compute units of the current device, cached per device.
-static int compute_units() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
 
 
 template <int DT>

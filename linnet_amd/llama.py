@@ -151,7 +151,7 @@ class Int4Llama:
     def head_torch(self, x, linear=None):
         return (linear or self.linear)(self._rms(x, self.norm), self.head)
 
-    def layer_fused(self, i, x, delta, parts=None, device_pos=False):
+    def layer_fused(self, i, x, delta, parts=None, device_pos=False, partial=False):
         """Layer i on the decode kernels and the joined int4 projections. `x` is the
         residual stream, updated in place; `delta` the previous layer's MLP output,
         not yet added (the norm adds it). Returns this layer's MLP output; `parts`,
@@ -173,7 +173,12 @@ class Int4Llama:
             parts["attn"] = o
         h = decode.rmsnorm(x, p["n2"], 1e-5, o, tiles=tiles)
         g, u = generated._int4_split(self.linear(h, p["gate_up"]), p["gate_up_rows"])
-        return self.linear(decode.silu_mul(g, u, tiles=tiles), p["down"])
+        a = decode.silu_mul(g, u, tiles=tiles)
+        if partial and tiles and x.shape[0] <= 32 and a.width > 4096:
+            # The split product's K-chunk sums, added by the next norm (`partial`:
+            # the caller hands the result on as that norm's delta).
+            return self.kernels.int4_linear_tiles_parts(a, *p["down"])
+        return self.linear(a, p["down"])
 
     def _tiles(self, x):
         """Whether the glue hands the projections x tiles: 17..64 rows, where the
@@ -292,7 +297,7 @@ class Int4Llama:
             x = x.clone()
             delta = None
             for i in range(len(self.layers)):
-                delta = self.layer_fused(i, x, delta, device_pos=True)
+                delta = self.layer_fused(i, x, delta, device_pos=True, partial=True)
             logits = self.head_fused(x, delta)
         self.pos_t.add_(1)
         if not capturing:
@@ -308,7 +313,7 @@ class Int4Llama:
             x = x.clone()  # the residual stream is updated in place
             delta = None
             for i in range(len(self.layers)):
-                delta = self.layer_fused(i, x, delta)
+                delta = self.layer_fused(i, x, delta, partial=True)
             return self.head_fused(x, delta)
         for i in range(len(self.layers)):
             x = self.layer_torch(i, x)

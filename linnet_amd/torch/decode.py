@@ -11,7 +11,7 @@ import torch
 
 from .. import _lib
 from ..errors import LinnetError
-from .kernels import XTiles, _on_gpu, _ptr, _stream
+from .kernels import SplitParts, XTiles, _on_gpu, _ptr, _stream
 
 
 def _bf16(what: str, *tensors: torch.Tensor) -> None:
@@ -20,13 +20,18 @@ def _bf16(what: str, *tensors: torch.Tensor) -> None:
             raise LinnetError(f"{what}: takes contiguous bf16 tensors, got {t.dtype}")
 
 
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: torch.Tensor | None = None,
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: torch.Tensor | SplitParts | None = None,
             tiles: bool = False) -> torch.Tensor | XTiles:
     """`h = x * rsqrt(mean(x^2) + eps) * weight` per row of x [rows, hidden]; with
     `delta`, first `x += delta` in place (rounded to bf16), as the residual add
     before a norm. weight: f32 [hidden]. `tiles`: h is returned as x tiles (for
-    `int4_linear_tiles`; hidden % 256 == 0), the same bits."""
-    device = _on_gpu("rmsnorm", x, weight, delta)
+    `int4_linear_tiles`; hidden % 256 == 0), the same bits. `delta` may be a split
+    product's partial sums (`int4_linear_tiles_parts`): they are added here, in
+    chunk order and rounded once, as the product's own reduction would."""
+    parts = delta if isinstance(delta, SplitParts) else None
+    if parts is not None:
+        delta = None
+    device = _on_gpu("rmsnorm", x, weight, delta, None if parts is None else parts.data)
     _bf16("rmsnorm", x, *(() if delta is None else (delta,)))
     if weight.dtype != torch.float32 or weight.numel() != x.shape[-1]:
         raise LinnetError("rmsnorm: weight is f32 [hidden]")
@@ -34,6 +39,14 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, delta: tor
     if delta is not None and delta.shape != x.shape:
         raise LinnetError("rmsnorm: delta has x's shape")
     rows = x.numel() // x.shape[-1]
+    if parts is not None:
+        if parts.data.dim() != 3 or tuple(parts.data.shape[1:]) != (rows, x.shape[-1]) or not parts.data.is_contiguous():
+            raise LinnetError("rmsnorm: split parts are a contiguous f32 [splits, rows, hidden]")
+        out = XTiles.empty(rows, x.shape[-1], x.dtype, device) if tiles else torch.empty_like(x)
+        with torch.cuda.device(device):
+            _lib.call("lnq_rmsnorm_parts", _ptr(x), _ptr(parts.data), parts.data.shape[0], _ptr(weight),
+                      _ptr(out.data if tiles else out), int(tiles), rows, x.shape[-1], float(eps), _stream(device))
+        return out
     if tiles:
         xt = XTiles.empty(rows, x.shape[-1], x.dtype, device)
         with torch.cuda.device(device):

@@ -231,6 +231,45 @@ def int4_linear_tiles(xt: XTiles, packed: torch.Tensor, scale: torch.Tensor, zer
     return y
 
 
+@dataclasses.dataclass
+class SplitParts:
+    """The K chunks' f32 partial sums [splits, rows, out] of a split product
+    (`lnq_int4_linear_tiles_parts`), left for a consumer that adds them in chunk
+    order and rounds once (`decode.rmsnorm` takes them as its residual delta)."""
+
+    data: torch.Tensor
+
+    def total(self, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        """The product they make: the chunks added in order, rounded once (torch ops)."""
+        v = self.data[0].clone()
+        for part in self.data[1:]:
+            v += part
+        return v.to(dtype)
+
+
+def int4_linear_tiles_parts(xt: XTiles, packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor) -> SplitParts:
+    """The split GEMV of `int4_linear_tiles` (1..32 rows, In > 4096, no bias)
+    without its reduction: the chunks' partial sums, whose ordered sum rounded
+    once is `int4_linear_tiles`'s output bit for bit."""
+    device = _on_gpu("int4_linear_tiles_parts", xt.data, packed, scale, zero)
+    rows, depth = xt.rows, xt.width
+    width, groups, half = packed.shape
+    group = 2 * half
+    if groups * group != depth:
+        raise LinnetError(f"int4_linear_tiles_parts: packed {tuple(packed.shape)} does not hold In={depth}")
+    code = _code(xt.dtype, "int4_linear_tiles_parts")
+    if scale.dtype != xt.dtype:
+        raise LinnetError("int4_linear_tiles_parts: scale has x's dtype")
+    packed, scale, zero = packed.contiguous(), scale.contiguous(), zero.contiguous()
+    with torch.cuda.device(device):
+        _, need = _workspace(rows, depth, width, group, code, _lib.KERNEL_SPLIT)
+        parts = torch.empty(max(need, 16) // 4, dtype=torch.float32, device=device)
+        splits = ctypes.c_int32(0)
+        _lib.call("lnq_int4_linear_tiles_parts", _ptr(xt.data), _ptr(packed), _ptr(scale), _ptr(zero), _ptr(parts),
+                  need, rows, depth, width, group, code, ctypes.byref(splits), _stream(device))
+    return SplitParts(parts[: splits.value * rows * width].view(splits.value, rows, width))
+
+
 @functools.lru_cache(maxsize=4096)
 def _workspace(rows: int, depth: int, width: int, group: int, code: int, kernel: int) -> tuple[int, int]:
     """(kernel code, workspace bytes) `lnq_int4_linear_ws` takes for the shape."""

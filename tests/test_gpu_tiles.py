@@ -63,6 +63,29 @@ def test_products_on_tiles_are_the_row_major_bits(rows, width, out, kernel, dtyp
                                         for c in range(0, rows, 32)]))
 
 
+@pytest.mark.parametrize("rows", [32, 20])
+def test_split_parts_add_up_to_the_product_and_feed_the_norm(rows: int) -> None:
+    """The split GEMV's partial sums (`int4_linear_tiles_parts`) added in chunk order
+    and rounded once are the split product's bits, and RMSNorm taking them as its
+    delta gives the bits it gives with that product as delta (row-major and tiles)."""
+    print(f"split parts rows={rows}", flush=True)
+    packed, scale, zero = _layer(4096, 14336, seed=rows)
+    a = torch.randn(rows, 14336, device=DEV).to(torch.bfloat16)
+    at = kernels.x_tiles(a)
+    parts = kernels.int4_linear_tiles_parts(at, packed, scale, zero)
+    assert parts.data.shape == (4, rows, 4096)
+    product = kernels.int4_linear_tiles(at, packed, scale, zero)
+    assert torch.equal(parts.total(), product)
+    x = torch.randn(rows, 4096, device=DEV).to(torch.bfloat16)
+    w = 1 + 0.1 * torch.randn(4096, device=DEV)
+    for tiles in (False, True):
+        x1, x2 = x.clone(), x.clone()
+        want = decode.rmsnorm(x1, w, 1e-5, product, tiles=tiles)
+        got = decode.rmsnorm(x2, w, 1e-5, parts, tiles=tiles)
+        assert torch.equal(x1, x2)
+        assert torch.equal(got.rows_major() if tiles else got, want.rows_major() if tiles else want)
+
+
 def test_tiles_entry_refuses_what_it_does_not_take() -> None:
     packed, scale, zero = _layer(512, 8192, seed=3)
     xt = kernels.x_tiles(torch.randn(32, 8192, device=DEV).to(torch.bfloat16))
