@@ -384,19 +384,23 @@ LNQ_API LnqStatus lnq_mm8(const uint8_t* q, const uint8_t* weight, const float* 
 
 /* lnq_mm8 with the kernel named: tile_n 128 or 256 output columns a workgroup,
  * LNQ_MM8_PERSISTENT (1) the persistent form (256 x 256 tiles, one workgroup a
- * compute unit walking its tiles; out % 256 == 0, in % 256 == 0), 0 for lnq_mm8's
- * own choice.
+ * compute unit walking its tiles; out % 256 == 0, in % 256 == 0),
+ * LNQ_MM8_STREAM (2) the weight-streaming form (256 x 128 tiles with x and
+ * weights in stages of their own, loaded by waves of their own), 0 for
+ * lnq_mm8's own choice. Every form sums the same MFMAs in the same k order:
+ * the same bits.
  * No counterpart in the reference (`torch._scaled_mm` / `int8_mm` choose
  * internally): lets a test run each instance. */
 #define LNQ_MM8_PERSISTENT 1
+#define LNQ_MM8_STREAM 2
 LNQ_API LnqStatus lnq_mm8_tiles(const uint8_t* q, const uint8_t* weight, const float* x_scale,
                                 const float* scale, void* y, int64_t rows, int64_t out_features,
                                 int64_t in_features, int32_t fp8, int32_t dtype, int32_t tile_n,
                                 void* stream);
 
 /* The kernel lnq_mm8 takes for rows x out_features x in_features (fp8 1: e4m3
- * operands, 0: int8) on the current device, as lnq_mm8_tiles names it (1, 128
- * or 256). */
+ * operands, 0: int8) on the current device, as lnq_mm8_tiles names it (1, 2,
+ * 128 or 256). */
 LNQ_API LnqStatus lnq_mm8_plan(int64_t rows, int64_t out_features, int64_t in_features,
                                int32_t fp8, int32_t* tile_n);
 

@@ -446,9 +446,11 @@ __global__ __launch_bounds__(256) void rows8_kernel(const typename Elem<DT>::sto
 }
 
 // The same per row with 16-byte loads and VEC-byte stores (K % VEC == 0 and
-// 16-byte aligned rows): a pass for max|x|, then a pass that quantizes from a
-// second read of the row (an L2 hit). Same arithmetic as rows8_kernel.
-template <int DT, int FP8>
+// 16-byte aligned rows). R > 0: each thread keeps its R vectors of the row in
+// registers between the pass for max|x| and the pass that quantizes (rows of
+// up to R * VEC * 256 elements); R == 0: the second pass reads the row again.
+// Same arithmetic as rows8_kernel.
+template <int DT, int FP8, int R>
 __global__ __launch_bounds__(256) void rows8_vec_kernel(const typename Elem<DT>::storage* __restrict__ x,
                                                         uint8_t* __restrict__ q, float* __restrict__ x_scale, int K) {
   using E = Elem<DT>;
@@ -473,23 +475,8 @@ __global__ __launch_bounds__(256) void rows8_vec_kernel(const typename Elem<DT>:
       for (int j = 0; j < 4; ++j) v[j] = w[j];
     }
   };
-  float top = 0.0f;
-  for (int i = VEC * threadIdx.x; i < K; i += VEC * 256) {
-    float v[VEC];
-    load(i, v);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) top = fmaxf(top, fabsf(v[j]));
-  }
-  top = wave_max(top);
-  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = top;
-  __syncthreads();
-  top = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
-  const float largest = FP8 ? 448.0f : 127.0f;
-  const float s = fmaxf(top, 1e-12f) / largest;
   uint8_t* dst = q + row * K;
-  for (int i = VEC * threadIdx.x; i < K; i += VEC * 256) {
-    float v[VEC];
-    load(i, v);
+  auto put = [&](int i, const float (&v)[VEC], float s) {
     uint32_t b[VEC / 4];
 #pragma unroll
     for (int j = 0; j < VEC / 4; ++j) b[j] = 0;
@@ -509,6 +496,50 @@ __global__ __launch_bounds__(256) void rows8_vec_kernel(const typename Elem<DT>:
       *reinterpret_cast<u32x2*>(dst + i) = u32x2{b[0], b[1]};
     } else {
       *reinterpret_cast<uint32_t*>(dst + i) = b[0];
+    }
+  };
+  auto scale_of = [&](float top) {
+    top = wave_max(top);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = top;
+    __syncthreads();
+    top = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
+    const float largest = FP8 ? 448.0f : 127.0f;
+    return fmaxf(top, 1e-12f) / largest;
+  };
+  float top = 0.0f;
+  float s;
+  if constexpr (R > 0) {
+    float v[R > 0 ? R : 1][VEC];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = VEC * (static_cast<int>(threadIdx.x) + 256 * r);
+      if (i < K) {
+        load(i, v[r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) v[r][j] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) top = fmaxf(top, fabsf(v[r][j]));
+    }
+    s = scale_of(top);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = VEC * (static_cast<int>(threadIdx.x) + 256 * r);
+      if (i < K) put(i, v[r], s);
+    }
+  } else {
+    for (int i = VEC * threadIdx.x; i < K; i += VEC * 256) {
+      float v[VEC];
+      load(i, v);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) top = fmaxf(top, fabsf(v[j]));
+    }
+    s = scale_of(top);
+    for (int i = VEC * threadIdx.x; i < K; i += VEC * 256) {
+      float v[VEC];
+      load(i, v);
+      put(i, v, s);
     }
   }
   if (threadIdx.x == 0) x_scale[row] = s;
@@ -685,17 +716,25 @@ LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t r
   const int K = (int)in_features;
   const int esize = dtype == LNQ_F32 ? 4 : 2;
   const bool vec = (K % (16 / esize)) == 0 && aligned(x, 16) && aligned(q, 8) && (static_cast<size_t>(K) * esize) % 16 == 0;
+  // Vectors of 16 bytes a thread holds: the row in registers up to 8 of them.
+  const int per_thread = vec ? (K / (16 / esize) + 255) / 256 : 0;
+  const int keep = per_thread <= 2 ? 2 : per_thread <= 4 ? 4 : per_thread <= 8 ? 8 : 0;
+#define LNQ_R8V(DT, F, R) \
+  hipLaunchKernelGGL((rows8_vec_kernel<DT, F, R>), grid, dim3(256), 0, s, static_cast<const typename Elem<DT>::storage*>(x), q, x_scale, K)
 #define LNQ_R8(DT, F)                                                                              \
-  if (vec)                                                                                         \
-    hipLaunchKernelGGL((rows8_vec_kernel<DT, F>), grid, dim3(256), 0, s,                          \
-                       static_cast<const typename Elem<DT>::storage*>(x), q, x_scale, K);          \
-  else                                                                                             \
+  if (vec) {                                                                                       \
+    if (keep == 2) LNQ_R8V(DT, F, 2);                                                              \
+    else if (keep == 4) LNQ_R8V(DT, F, 4);                                                         \
+    else if (keep == 8) LNQ_R8V(DT, F, 8);                                                         \
+    else LNQ_R8V(DT, F, 0);                                                                        \
+  } else                                                                                           \
     hipLaunchKernelGGL((rows8_kernel<DT, F>), grid, dim3(256), 0, s,                              \
                        static_cast<const typename Elem<DT>::storage*>(x), q, x_scale, K)
   if (dtype == LNQ_BF16) { if (fp8) { LNQ_R8(LNQ_BF16, 1); } else { LNQ_R8(LNQ_BF16, 0); } }
   else if (dtype == LNQ_F16) { if (fp8) { LNQ_R8(LNQ_F16, 1); } else { LNQ_R8(LNQ_F16, 0); } }
   else { if (fp8) { LNQ_R8(LNQ_F32, 1); } else { LNQ_R8(LNQ_F32, 0); } }
 #undef LNQ_R8
+#undef LNQ_R8V
   return launched("rows8");
 }
 
@@ -704,10 +743,13 @@ LNQ_API LnqStatus lnq_rows8(const void* x, uint8_t* q, float* x_scale, int64_t r
 // FLOP of 128-column ones, but only pay while they still give every compute
 // unit a tile; there, FP8 takes the persistent form where it applies (config 4
 // at 4096 rows: 2468 against 2173 TFLOP/s for the 256-column tiles; int8 stays
-// on the tiles: 2231 against 2177).
+// on the tiles: 2231 against 2177). Below that, 128-column tiles; FP8 past 128
+// rows in the weight-streaming form (config 4 at 256 rows: 70.5 against 73.2
+// us for the 128-column tile kernel; at 16 or 64 rows it is slower, and int8
+// gains nothing at 256).
 static int mm8_kernel_for(int M, int N, int K, bool fp8) {
   const long tiles256 = static_cast<long>((M + mm8::BM - 1) / mm8::BM) * ((N + 255) / 256);
-  if (tiles256 < compute_units()) return 128;
+  if (tiles256 < compute_units()) return fp8 && M > 128 ? LNQ_MM8_STREAM : 128;
   return fp8 && N % 256 == 0 && K % 256 == 0 ? LNQ_MM8_PERSISTENT : 256;
 }
 
@@ -721,8 +763,9 @@ LNQ_API LnqStatus lnq_mm8_tiles(const uint8_t* qx, const uint8_t* weight, const 
               (long long)out_features, (long long)in_features);
   LNQ_REQUIRE(rows <= INT32_MAX && out_features <= INT32_MAX && in_features <= INT32_MAX,
               "lnq_mm8: sizes exceed 2^31");
-  LNQ_REQUIRE(tile_n == 0 || tile_n == LNQ_MM8_PERSISTENT || tile_n == 128 || tile_n == 256,
-              "lnq_mm8: tile_n is 0, 1 (persistent), 128 or 256, not %d", tile_n);
+  LNQ_REQUIRE(tile_n == 0 || tile_n == LNQ_MM8_PERSISTENT || tile_n == LNQ_MM8_STREAM || tile_n == 128 ||
+                  tile_n == 256,
+              "lnq_mm8: tile_n is 0, 1 (persistent), 2 (streaming), 128 or 256, not %d", tile_n);
   LNQ_REQUIRE(tile_n != LNQ_MM8_PERSISTENT || (out_features % 256 == 0 && in_features % 256 == 0),
               "lnq_mm8: the persistent form takes out %% 256 == 0 and in %% 256 == 0, got out=%lld in=%lld",
               (long long)out_features, (long long)in_features);
@@ -747,6 +790,16 @@ LNQ_API LnqStatus lnq_mm8_tiles(const uint8_t* qx, const uint8_t* weight, const 
     else { if (fp8) { LNQ_MM8P(LNQ_F16, 1); } else { LNQ_MM8P(LNQ_F16, 0); } }
 #undef LNQ_MM8P
     return launched("mm8p");
+  }
+  if (bn == LNQ_MM8_STREAM) {
+    const dim3 grid(((M + mm8w::BM - 1) / mm8w::BM) * ((N + mm8w::BN - 1) / mm8w::BN));
+#define LNQ_MM8W(DT, F)                                                                                        \
+  hipLaunchKernelGGL((mm8w_kernel<DT, F, 3, 4>), grid, dim3(mm8w::THREADS), 0, s, qx, weight, x_scale, scale, \
+                     ys, M, N, K)
+    if (dtype == LNQ_BF16) { if (fp8) { LNQ_MM8W(LNQ_BF16, 1); } else { LNQ_MM8W(LNQ_BF16, 0); } }
+    else { if (fp8) { LNQ_MM8W(LNQ_F16, 1); } else { LNQ_MM8W(LNQ_F16, 0); } }
+#undef LNQ_MM8W
+    return launched("mm8w");
   }
   const bool wide = bn == 256;
   const int tiles = ((M + mm8::BM - 1) / mm8::BM) * ((N + bn - 1) / bn);

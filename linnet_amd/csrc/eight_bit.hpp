@@ -366,6 +366,278 @@ __global__ __launch_bounds__(mm8::THREADS, 1) void mm8_kernel(
   }
 }
 
+// ------------------------------------------ weight-streaming 256 x 128 form
+// mm8w_kernel: mm8_kernel<.., 128>'s tiles, waves and MFMA schedule, for the
+// shapes that stream the weight (few row tiles: config 4 at 256 rows). There a
+// tile keeps two steps of its 16 KB weight step in flight, too few for HBM's
+// latency, and more stages of x beside them do not fit. So the operands get
+// stages of their own -- SX of x (32 KB each) and SW of weights (16 KB each),
+// loaded SX - 1 and SW - 1 steps ahead -- and their loads go to waves of their
+// own: waves 0..3 load x (8 loads of 1 KB a step), waves 4..7 the weights (4).
+// Loads retire in order per wave, so a wave waiting for its x of step s + 1
+// waits for no weight loads, and one waiting for its weights of s + 1 leaves
+// those of s + 2 .. s + SW - 1 in flight. Each role runs a K loop of its own
+// (the same steps and barriers), so no step branches on the role. Config 4 at
+// 256 rows (us): (SX, SW) = (3, 4) 70.5, (3, 3) 72.9, (2, 4) 74.0, (2, 5)
+// 75.4, (2, 6) 75.5; the 128-column tile kernel 73.2. The same MFMAs in the
+// same k order as mm8_kernel: the same bits.
+namespace mm8w {
+constexpr int BM = 256, BN = 128, BK = 128, THREADS = 512;
+constexpr int XL = 8;  // x loads of an x wave a step (32 KB over 4 waves)
+constexpr int WL = 4;  // weight loads of a weight wave a step (16 KB over 4 waves)
+}  // namespace mm8w
+
+template <int DT, int FP8, int SX, int SW>
+__global__ __launch_bounds__(mm8w::THREADS, 1) void mm8w_kernel(
+    const uint8_t* __restrict__ qx, const uint8_t* __restrict__ weight,
+    const float* __restrict__ x_scale, const float* __restrict__ scale,
+    uint16_t* __restrict__ y, int M, int N, int K) {
+  using namespace mm8w;
+  static_assert(SX >= 2 && SX <= 3 && SW >= 2 && SW <= 6 && SX * BM * BK + SW * BN * BK <= 160 * 1024, "LDS");
+  using E = Elem<DT>;
+  constexpr int FA = 2, FB = 2, WAVES_N = 2;  // waves of 64 x 64, 4 x 2
+  constexpr int NMF = FA * FB;
+  constexpr int KPM = FP8 ? 64 : 32;
+  constexpr int KK = BK / KPM;
+  constexpr int CPL = KPM / 32;
+  using Op = typename std::conditional<FP8, i32x8, i32x4>::type;
+  using Acc = typename std::conditional<FP8, f32x16, i32x16>::type;
+  // A stage array of its own each (the compiler tracks LDS-bound loads per
+  // array); unused stages are never declared, so the used ones may fill all
+  // 160 KB.
+  __shared__ __attribute__((aligned(16))) uint8_t A0[BM * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t A1[BM * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t B0[BN * BK];
+  __shared__ __attribute__((aligned(16))) uint8_t B1[BN * BK];
+  uint8_t *A2 = A0, *B2 = B0, *B3 = B0, *B4 = B0, *B5 = B0;
+  if constexpr (SX > 2) {
+    __shared__ __attribute__((aligned(16))) uint8_t a2[BM * BK];
+    A2 = a2;
+  }
+  if constexpr (SW > 2) {
+    __shared__ __attribute__((aligned(16))) uint8_t b2[BN * BK];
+    B2 = b2;
+  }
+  if constexpr (SW > 3) {
+    __shared__ __attribute__((aligned(16))) uint8_t b3[BN * BK];
+    B3 = b3;
+  }
+  if constexpr (SW > 4) {
+    __shared__ __attribute__((aligned(16))) uint8_t b4[BN * BK];
+    B4 = b4;
+  }
+  if constexpr (SW > 5) {
+    __shared__ __attribute__((aligned(16))) uint8_t b5[BN * BK];
+    B5 = b5;
+  }
+  LNQ_MFMA_IN_AGPRS();
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool xw = wave < 4;  // this wave's loads: x (waves 0..3) or weights (4..7)
+  const int lw = wave & 3;
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  mm8_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  if (tm >= tiles_m || tn >= tiles_n) return;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int steps = K / BK;
+
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(qx, static_cast<uint32_t>(static_cast<size_t>(M) * K));
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(weight, static_cast<uint32_t>(static_cast<size_t>(N) * K));
+  const __amdgpu_buffer_rsrc_t rnull = buffer_rsrc(weight, 0);
+
+  // Load i of loading wave lw writes stage rows 32 i + 8 lw .. + 7 (1 KB; lane
+  // l: row 32 i + 8 lw + l / 8, stored column l % 8 holding source column
+  // (l % 8) ^ key(row), key = (row >> 1) & 7, the same for every i).
+  const int lrow8 = 8 * lw + (lane >> 3);
+  const int lcol = (lane & 7) ^ ((lrow8 >> 1) & 7);
+  const int off_x = (m0 + lrow8) * K + lcol * 16, off_w = (n0 + lrow8) * K + lcol * 16;
+  const int lds_w = lw * 1024;
+  // Load i (x wave: 0..XL-1, weight wave: 0..WL-1) into stage `dst` through
+  // descriptor r at step offset k0.
+  auto load_x = [&](uint8_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) __attribute__((always_inline)) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 32 * BK), 16, off_x + i * 32 * K, k0, 0, 0);
+  };
+  auto load_w = [&](uint8_t* dst, __amdgpu_buffer_rsrc_t r, int k0, int i) __attribute__((always_inline)) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(dst + lds_w + i * 32 * BK), 16, off_w + i * 32 * K, k0, 0, 0);
+  };
+
+  Acc acc[FA][FB];
+#pragma unroll
+  for (int a = 0; a < FA; ++a)
+#pragma unroll
+    for (int b = 0; b < FB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
+
+  const int lrow = lane & 31;
+  const int lk = lane >> 5;
+  uint32_t aoff[KK][CPL], boff[KK][CPL];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c16 = kk * 2 * CPL + lk * CPL + j;
+      const uint32_t col = static_cast<uint32_t>((c16 ^ ((lrow >> 1) & 7)) << 4);
+      aoff[kk][j] = static_cast<uint32_t>((wm * FA * 32 + lrow) * BK) + col;
+      boff[kk][j] = static_cast<uint32_t>((wn * FB * 32 + lrow) * BK) + col;
+    }
+  auto rd = [&](const uint8_t* stage, uint32_t off, int frag) __attribute__((always_inline)) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(stage + off + frag * 4096);
+  };
+  auto set_op = [](Op& o, int j, u32x4 v) __attribute__((always_inline)) {
+    if constexpr (FP8) {
+      o[4 * j + 0] = (int)v.x;
+      o[4 * j + 1] = (int)v.y;
+      o[4 * j + 2] = (int)v.z;
+      o[4 * j + 3] = (int)v.w;
+    } else {
+      o = __builtin_bit_cast(i32x4, v);
+    }
+  };
+  auto mma = [](const Op& a, const Op& b, Acc c) __attribute__((always_inline)) -> Acc {
+    if constexpr (FP8)
+      return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+    else
+      return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  };
+  Op af[2][FA], bf[2][FB];
+  constexpr int READS = (FA + FB) * CPL;
+  auto read_one = [&](int set, const uint8_t* as, const uint8_t* bs, int kk, int r) __attribute__((always_inline)) {
+    const int f = r / CPL, j = r % CPL;
+    if (f < FA) set_op(af[set][f], j, rd(as, aoff[kk][j], f));
+    else set_op(bf[set][f - FA], j, rd(bs, boff[kk][j], f - FA));
+  };
+  auto region = [&](int cur, const uint8_t* as, const uint8_t* bs, int nkk, auto&& vm) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sl = 0; sl < NMF; ++sl) {
+      acc[sl / FB][sl % FB] = mma(bf[cur][sl % FB], af[cur][sl / FB], acc[sl / FB][sl % FB]);
+#pragma unroll
+      for (int r = sl * READS / NMF; r < (sl + 1) * READS / NMF; ++r) read_one(cur ^ 1, as, bs, nkk, r);
+      vm(sl);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Step s on stages (ac, bc), the next step's on (an, bn); this wave's loads
+  // over the first kk: x of step s + SX - 1 into al (an x wave, X) or weights
+  // of step s + SW - 1 into bl -- stages last read before the previous barrier.
+  // Then this wave's loads of step s + 1 have landed (x waves leave the SX - 2
+  // later steps' in flight, weight waves the SW - 2 later steps'), the barrier,
+  // and the last kk reads the next step's first operands.
+  auto step = [&](auto XW, int s, const uint8_t* ac, const uint8_t* bc, const uint8_t* an, const uint8_t* bn,
+                  uint8_t* al, uint8_t* bl) __attribute__((always_inline)) {
+    constexpr bool X = decltype(XW)::value;
+    const int jl = s + (X ? SX : SW) - 1;
+    const __amdgpu_buffer_rsrc_t q = jl < steps ? (X ? ra : rb) : rnull;
+    const int k0 = jl < steps ? jl * BK : 0;
+    auto vm = [&](int kk, int sl) __attribute__((always_inline)) {
+      if (kk != 0) return;
+      if constexpr (X) {
+#pragma unroll
+        for (int i = 0; i < XL; ++i)
+          if (sl == (i * NMF) / XL) load_x(al, q, k0, i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < WL; ++i)
+          if (sl == (i * NMF) / WL) load_w(bl, q, k0, i);
+      }
+    };
+#pragma unroll
+    for (int kk = 0; kk + 1 < KK; ++kk) region(kk & 1, ac, bc, kk + 1, [&](int sl) __attribute__((always_inline)) { vm(kk, sl); });
+    if constexpr (X) __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"((SX - 2) * XL) : "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"((SW - 2) * WL) : "memory");
+    __builtin_amdgcn_s_barrier();
+    region((KK - 1) & 1, an, bn, 0, [&](int) __attribute__((always_inline)) {});
+  };
+
+  // The whole K loop for one role (x waves, X, or weight waves): the same
+  // steps and barriers for both, the role fixed at compile time so a step
+  // holds no branch. Prologue: x of steps 0 .. SX - 2 or weights of steps
+  // 0 .. SW - 2 requested, step 0 waited for, its first operands read.
+  uint8_t* const As[3] = {A0, A1, A2};
+  uint8_t* const Bs[6] = {B0, B1, B2, B3, B4, B5};
+  auto run = [&](auto XW) __attribute__((always_inline)) {
+    constexpr bool X = decltype(XW)::value;
+    if constexpr (X) {
+#pragma unroll
+      for (int j = 0; j < SX - 1; ++j) {
+        const __amdgpu_buffer_rsrc_t q = j < steps ? ra : rnull;
+        const int k0 = j < steps ? j * BK : 0;
+#pragma unroll
+        for (int i = 0; i < XL; ++i) load_x(As[j], q, k0, i);
+      }
+      __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((SX - 2) * XL) : "memory");
+    } else {
+#pragma unroll
+      for (int j = 0; j < SW - 1; ++j) {
+        const __amdgpu_buffer_rsrc_t q = j < steps ? rb : rnull;
+        const int k0 = j < steps ? j * BK : 0;
+#pragma unroll
+        for (int i = 0; i < WL; ++i) load_w(Bs[j], q, k0, i);
+      }
+      __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((SW - 2) * WL) : "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int r = 0; r < READS; ++r) read_one(0, A0, B0, 0, r);
+
+    // Step s on stages (A s % SX, B s % SW); they cycle every L = lcm(SX, SW).
+    constexpr int L = SX == 2 ? (SW % 2 == 0 ? SW : 2 * SW) : (SW % 3 == 0 ? SW : 3 * SW);
+#define LNQ_MM8W_STEP(S_, J_)                                                                                 \
+  step(XW, S_, As[(J_) % SX], Bs[(J_) % SW], As[((J_) + 1) % SX], Bs[((J_) + 1) % SW], As[((J_) + SX - 1) % SX], \
+       Bs[((J_) + SW - 1) % SW])
+    int ks = 0;
+    for (; ks + L <= steps; ks += L) {
+#pragma unroll
+      for (int j = 0; j < L; ++j) LNQ_MM8W_STEP(ks + j, j);
+    }
+#pragma unroll
+    for (int j = 0; j + 1 < L; ++j)
+      if (ks + j < steps) LNQ_MM8W_STEP(ks + j, j);
+#undef LNQ_MM8W_STEP
+  };
+  if (xw) run(std::true_type{});
+  else run(std::false_type{});
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Epilogue (mm8_kernel's).
+  const bool vec_out = (N & 3) == 0;
+#pragma unroll
+  for (int a = 0; a < FA; ++a) {
+    const int m = m0 + wm * FA * 32 + a * 32 + (lane & 31);
+    if (m >= M) continue;
+    const float xs = x_scale[m];
+    uint16_t* yrow = y + static_cast<size_t>(m) * N;
+#pragma unroll
+    for (int b = 0; b < FB; ++b) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int n = n0 + wn * FB * 32 + b * 32 + 8 * q4 + 4 * (lane >> 5);
+        uint16_t out[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float ws = n + i < N ? scale[n + i] : 0.f;
+          out[i] = E::from_f32(static_cast<float>(acc[a][b][4 * q4 + i]) * xs * ws);
+        }
+        if (vec_out && n + 3 < N) {
+          *reinterpret_cast<u32x2*>(yrow + n) =
+              u32x2{static_cast<uint32_t>(out[0]) | (static_cast<uint32_t>(out[1]) << 16),
+                    static_cast<uint32_t>(out[2]) | (static_cast<uint32_t>(out[3]) << 16)};
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < N) yrow[n + i] = out[i];
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------- persistent 256 x 256 form
 // mm8p_kernel: one workgroup per CU walks its tiles (tile b, b + G, b + 2G, ..
 // of the grid's XCD-grouped order, G workgroups), and the k-steps of all its

@@ -643,8 +643,8 @@ def int8_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype, fp8: bool,
          tile_n: int = 0) -> torch.Tensor:
     device = _on_gpu("mm8", q, weight, x_scale, scale)
-    if tile_n not in (0, MM8_PERSISTENT, 128, 256):
-        raise LinnetError(f"mm8: tile_n is 0 (automatic), 1 (persistent), 128 or 256, not {tile_n}")
+    if tile_n not in (0, MM8_PERSISTENT, MM8_STREAM, 128, 256):
+        raise LinnetError(f"mm8: tile_n is 0 (automatic), 1 (persistent), 2 (streaming), 128 or 256, not {tile_n}")
     rows, depth = q.shape
     width = weight.shape[0]
     if weight.shape[1] != depth:
@@ -662,13 +662,16 @@ def _mm8(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: to
     return y
 
 
-# `tile_n` naming the persistent 256 x 256 form of the 8-bit product.
+# `tile_n` naming the persistent 256 x 256 form of the 8-bit product, and its
+# weight-streaming 256 x 128 form.
 MM8_PERSISTENT = 1
+MM8_STREAM = 2
 
 
 def mm8_plan(rows: int, out_features: int, in_features: int, fp8: bool = True) -> int:
     """The kernel `fp8_mm` (fp8 True) or `int8_mm` takes for this shape on the
-    current device: the tile width (128 or 256 output columns) or MM8_PERSISTENT."""
+    current device: the tile width (128 or 256 output columns), MM8_PERSISTENT or
+    MM8_STREAM."""
     tile = ctypes.c_int32(0)
     _lib.call("lnq_mm8_plan", rows, out_features, in_features, int(fp8), ctypes.byref(tile))
     return tile.value
@@ -733,7 +736,8 @@ def int8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale:
             tile_n: int = 0) -> torch.Tensor:
     """`(q @ weight.T) * x_scale * scale` in `dtype` for int8 rows and int8 weights
     with one scale a row, summed exactly in int32 on MFMA (`kernels.py:805-915`).
-    `tile_n` (128 or 256) forces the tile width, 0 lets the library choose."""
+    `tile_n` (128, 256, MM8_PERSISTENT or MM8_STREAM) names the kernel, 0 lets
+    the library choose; every kernel gives the same bits."""
     return _mm8(q, weight, x_scale, scale, dtype, False, tile_n)
 
 
@@ -742,7 +746,8 @@ def fp8_mm(q: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, scale: 
     """`(q @ weight.T) * x_scale * scale` in `dtype` for FP8 E4M3 rows and weights on
     gfx950's FP8 MFMA, summed in f32: what `torch._scaled_mm(q, W.t(), scale_a,
     scale_b, out_dtype)` computes for the reference (`torch/quantized.py:129`).
-    `tile_n` (128 or 256) forces the tile width, 0 lets the library choose."""
+    `tile_n` (128, 256, MM8_PERSISTENT or MM8_STREAM) names the kernel, 0 lets
+    the library choose; every kernel gives the same bits."""
     return _mm8(q, weight, x_scale, scale, dtype, True, tile_n)
 
 

@@ -251,7 +251,9 @@ def test_plan_queries_name_the_kernel_without_a_device() -> None:
         kernels.int4_linear_plan(32, 14336, 4094, 128, kernel="split")
     assert kernels.mm8_plan(4096, 28672, 8192) == kernels.MM8_PERSISTENT
     assert kernels.mm8_plan(4096, 28672, 8192, fp8=False) == 256
-    assert kernels.mm8_plan(256, 28672, 8192) == 128
+    assert kernels.mm8_plan(256, 28672, 8192) == kernels.MM8_STREAM
+    assert kernels.mm8_plan(256, 28672, 8192, fp8=False) == 128
+    assert kernels.mm8_plan(64, 28672, 8192) == 128
     with pytest.raises(LinnetError, match="tile_n"):
         _lib.call("lnq_mm8_tiles", *[ctypes.c_void_p(256)] * 5, 4, 256, 128, 1, _lib.BF16, 64, None)
 

@@ -250,6 +250,43 @@ def test_mm8_persistent_form_refuses_other_shapes() -> None:
                             torch.ones(n, device=DEV), torch.bfloat16, tile_n=kernels.MM8_PERSISTENT)
 
 
+@pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize(("rows", "k", "n", "dtype"), [
+    (256, 8192, 28672, torch.bfloat16),  # config 4 at 256 rows: 224 tiles, 64 steps (5 cycles of 12, 4 more)
+    (333, 1024, 700, torch.bfloat16),    # ragged rows and columns, 8 steps: no full cycle
+    (7, 128, 256, torch.float16),        # one step: later stages loaded from past K (zeros)
+    (40, 1536, 4096, torch.bfloat16),    # 12 steps: one full cycle, nothing after it
+])
+def test_mm8_streaming_form(fp8: bool, rows: int, k: int, n: int, dtype: torch.dtype) -> None:
+    """The weight-streaming form (x and weights in stages of their own, loaded by
+    waves of their own) bit for bit against the 128-column tile kernel, which
+    sums the same MFMAs in the same k order, and against the f64 product of the
+    rounded operands."""
+    print(f"mm8 streaming fp8={fp8} rows={rows} k={k} n={n} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows + n)
+    x = torch.randn(rows, k, generator=g, device=DEV).to(dtype)
+    if fp8:
+        wq = (torch.randn(n, k, generator=g, device=DEV) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+        ws = torch.rand(n, generator=g, device=DEV) * 0.01 + 0.001
+        qx, xs = kernels.fp8_rows(x)
+        run = lambda t: kernels.fp8_mm(qx, wq, xs, ws, dtype, tile_n=t)  # noqa: E731
+    else:
+        wq = torch.randint(-127, 128, (n, k), generator=g, device=DEV, dtype=torch.int8)
+        ws = torch.rand(n, generator=g, device=DEV) * 0.01 + 0.001
+        qx, xs = kernels.int8_rows(x)
+        run = lambda t: kernels.int8_mm(qx, wq, xs, ws, dtype, tile_n=t)  # noqa: E731
+    got = run(kernels.MM8_STREAM)
+    assert torch.equal(got, run(128))
+    if kernels.mm8_plan(rows, n, k, fp8) == kernels.MM8_STREAM:
+        assert torch.equal(got, run(0))
+    pick = _sample_rows(rows, seed=4) if rows > 64 else np.arange(rows)
+    wbytes = wq.cpu().view(torch.uint8).numpy() if fp8 else wq.cpu().numpy()
+    qxb = qx[pick].cpu().view(torch.uint8).numpy() if fp8 else qx[pick].cpu().numpy()
+    ref = linear.rows8_product_f64(qxb, xs[pick].cpu().numpy(), wbytes, ws.cpu().numpy(), fp8)
+    err, top = _report(f"mm8 streaming fp8={fp8}", got[pick].float().cpu().numpy(), ref)
+    assert err <= 1e-2 * top
+
+
 @pytest.mark.parametrize(("rows", "k", "n", "group", "dtype"), [
     (333, 1024, 768, 128, torch.bfloat16),   # a partial row tile
     (1100, 512, 14336, 128, torch.bfloat16),  # 280 tiles: some workgroups two
