@@ -254,6 +254,9 @@ def test_plan_queries_name_the_kernel_without_a_device() -> None:
     assert kernels.mm8_plan(256, 28672, 8192) == kernels.MM8_STREAM
     assert kernels.mm8_plan(256, 28672, 8192, fp8=False) == 128
     assert kernels.mm8_plan(64, 28672, 8192) == 128
+    assert kernels.mm8_plan(128, 28672, 8192) == 128  # the streaming form past 128 rows only
+    assert kernels.mm8_plan(129, 28672, 8192) == kernels.MM8_STREAM
+    assert kernels.mm8_plan(1024, 28672, 8192) == kernels.MM8_PERSISTENT  # 448 tiles of 256 x 256
     with pytest.raises(LinnetError, match="tile_n"):
         _lib.call("lnq_mm8_tiles", *[ctypes.c_void_p(256)] * 5, 4, 256, 128, 1, _lib.BF16, 64, None)
 
