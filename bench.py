@@ -4,10 +4,12 @@ Headline (BASELINE.json `metric`, config 2): the W4A16 group-128 decode GEMV,
 M=1, K=4096, N=14336 (Llama-3-8B MLP up/gate), as GB/s of algorithmic bytes
 (packed weight + bf16 scales + u8 zeros + x + y) against HBM peak. A "step" is
 one `lnq_int4_linear` call over one batch (one token) with every operand
-resident in HBM (the output too: a preallocated tensor written each call); the steps rotate over enough distinct weight copies (> 256 MB,
-the Infinity Cache) that each call streams its weight from HBM. Launches are
-recorded in a HIP graph and replayed, and the timed region is bracketed by HIP
-events on the stream the kernels run on.
+resident in HBM (the output too: a preallocated tensor written each call); the
+steps rotate over enough distinct weight copies (> 256 MB, the Infinity Cache)
+that each call streams its weight from HBM. The timed calls are made eagerly
+behind untimed graph replays of the same calls queued on the stream, so the GPU
+runs them back to back, and the timed region is bracketed by HIP events on that
+stream (`gemv.M1_graph_replay_us`: the same calls timed as one graph replay).
 
 Also reported (extra keys): M=4 and M=16 GEMV, the prefill dequant-GEMM
 (config 3: M=2048 over three (K, N)) in TFLOP/s against bf16 MFMA peak beside
@@ -73,19 +75,30 @@ def main() -> int:
     props = torch.cuda.get_device_properties(dev)
     stream = torch.cuda.current_stream(dev)
 
-    def timed_graph(launches: list, steps: int, warmup: int) -> float:
-        """Seconds per call over exactly `steps` calls, cycling through
-        `launches`: `warmup` untimed eager calls, then the `steps` calls recorded
-        into one HIP graph and replayed untimed until about 20 ms of GPU time
-        have passed (the clock a decode loop runs at), then, after a
-        synchronization, one more untimed replay and the timed one between HIP
-        events on the stream the kernels run on, synchronized after. The untimed
-        replay queued ahead keeps the GPU busy while the timed replay is
-        submitted, so the events see the `steps` calls back to back, as in a
-        decode loop, and not the graph's submission from an idle queue (~20 us,
-        1 us a call when 20 calls are timed)."""
+    def timed_graph(launches: list, steps: int, warmup: int, replay: list | None = None, eager: bool = True) -> float:
+        """Seconds per call over exactly `steps` calls of the entry point,
+        cycling through `launches`, timed between HIP events on the stream the
+        kernels run on.
+
+        `warmup` untimed eager calls, then the `steps` calls recorded into one
+        HIP graph and replayed untimed until about 20 ms of GPU time have
+        passed (the clock a decode loop runs at). The timed calls are then made
+        eagerly, queued right behind more untimed replays: the host submits
+        them (~13 us a call through Python) while the GPU still works through
+        the replays, so the events see the `steps` calls back to back, as a
+        decode loop's GPU does, with no graph launch inside the timed region
+        (one replay of a graph adds ~8 us, 0.4 us a call when 20 calls are
+        timed). The queued replays are sized from the measured submission time,
+        and the run checks that the host finished submitting before the GPU
+        reached the first timed call; it retries with more queued work, then
+        raises, rather than time an idle GPU. A list passed as `replay` receives
+        the seconds per call of the same calls timed as one graph replay (one
+        replay queued ahead of it); `eager=False` returns that figure instead,
+        for calls that wait on the device by design (a load-time check)."""
+        t0 = time.perf_counter()
         for i in range(max(warmup, len(launches))):
             launches[i % len(launches)]()
+        host_call = (time.perf_counter() - t0) / max(warmup, len(launches))
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
@@ -93,21 +106,42 @@ def main() -> int:
                 launches[i % len(launches)]()
         graph.replay()
         torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        queued, start, end = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         start.record(stream)
         graph.replay()
         end.record(stream)
         torch.cuda.synchronize()
-        for _ in range(min(400, int(20.0 / max(start.elapsed_time(end), 1e-3)))):
+        replay_ms = max(start.elapsed_time(end), 1e-3)
+        for _ in range(min(400, int(20.0 / replay_ms))):
             graph.replay()
         torch.cuda.synchronize()
-        graph.replay()
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        del graph
-        return start.elapsed_time(end) / 1e3 / steps
+        if replay is not None or not eager:
+            graph.replay()
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+            torch.cuda.synchronize()
+            if not eager:
+                del graph
+                return start.elapsed_time(end) / 1e3 / steps
+            replay.append(start.elapsed_time(end) / 1e3 / steps)
+        ahead = 1 + int(2.0 * steps * host_call * 1e3 / replay_ms)
+        for _ in range(3):
+            t0 = time.perf_counter()
+            queued.record(stream)
+            for _ in range(ahead):
+                graph.replay()
+            start.record(stream)
+            for i in range(steps):
+                launches[i % len(launches)]()
+            end.record(stream)
+            submitted_ms = (time.perf_counter() - t0) * 1e3
+            torch.cuda.synchronize()
+            if submitted_ms < 0.9 * queued.elapsed_time(start):
+                del graph
+                return start.elapsed_time(end) / 1e3 / steps
+            ahead *= 4
+        raise RuntimeError(f"the host could not queue {steps} calls ahead of the GPU")
 
     def int4_layers(n: int, k: int, copies: int, seed: int = 0):
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -142,11 +176,13 @@ def main() -> int:
             x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
             y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)  # resident output, written each call
             launches = [lambda l=l, x=x, y=y: kernels.int4_linear(x, *l, out=y) for l in layers]
-            sec = timed_graph(launches, args.steps, args.warmup)
+            replay: list = []
+            sec = timed_graph(launches, args.steps, args.warmup, replay if m == 1 else None)
             gbps = gemv_bytes(m, k, n) / sec / 1e9
             gemv[f"M{m}"] = {"us": round(sec * 1e6, 3), "gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
             if m == 1:
                 headline = (sec, gbps)
+                gemv["M1_graph_replay_us"] = round(replay[0] * 1e6, 3)
         # GPTQ's activation order at one token: the take_inputs gather fused
         # into the GEMV's x staging (lnq_int4_linear_ordered).
         order = torch.randperm(k, generator=g, device=dev).to(torch.int32)
@@ -612,7 +648,9 @@ def checkpoint_repack(torch, kernels, dev, timed_graph, with_cpu: bool) -> dict[
         order = torch.from_numpy(rng.permutation(in_f).astype(np.int32)).to(dev) if act else None
         offset = 1 if method == "gptq" else 0
         launches = [lambda w=w: kernels.int4_repack(w, zeros, method, group, offset, order) for w in words]
-        sec = timed_graph(launches, 200, 10)
+        # One graph replay: the act-order call checks its order on the host
+        # (one device wait a call) when it is not being captured.
+        sec = timed_graph(launches, 200, 10, eager=False)
         entry = {"us": round(sec * 1e6, 2), "gbps": round(nbytes / sec / 1e9, 1),
                  "frac_hbm_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBPS, 4)}
         if with_cpu:
