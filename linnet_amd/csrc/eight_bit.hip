@@ -226,10 +226,8 @@ __global__ __launch_bounds__(256) void w8_skinny_kernel(
 // odd ones, and row r's sum is C[0][r] + C[1][8 + r]. Two loads (rows 0-7 and
 // 8-15) per 128 inputs, each two MFMA 16x16x32 (bytes 0-7 and 8-15 of a piece).
 //
-// NW waves split K (4, or 16 for K = 4096: every CU then holds 16 waves of 2
-// steps, their loads all in flight at once, and a wave's steps are multiplied as
-// soon as its own loads land instead of after a quarter of K); D loads in flight
-// per wave.
+// NW waves split K; D loads in flight per wave. K = 4096 runs
+// w8_row_slices_kernel below instead.
 template <int DT, int FP8, int NW = 4, int D = 16>
 __global__ __launch_bounds__(64 * NW) void w8_row_kernel(const uint16_t* __restrict__ x,
                                                          const uint8_t* __restrict__ weight,
@@ -358,6 +356,129 @@ __global__ __launch_bounds__(64 * NW) void w8_row_kernel(const uint16_t* __restr
   }
   // Lane col (j = 0) holds A row 0 in register 0 and row 1 in register 1: row
   // col % 8 of half h is C[0][col % 8] + C[1][8 + col % 8].
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float mine = col < 8 ? acc[h][0] : acc[h][1];
+    const float v = mine + __shfl_xor(mine, 8, 64);
+    if (j == 0 && col < 8) red[wave][8 * h + col] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int n = n0 + threadIdx.x;
+    float v = red[0][threadIdx.x];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[w][threadIdx.x];
+    if (n < N) y[n] = E::from_f32(v);
+  }
+}
+
+// One row of x at K = 4096 (config 1's int8 4096 x 4096 GEMV): the workgroups
+// and loads of w8_row_kernel (16 output features, lane l reading row l % 8,
+// piece l / 8 of a 128-input step), with K split over 16 waves of 2 steps, so
+// every load of a CU is in flight at once and each wave multiplies as soon as
+// its own loads land. Each wave loads just the 256 inputs of x its steps use,
+// straight into its MFMA A-operand registers (32 bytes of x a lane a step,
+// issued before the weights): no LDS stage of x and no workgroup barrier ahead of
+// the products (6.2 -> 5.6 us for config 1). The sums are w8_row_kernel's, in
+// the same order (the same bits).
+template <int DT, int FP8>
+__global__ __launch_bounds__(1024) void w8_row_slices_kernel(const uint16_t* __restrict__ x,
+                                                             const uint8_t* __restrict__ weight,
+                                                             const float* __restrict__ scale,
+                                                             uint16_t* __restrict__ y, int N, int G, int row_block,
+                                                             int scale_cols) {
+  using E = Elem<DT>;
+  constexpr float offset = FP8 ? 0.0f : 128.0f;
+  constexpr int K = 4096;
+  constexpr int NW = 16;
+  constexpr int PW = K / 128 / NW;  // steps a wave
+  __shared__ float red[NW][16];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int j = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int sb = wave * PW;
+  const int steps_per_group = G >> 7;
+
+  const uint8_t* wrow[2];
+  const float* srow[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    wrow[h] = weight + static_cast<size_t>(min(n0 + 8 * h + (lane & 7), N - 1)) * K + 16 * (lane >> 3);
+    const int srow_n = min(n0 + 8 * h + (col & 7), N - 1);
+    srow[h] = scale + static_cast<size_t>(srow_n / row_block) * scale_cols;
+  }
+  u32x4 ones;
+  ones.x = ones.y = ones.z = ones.w = E::ONE2;
+  f32x4 acc[2], C[2], Cx;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+    C[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  Cx = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // A row m (lane m = l % 16) takes x at piece 2 j + (m & 1) of each step; rows
+  // 2..15 repeat rows 0 / 1 and their outputs are not used.
+  const int apiece = 2 * j + (col & 1);
+  u32x4 xa[PW][2];
+#pragma unroll
+  for (int i = 0; i < PW; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) xa[i][t] = *reinterpret_cast<const u32x4*>(&x[128 * (sb + i) + 16 * apiece + 8 * t]);
+  const int g_first = sb / steps_per_group;
+  float s_first[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) s_first[h] = srow[h][g_first];
+  __asm__ volatile("" ::: "memory");
+  u32x4 rw[2 * PW];
+#pragma unroll
+  for (int i = 0; i < 2 * PW; ++i)
+    rw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[i & 1] + 128 * (sb + (i >> 1))));
+
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int step = sb + i;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 w = rw[2 * i + h];
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        uint32_t b0, b1, b2, b3;
+        widen4<DT, FP8>(words[2 * t], b0, b1);
+        widen4<DT, FP8>(words[2 * t + 1], b2, b3);
+        C[h] = mfma16x16x32<DT>(xa[i][t], u32x4{b0, b1, b2, b3}, C[h]);
+      }
+    }
+    if constexpr (!FP8) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) Cx = mfma16x16x32<DT>(xa[i][t], ones, Cx);
+    }
+    // A group closes at its last step or where this wave's steps end.
+    if ((step + 1) % steps_per_group == 0 || i + 1 == PW) {
+      const int g = step / steps_per_group;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float sc = s_first[h];
+        if (g != g_first) {
+          // (The asm keeps this load in its branch, as in w8_row_kernel.)
+          __asm__ volatile("" ::: "memory");
+          sc = srow[h][g];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float d = FP8 ? C[h][r] : fmaf(-offset, Cx[r], C[h][r]);
+          acc[h][r] = fmaf(sc, d, acc[h][r]);
+        }
+        C[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      Cx = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  // Row col % 8 of half h is C[0][col % 8] + C[1][8 + col % 8] (w8_row_kernel).
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float mine = col < 8 ? acc[h][0] : acc[h][1];
@@ -582,8 +703,8 @@ static void launch_w8_skinny(const void* x, const uint8_t* w, const float* s, vo
   const auto* xs = static_cast<const uint16_t*>(x);
   auto* ys = static_cast<uint16_t*>(y);
   if (M == 1 && K == 4096 && G % 128 == 0)
-    hipLaunchKernelGGL((w8_row_kernel<DT, FP8, 16, 4>), dim3((N + 15) / 16), dim3(1024), K * 2, stream, xs, w, s, ys, N,
-                       K, G, rb, cols);
+    hipLaunchKernelGGL((w8_row_slices_kernel<DT, FP8>), dim3((N + 15) / 16), dim3(1024), 0, stream, xs, w, s, ys, N, G,
+                       rb, cols);
   else if (M == 1 && K <= 32768 && K % 512 == 0 && G % 128 == 0)
     hipLaunchKernelGGL((w8_row_kernel<DT, FP8>), dim3((N + 15) / 16), dim3(256), K * 2, stream, xs, w, s, ys, N, K, G,
                        rb, cols);

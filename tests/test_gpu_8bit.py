@@ -132,11 +132,12 @@ def test_weight_only_kernels(fp8: bool, rows: int, out: int, group: int, row_blo
 @pytest.mark.parametrize(("out", "width", "group", "row_block", "dtype"), [
     (300, 1024, 0, 1, torch.bfloat16), (77, 2048, 128, 1, torch.float16), (256, 4096, 128, 128, torch.bfloat16),
     (40, 384, 0, 1, torch.bfloat16), (1000, 8192, 256, 1, torch.bfloat16), (128, 16384, 0, 1, torch.float16),
-    (24, 512, 64, 1, torch.bfloat16),
+    (24, 512, 64, 1, torch.bfloat16), (300, 4096, 0, 1, torch.float16), (40, 4096, 256, 1, torch.bfloat16),
 ])
 def test_one_row_kernels(fp8: bool, out: int, width: int, group: int, row_block: int, dtype: torch.dtype) -> None:
-    """One row of x: the wide-read one-row kernel (K % 512 == 0, groups of 128k) and
-    the skinny kernel's one-row form (the rest), against the f64 product."""
+    """One row of x: the wide-read one-row kernels (K % 512 == 0, groups of 128k;
+    K = 4096 on the per-wave x slices kernel, with ragged outputs) and the
+    skinny kernel's one-row form (the rest), against the f64 product."""
     if group and out % row_block:
         pytest.skip("blocks tile the weight")
     q, scale, deq = _eight_bit(out, width, fp8, seed=out + width, group=group, row_block=row_block)
