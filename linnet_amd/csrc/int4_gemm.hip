@@ -39,7 +39,7 @@
 // loads pick their source column so that the contiguous LDS writes of one
 // buffer_load ... lds land in that layout.
 //
-// Workgroups are numbered so that each XCD (workgroup b runs on XCD b % 8)
+// Workgroups are numbered so that each XCD (workgroups b with one b % 8 run on one XCD)
 // owns a contiguous run of tiles, ordered in groups of 4 row tiles: the
 // tiles resident on one XCD share x and W tiles in its L2.
 //
