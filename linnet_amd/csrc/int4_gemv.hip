@@ -48,6 +48,8 @@
 //   lnq_rmsnorm's x * r * w rounded to bf16 by that rounding. SiLU(g) * u: each
 //   wave loads its u slice beside g; lanes l and l + 32 hold the same chunk, so
 //   each half computes half of it and they exchange (the bits of lnq_silu_mul).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace lnq {
@@ -1123,7 +1125,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float v = fmaf(s0, fmaf(-z0, x0[i], C[b][0][i]), s1 * fmaf(-z1, x1[i], C[b][1][i]));
-        if (col < CW) red[((((b * 4 + i) * 4 + j) * CW + col) + 4 * wave) & (32 * CW - 1)] = v;
+        if (col < CW) red[((b * 4 + i) * 4 + j) * CW + col] = v;
       }
     }
   }
@@ -1131,27 +1133,36 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
   // The waves' partial sums added four outputs at a time: thread t takes quads
   // t, t + 64 nw, .. of the workgroup (tile T: 32 row slots x CW / 4 column
   // quads, slot s = 16 b + 4 i + j holding x row 16 b + 4 j + i), reads the quad
-  // of every wave (16 contiguous bytes at the rotated place it was written to)
-  // and adds them in wave order. No lane exchange: one LDS read a wave a quad.
+  // of every wave (16 contiguous bytes, at the same place in each wave's part:
+  // one read instruction covers 1 KB of one part, so no bank is hit twice) and
+  // adds them in wave order. No lane exchange: one LDS read a wave a quad. With
+  // all 16 waves (K = 4096) the wave loop has no condition (no selects).
   constexpr int TQ = 32 * 16 / 4;  // quads of a full tile
   constexpr int QUADS = HALF ? (NT - 1) * TQ + TQ / 2 : NT * TQ;
+  static_assert(TQ % 64 == 0 && QUADS % 64 == 0, "a wave's quads lie in one tile");
   for (int qd = threadIdx.x; qd < QUADS; qd += blockDim.x) {
-    const int T = qd / TQ, r = qd % TQ;
+    // The 64 quads of a wave are consecutive and a tile holds a multiple of 64:
+    // the tile is the wave's (scalar), so its array is not selected lane by lane.
+    const int T = __builtin_amdgcn_readfirstlane(qd / TQ), r = qd % TQ;
     const int cw = outs(T);
     const int cq = cw / 4;  // column quads of the tile
     const int slot = r / cq, c4 = 4 * (r % cq);
     const int e = slot * cw + c4;
     // Every wave's quad requested before the first add (one LDS round trip).
-    f32x4 p[gemv::MAX_WAVES];
+    auto gather = [&](auto all) -> f32x4 {
+      f32x4 p[gemv::MAX_WAVES];
 #pragma unroll
-    for (int w = 0; w < gemv::MAX_WAVES; ++w)
-      if (w < nw)
-        p[w] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(tile_lds(T, w)) +
-                                               ((e + 4 * w) & (32 * cw - 1)));
-    f32x4 v = p[0];
+      for (int w = 0; w < gemv::MAX_WAVES; ++w)
+        if (decltype(all)::value || w < nw)
+          p[w] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(tile_lds(T, w)) + e);
+      f32x4 acc = p[0];
 #pragma unroll
-    for (int w = 1; w < gemv::MAX_WAVES; ++w)
-      if (w < nw) v = f32x4{v[0] + p[w][0], v[1] + p[w][1], v[2] + p[w][2], v[3] + p[w][3]};
+      for (int w = 1; w < gemv::MAX_WAVES; ++w)
+        if (decltype(all)::value || w < nw)
+          acc = f32x4{acc[0] + p[w][0], acc[1] + p[w][1], acc[2] + p[w][2], acc[3] + p[w][3]};
+      return acc;
+    };
+    const f32x4 v = nw == gemv::MAX_WAVES ? gather(std::true_type{}) : gather(std::false_type{});
     const int m = (slot & 16) | ((slot & 3) << 2) | ((slot >> 2) & 3);
     const int n = n0 + 16 * T + c4;
     if (m >= M || 16 * T + c4 >= R) continue;
