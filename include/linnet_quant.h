@@ -176,7 +176,8 @@ LNQ_API LnqStatus lnq_int4_linear_workspace(int64_t rows, int64_t in_features, i
  * instruction read 16 rows x 64 bytes, a third of the rate of whole lines). For rows
  * x in values (in % 256 == 0), chunks of 32 rows of in * 32 values; within a chunk,
  * value (m, k) sits at ((k / 256 * 16 + 8 (m / 16 % 2) + 4 (k / 128 % 2) + k / 32 % 4)
- * * 64 + 16 (k / 8 % 4) + m % 16) * 8 + k % 8. lnq_x_tiles writes them from row-major
+ * * 64 + 16 (k / 8 % 4) + m % 16) * 8 + 2 (k % 4) + k % 8 / 4 (each 8 consecutive
+ * inputs in the order 0, 4, 1, 5, 2, 6, 3, 7). lnq_x_tiles writes them from row-major
  * x (2-byte values; rows of the last chunk past `rows` zero; x, xt 16-byte aligned).
  * No counterpart in the reference (a layout of this library's decode kernels). */
 LNQ_API LnqStatus lnq_x_tiles(const void* x, void* xt, int64_t rows, int64_t in_features, void* stream);

@@ -88,12 +88,14 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 // rate of one reading whole 128-byte lines). Rows come in chunks of 32 (K * 32
 // values each); a chunk holds K / 256 slices of 16 operands 8 b + 4 H + t, and
 // lane 16 j + c of an operand holds row 16 b + c, inputs 256 s + 128 H + 32 t +
-// 8 j .. + 7. The index of value (m, k) (K % 256 == 0):
+// 8 j .. + 7 in pair order (0, 4, 1, 5, 2, 6, 3, 7: the order of the widened
+// weights, see permute_x8), so the GEMVs multiply them as loaded. The index of
+// value (m, k) (K % 256 == 0):
 __host__ __device__ inline size_t x_tile_index(int m, int k, int K) {
   const int chunk = m >> 5, b = (m >> 4) & 1, c = m & 15;
   const int s = k >> 8, H = (k >> 7) & 1, t = (k >> 5) & 3, j = (k >> 3) & 3, e = k & 7;
   return static_cast<size_t>(chunk) * K * 32 +
-         ((static_cast<size_t>(s) * 16 + 8 * b + 4 * H + t) * 64 + 16 * j + c) * 8 + e;
+         ((static_cast<size_t>(s) * 16 + 8 * b + 4 * H + t) * 64 + 16 * j + c) * 8 + 2 * (e & 3) + (e >> 2);
 }
 
 __device__ inline uint16_t f32_to_bf16_bits(float f) {

@@ -196,7 +196,8 @@ __global__ __launch_bounds__(decode::THREADS) void rmsnorm_vec_kernel(uint16_t* 
     const int i = threadIdx.x + c * decode::THREADS;
     if (i >= chunks) continue;
     uint16_t* dst = TILES ? h + x_tile_index(blockIdx.x, 8 * i, hidden) : hr + 8 * i;
-    *reinterpret_cast<u32x4*>(dst) = norm_bf16x8(v[c], scale, wv[c][0], wv[c][1]);
+    const u32x4 out = norm_bf16x8(v[c], scale, wv[c][0], wv[c][1]);
+    *reinterpret_cast<u32x4*>(dst) = TILES ? permute_x8(out) : out;  // tiles: 8 values in pair order
   }
 }
 

@@ -1032,10 +1032,11 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- x (and the scales) landed: each row's sums over both halves on the
-  // matrix core (A = x, B = ones: lane (col, j) register i is the sum of x row
-  // 16 b + 4 j + i, the row its output register i holds), then the A operands
-  // in pair order.
+  // ---- x (and the scales) landed: the A operands in pair order (x tiles hold
+  // them so already), then each row's sums over both halves on the matrix core
+  // (A = x, B = ones: lane (col, j) register i is the sum of x row 16 b + 4 j +
+  // i, the row its output register i holds), taken on the operands in pair order
+  // in both cases so that tiles and row-major x give the same bits.
   wait_vm<U8>();
   __builtin_amdgcn_sched_barrier(0);
   u32x4 ones;
@@ -1047,8 +1048,8 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows32_kernel(
       f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
+        if constexpr (!XT) xa[b][H][t] = permute_x8(xa[b][H][t]);
         sum = mfma16x16x32<DT>(xa[b][H][t], ones, sum);
-        xa[b][H][t] = permute_x8(xa[b][H][t]);
       }
       if (col == 0) *reinterpret_cast<f32x4*>(&XS[wave][b][H][4 * j]) = sum;
     }
@@ -1407,7 +1408,8 @@ static void launch_split_dt(const void* x, const uint8_t* packed, const void* sc
 
 // rows x K values, row-major, to x tiles (x_tile_index; chunks of 32 rows, rows
 // past `rows` of the last chunk zero): thread t of workgroup (chunk, slice)
-// moves the 16-byte pieces t, t + 256, t + 512, t + 768 of the slice's 16 KB.
+// moves the 16-byte pieces t, t + 256, t + 512, t + 768 of the slice's 16 KB,
+// each put in pair order.
 __global__ __launch_bounds__(256) void x_tiles_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xt,
                                                       int rows, int K) {
   const int chunk = blockIdx.y, s = blockIdx.x;
@@ -1419,7 +1421,7 @@ __global__ __launch_bounds__(256) void x_tiles_kernel(const uint16_t* __restrict
     const int m = 32 * chunk + 16 * (op >> 3) + (lane & 15);
     const int k = 256 * s + 128 * ((op >> 2) & 1) + 32 * (op & 3) + 8 * (lane >> 4);
     u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (m < rows) v = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m) * K + k);
+    if (m < rows) v = permute_x8(*reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m) * K + k));
     *reinterpret_cast<u32x4*>(out + static_cast<size_t>(piece) * 8) = v;
   }
 }

@@ -176,8 +176,9 @@ class XTiles:
     def rows_major(self) -> torch.Tensor:
         """The [rows, width] tensor the tiles hold (a torch reordering, for tests)."""
         chunks = self.data.numel() // (32 * self.width)
-        t = self.data.view(chunks, self.width // 256, 2, 2, 4, 4, 16, 8)  # chunk, s, b, H, t, j, c, e
-        t = t.permute(0, 2, 6, 1, 3, 4, 5, 7).reshape(chunks * 32, self.width)
+        # chunk, s, b, H, t, j, c, then element e = e_lo + 4 e_hi at place 2 e_lo + e_hi
+        t = self.data.view(chunks, self.width // 256, 2, 2, 4, 4, 16, 4, 2)
+        t = t.permute(0, 2, 6, 1, 3, 4, 5, 8, 7).reshape(chunks * 32, self.width)
         return t[: self.rows]
 
 

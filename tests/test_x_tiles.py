@@ -12,12 +12,15 @@ from linnet_amd.torch.kernels import XTiles
 
 def _index(m: int, k: int, width: int) -> int:
     """Value (m, k)'s place: chunk m // 32; operand 8 (m // 16 % 2) + 4 (k // 128 %
-    2) + k // 32 % 4 of slice k // 256; lane 16 (k // 8 % 4) + m % 16; element k % 8."""
+    2) + k // 32 % 4 of slice k // 256; lane 16 (k // 8 % 4) + m % 16; within the
+    lane's 8 values, the pair order 0, 4, 1, 5, 2, 6, 3, 7 (element e at 2 (e % 4)
+    + e // 4)."""
     chunk, mm = divmod(m, 32)
     s, kk = divmod(k, 256)
     op = 8 * (mm // 16) + 4 * (kk // 128) + (kk // 32) % 4
     lane = 16 * ((kk // 8) % 4) + mm % 16
-    return chunk * width * 32 + ((s * 16 + op) * 64 + lane) * 8 + kk % 8
+    e = kk % 8
+    return chunk * width * 32 + ((s * 16 + op) * 64 + lane) * 8 + [0, 2, 4, 6, 1, 3, 5, 7][e]
 
 
 @pytest.mark.parametrize(("rows", "width"), [(1, 256), (17, 512), (32, 256), (45, 768)])
