@@ -701,7 +701,7 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   // Once a wave has folded its tiles it writes its partial sums of tile T (16
   // output rows) over its own part of tile T's array, which only it reads:
   // element e = 64 i + lane (x row 4 (lane / 16) + i, output row 16 T +
-  // lane % 16) at float (e + 4 w) % 256 of wave w's part. The rotation by 4 w
+  // lane % 16) at float 64 i + (lane ^ 4 w) of wave w's part. The XOR by 4 w
   // puts the four waves a read instruction touches (lanes 16 q + c read wave
   // 4 q + w, parts 2048 or 1024 bytes apart) in distinct banks.
   static_assert(gemv::tile_wave_bytes(U8, NT - 1) >= 256 * 4, "partial sums fit a wave's part of a tile");
@@ -882,13 +882,17 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
       acc[T][i] = fmaf(s0, fmaf(-z0, xs[0][i], cf[T][0][i]), s1 * fmaf(-z1, xs[1][i], cf[T][1][i]));
   }
   // ---- the cross-wave sum through the wave's own (now unread) tile parts.
+  // Element 64 i + l of a wave's part sits at 64 i + (l ^ 4 wave): the XOR spreads
+  // the four waves a read instruction touches over distinct banks (as a rotation
+  // by 4 wave would) and leaves 64 i a constant offset.
+  const int lrot = lane ^ (4 * wave);
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
     float* red = reinterpret_cast<float*>(tile_lds(T, wave));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 4 * j + i;
-      if (m < MX) red[(64 * i + lane + 4 * wave) & 255] = acc[T][i];
+      if (m < MX) red[64 * i + lrot] = acc[T][i];
     }
   }
   __syncthreads();
@@ -901,11 +905,12 @@ __global__ __launch_bounds__(64 * gemv::MAX_WAVES) void int4_gemv_rows_kernel(
   const int q = j;
   auto pass = [&](const int o, float (&r)[4]) {
     const int T = min(o / MX, NT - 1), m = o % MX;
-    const int e = 64 * (m & 3) + 16 * (m >> 2) + col;
+    // (16 (m / 4) + col) ^ (4 wv) < 64: wave wv's element 64 (m % 4) + 16 (m / 4) + col.
+    const int e = (16 * (m >> 2) + col) ^ (16 * q);
 #pragma unroll
     for (int w = 0; w < gemv::MAX_WAVES / 4; ++w) {
       const int wv = 4 * q + w;
-      r[w] = reinterpret_cast<const float*>(tile_lds(T, wv))[(e + 4 * wv) & 255];
+      r[w] = reinterpret_cast<const float*>(tile_lds(T, wv))[64 * (m & 3) + (e ^ (4 * w))];
     }
   };
   auto finish = [&](const int o, const float (&r)[4]) {
