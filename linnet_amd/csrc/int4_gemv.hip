@@ -1308,7 +1308,13 @@ static void launch_gemv_dt(const void* x, const uint8_t* packed, const void* sca
                            const void* bias, void* y, int N, int K, int G, const int32_t* order, int kind,
                            GemvPrologue pro, hipStream_t stream) {
 #define LNQ_GEMV_U8(U_) launch_gemv_u8<DT, U_>(x, packed, scale, zero, bias, y, N, K, G, order, kind, pro, stream)
-  switch ((N + 2047) / 2048) {
+  // Rows a workgroup, 8 * U8: the rounds of one workgroup a CU that 64-row
+  // workgroups need, then the fewest rows that fill that many rounds (up to one
+  // round: ceil(N / 2048) on 256 CUs; N = 28672: two full rounds of 56 rows,
+  // not 1.75 of 64, the second leaving a quarter of the CUs idle).
+  const int cus = compute_units();
+  const int rounds = (N + 64 * cus - 1) / (64 * cus);
+  switch ((N + 8 * cus * rounds - 1) / (8 * cus * rounds)) {
     case 1: LNQ_GEMV_U8(1); break;
     case 2: LNQ_GEMV_U8(2); break;
     case 3: LNQ_GEMV_U8(3); break;
