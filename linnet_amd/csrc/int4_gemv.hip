@@ -1346,7 +1346,18 @@ static void launch_rows_u8(const void* x, const uint8_t* packed, const void* sca
 template <int DT, int MX>
 static void launch_rows_dt(const void* x, const uint8_t* packed, const void* scale, const uint8_t* zero,
                            const void* bias, void* y, int M, int N, int K, int G, hipStream_t stream) {
-  switch ((N + 2047) / 2048) {
+  // Rows a workgroup: ceil(N / 2048) up to 64 (one round on 256 CUs); past that
+  // 64, unless 64-row workgroups would leave their last round less than half
+  // full: then the fewest rows that fill whole rounds (each workgroup reads all
+  // of x, so more of them cost more where the last round is nearly full anyway:
+  // N = 28672 at 4 / 16 rows 15.5 / 21.4 us on 448 workgroups of 64 rows against
+  // 16.3 / 22.0 on 512 of 56; N = 20000 14.96 / 20.96 on 313 of 64 against 12.58
+  // / 18.47 on 500 of 40).
+  const int cus = compute_units();
+  const int rounds = (N + 64 * cus - 1) / (64 * cus);
+  const int last = ((N + 63) / 64) % cus;
+  const int u8 = rounds > 1 && (last == 0 || 2 * last >= cus) ? 8 : (N + 8 * cus * rounds - 1) / (8 * cus * rounds);
+  switch (u8) {
     case 1: launch_rows_u8<DT, 1, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
     case 2: launch_rows_u8<DT, 2, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
     case 3: launch_rows_u8<DT, 3, MX>(x, packed, scale, zero, bias, y, M, N, K, G, stream); break;
