@@ -210,8 +210,9 @@ def test_unsupported_groups_fall_back_to_the_dequantized_weight() -> None:
         (1000, 8192, 256, torch.float16),  # S = 2, group 256, 8 rows
         (5000, 6144, 128, torch.bfloat16),  # S = 2, 12 waves, 24 rows (odd U8)
         (3000, 12288, 1024, torch.bfloat16),  # S = 3, group 1024, 16 rows
-        (20000, 1024, 128, torch.bfloat16),  # past 16384 outputs: 313 workgroups of 64 rows
-        (40008, 512, 128, torch.float16),  # 626 workgroups, ragged last
+        (20000, 1024, 128, torch.bfloat16),  # past 16384 outputs: two whole rounds, 500 workgroups of 40 rows
+        (28672, 1024, 128, torch.bfloat16),  # two whole rounds: 512 workgroups of 56 rows (odd U8)
+        (40008, 512, 128, torch.float16),  # three rounds: 715 workgroups of 56 rows, ragged last
     ],
 )
 def test_one_token_gemv_multiplies_the_dequantized_weight(out: int, width: int, group: int, dtype: torch.dtype) -> None:
@@ -299,6 +300,9 @@ def test_one_token_gemv_is_chosen_for_one_row_and_refuses_other_shapes() -> None
         (32, 16384, 256, 128, torch.float16),  # U8 = 8, one wave
         (31, 100, 4096, 128, torch.bfloat16),  # one short workgroup
         (29, 28672, 4096, 128, torch.bfloat16),  # past 16384 outputs: more workgroups than CUs
+        (4, 20000, 1024, 128, torch.bfloat16),  # 64-row workgroups would leave a last round 22% full:
+        (16, 20000, 1024, 128, torch.float16),  # whole rounds instead, 500 workgroups of 40 rows
+        (9, 28672, 1024, 128, torch.bfloat16),  # last round 75% full: 448 workgroups of 64 rows
     ],
 )
 def test_few_token_gemv_multiplies_the_dequantized_weight(rows: int, out: int, width: int, group: int, dtype: torch.dtype) -> None:
